@@ -1,0 +1,369 @@
+"""ctypes bindings for the two in-tree libraries of aet-cnn on MI355X.
+
+``libach.so``    -- the gfx950 HIP kernels behind ``include/aetcnn_ops.h``
+``libaetcnn.so`` -- the C host layer (network / layer structs) behind
+                    ``include/aetcnn_net.h``
+
+The bindings are plumbing for tests and benchmarks: every computation runs
+in the libraries.  Loading fails loudly when a library has not been built;
+there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.path.join(PKG_DIR, "lib")
+
+ACH_OK = 0
+ACH_EINVAL = -1
+ACH_EWORKSPACE = -2
+ACH_EHIP = -3
+ACH_EUNSUPPORTED = -4
+
+LOGISTIC, RELU, LINEAR, LEAKY = 0, 1, 3, 7
+
+AN_CONVOLUTIONAL, AN_MAXPOOL, AN_AVGPOOL, AN_DROPOUT, AN_SOFTMAX = 0, 1, 2, 3, 4
+
+_vp = C.c_void_p
+_sz = C.c_size_t
+_i = C.c_int
+_f = C.c_float
+_u64 = C.c_uint64
+_u32 = C.c_uint32
+
+
+class ConvDesc(C.Structure):
+    _fields_ = [("batch", _i), ("c", _i), ("h", _i), ("w", _i), ("n", _i),
+                ("size", _i), ("stride", _i), ("pad", _i)]
+
+
+# name -> (restype, argtypes)
+_OPS = {
+    "ach_version": (C.c_char_p, []),
+    "ach_device_count": (_i, []),
+    "ach_set_device": (_i, [_i]),
+    "ach_last_hip_error": (C.c_char_p, []),
+    "ach_malloc": (_i, [C.POINTER(_vp), _sz]),
+    "ach_free": (_i, [_vp]),
+    "ach_host_alloc": (_i, [C.POINTER(_vp), _sz]),
+    "ach_host_free": (_i, [_vp]),
+    "ach_memcpy_h2d": (_i, [_vp, _vp, _sz, _vp]),
+    "ach_memcpy_d2h": (_i, [_vp, _vp, _sz, _vp]),
+    "ach_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
+    "ach_stream_create": (_i, [C.POINTER(_vp)]),
+    "ach_stream_destroy": (_i, [_vp]),
+    "ach_stream_sync": (_i, [_vp]),
+    "ach_device_sync": (_i, []),
+    "ach_event_create": (_i, [C.POINTER(_vp)]),
+    "ach_event_destroy": (_i, [_vp]),
+    "ach_event_record": (_i, [_vp, _vp]),
+    "ach_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
+    "ach_fill": (_i, [_vp, _sz, _f, _vp]),
+    "ach_axpy": (_i, [_sz, _f, _vp, _vp, _vp]),
+    "ach_scal": (_i, [_sz, _f, _vp, _vp]),
+    "ach_gemm": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
+    "ach_im2col": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "ach_col2im": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "ach_conv_out_h": (_i, [C.POINTER(ConvDesc)]),
+    "ach_conv_out_w": (_i, [C.POINTER(ConvDesc)]),
+    "ach_conv_fwd_workspace": (_sz, [C.POINTER(ConvDesc)]),
+    "ach_conv_fwd": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_conv_bwd_data_workspace": (_sz, [C.POINTER(ConvDesc)]),
+    "ach_conv_bwd_data": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_conv_bwd_filter_workspace": (_sz, [C.POINTER(ConvDesc)]),
+    "ach_conv_bwd_filter": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_add_bias": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "ach_bias_grad_workspace": (_sz, [_i, _i, _i]),
+    "ach_bias_grad": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "ach_bn_workspace": (_sz, [_i, _i, _i]),
+    "ach_bn_train_fwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                              _vp, _sz, _vp]),
+    "ach_bn_train_fwd_from_x": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                                     _vp, _sz, _vp]),
+    "ach_bn_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                        _vp, _sz, _vp]),
+    "ach_activate": (_i, [_vp, _sz, _i, _vp]),
+    "ach_gradient": (_i, [_vp, _sz, _i, _vp, _vp]),
+    "ach_maxpool_out": (_i, [_i, _i, _i, _i]),
+    "ach_maxpool_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "ach_maxpool_bwd": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "ach_avgpool_fwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "ach_avgpool_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "ach_softmax_workspace": (_sz, [_i, _i]),
+    "ach_softmax_xent": (_i, [_vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_dropout_uniform": (_f, [_u64, _u32, _u32, _u32]),
+    "ach_dropout_fwd": (_i, [_vp, _sz, _f, _u64, _u32, _u32, _vp]),
+    "ach_dropout_bwd": (_i, [_vp, _sz, _f, _u64, _u32, _u32, _vp]),
+    "ach_conv_update": (_i, [_sz, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _i, _f, _f, _f, _vp]),
+    "ach_sgd_update": (_i, [_sz, _vp, _vp, _f, _f, _f, _vp]),
+}
+
+_NET = {
+    "an_rand_seed": (None, [C.c_uint]),
+    "an_network_create": (_vp, [_i, _i, _i, _i]),
+    "an_add_convolutional": (_i, [_vp, _i, _i, _i, _i, _i, _i]),
+    "an_add_maxpool": (_i, [_vp, _i, _i, _i]),
+    "an_add_avgpool": (_i, [_vp]),
+    "an_add_dropout": (_i, [_vp, _f]),
+    "an_add_softmax": (_i, [_vp, _i, _f]),
+    "an_set_hyper": (None, [_vp, _f, _f, _f]),
+    "an_set_dropout_seed": (None, [_vp, _u64]),
+    "an_finalize": (_i, [_vp]),
+    "an_free": (None, [_vp]),
+    "an_parse_cfg": (_vp, [C.c_char_p]),
+    "an_stream": (_vp, [_vp]),
+    "an_set_input": (_i, [_vp, _vp, _vp]),
+    "an_set_input_device": (_i, [_vp, _vp, _vp]),
+    "an_train_step": (_i, [_vp]),
+    "an_get_loss": (_i, [_vp, C.POINTER(_f)]),
+    "an_train": (_i, [_vp, _vp, _vp, C.POINTER(_f)]),
+    "an_forward": (_i, [_vp, _i]),
+    "an_backward": (_i, [_vp]),
+    "an_update": (_i, [_vp]),
+    "an_n_layers": (_i, [_vp]),
+    "an_batch": (_i, [_vp]),
+    "an_input": (_vp, [_vp]),
+    "an_truth": (_vp, [_vp]),
+    "an_classes": (_i, [_vp]),
+    "an_seen": (_u64, [_vp]),
+    "an_iteration": (_i, [_vp]),
+    "an_layer_buffer": (_vp, [_vp, _i, _i, C.POINTER(_sz)]),
+    "an_step_conv_gflop": (C.c_double, [_vp]),
+}
+
+_libs = {}
+
+
+def _load(name: str, table: dict) -> C.CDLL:
+    if name in _libs:
+        return _libs[name]
+    path = os.path.join(LIB_DIR, name)
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is not built; run __graft_entry__.build() (make -C aet-cnn_amd)")
+    lib = C.CDLL(path)
+    for fn, (res, args) in table.items():
+        f = getattr(lib, fn)
+        f.restype = res
+        f.argtypes = args
+    _libs[name] = lib
+    return lib
+
+
+def ops() -> C.CDLL:
+    """The HIP kernel library (include/aetcnn_ops.h)."""
+    return _load("libach.so", _OPS)
+
+
+def net_lib() -> C.CDLL:
+    """The C host network library (include/aetcnn_net.h)."""
+    ops()
+    return _load("libaetcnn.so", _NET)
+
+
+def op_symbols():
+    return sorted(_OPS)
+
+
+def net_symbols():
+    return sorted(_NET)
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str = ""):
+    if rc != ACH_OK:
+        err = ops().ach_last_hip_error().decode()
+        raise HipError(f"{what} failed with code {rc} ({err})")
+
+
+def gpu_available() -> bool:
+    try:
+        return ops().ach_device_count() > 0
+    except (OSError, RuntimeError):
+        return False
+
+
+class DeviceArray:
+    """A device allocation made through ach_malloc, with numpy transfers."""
+
+    def __init__(self, shape, dtype=np.float32):
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = _vp()
+        check(ops().ach_malloc(C.byref(p), max(self.nbytes, 4)), "ach_malloc")
+        self.ptr = p.value
+        self._owned = True
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray, stream=None) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        d.upload(a, stream)
+        return d
+
+    @classmethod
+    def wrap(cls, ptr: int, shape, dtype=np.float32) -> "DeviceArray":
+        d = cls.__new__(cls)
+        d.shape = tuple(shape) if isinstance(shape, (tuple, list)) else (int(shape),)
+        d.dtype = np.dtype(dtype)
+        d.nbytes = int(np.prod(d.shape, dtype=np.int64)) * d.dtype.itemsize
+        d.ptr = ptr
+        d._owned = False
+        return d
+
+    def upload(self, a: np.ndarray, stream=None):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.nbytes, self.nbytes)
+        check(ops().ach_memcpy_h2d(self.ptr, a.ctypes.data, self.nbytes, stream), "h2d")
+
+    def numpy(self, stream=None) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        check(ops().ach_memcpy_d2h(out.ctypes.data, self.ptr, self.nbytes, stream), "d2h")
+        return out
+
+    def zero(self, stream=None):
+        check(ops().ach_fill(self.ptr, self.nbytes // 4, 0.0, stream), "fill")
+
+    def free(self):
+        if self._owned and self.ptr:
+            ops().ach_free(self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Network:
+    """Thin owner of an ``an_network*`` built layer by layer."""
+
+    def __init__(self, batch: int, h: int, w: int, c: int):
+        self.lib = net_lib()
+        self.h = self.lib.an_network_create(batch, h, w, c)
+        if not self.h:
+            raise ValueError("an_network_create failed")
+        self.batch = batch
+
+    @classmethod
+    def from_cfg(cls, path: str) -> "Network":
+        lib = net_lib()
+        h = lib.an_parse_cfg(path.encode())
+        if not h:
+            raise ValueError(f"an_parse_cfg({path}) failed")
+        n = cls.__new__(cls)
+        n.lib = lib
+        n.h = h
+        n.batch = lib.an_batch(h)
+        return n
+
+    def conv(self, filters, size, stride, pad, activation, bn):
+        r = self.lib.an_add_convolutional(self.h, filters, size, stride, pad, activation, int(bn))
+        if r < 0:
+            raise ValueError(f"an_add_convolutional: {r}")
+        return r
+
+    def maxpool(self, size, stride, padding):
+        r = self.lib.an_add_maxpool(self.h, size, stride, padding)
+        if r < 0:
+            raise ValueError(f"an_add_maxpool: {r}")
+        return r
+
+    def avgpool(self):
+        return self.lib.an_add_avgpool(self.h)
+
+    def dropout(self, p):
+        r = self.lib.an_add_dropout(self.h, p)
+        if r < 0:
+            raise ValueError(f"an_add_dropout: {r}")
+        return r
+
+    def softmax(self, groups=1, temperature=1.0):
+        return self.lib.an_add_softmax(self.h, groups, temperature)
+
+    def hyper(self, lr, momentum, decay):
+        self.lib.an_set_hyper(self.h, lr, momentum, decay)
+
+    def dropout_seed(self, seed):
+        self.lib.an_set_dropout_seed(self.h, seed)
+
+    def finalize(self):
+        check(self.lib.an_finalize(self.h), "an_finalize")
+
+    @property
+    def stream(self):
+        return self.lib.an_stream(self.h)
+
+    def n_layers(self):
+        return self.lib.an_n_layers(self.h)
+
+    def set_input(self, x: np.ndarray, truth: Optional[np.ndarray]):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        t = None if truth is None else np.ascontiguousarray(truth, dtype=np.float32)
+        check(self.lib.an_set_input(self.h, x.ctypes.data, None if t is None else t.ctypes.data),
+              "an_set_input")
+
+    def train(self, x: np.ndarray, truth: np.ndarray) -> float:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        t = np.ascontiguousarray(truth, dtype=np.float32)
+        loss = _f()
+        check(self.lib.an_train(self.h, x.ctypes.data, t.ctypes.data, C.byref(loss)), "an_train")
+        return loss.value
+
+    def train_step(self):
+        check(self.lib.an_train_step(self.h), "an_train_step")
+
+    def loss(self) -> float:
+        v = _f()
+        check(self.lib.an_get_loss(self.h, C.byref(v)), "an_get_loss")
+        return v.value
+
+    def forward(self, train=1):
+        check(self.lib.an_forward(self.h, train), "an_forward")
+
+    def backward(self):
+        check(self.lib.an_backward(self.h), "an_backward")
+
+    def update(self):
+        check(self.lib.an_update(self.h), "an_update")
+
+    def buffer(self, layer: int, which: int) -> Optional[np.ndarray]:
+        n = _sz()
+        p = self.lib.an_layer_buffer(self.h, layer, which, C.byref(n))
+        if not p or n.value == 0:
+            return None
+        dt = np.int32 if which == 14 else np.float32
+        out = np.empty(n.value, dtype=dt)
+        check(ops().ach_memcpy_d2h(out.ctypes.data, p, out.nbytes, self.stream), "d2h")
+        return out
+
+    def set_buffer(self, layer: int, which: int, values: np.ndarray):
+        n = _sz()
+        p = self.lib.an_layer_buffer(self.h, layer, which, C.byref(n))
+        v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        assert p and v.size == n.value, (layer, which, v.size, n.value)
+        check(ops().ach_memcpy_h2d(p, v.ctypes.data, v.nbytes, self.stream), "h2d")
+
+    def conv_gflop(self) -> float:
+        return self.lib.an_step_conv_gflop(self.h)
+
+    def close(self):
+        if self.h:
+            self.lib.an_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,639 @@
+// Bandwidth-bound operators and runtime plumbing behind include/aetcnn_ops.h.
+//
+// Reference behaviour replaced (paths under /root/reference/src/com/ai/dnn/):
+//   BLAS-1 fill/axpy/scal     mtcs/MtcsTool.c:33-132, DnnUtils.c:428-432
+//   im2col / col2im           Im2Col.c:65-103, 155-192
+//   add bias / bias gradient  IOData.c:43-55, BiasData.c:40-57
+//   activate / gradientArray  Activation.c:160-179, 233-239
+//   max-pool fwd / bwd        MaxPoolLayer.c:237-272, 318-331
+//   global avg-pool fwd / bwd AvgPoolLayer.c:29-46, 73-88
+//   softmax + cross-entropy   SoftMaxLayer.c:47-119
+//   dropout                   DropoutLayer.c:55-86
+//   SGD momentum/decay update ConvolutionalLayer.c:959-980
+// All elementwise kernels are grid-stride loops over coalesced addresses;
+// reductions are per-block in a fixed order (no float atomics), so every run
+// is bit-reproducible.
+#include "common.hpp"
+
+#include <float.h>
+#include <stdio.h>
+#include <string.h>
+
+namespace ach {
+
+static thread_local char g_last_err[256] = "no error";
+
+void set_hip_error(hipError_t e)
+{
+    snprintf(g_last_err, sizeof(g_last_err), "%s: %s", hipGetErrorName(e),
+             hipGetErrorString(e));
+}
+
+// ---- BLAS-1 ----------------------------------------------------------------
+__global__ void k_fill(float *x, size_t n, float v)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        x[i] = v;
+}
+
+__global__ void k_axpy(size_t n, float a, const float *__restrict__ x, float *__restrict__ y)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] += a * x[i];
+}
+
+__global__ void k_scal(size_t n, float a, float *x)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        x[i] *= a;
+}
+
+// ---- im2col / col2im (one image) ----------------------------------------------
+__global__ void k_im2col(const float *__restrict__ im, int C, int H, int W, int kh, int kw,
+                         int ph, int pw, int sh, int sw, int OH, int OW,
+                         float *__restrict__ col)
+{
+    const size_t total = (size_t)C * kh * kw * OH * OW;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int ow = (int)(i % OW);
+        size_t r = i / OW;
+        const int oh = (int)(r % OH);
+        r /= OH;
+        const int kj = (int)(r % kw);
+        r /= kw;
+        const int ki = (int)(r % kh);
+        const int c = (int)(r / kh);
+        const int ih = oh * sh - ph + ki, iw = ow * sw - pw + kj;
+        col[i] = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                     ? im[((size_t)c * H + ih) * W + iw]
+                     : 0.f;
+    }
+}
+
+// Gather form of col2im: every image pixel adds its column entries in the
+// reference's (ki, kj) scan order starting from zero -> bit-identical sums.
+__global__ void k_col2im(const float *__restrict__ col, int C, int H, int W, int kh, int kw,
+                         int ph, int pw, int sh, int sw, int OH, int OW,
+                         float *__restrict__ im)
+{
+    const size_t total = (size_t)C * H * W;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int w = (int)(i % W);
+        const int h = (int)((i / W) % H);
+        const int c = (int)(i / ((size_t)W * H));
+        float v = 0.f;
+        for (int ki = 0; ki < kh; ++ki) {
+            const int t = h + ph - ki;
+            if (t < 0 || t % sh) continue;
+            const int oh = t / sh;
+            if (oh >= OH) continue;
+            for (int kj = 0; kj < kw; ++kj) {
+                const int u = w + pw - kj;
+                if (u < 0 || u % sw) continue;
+                const int ow = u / sw;
+                if (ow >= OW) continue;
+                v += col[((((size_t)c * kh + ki) * kw + kj) * OH + oh) * OW + ow];
+            }
+        }
+        im[i] = v;
+    }
+}
+
+// ---- bias --------------------------------------------------------------------
+__global__ void k_add_bias(float *out, const float *__restrict__ b, size_t total, int n,
+                           int spatial)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x)
+        out[i] += b[(i / spatial) % n];
+}
+
+// one block per channel; double accumulation; updates[c] += sum
+__global__ void __launch_bounds__(256) k_bias_grad(float *updates, const float *__restrict__ d,
+                                                   int batch, int n, int spatial)
+{
+    __shared__ double sh[4];
+    const int c = blockIdx.x;
+    double s = 0;
+    const int tot = batch * spatial;
+    for (int i = threadIdx.x; i < tot; i += 256) {
+        const int b = i / spatial, q = i - b * spatial;
+        s += d[((size_t)b * n + c) * spatial + q];
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) updates[c] += (float)(sh[0] + sh[1] + sh[2] + sh[3]);
+}
+
+// ---- activations ---------------------------------------------------------------
+__global__ void k_activate(float *x, size_t n, int act)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        x[i] = act_forward(x[i], act);
+}
+
+__global__ void k_gradient(const float *__restrict__ y, size_t n, int act, float *d)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        d[i] *= act_gradient(y[i], act);
+}
+
+// ---- max-pool --------------------------------------------------------------------
+__global__ void k_maxpool_fwd(const float *__restrict__ in, int batch, int C, int H, int W,
+                              int size, int stride, int pad, int OH, int OW,
+                              float *__restrict__ out, int32_t *__restrict__ idx)
+{
+    const size_t total = (size_t)batch * C * OH * OW;
+    const int off = -pad / 2;
+    for (size_t o = blockIdx.x * (size_t)blockDim.x + threadIdx.x; o < total;
+         o += (size_t)gridDim.x * blockDim.x) {
+        const int j = (int)(o % OW);
+        const int i = (int)((o / OW) % OH);
+        const size_t bc = o / ((size_t)OW * OH);
+        float mx = -FLT_MAX;
+        int mi = -1;
+        for (int n = 0; n < size; ++n)
+            for (int m = 0; m < size; ++m) {
+                const int ch = off + i * stride + n, cw = off + j * stride + m;
+                const int index = cw + W * (ch + H * (int)bc);
+                const bool valid = ch >= 0 && ch < H && cw >= 0 && cw < W;
+                const float v = valid ? in[index] : -FLT_MAX;
+                mi = (v > mx) ? index : mi;
+                mx = (v > mx) ? v : mx;
+            }
+        out[o] = mx;
+        if (idx) idx[o] = mi;
+    }
+}
+
+__device__ __forceinline__ int floor_div(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+
+// Gather: each input pixel visits, in ascending output order, the outputs
+// whose window holds it and adds the ones whose argmax is this pixel.
+__global__ void k_maxpool_bwd(const float *__restrict__ dout, const int32_t *__restrict__ idx,
+                              int batch, int C, int H, int W, int size, int stride, int pad,
+                              int OH, int OW, float *din)
+{
+    const size_t total = (size_t)batch * C * H * W;
+    const int off = -pad / 2;
+    for (size_t p = blockIdx.x * (size_t)blockDim.x + threadIdx.x; p < total;
+         p += (size_t)gridDim.x * blockDim.x) {
+        const int w = (int)(p % W);
+        const int h = (int)((p / W) % H);
+        const size_t bc = p / ((size_t)W * H);
+        // output row i covers rows off + i*stride .. + size-1
+        int i0 = floor_div(h - off - size, stride) + 1, i1 = floor_div(h - off, stride);
+        int j0 = floor_div(w - off - size, stride) + 1, j1 = floor_div(w - off, stride);
+        i0 = max(i0, 0); j0 = max(j0, 0);
+        i1 = min(i1, OH - 1); j1 = min(j1, OW - 1);
+        float v = din[p];
+        const size_t obase = bc * OH * OW;
+        for (int i = i0; i <= i1; ++i)
+            for (int j = j0; j <= j1; ++j) {
+                const size_t o = obase + (size_t)i * OW + j;
+                if (idx[o] == (int32_t)p) v += dout[o];
+            }
+        din[p] = v;
+    }
+}
+
+// ---- global average pool -------------------------------------------------------
+__global__ void k_avgpool_fwd(const float *__restrict__ in, int bc_total, int HW,
+                              float *__restrict__ out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= bc_total) return;
+    const float *p = in + (size_t)i * HW;
+    float s = 0.f;
+    for (int k = 0; k < HW; ++k) s += p[k];
+    out[i] = s / HW;
+}
+
+__global__ void k_avgpool_bwd(const float *__restrict__ dout, size_t total, int HW,
+                              float *din)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x)
+        din[i] += dout[i / HW] / HW;
+}
+
+// ---- softmax + cross-entropy -------------------------------------------------------
+// One wave per (image, group) row.  e = (float)exp(double(x/T - max/T)) as
+// the reference (double exp of a float argument); p = e/sum.
+__global__ void __launch_bounds__(256) k_softmax_xent(const float *__restrict__ in, int rows,
+                                                      int n, float T,
+                                                      const float *__restrict__ truth,
+                                                      float *__restrict__ out,
+                                                      float *__restrict__ delta,
+                                                      float *__restrict__ err,
+                                                      float *__restrict__ row_err)
+{
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *x = in + (size_t)row * n;
+    float *o = out + (size_t)row * n;
+    float mx = -FLT_MAX;
+    for (int i = lane; i < n; i += 64) mx = fmaxf(mx, x[i]);
+    mx = wave_max(mx);
+    const float lt = mx / T;
+    float s = 0.f;
+    for (int i = lane; i < n; i += 64) {
+        const float e = (float)exp((double)(x[i] / T - lt));
+        o[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    float es = 0.f;
+    for (int i = lane; i < n; i += 64) {
+        const float p = o[i] / s;
+        o[i] = p;
+        if (truth) {
+            const float t = truth[(size_t)row * n + i];
+            const float e = (t != 0.f) ? -logf(p) : 0.f;
+            err[(size_t)row * n + i] = e;
+            delta[(size_t)row * n + i] = t - p;
+            es += e;
+        }
+    }
+    if (truth) {
+        es = wave_sum(es);
+        if (lane == 0) row_err[row] = es;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_sum_rows(const float *__restrict__ row_err, int rows,
+                                                  float *cost)
+{
+    __shared__ double sh[4];
+    double s = 0;
+    for (int i = threadIdx.x; i < rows; i += 256) s += row_err[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) *cost = (float)(sh[0] + sh[1] + sh[2] + sh[3]);
+}
+
+// ---- dropout -------------------------------------------------------------------------
+__global__ void k_dropout(float *x, size_t n, float p, float scale, uint64_t seed,
+                          uint32_t iter, uint32_t layer)
+{
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const float r = dropout_uniform(seed, iter, layer, (uint32_t)i);
+        x[i] = (r < p) ? 0.f : x[i] * scale;
+    }
+}
+
+// ---- SGD ---------------------------------------------------------------------------------
+// v += decay_coef*w; w += lr_coef*v; v *= momentum  (WeightData.c:45-78)
+__global__ void k_sgd(size_t n, float *__restrict__ w, float *__restrict__ v, float dc,
+                      float lc, float mom)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t n4 = n >> 2;
+    float4 *w4 = reinterpret_cast<float4 *>(w);
+    float4 *v4 = reinterpret_cast<float4 *>(v);
+    const bool vec = ((((uintptr_t)w) | ((uintptr_t)v)) & 15) == 0;
+    size_t done = 0;
+    if (vec) {
+        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+            float4 a = w4[i], u = v4[i];
+            u.x += dc * a.x; u.y += dc * a.y; u.z += dc * a.z; u.w += dc * a.w;
+            a.x += lc * u.x; a.y += lc * u.y; a.z += lc * u.z; a.w += lc * u.w;
+            u.x *= mom; u.y *= mom; u.z *= mom; u.w *= mom;
+            w4[i] = a;
+            v4[i] = u;
+        }
+        done = n4 * 4;
+    }
+    for (size_t i = done + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+        float u = v[i] + dc * w[i];
+        w[i] += lc * u;
+        v[i] = u * mom;
+    }
+}
+
+}  // namespace ach
+
+using namespace ach;
+
+extern "C" {
+
+const char *ach_version(void) { return "aetcnn-hip gfx950 0.1"; }
+
+int ach_device_count(void)
+{
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int ach_set_device(int dev) { return check(hipSetDevice(dev)); }
+const char *ach_last_hip_error(void) { return g_last_err; }
+
+int ach_malloc(void **ptr, size_t bytes)
+{
+    if (!ptr) return ACH_EINVAL;
+    *ptr = nullptr;
+    if (bytes == 0) bytes = 256;
+    return check(hipMalloc(ptr, bytes));
+}
+
+int ach_free(void *ptr) { return ptr ? check(hipFree(ptr)) : ACH_OK; }
+
+int ach_host_alloc(void **ptr, size_t bytes)
+{
+    if (!ptr) return ACH_EINVAL;
+    return check(hipHostMalloc(ptr, bytes ? bytes : 64, hipHostMallocDefault));
+}
+
+int ach_host_free(void *ptr) { return ptr ? check(hipHostFree(ptr)) : ACH_OK; }
+
+int ach_memcpy_h2d(void *dst, const void *src, size_t bytes, ach_stream_t s)
+{
+    if (!bytes) return ACH_OK;
+    if (!dst || !src) return ACH_EINVAL;
+    int rc = check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(s)));
+    if (rc) return rc;
+    return check(hipStreamSynchronize(as_stream(s)));
+}
+
+int ach_memcpy_d2h(void *dst, const void *src, size_t bytes, ach_stream_t s)
+{
+    if (!bytes) return ACH_OK;
+    if (!dst || !src) return ACH_EINVAL;
+    int rc = check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(s)));
+    if (rc) return rc;
+    return check(hipStreamSynchronize(as_stream(s)));
+}
+
+int ach_memcpy_d2d(void *dst, const void *src, size_t bytes, ach_stream_t s)
+{
+    if (!bytes) return ACH_OK;
+    if (!dst || !src) return ACH_EINVAL;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(s)));
+}
+
+int ach_stream_create(ach_stream_t *s)
+{
+    if (!s) return ACH_EINVAL;
+    hipStream_t st;
+    int rc = check(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    *s = rc ? nullptr : (ach_stream_t)st;
+    return rc;
+}
+
+int ach_stream_destroy(ach_stream_t s) { return s ? check(hipStreamDestroy(as_stream(s))) : ACH_OK; }
+int ach_stream_sync(ach_stream_t s) { return check(hipStreamSynchronize(as_stream(s))); }
+int ach_device_sync(void) { return check(hipDeviceSynchronize()); }
+
+int ach_event_create(void **ev)
+{
+    if (!ev) return ACH_EINVAL;
+    hipEvent_t e;
+    int rc = check(hipEventCreate(&e));
+    *ev = rc ? nullptr : (void *)e;
+    return rc;
+}
+
+int ach_event_destroy(void *ev) { return ev ? check(hipEventDestroy((hipEvent_t)ev)) : ACH_OK; }
+
+int ach_event_record(void *ev, ach_stream_t s)
+{
+    if (!ev) return ACH_EINVAL;
+    return check(hipEventRecord((hipEvent_t)ev, as_stream(s)));
+}
+
+int ach_event_elapsed_ms(void *a, void *b, float *ms)
+{
+    if (!a || !b || !ms) return ACH_EINVAL;
+    int rc = check(hipEventSynchronize((hipEvent_t)b));
+    if (rc) return rc;
+    return check(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+}
+
+int ach_fill(float *x, size_t n, float v, ach_stream_t s)
+{
+    if (!n) return ACH_OK;
+    if (!x) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_fill, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), x, n, v);
+    return check_launch();
+}
+
+int ach_axpy(size_t n, float a, const float *x, float *y, ach_stream_t s)
+{
+    if (!n) return ACH_OK;
+    if (!x || !y) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_axpy, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), n, a, x, y);
+    return check_launch();
+}
+
+int ach_scal(size_t n, float a, float *x, ach_stream_t s)
+{
+    if (!n) return ACH_OK;
+    if (!x) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_scal, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), n, a, x);
+    return check_launch();
+}
+
+int ach_im2col(const float *im, int C, int H, int W, int kh, int kw, int ph, int pw, int sh,
+               int sw, float *col, ach_stream_t s)
+{
+    if (!im || !col || C <= 0 || H <= 0 || W <= 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 ||
+        ph < 0 || pw < 0)
+        return ACH_EINVAL;
+    const int OH = (H + 2 * ph - kh) / sh + 1, OW = (W + 2 * pw - kw) / sw + 1;
+    if (OH <= 0 || OW <= 0) return ACH_EINVAL;
+    const size_t tot = (size_t)C * kh * kw * OH * OW;
+    hipLaunchKernelGGL(k_im2col, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), im, C, H,
+                       W, kh, kw, ph, pw, sh, sw, OH, OW, col);
+    return check_launch();
+}
+
+int ach_col2im(const float *col, int C, int H, int W, int kh, int kw, int ph, int pw, int sh,
+               int sw, float *im, ach_stream_t s)
+{
+    if (!im || !col || C <= 0 || H <= 0 || W <= 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 ||
+        ph < 0 || pw < 0)
+        return ACH_EINVAL;
+    const int OH = (H + 2 * ph - kh) / sh + 1, OW = (W + 2 * pw - kw) / sw + 1;
+    if (OH <= 0 || OW <= 0) return ACH_EINVAL;
+    const size_t tot = (size_t)C * H * W;
+    hipLaunchKernelGGL(k_col2im, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), col, C, H,
+                       W, kh, kw, ph, pw, sh, sw, OH, OW, im);
+    return check_launch();
+}
+
+int ach_add_bias(float *out, const float *b, int batch, int n, int spatial, ach_stream_t s)
+{
+    if (!out || !b || batch <= 0 || n <= 0 || spatial <= 0) return ACH_EINVAL;
+    const size_t tot = (size_t)batch * n * spatial;
+    hipLaunchKernelGGL(k_add_bias, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), out, b,
+                       tot, n, spatial);
+    return check_launch();
+}
+
+size_t ach_bias_grad_workspace(int, int, int) { return 0; }
+
+int ach_bias_grad(float *updates, const float *delta, int batch, int n, int spatial, void *,
+                  size_t, ach_stream_t s)
+{
+    if (!updates || !delta || batch <= 0 || n <= 0 || spatial <= 0) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_bias_grad, dim3(n), dim3(256), 0, as_stream(s), updates, delta, batch,
+                       n, spatial);
+    return check_launch();
+}
+
+int ach_activate(float *x, size_t n, int act, ach_stream_t s)
+{
+    if (act == ACH_LINEAR || n == 0) return ACH_OK;  // IOData.c:68-69: LINEAR is skipped
+    if (!x) return ACH_EINVAL;
+    if (act != ACH_LEAKY && act != ACH_RELU && act != ACH_LOGISTIC) return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL(k_activate, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), x, n, act);
+    return check_launch();
+}
+
+int ach_gradient(const float *y, size_t n, int act, float *d, ach_stream_t s)
+{
+    if (n == 0) return ACH_OK;
+    if (!y || !d) return ACH_EINVAL;
+    if (act == ACH_LINEAR) return ACH_OK;  // linear_gradient == 1
+    if (act != ACH_LEAKY && act != ACH_RELU && act != ACH_LOGISTIC) return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL(k_gradient, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), y, n, act,
+                       d);
+    return check_launch();
+}
+
+int ach_maxpool_out(int in, int size, int stride, int padding)
+{
+    if (size <= 0 || stride <= 0) return -1;
+    return (in + padding - size) / stride + 1;
+}
+
+static bool pool_ok(int batch, int c, int h, int w, int size, int stride, int pad)
+{
+    if (batch <= 0 || c <= 0 || h <= 0 || w <= 0 || size <= 0 || stride <= 0 || pad < 0)
+        return false;
+    if ((double)batch * c * h * w >= 2147483647.0) return false;  // int32 indexes
+    return ach_maxpool_out(h, size, stride, pad) > 0 && ach_maxpool_out(w, size, stride, pad) > 0;
+}
+
+int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, int stride,
+                    int pad, float *out, int32_t *idx, ach_stream_t s)
+{
+    if (!in || !out || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
+    const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
+    const size_t tot = (size_t)batch * c * OH * OW;
+    hipLaunchKernelGGL(k_maxpool_fwd, dim3(grid_for(tot, 256, 256u * 64u)), dim3(256), 0,
+                       as_stream(s), in, batch, c, h, w, size, stride, pad, OH, OW, out, idx);
+    return check_launch();
+}
+
+int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
+                    int size, int stride, int pad, float *din, ach_stream_t s)
+{
+    if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
+    const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
+    const size_t tot = (size_t)batch * c * h * w;
+    hipLaunchKernelGGL(k_maxpool_bwd, dim3(grid_for(tot, 256, 256u * 64u)), dim3(256), 0,
+                       as_stream(s), dout, idx, batch, c, h, w, size, stride, pad, OH, OW, din);
+    return check_launch();
+}
+
+int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out, ach_stream_t s)
+{
+    if (!in || !out || batch <= 0 || c <= 0 || spatial <= 0) return ACH_EINVAL;
+    const int bc = batch * c;
+    hipLaunchKernelGGL(k_avgpool_fwd, dim3((bc + 255) / 256), dim3(256), 0, as_stream(s), in, bc,
+                       spatial, out);
+    return check_launch();
+}
+
+int ach_avgpool_bwd(const float *dout, int batch, int c, int spatial, float *din, ach_stream_t s)
+{
+    if (!dout || !din || batch <= 0 || c <= 0 || spatial <= 0) return ACH_EINVAL;
+    const size_t tot = (size_t)batch * c * spatial;
+    hipLaunchKernelGGL(k_avgpool_bwd, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), dout,
+                       tot, spatial, din);
+    return check_launch();
+}
+
+size_t ach_softmax_workspace(int batch, int groups)
+{
+    if (batch <= 0 || groups <= 0) return 0;
+    return (size_t)batch * groups * sizeof(float);
+}
+
+int ach_softmax_xent(const float *in, int batch, int inputs, int groups, float T,
+                     const float *truth, float *out, float *delta, float *err, float *cost,
+                     void *ws, size_t ws_bytes, ach_stream_t s)
+{
+    if (!in || !out || batch <= 0 || inputs <= 0 || groups <= 0 || inputs % groups) return ACH_EINVAL;
+    if (truth && (!delta || !err || !cost)) return ACH_EINVAL;
+    const int rows = batch * groups, n = inputs / groups;
+    if (truth && (!ws || ws_bytes < ach_softmax_workspace(batch, groups))) return ACH_EWORKSPACE;
+    hipStream_t st = as_stream(s);
+    hipLaunchKernelGGL(k_softmax_xent, dim3((rows + 3) / 4), dim3(256), 0, st, in, rows, n, T,
+                       truth, out, delta, err, (float *)ws);
+    int rc = check_launch();
+    if (rc || !truth) return rc;
+    hipLaunchKernelGGL(k_sum_rows, dim3(1), dim3(256), 0, st, (const float *)ws, rows, cost);
+    return check_launch();
+}
+
+float ach_dropout_uniform(uint64_t seed, uint32_t iter, uint32_t layer, uint32_t i)
+{
+    return dropout_uniform(seed, iter, layer, i);
+}
+
+int ach_dropout_fwd(float *x, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
+                    ach_stream_t s)
+{
+    if (n == 0) return ACH_OK;
+    if (!x || !(p >= 0.f && p < 1.f) || n > 0xffffffffull) return ACH_EINVAL;
+    const float scale = (float)(1. / (1.0 - p));
+    hipLaunchKernelGGL(k_dropout, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), x, n, p,
+                       scale, seed, iter, layer);
+    return check_launch();
+}
+
+int ach_dropout_bwd(float *d, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
+                    ach_stream_t s)
+{
+    return ach_dropout_fwd(d, n, p, seed, iter, layer, s);
+}
+
+int ach_sgd_update(size_t n, float *w, float *v, float dc, float lc, float mom, ach_stream_t s)
+{
+    if (n == 0) return ACH_OK;
+    if (!w || !v) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_sgd, dim3(grid_for((n + 3) / 4, 256, 256u * 32u)), dim3(256), 0,
+                       as_stream(s), n, w, v, dc, lc, mom);
+    return check_launch();
+}
+
+int ach_conv_update(size_t nweights, float *weights, float *weight_updates, size_t n,
+                    float *biases, float *bias_updates, float *scales, float *scale_updates,
+                    int batch, float lr, float momentum, float decay, ach_stream_t s)
+{
+    if (batch <= 0) return ACH_EINVAL;
+    if ((scales == nullptr) != (scale_updates == nullptr)) return ACH_EINVAL;
+    const float a1 = -decay * batch;
+    const float a2 = lr / batch;
+    int rc = ach_sgd_update(nweights, weights, weight_updates, a1, a2, momentum, s);
+    if (rc) return rc;
+    rc = ach_sgd_update(n, biases, bias_updates, 0.f, a2, momentum, s);
+    if (rc || !scales) return rc;
+    return ach_sgd_update(n, scales, scale_updates, 0.f, a2, momentum, s);
+}
+
+}  // extern "C"

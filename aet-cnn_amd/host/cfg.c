@@ -1,0 +1,211 @@
+/*
+ * cfg.c -- darknet-style .cfg files -> an_network.  Follows the reference's
+ * ConfigFile (ConfigFile.c:12-208, INI groups and key=value pairs, '#' and
+ * ';' comments) and the defaults of NetworkFactory (paths relative to
+ * /root/reference/src/com/ai/dnn/):
+ *   [net]            parseNetOption NetworkFactory.c:671-700
+ *                    batch=1 learning_rate=.001 momentum=.9 decay=.0001
+ *                    subdivisions=1 (batch /= subdivisions)
+ *   [convolutional]  createConvolutional NetworkFactory.c:77-103
+ *                    filters=1 size=1 stride=1 pad=0 padding=0
+ *                    (pad=1 -> padding=size/2) activation=logistic
+ *                    batch_normalize=0
+ *   [maxpool]        createMaxPool NetworkFactory.c:543-548
+ *                    stride=1 size=stride padding=size-1
+ *   [avgpool]        createAvgPool NetworkFactory.c:572-584
+ *   [dropout]        createDropoutLayer NetworkFactory.c:328-329  probability=.2
+ *   [softmax]        createSoftMax NetworkFactory.c:586-601 groups=1 temperature=1
+ * Keys this build does not implement (xnor, groups>1 convs, dilation,
+ * antialiasing, ...) are rejected when set to a non-default value.
+ */
+#include "aetcnn_net.h"
+
+#include <ctype.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define CFG_MAX_KV 64
+
+typedef struct {
+    char name[64];
+    int nkv;
+    char key[CFG_MAX_KV][64];
+    char val[CFG_MAX_KV][128];
+} cfg_group;
+
+static char *trim(char *s)
+{
+    while (*s && isspace((unsigned char)*s)) ++s;
+    char *e = s + strlen(s);
+    while (e > s && isspace((unsigned char)e[-1])) *--e = 0;
+    return s;
+}
+
+static const char *find(const cfg_group *g, const char *k)
+{
+    for (int i = 0; i < g->nkv; ++i)
+        if (!strcmp(g->key[i], k)) return g->val[i];
+    return NULL;
+}
+
+static int geti(const cfg_group *g, const char *k, int def)
+{
+    const char *v = find(g, k);
+    return v ? atoi(v) : def;
+}
+
+static float getf(const cfg_group *g, const char *k, float def)
+{
+    const char *v = find(g, k);
+    return v ? (float)atof(v) : def;
+}
+
+static int activation_id(const char *s)
+{
+    /* Activation.getActivation (Activation.c:104-120) names */
+    if (!strcmp(s, "logistic")) return ACH_LOGISTIC;
+    if (!strcmp(s, "relu")) return ACH_RELU;
+    if (!strcmp(s, "linear")) return ACH_LINEAR;
+    if (!strcmp(s, "leaky")) return ACH_LEAKY;
+    return -1;
+}
+
+static int read_groups(const char *path, cfg_group **out, int *count)
+{
+    FILE *f = fopen(path, "r");
+    if (!f) {
+        fprintf(stderr, "an_parse_cfg: cannot open %s\n", path);
+        return -1;
+    }
+    int cap = 16, n = 0;
+    cfg_group *gs = (cfg_group *)calloc(cap, sizeof(cfg_group));
+    char line[512];
+    int lineno = 0;
+    while (fgets(line, sizeof(line), f)) {
+        ++lineno;
+        char *s = trim(line);
+        if (!*s || *s == '#' || *s == ';') continue;
+        if (*s == '[') {
+            char *e = strchr(s, ']');
+            if (!e) goto bad;
+            *e = 0;
+            if (n == cap) {
+                cap *= 2;
+                gs = (cfg_group *)realloc(gs, sizeof(cfg_group) * cap);
+            }
+            memset(&gs[n], 0, sizeof(cfg_group));
+            snprintf(gs[n].name, sizeof(gs[n].name), "%s", trim(s + 1));
+            ++n;
+            continue;
+        }
+        char *eq = strchr(s, '=');
+        if (!eq || n == 0) goto bad;
+        *eq = 0;
+        cfg_group *g = &gs[n - 1];
+        if (g->nkv == CFG_MAX_KV) goto bad;
+        snprintf(g->key[g->nkv], sizeof(g->key[0]), "%s", trim(s));
+        snprintf(g->val[g->nkv], sizeof(g->val[0]), "%s", trim(eq + 1));
+        g->nkv++;
+    }
+    fclose(f);
+    *out = gs;
+    *count = n;
+    return 0;
+bad:
+    fprintf(stderr, "an_parse_cfg: %s:%d: cannot parse line\n", path, lineno);
+    fclose(f);
+    free(gs);
+    return -1;
+}
+
+static int unsupported(const cfg_group *g, const char *key, int def)
+{
+    const char *v = find(g, key);
+    if (v && atoi(v) != def) {
+        fprintf(stderr, "an_parse_cfg: [%s] %s=%s is not supported\n", g->name, key, v);
+        return 1;
+    }
+    return 0;
+}
+
+an_network *an_parse_cfg(const char *path)
+{
+    cfg_group *gs = NULL;
+    int ng = 0;
+    if (!path || read_groups(path, &gs, &ng)) return NULL;
+    an_network *net = NULL;
+    if (ng == 0 || (strcmp(gs[0].name, "net") && strcmp(gs[0].name, "network"))) {
+        fprintf(stderr, "an_parse_cfg: first section must be [net] or [network]\n");
+        goto fail;
+    }
+    {
+        const cfg_group *g = &gs[0];
+        int batch = geti(g, "batch", 1);
+        const int subdivs = geti(g, "subdivisions", 1);
+        if (subdivs <= 0) goto fail;
+        batch /= subdivs;
+        if (batch < 1) batch = 1;
+        const int h = geti(g, "height", 0), w = geti(g, "width", 0), c = geti(g, "channels", 0);
+        net = an_network_create(batch, h, w, c);
+        if (!net) {
+            fprintf(stderr, "an_parse_cfg: [net] needs height, width and channels\n");
+            goto fail;
+        }
+        an_set_hyper(net, getf(g, "learning_rate", .001f), getf(g, "momentum", .9f),
+                     getf(g, "decay", .0001f));
+    }
+    for (int i = 1; i < ng; ++i) {
+        const cfg_group *g = &gs[i];
+        int rc;
+        if (!strcmp(g->name, "convolutional") || !strcmp(g->name, "conv")) {
+            if (unsupported(g, "groups", 1) || unsupported(g, "dilation", 1) ||
+                unsupported(g, "xnor", 0) || unsupported(g, "binary", 0) ||
+                unsupported(g, "antialiasing", 0) || unsupported(g, "cbn", 0))
+                goto fail;
+            const int size = geti(g, "size", 1);
+            const int stride = geti(g, "stride", 1);
+            int padding = geti(g, "padding", 0);
+            if (geti(g, "pad", 0)) padding = size / 2;
+            const char *an = find(g, "activation");
+            const int act = activation_id(an ? an : "logistic");
+            if (act < 0) {
+                fprintf(stderr, "an_parse_cfg: activation %s is not supported\n", an);
+                goto fail;
+            }
+            rc = an_add_convolutional(net, geti(g, "filters", 1), size, stride, padding, act,
+                                      geti(g, "batch_normalize", 0));
+        } else if (!strcmp(g->name, "maxpool") || !strcmp(g->name, "max")) {
+            if (unsupported(g, "maxpool_depth", 0) || unsupported(g, "antialiasing", 0))
+                goto fail;
+            const int stride = geti(g, "stride", 1);
+            const int size = geti(g, "size", stride);
+            rc = an_add_maxpool(net, size, stride, geti(g, "padding", size - 1));
+        } else if (!strcmp(g->name, "avgpool") || !strcmp(g->name, "avg")) {
+            rc = an_add_avgpool(net);
+        } else if (!strcmp(g->name, "dropout")) {
+            if (unsupported(g, "dropblock", 0)) goto fail;
+            rc = an_add_dropout(net, getf(g, "probability", .2f));
+        } else if (!strcmp(g->name, "softmax") || !strcmp(g->name, "soft")) {
+            rc = an_add_softmax(net, geti(g, "groups", 1), getf(g, "temperature", 1.f));
+        } else {
+            fprintf(stderr, "an_parse_cfg: layer type [%s] is not supported\n", g->name);
+            goto fail;
+        }
+        if (rc < 0) {
+            fprintf(stderr, "an_parse_cfg: cannot build [%s] (section %d): code %d\n", g->name,
+                    i, rc);
+            goto fail;
+        }
+    }
+    if (an_finalize(net) != ACH_OK) {
+        fprintf(stderr, "an_parse_cfg: finalize failed\n");
+        goto fail;
+    }
+    free(gs);
+    return net;
+fail:
+    free(gs);
+    an_free(net);
+    return NULL;
+}

@@ -1,0 +1,747 @@
+/*
+ * network.c -- the reference's network runtime and layer objects as plain C,
+ * driving the HIP kernels through aetcnn_ops.h only.  Paths are relative to
+ * /root/reference/src/com/ai/dnn/.
+ *
+ * Memory: every per-layer tensor lives in one device arena; all conv weights
+ * (and their momentum buffers) are contiguous so the SGD update of the whole
+ * network is two launches (decayed weights; biases + scales without decay)
+ * instead of the reference GPU path's five launches per layer
+ * (mtcs/MtcsConvLayer.c:618-630).
+ */
+#include "aetcnn_net.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define AN_CHECK(expr)                \
+    do {                              \
+        int rc_ = (expr);             \
+        if (rc_ != ACH_OK) return rc_; \
+    } while (0)
+
+struct an_network {
+    int batch, h, w, c, inputs;
+    int n, cap;
+    an_layer **layers;
+    float learning_rate, momentum, decay;
+    uint64_t dropout_seed;
+    int cur_iteration;
+    uint64_t seen;
+    int finalized;
+    ach_stream_t stream;
+    /* device memory */
+    void *arena;
+    size_t arena_bytes;
+    float *workspace;
+    size_t workspace_bytes;
+    float *input, *truth;
+    int classes;
+    float *wflat, *vflat;          /* all conv weights / weight_updates     */
+    size_t nweights_total;
+    float *bflat, *bvflat;         /* biases (+scales) / their updates       */
+    size_t nbias_total;
+    float *zero_region;            /* deltas that need zeroing per forward */
+    size_t zero_floats;
+    /* host copies of initial parameters until finalize */
+    float **init_w;
+};
+
+/* ---- randUniform over glibc rand() (DnnUtils.c:196-209) ------------------- */
+void an_rand_seed(unsigned seed) { srand(seed); }
+
+static float rand_uniform(float min, float max)
+{
+    if (max < min) {
+        float s = min;
+        min = max;
+        max = s;
+    }
+    return ((float)rand() / RAND_MAX * (max - min)) + min;
+}
+
+an_network *an_network_create(int batch, int h, int w, int c)
+{
+    if (batch <= 0 || h <= 0 || w <= 0 || c <= 0) return NULL;
+    an_network *net = (an_network *)calloc(1, sizeof(an_network));
+    if (!net) return NULL;
+    net->batch = batch;
+    net->h = h;
+    net->w = w;
+    net->c = c;
+    net->inputs = h * w * c;
+    /* parseNetOption defaults (NetworkFactory.c:677-685) */
+    net->learning_rate = .001f;
+    net->momentum = .9f;
+    net->decay = .0001f;
+    net->dropout_seed = 0x5eed;
+    return net;
+}
+
+static an_layer *push_layer(an_network *net)
+{
+    if (net->finalized) return NULL;
+    if (net->n == net->cap) {
+        int cap = net->cap ? 2 * net->cap : 16;
+        an_layer **nl = (an_layer **)realloc(net->layers, sizeof(an_layer *) * cap);
+        float **ni = (float **)realloc(net->init_w, sizeof(float *) * cap);
+        if (!nl || !ni) return NULL;
+        net->layers = nl;
+        net->init_w = ni;
+        net->cap = cap;
+    }
+    an_layer *l = (an_layer *)calloc(1, sizeof(an_layer));
+    if (!l) return NULL;
+    l->index = net->n;
+    l->batch = net->batch;
+    if (net->n == 0) {
+        l->h = net->h;
+        l->w = net->w;
+        l->c = net->c;
+    } else {
+        an_layer *p = net->layers[net->n - 1];
+        l->h = p->out_h;
+        l->w = p->out_w;
+        l->c = p->out_c;
+    }
+    l->inputs = l->h * l->w * l->c;
+    net->layers[net->n] = l;
+    net->init_w[net->n] = NULL;
+    return l;
+}
+
+/* ======================================================================== */
+/* Convolutional layer: ConvolutionalLayer.c:684-854 (forward), :863-948
+ * (backward), :959-980 (update).                                          */
+static ach_conv_desc conv_desc(const an_layer *l)
+{
+    ach_conv_desc d;
+    d.batch = l->batch;
+    d.c = l->c;
+    d.h = l->h;
+    d.w = l->w;
+    d.n = l->n;
+    d.size = l->size;
+    d.stride = l->stride;
+    d.pad = l->pad;
+    return d;
+}
+
+static int fusable(int act) { return act == ACH_LEAKY || act == ACH_RELU || act == ACH_LINEAR; }
+
+static int conv_forward(an_network *net, an_layer *l, an_state st)
+{
+    ach_conv_desc d = conv_desc(l);
+    const int spatial = l->out_h * l->out_w;
+    ach_stream_t s = net->stream;
+    if (l->batch_normalize) {
+        /* conv output goes straight into NormData.x; BN writes output */
+        AN_CHECK(ach_conv_fwd(&d, st.input, l->weights, l->x, st.workspace,
+                              st.workspace_bytes, s));
+        const int act = fusable(l->activation) ? l->activation : ACH_LINEAR;
+        AN_CHECK(ach_bn_train_fwd_from_x(l->x, l->output, l->batch, l->n, spatial, l->scales,
+                                         l->biases, l->mean, l->variance, l->rolling_mean,
+                                         l->rolling_variance, act, st.workspace,
+                                         st.workspace_bytes, s));
+        if (!fusable(l->activation))
+            AN_CHECK(ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s));
+        return ACH_OK;
+    }
+    AN_CHECK(ach_conv_fwd(&d, st.input, l->weights, l->output, st.workspace,
+                          st.workspace_bytes, s));
+    AN_CHECK(ach_add_bias(l->output, l->biases, l->batch, l->n, spatial, s));
+    return ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s);
+}
+
+static int conv_backward(an_network *net, an_layer *l, an_state st)
+{
+    ach_conv_desc d = conv_desc(l);
+    const int spatial = l->out_h * l->out_w;
+    ach_stream_t s = net->stream;
+    const size_t nout = (size_t)l->batch * l->outputs;
+    if (l->batch_normalize) {
+        int act = ACH_LINEAR;
+        if (l->activation == ACH_LEAKY || l->activation == ACH_RELU)
+            act = l->activation; /* gradient fused into the BN passes */
+        else
+            AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));
+        AN_CHECK(ach_bn_bwd(l->delta, l->batch, l->n, spatial, l->x, NULL, l->mean,
+                            l->variance, l->scales, l->biases, l->scale_updates,
+                            l->mean_delta, l->variance_delta, act, st.workspace,
+                            st.workspace_bytes, s));
+    } else {
+        AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));
+        AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial,
+                               st.workspace, st.workspace_bytes, s));
+    }
+    AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, st.workspace,
+                                 st.workspace_bytes, s));
+    if (st.delta)
+        AN_CHECK(ach_conv_bwd_data(&d, l->delta, l->weights, st.delta, st.workspace,
+                                   st.workspace_bytes, s));
+    return ACH_OK;
+}
+
+/* per-layer update for callers that drive layers one by one; an_update
+ * uses the flat buffers instead (same arithmetic, fewer launches).        */
+static int conv_update(an_network *net, an_layer *l, int batch, float lr, float momentum,
+                       float decay)
+{
+    return ach_conv_update((size_t)l->nweights, l->weights, l->weight_updates, (size_t)l->n,
+                           l->biases, l->bias_updates, l->scales, l->scale_updates, batch, lr,
+                           momentum, decay, net->stream);
+}
+
+int an_add_convolutional(an_network *net, int filters, int size, int stride, int pad,
+                         int activation, int batch_normalize)
+{
+    if (!net || filters <= 0 || size <= 0 || stride <= 0 || pad < 0) return ACH_EINVAL;
+    if (activation != ACH_LEAKY && activation != ACH_RELU && activation != ACH_LINEAR &&
+        activation != ACH_LOGISTIC)
+        return ACH_EUNSUPPORTED;
+    an_layer *l = push_layer(net);
+    if (!l) return ACH_EINVAL;
+    l->type = AN_CONVOLUTIONAL;
+    l->n = filters;
+    l->size = size;
+    l->stride = stride;
+    l->pad = pad;
+    l->activation = activation;
+    l->batch_normalize = batch_normalize ? 1 : 0;
+    l->out_h = (l->h + 2 * pad - size) / stride + 1;
+    l->out_w = (l->w + 2 * pad - size) / stride + 1;
+    l->out_c = filters;
+    if (l->h + 2 * pad < size || l->w + 2 * pad < size || l->out_h <= 0 || l->out_w <= 0) {
+        free(l);
+        return ACH_EINVAL;
+    }
+    l->outputs = l->out_h * l->out_w * l->out_c;
+    l->nweights = l->c * filters * size * size;
+    l->forward = conv_forward;
+    l->backward = conv_backward;
+    l->update = conv_update;
+    /* ConvKernel.initData (WeightData.c:153-166), in construction order */
+    float *w = (float *)malloc(sizeof(float) * l->nweights);
+    if (!w) {
+        free(l);
+        return ACH_EINVAL;
+    }
+    const float scale = sqrt(2. / (size * size * l->c));
+    for (int i = 0; i < l->nweights; ++i) w[i] = scale * rand_uniform(-1, 1);
+    net->init_w[net->n] = w;
+    return net->n++;
+}
+
+/* ======================================================================== */
+/* Max-pool: MaxPoolLayer.c:237-272 / :318-331, defaults from createMaxPool
+ * (NetworkFactory.c:543-570: padding = size-1 unless given).              */
+static int maxpool_forward(an_network *net, an_layer *l, an_state st)
+{
+    return ach_maxpool_fwd(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride, l->pad,
+                           l->output, l->indexes, net->stream);
+}
+
+static int maxpool_backward(an_network *net, an_layer *l, an_state st)
+{
+    if (!st.delta) return ACH_OK;
+    return ach_maxpool_bwd(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size, l->stride,
+                           l->pad, st.delta, net->stream);
+}
+
+int an_add_maxpool(an_network *net, int size, int stride, int padding)
+{
+    if (!net || size <= 0 || stride <= 0 || padding < 0) return ACH_EINVAL;
+    an_layer *l = push_layer(net);
+    if (!l) return ACH_EINVAL;
+    l->type = AN_MAXPOOL;
+    l->size = size;
+    l->stride = stride;
+    l->pad = padding;
+    l->out_h = ach_maxpool_out(l->h, size, stride, padding);
+    l->out_w = ach_maxpool_out(l->w, size, stride, padding);
+    l->out_c = l->c;
+    if (l->out_h <= 0 || l->out_w <= 0) {
+        free(l);
+        return ACH_EINVAL;
+    }
+    l->outputs = l->out_h * l->out_w * l->out_c;
+    l->forward = maxpool_forward;
+    l->backward = maxpool_backward;
+    return net->n++;
+}
+
+/* ======================================================================== */
+/* Global average pool: AvgPoolLayer.c:17-88.                               */
+static int avgpool_forward(an_network *net, an_layer *l, an_state st)
+{
+    return ach_avgpool_fwd(st.input, l->batch, l->c, l->h * l->w, l->output, net->stream);
+}
+
+static int avgpool_backward(an_network *net, an_layer *l, an_state st)
+{
+    if (!st.delta) return ACH_OK;
+    return ach_avgpool_bwd(l->delta, l->batch, l->c, l->h * l->w, st.delta, net->stream);
+}
+
+int an_add_avgpool(an_network *net)
+{
+    if (!net) return ACH_EINVAL;
+    an_layer *l = push_layer(net);
+    if (!l) return ACH_EINVAL;
+    l->type = AN_AVGPOOL;
+    l->out_h = l->out_w = 1;
+    l->out_c = l->c;
+    l->outputs = l->c;
+    l->forward = avgpool_forward;
+    l->backward = avgpool_backward;
+    return net->n++;
+}
+
+/* ======================================================================== */
+/* Dropout: DropoutLayer.c:55-86; shares the previous layer's output and
+ * delta (NetworkFactory.c:644-650).                                        */
+static int dropout_forward(an_network *net, an_layer *l, an_state st)
+{
+    if (!st.train) return ACH_OK;
+    return ach_dropout_fwd((float *)st.input, (size_t)l->batch * l->inputs, l->probability,
+                           net->dropout_seed, (uint32_t)net->cur_iteration, (uint32_t)l->index,
+                           net->stream);
+}
+
+static int dropout_backward(an_network *net, an_layer *l, an_state st)
+{
+    if (!st.delta) return ACH_OK;
+    return ach_dropout_bwd(st.delta, (size_t)l->batch * l->inputs, l->probability,
+                           net->dropout_seed, (uint32_t)net->cur_iteration, (uint32_t)l->index,
+                           net->stream);
+}
+
+int an_add_dropout(an_network *net, float probability)
+{
+    if (!net || net->n == 0 || !(probability >= 0.f && probability < 1.f)) return ACH_EINVAL;
+    an_layer *l = push_layer(net);
+    if (!l) return ACH_EINVAL;
+    l->type = AN_DROPOUT;
+    l->probability = probability;
+    l->out_h = l->h;
+    l->out_w = l->w;
+    l->out_c = l->c;
+    l->outputs = l->inputs;
+    l->shares_prev = 1;
+    l->forward = dropout_forward;
+    l->backward = dropout_backward;
+    return net->n++;
+}
+
+/* ======================================================================== */
+/* Softmax + cross-entropy: SoftMaxLayer.c:99-119, :291-316.                */
+static int softmax_forward(an_network *net, an_layer *l, an_state st)
+{
+    return ach_softmax_xent(st.input, l->batch, l->inputs, l->groups, l->temperature,
+                            st.truth, l->output, l->delta, l->loss, l->cost, st.workspace,
+                            st.workspace_bytes, net->stream);
+}
+
+static int softmax_backward(an_network *net, an_layer *l, an_state st)
+{
+    if (!st.delta) return ACH_OK;
+    return ach_axpy((size_t)l->batch * l->inputs, 1.f, l->delta, st.delta, net->stream);
+}
+
+int an_add_softmax(an_network *net, int groups, float temperature)
+{
+    if (!net || groups <= 0) return ACH_EINVAL;
+    an_layer *l = push_layer(net);
+    if (!l) return ACH_EINVAL;
+    if (l->inputs % groups) {
+        free(l);
+        return ACH_EINVAL;
+    }
+    l->type = AN_SOFTMAX;
+    l->groups = groups;
+    l->temperature = temperature;
+    l->out_h = l->h;
+    l->out_w = l->w;
+    l->out_c = l->c;
+    l->outputs = l->inputs;
+    l->forward = softmax_forward;
+    l->backward = softmax_backward;
+    return net->n++;
+}
+
+void an_set_hyper(an_network *net, float learning_rate, float momentum, float decay)
+{
+    net->learning_rate = learning_rate;
+    net->momentum = momentum;
+    net->decay = decay;
+}
+
+void an_set_dropout_seed(an_network *net, uint64_t seed) { net->dropout_seed = seed; }
+
+/* ======================================================================== */
+/* Arena layout and workspace sizing (NetworkFactory.c:999-1005 sizes one
+ * shared workspace to the largest layer need).                             */
+static size_t al(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+
+typedef struct {
+    char *base;
+    size_t off;
+    int dry;
+} bump;
+
+static void *take(bump *b, size_t bytes)
+{
+    void *p = b->dry ? NULL : (void *)(b->base + b->off);
+    b->off += al(bytes);
+    return p;
+}
+
+static size_t layer_ws(const an_layer *l, int batch)
+{
+    size_t ws = 0;
+    if (l->type == AN_CONVOLUTIONAL) {
+        ach_conv_desc d = conv_desc(l);
+        size_t a = ach_conv_fwd_workspace(&d), b = ach_conv_bwd_data_workspace(&d),
+               c = ach_conv_bwd_filter_workspace(&d);
+        ws = a > b ? a : b;
+        ws = ws > c ? ws : c;
+        if (l->batch_normalize) {
+            size_t n = ach_bn_workspace(batch, l->n, l->out_h * l->out_w);
+            ws = ws > n ? ws : n;
+        }
+    } else if (l->type == AN_SOFTMAX) {
+        ws = ach_softmax_workspace(batch, l->groups);
+    }
+    return ws;
+}
+
+/* lay out every device tensor; b->dry only measures */
+static void layout(an_network *net, bump *b)
+{
+    const size_t B = (size_t)net->batch;
+    /* 1. deltas that must be zeroed each forward, contiguous */
+    size_t zstart = b->off;
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->shares_prev || !l->zero_delta) continue;
+        l->delta = (float *)take(b, sizeof(float) * B * l->outputs);
+    }
+    net->zero_region = b->dry ? NULL : (float *)(b->base + zstart);
+    net->zero_floats = (b->off - zstart) / sizeof(float);
+    /* 2. per-layer tensors (flat parameters are carved by an_finalize) */
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        const size_t bo = B * l->outputs;
+        if (l->shares_prev) {
+            if (!b->dry) {
+                l->output = net->layers[i - 1]->output;
+                l->delta = net->layers[i - 1]->delta;
+            }
+            continue;
+        }
+        l->output = (float *)take(b, sizeof(float) * bo);
+        if (!l->zero_delta) l->delta = (float *)take(b, sizeof(float) * bo);
+        if (l->type == AN_CONVOLUTIONAL && l->batch_normalize) {
+            l->x = (float *)take(b, sizeof(float) * bo);
+            l->mean = (float *)take(b, sizeof(float) * l->n);
+            l->variance = (float *)take(b, sizeof(float) * l->n);
+            l->rolling_mean = (float *)take(b, sizeof(float) * l->n);
+            l->rolling_variance = (float *)take(b, sizeof(float) * l->n);
+            l->mean_delta = (float *)take(b, sizeof(float) * l->n);
+            l->variance_delta = (float *)take(b, sizeof(float) * l->n);
+        } else if (l->type == AN_MAXPOOL) {
+            l->indexes = (int32_t *)take(b, sizeof(int32_t) * bo);
+        } else if (l->type == AN_SOFTMAX) {
+            l->loss = (float *)take(b, sizeof(float) * bo);
+            l->cost = (float *)take(b, sizeof(float) * 4);
+        }
+    }
+    /* 3. input, truth, workspace */
+    net->input = (float *)take(b, sizeof(float) * B * net->inputs);
+    net->truth = (float *)take(b, sizeof(float) * B * (net->classes > 0 ? net->classes : 1));
+    size_t ws = 0;
+    for (int i = 0; i < net->n; ++i) {
+        size_t w = layer_ws(net->layers[i], net->batch);
+        if (w > ws) ws = w;
+    }
+    net->workspace_bytes = ws;
+    net->workspace = (float *)take(b, ws ? ws : 256);
+}
+
+int an_finalize(an_network *net)
+{
+    if (!net || net->finalized || net->n == 0) return ACH_EINVAL;
+    an_layer *last = net->layers[net->n - 1];
+    net->classes = last->outputs;
+    /* deltas the next layer accumulates into (+=) must start at zero:
+     * maxpool / avgpool / softmax backward add into their input delta.    */
+    for (int i = 1; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type == AN_MAXPOOL || l->type == AN_AVGPOOL || l->type == AN_SOFTMAX) {
+            int j = i - 1;
+            while (j > 0 && net->layers[j]->shares_prev) --j;
+            net->layers[j]->zero_delta = 1;
+        }
+    }
+    /* flat parameter buffers use 64-float aligned per-layer slots */
+    bump dry = {NULL, 0, 1};
+    layout(net, &dry);
+    size_t nw = 0, nb = 0;
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        nw += (size_t)((l->nweights + 63) & ~63);
+        nb += (size_t)((l->n + 63) & ~63) * (l->batch_normalize ? 2 : 1);
+    }
+    const size_t extra = al(sizeof(float) * nw) * 2 + al(sizeof(float) * nb) * 2;
+    net->arena_bytes = dry.off + extra;
+    AN_CHECK(ach_malloc(&net->arena, net->arena_bytes));
+    AN_CHECK(ach_stream_create(&net->stream));
+    bump real = {(char *)net->arena, 0, 0};
+    layout(net, &real);
+    /* flat parameter buffers at the arena tail */
+    char *tail = (char *)net->arena + real.off;
+    net->wflat = (float *)tail;
+    tail += al(sizeof(float) * nw);
+    net->vflat = (float *)tail;
+    tail += al(sizeof(float) * nw);
+    net->bflat = (float *)tail;
+    tail += al(sizeof(float) * nb);
+    net->bvflat = (float *)tail;
+    net->nweights_total = nw;
+    net->nbias_total = nb;
+    size_t ow = 0, ob = 0;
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        l->weights = net->wflat + ow;
+        l->weight_updates = net->vflat + ow;
+        ow += (size_t)((l->nweights + 63) & ~63);
+        l->biases = net->bflat + ob;
+        l->bias_updates = net->bvflat + ob;
+        ob += (size_t)((l->n + 63) & ~63);
+        if (l->batch_normalize) {
+            l->scales = net->bflat + ob;
+            l->scale_updates = net->bvflat + ob;
+            ob += (size_t)((l->n + 63) & ~63);
+        } else {
+            l->scales = l->scale_updates = NULL;
+        }
+    }
+    /* zero everything once (momentum buffers, biases, stats, deltas) */
+    AN_CHECK(ach_fill((float *)net->arena, net->arena_bytes / sizeof(float), 0.f, net->stream));
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        AN_CHECK(ach_memcpy_h2d(l->weights, net->init_w[i], sizeof(float) * l->nweights,
+                                net->stream));
+        free(net->init_w[i]);
+        net->init_w[i] = NULL;
+        if (l->batch_normalize) /* ScaleData.init(1.0) */
+            AN_CHECK(ach_fill(l->scales, (size_t)l->n, 1.f, net->stream));
+    }
+    AN_CHECK(ach_stream_sync(net->stream));
+    net->finalized = 1;
+    return ACH_OK;
+}
+
+void an_free(an_network *net)
+{
+    if (!net) return;
+    for (int i = 0; i < net->n; ++i) {
+        if (net->init_w) free(net->init_w[i]);
+        free(net->layers[i]);
+    }
+    free(net->layers);
+    free(net->init_w);
+    if (net->stream) ach_stream_sync(net->stream);
+    ach_free(net->arena);
+    ach_stream_destroy(net->stream);
+    free(net);
+}
+
+/* ======================================================================== */
+ach_stream_t an_stream(an_network *net) { return net->stream; }
+
+int an_set_input(an_network *net, const float *host_input, const float *host_truth)
+{
+    if (!net || !net->finalized || !host_input) return ACH_EINVAL;
+    AN_CHECK(ach_memcpy_h2d(net->input, host_input, sizeof(float) * net->batch * net->inputs,
+                            net->stream));
+    if (host_truth)
+        AN_CHECK(ach_memcpy_h2d(net->truth, host_truth,
+                                sizeof(float) * net->batch * net->classes, net->stream));
+    return ACH_OK;
+}
+
+int an_set_input_device(an_network *net, const float *dev_input, const float *dev_truth)
+{
+    if (!net || !net->finalized || !dev_input) return ACH_EINVAL;
+    AN_CHECK(ach_memcpy_d2d(net->input, dev_input, sizeof(float) * net->batch * net->inputs,
+                            net->stream));
+    if (dev_truth)
+        AN_CHECK(ach_memcpy_d2d(net->truth, dev_truth,
+                                sizeof(float) * net->batch * net->classes, net->stream));
+    return ACH_OK;
+}
+
+static an_state base_state(an_network *net)
+{
+    an_state st;
+    st.truth = net->truth;
+    st.input = net->input;
+    st.delta = NULL;
+    st.workspace = net->workspace;
+    st.workspace_bytes = net->workspace_bytes;
+    st.train = 1;
+    st.index = 0;
+    return st;
+}
+
+/* NNetwork.forward (NNetwork.c:382-396): deltas start at zero, then every
+ * layer runs with state.input = previous output.                           */
+int an_forward(an_network *net, int train)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    an_state st = base_state(net);
+    st.train = train;
+    if (train && net->zero_floats)
+        AN_CHECK(ach_fill(net->zero_region, net->zero_floats, 0.f, net->stream));
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        st.index = i;
+        AN_CHECK(l->forward(net, l, st));
+        st.input = l->output;
+    }
+    return ACH_OK;
+}
+
+/* NNetwork.backward (NNetwork.c:627-654).                                 */
+int an_backward(an_network *net)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    an_state st = base_state(net);
+    for (int i = net->n - 1; i >= 0; --i) {
+        st.index = i;
+        if (i == 0) {
+            st.input = net->input;
+            st.delta = NULL;
+        } else {
+            st.input = net->layers[i - 1]->output;
+            st.delta = net->layers[i - 1]->delta;
+        }
+        an_layer *l = net->layers[i];
+        AN_CHECK(l->backward(net, l, st));
+    }
+    return ACH_OK;
+}
+
+/* NNetwork.updateCPU (NNetwork.c:667-680) with the constant rate policy:
+ * every conv layer's update, as two launches over the flat buffers.        */
+int an_update(an_network *net)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    const int batch = net->batch; /* batch * subdivisions, subdivisions = 1 */
+    const float rate = net->learning_rate;
+    const float a1 = -net->decay * batch;
+    const float a2 = rate / batch;
+    AN_CHECK(ach_sgd_update(net->nweights_total, net->wflat, net->vflat, a1, a2, net->momentum,
+                            net->stream));
+    return ach_sgd_update(net->nbias_total, net->bflat, net->bvflat, 0.f, a2, net->momentum,
+                          net->stream);
+}
+
+int an_train_step(an_network *net)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    net->seen += (uint64_t)net->batch;
+    AN_CHECK(an_forward(net, 1));
+    AN_CHECK(an_backward(net));
+    net->cur_iteration += 1;
+    return an_update(net);
+}
+
+int an_get_loss(an_network *net, float *loss)
+{
+    if (!net || !net->finalized || !loss) return ACH_EINVAL;
+    float sum = 0;
+    int count = 0;
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_SOFTMAX) continue;
+        float c = 0;
+        AN_CHECK(ach_memcpy_d2h(&c, l->cost, sizeof(float), net->stream));
+        sum += c;
+        ++count;
+    }
+    /* getNetworkCost (NNetwork.c:611-624), then / (subdivisions*batch) */
+    const float cost = count ? sum / count : 0.f;
+    *loss = cost / net->batch;
+    if (isnan(*loss)) return ACH_EINVAL; /* the CPU path aborts on NaN */
+    return ACH_OK;
+}
+
+int an_train(an_network *net, const float *host_input, const float *host_truth, float *loss)
+{
+    AN_CHECK(an_set_input(net, host_input, host_truth));
+    AN_CHECK(an_train_step(net));
+    return an_get_loss(net, loss);
+}
+
+/* ======================================================================== */
+int an_n_layers(const an_network *net) { return net ? net->n : 0; }
+an_layer *an_get_layer(an_network *net, int i)
+{
+    return (net && i >= 0 && i < net->n) ? net->layers[i] : NULL;
+}
+int an_batch(const an_network *net) { return net->batch; }
+float *an_input(an_network *net) { return net->input; }
+float *an_truth(an_network *net) { return net->truth; }
+int an_classes(const an_network *net) { return net->classes; }
+uint64_t an_seen(const an_network *net) { return net->seen; }
+int an_iteration(const an_network *net) { return net->cur_iteration; }
+
+void *an_layer_buffer(an_network *net, int li, int which, size_t *count)
+{
+    *count = 0;
+    an_layer *l = an_get_layer(net, li);
+    if (!l) return NULL;
+    const size_t bo = (size_t)l->batch * l->outputs;
+    void *p = NULL;
+    size_t n = 0;
+    switch (which) {
+    case 0: p = l->output; n = bo; break;
+    case 1: p = l->delta; n = bo; break;
+    case 2: p = l->weights; n = (size_t)l->nweights; break;
+    case 3: p = l->weight_updates; n = (size_t)l->nweights; break;
+    case 4: p = l->biases; n = (size_t)l->n; break;
+    case 5: p = l->bias_updates; n = (size_t)l->n; break;
+    case 6: p = l->scales; n = (size_t)l->n; break;
+    case 7: p = l->scale_updates; n = (size_t)l->n; break;
+    case 8: p = l->rolling_mean; n = (size_t)l->n; break;
+    case 9: p = l->rolling_variance; n = (size_t)l->n; break;
+    case 10: p = l->mean; n = (size_t)l->n; break;
+    case 11: p = l->variance; n = (size_t)l->n; break;
+    case 12: p = l->x; n = bo; break;
+    case 14: p = l->indexes; n = bo; break;
+    case 15: p = l->loss; n = bo; break;
+    default: break;
+    }
+    if (p) *count = n;
+    return p;
+}
+
+double an_step_conv_gflop(const an_network *net)
+{
+    double tot = 0;
+    for (int i = 0; i < net->n; ++i) {
+        const an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        const double f = 2.0 * l->batch * l->n * l->out_h * l->out_w * (double)l->c * l->size *
+                         l->size;
+        tot += f * (i == 0 ? 2 : 3); /* layer 0 has no input gradient */
+    }
+    return tot / 1e9;
+}

@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark: aet-cnn CNN training step on one MI355X.
+
+Headline (BASELINE.json metric): train images/s of the darknet-style 32x32
+classifier (config 3: 9x conv3x3+BN+leaky, 1x1 conv, pools, dropout,
+softmax) at batch 128, fp32, one full SGD step per iteration, plus the conv
+fwd+dgrad+wgrad TFLOP/s of the config-1 layer sweep.  Inputs are synthetic
+(seeded uniform pixels and labels) and resident in HBM before timing.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "aet-cnn_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+SWEEP = [  # config 1: (C_in, C_out, H, k, pad)
+    (3, 128, 32, 3, 1), (128, 128, 32, 3, 1), (128, 256, 16, 3, 1), (256, 256, 16, 3, 1),
+    (256, 512, 8, 3, 1), (512, 512, 8, 3, 1), (512, 10, 8, 1, 0),
+]
+ROOFLINE_SHAPE = (256, 256, 16, 3, 1)  # dominant kernel probe: conv fwd GEMM
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def train_phase(aetcnn, configs, name, steps, warmup, batch):
+    lib = aetcnn.net_lib()
+    lib.an_rand_seed(1)
+    B, h, w, c = configs.dims(name, batch)
+    net = aetcnn.Network(B, h, w, c)
+    configs.build(net, name)
+    net.finalize()
+    x, truth, _ = configs.synthetic_batch(name, 1234, B)
+    net.set_input(x, truth)  # resident in HBM from here on
+    ops = aetcnn.ops()
+    for i in range(warmup):
+        net.train_step()
+    first_loss = net.loss() if warmup else float("nan")
+    ops.ach_device_sync()
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    ops.ach_event_create(C.byref(ev0))
+    ops.ach_event_create(C.byref(ev1))
+    t0 = time.perf_counter()
+    ops.ach_event_record(ev0, net.stream)
+    for i in range(steps):
+        net.train_step()
+    ops.ach_event_record(ev1, net.stream)
+    aetcnn.check(ops.ach_device_sync(), "sync")
+    t1 = time.perf_counter()
+    ms = C.c_float()
+    ops.ach_event_elapsed_ms(ev0, ev1, C.byref(ms))
+    loss = net.loss()
+    gflop = net.conv_gflop()
+    net.close()
+    return dict(wall_s=t1 - t0, gpu_ms=ms.value, loss=loss, first_loss=first_loss,
+                gflop_step=gflop, batch=B)
+
+
+def time_launch(ops, stream, fn, reps):
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    ops.ach_event_create(C.byref(e0))
+    ops.ach_event_create(C.byref(e1))
+    fn()  # warm
+    ops.ach_event_record(e0, stream)
+    for _ in range(reps):
+        fn()
+    ops.ach_event_record(e1, stream)
+    ms = C.c_float()
+    aetcnn_check(ops.ach_event_elapsed_ms(e0, e1, C.byref(ms)), "event")
+    ops.ach_event_destroy(e0)
+    ops.ach_event_destroy(e1)
+    return ms.value / reps
+
+
+def aetcnn_check(rc, what):
+    import aetcnn
+    aetcnn.check(rc, what)
+
+
+def sweep_phase(aetcnn, batch, reps):
+    ops = aetcnn.ops()
+    D = aetcnn.DeviceArray
+    stream = C.c_void_p()
+    aetcnn.check(ops.ach_stream_create(C.byref(stream)), "stream")
+    rng = np.random.default_rng(0)
+    rows = []
+    tot_flop = tot_ms = 0.0
+    probe = None
+    for (ci, co, hw, k, p) in SWEEP:
+        d = aetcnn.ConvDesc(batch, ci, hw, hw, co, k, 1, p)
+        oh = (hw + 2 * p - k) + 1
+        x = D.from_numpy(rng.uniform(-1, 1, (batch, ci, hw, hw)).astype(np.float32))
+        w = D.from_numpy((rng.standard_normal((co, ci, k, k)) * 0.05).astype(np.float32))
+        y = D((batch, co, oh, oh))
+        dy = D.from_numpy(rng.uniform(-1, 1, (batch, co, oh, oh)).astype(np.float32))
+        dx = D((batch, ci, hw, hw))
+        dw = D((co, ci, k, k))
+        dw.zero()
+        wsz = max(ops.ach_conv_bwd_data_workspace(C.byref(d)),
+                  ops.ach_conv_bwd_filter_workspace(C.byref(d)), 256)
+        ws = D(wsz // 4)
+        flop = 2.0 * batch * co * oh * oh * ci * k * k
+
+        def fwd():
+            aetcnn.check(ops.ach_conv_fwd(C.byref(d), x.ptr, w.ptr, y.ptr, ws.ptr, wsz, stream))
+
+        def dgrad():
+            aetcnn.check(ops.ach_conv_bwd_data(C.byref(d), dy.ptr, w.ptr, dx.ptr, ws.ptr, wsz,
+                                               stream))
+
+        def wgrad():
+            aetcnn.check(ops.ach_conv_bwd_filter(C.byref(d), x.ptr, dy.ptr, dw.ptr, ws.ptr, wsz,
+                                                 stream))
+
+        t = [time_launch(ops, stream, f, reps) for f in (fwd, dgrad, wgrad)]
+        row = dict(shape=f"{ci}->{co}@{hw}x{hw} k{k}", gflop_pass=flop / 1e9,
+                   ms=[round(v, 4) for v in t],
+                   tflops=[round(flop / (v * 1e-3) / 1e12, 2) for v in t])
+        rows.append(row)
+        tot_flop += 3 * flop
+        tot_ms += sum(t)
+        if (ci, co, hw, k, p) == ROOFLINE_SHAPE:
+            probe = dict(kernel="k_mfma_gemm<FwdProblem<3>> (conv fwd implicit GEMM)",
+                         shape=row["shape"] + f" b{batch}", flop=flop, ms=t[0])
+        log(f"sweep {row['shape']}: fwd/dgrad/wgrad {row['tflops']} TFLOP/s")
+        for a in (x, w, y, dy, dx, dw, ws):
+            a.free()
+    ops.ach_stream_destroy(stream)
+    return rows, tot_flop / (tot_ms * 1e-3) / 1e12, probe
+
+
+def cpu_phase(configs, name, batch, steps):
+    """The oracle (CPU restatement of the reference CPU path) on a bounded
+    sample: `steps` training steps of the same network at a small batch."""
+    import oracle_lib
+    L = oracle_lib.lib()
+    L.or_set_gemm_parallel(1)
+    L.or_rand_seed(1)
+    B, h, w, c = configs.dims(name, batch)
+    onet = oracle_lib.OracleNet(B, h, w, c)
+    configs.build(onet, name)
+    onet.finalize()
+    x, truth, _ = configs.synthetic_batch(name, 1234, B)
+    onet.train(x, truth)  # warm-up step
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        onet.train(x, truth)
+    dt = time.perf_counter() - t0
+    threads = L.or_max_threads()
+    onet.close()
+    return dict(value=round(B * steps / dt, 3), unit="images/s", cores=int(threads),
+                kind="port",
+                sample=f"oracle {name} net, batch {B}, {steps} timed steps after 1 warm-up, "
+                       f"row-parallel GEMM on {threads} OpenMP threads ({dt:.1f} s)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="darknet", choices=["darknet", "tiny", "alexnet"])
+    ap.add_argument("--sweep-reps", type=int, default=5)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-batch", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU data parallelism is design-only", file=sys.stderr)
+        sys.exit(2)
+
+    import aetcnn
+    from aetcnn import configs
+    ops = aetcnn.ops()
+    if ops.ach_device_count() < 1:
+        print("bench.py: no HIP device", file=sys.stderr)
+        sys.exit(1)
+    aetcnn.check(ops.ach_set_device(0), "set_device")
+
+    log(f"training phase: {args.config} b128, warmup {args.warmup}, steps {args.steps}")
+    tr = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None)
+    ms_step = tr["wall_s"] * 1e3 / args.steps
+    ips = tr["batch"] * args.steps / tr["wall_s"]
+    step_tflops = tr["gflop_step"] / (ms_step * 1e-3) / 1e3
+    log(f"{ms_step:.3f} ms/step ({tr['gpu_ms'] / args.steps:.3f} GPU ms), {ips:.1f} img/s, "
+        f"conv {step_tflops:.2f} TFLOP/s, loss {tr['first_loss']:.4f} -> {tr['loss']:.4f}")
+
+    sweep_rows, sweep_tflops, probe = [], None, None
+    if not args.no_sweep:
+        sweep_rows, sweep_tflops, probe = sweep_phase(aetcnn, 128, args.sweep_reps)
+        log(f"conv sweep fwd+dgrad+wgrad: {sweep_tflops:.2f} TFLOP/s")
+
+    roofline = None
+    if probe:
+        ach = probe["flop"] / (probe["ms"] * 1e-3) / 1e12
+        roofline = dict(bound="mfma", achieved=round(ach, 3), peak=MFMA_FP32_PEAK_TFLOPS,
+                        unit="TFLOP/s", frac=round(ach / MFMA_FP32_PEAK_TFLOPS, 4),
+                        traffic=None, kernel=probe["kernel"], shape=probe["shape"],
+                        avg_launch_ms=round(probe["ms"], 5),
+                        flop_per_launch=probe["flop"])
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle) ...")
+        try:
+            cpu = cpu_phase(configs, args.config, args.cpu_batch, args.cpu_steps)
+            log(f"cpu baseline: {cpu['value']} img/s on {cpu['cores']} threads")
+        except Exception as e:  # the oracle is optional on the box
+            log(f"cpu baseline skipped: {e}")
+
+    out = {
+        "metric": "train images/s, fp32 32x32 13-conv net b=128; conv fwd+bwd TFLOP/s",
+        "value": round(ips, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: seeded uniform [0,1) pixels, uniform labels, one resident batch",
+        "config": {"workload": f"{args.config} classifier full training step (fwd+bwd+SGD)",
+                   "global_batch": tr["batch"], "input": "3x32x32" if args.config != "alexnet"
+                   else "3x227x227", "parallelism": "single GPU"},
+        "conv_step_tflops": round(step_tflops, 3),
+        "conv_sweep_tflops": None if sweep_tflops is None else round(sweep_tflops, 3),
+        "conv_sweep": sweep_rows,
+        "loss_first_last": [round(tr["first_loss"], 5), round(tr["loss"], 5)],
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

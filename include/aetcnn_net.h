@@ -1,0 +1,155 @@
+/*
+ * aetcnn_net.h -- C host layer: the reference's network and layer objects
+ * (NNetwork / NLayer and its subclasses) as plain C structs with a
+ * per-layer forward / backward / update function table, driving the HIP
+ * kernels of aetcnn_ops.h.  Paths are relative to
+ * /root/reference/src/com/ai/dnn/.
+ *
+ *   an_network            NNetwork (NNetwork.h:28-198)
+ *   an_layer              NLayer (NLayer.h:55-196) + ConvolutionalLayer,
+ *                         MaxPoolLayer, AvgPoolLayer, DropoutLayer,
+ *                         SoftMaxLayer fields
+ *   an_state              NetworkState (NLayer.h:21-29)
+ *   an_add_*              NetworkFactory.create* (NetworkFactory.c:77-173,
+ *                         543-601, 615-666)
+ *   an_forward/backward   NNetwork.forward/backward (NNetwork.c:382-396,
+ *                         627-654)
+ *   an_update             NNetwork.updateCPU (NNetwork.c:667-680)
+ *   an_train              NNetwork.train (NNetwork.c:740-758, 762-805)
+ *
+ * All tensors live in device memory (one arena per network); host pointers
+ * appear only where a function says "host".  Functions return 0 / ACH_OK or
+ * a negative ACH_E* code from aetcnn_ops.h.
+ */
+#ifndef AETCNN_NET_H
+#define AETCNN_NET_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "aetcnn_ops.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    AN_CONVOLUTIONAL = 0,
+    AN_MAXPOOL = 1,
+    AN_AVGPOOL = 2,
+    AN_DROPOUT = 3,
+    AN_SOFTMAX = 4
+} an_layer_type;
+
+typedef struct an_network an_network;
+typedef struct an_layer an_layer;
+
+/* NetworkState (NLayer.h:21-29): passed by value to every layer call. */
+typedef struct {
+    const float *truth;   /* device [batch][classes] one-hot, or NULL  */
+    const float *input;   /* device, previous layer's output            */
+    float *delta;         /* device, previous layer's delta, or NULL    */
+    float *workspace;     /* device scratch shared by all layers        */
+    size_t workspace_bytes;
+    int train;
+    int index;
+} an_state;
+
+struct an_layer {
+    an_layer_type type;
+    int index;
+    int batch, inputs, outputs;
+    int h, w, c, out_h, out_w, out_c;
+    /* convolutional (ConvolutionalLayer.h:20-114) */
+    int n, size, stride, pad, activation, batch_normalize, nweights;
+    float *weights, *weight_updates, *biases, *bias_updates;
+    float *scales, *scale_updates;
+    float *mean, *variance, *rolling_mean, *rolling_variance;
+    float *mean_delta, *variance_delta;
+    float *x;               /* pre-BN conv output (NormData.x)              */
+    /* maxpool */
+    int32_t *indexes;
+    /* dropout */
+    float probability;
+    int shares_prev;        /* output/delta alias the previous layer's    */
+    /* softmax */
+    int groups;
+    float temperature;
+    float *loss;            /* per-element cross-entropy                   */
+    float *cost;            /* device scalar: sum(loss)                    */
+    /* common */
+    float *output, *delta;
+    int zero_delta;         /* delta is accumulated into by the next layer */
+    int (*forward)(an_network *net, an_layer *l, an_state st);
+    int (*backward)(an_network *net, an_layer *l, an_state st);
+    int (*update)(an_network *net, an_layer *l, int batch, float lr, float momentum,
+                  float decay);
+};
+
+/* ---- construction ------------------------------------------------------- */
+/* Seeds the glibc rand() stream the weight init draws from
+ * (WeightData.c:153-166 via DnnUtils.randUniform, DnnUtils.c:196-209).  The
+ * reference initialises weights before any srand(), i.e. from seed 1.       */
+void an_rand_seed(unsigned seed);
+an_network *an_network_create(int batch, int h, int w, int c);
+/* return the new layer's index or a negative error                          */
+int an_add_convolutional(an_network *net, int filters, int size, int stride, int pad,
+                         int activation, int batch_normalize);
+int an_add_maxpool(an_network *net, int size, int stride, int padding);
+int an_add_avgpool(an_network *net);
+int an_add_dropout(an_network *net, float probability);
+int an_add_softmax(an_network *net, int groups, float temperature);
+void an_set_hyper(an_network *net, float learning_rate, float momentum, float decay);
+void an_set_dropout_seed(an_network *net, uint64_t seed);
+/* allocate device memory, upload initial parameters, size the workspace   */
+int an_finalize(an_network *net);
+void an_free(an_network *net);
+/* Builds a network from a darknet-style .cfg file (ConfigFile.c:12-208,
+ * NetworkFactory.c:615-1013): [net] batch/subdivisions/width/height/channels/
+ * learning_rate/momentum/decay; [convolutional] filters/size/stride/pad/
+ * padding/activation/batch_normalize; [maxpool] size/stride/padding;
+ * [avgpool]; [dropout] probability; [softmax] groups/temperature.  Returns
+ * NULL on error (message on stderr).  The network is finalized.            */
+an_network *an_parse_cfg(const char *path);
+
+/* ---- training ------------------------------------------------------------- */
+ach_stream_t an_stream(an_network *net);
+/* copy one batch from host buffers into the network's input/truth        */
+int an_set_input(an_network *net, const float *host_input, const float *host_truth);
+/* the same from device buffers (device-to-device copy on the net stream) */
+int an_set_input_device(an_network *net, const float *dev_input, const float *dev_truth);
+/* NNetwork.train(input, truth) + update, on the resident input: enqueues the
+ * whole step on the network's stream and returns without synchronising;
+ * the loss stays on the device until an_get_loss.                          */
+int an_train_step(an_network *net);
+/* synchronises and returns sum(cost)/batch of the last step (NNetwork.c:804) */
+int an_get_loss(an_network *net, float *loss);
+/* host-buffer convenience: set_input + train_step + get_loss               */
+int an_train(an_network *net, const float *host_input, const float *host_truth, float *loss);
+int an_forward(an_network *net, int train);
+int an_backward(an_network *net);
+int an_update(an_network *net);
+
+/* ---- introspection (tests, checkpoints) ------------------------------------ */
+int an_n_layers(const an_network *net);
+an_layer *an_get_layer(an_network *net, int i);
+int an_batch(const an_network *net);
+/* device pointers of the network's input and truth buffers                 */
+float *an_input(an_network *net);
+float *an_truth(an_network *net);
+int an_classes(const an_network *net);
+uint64_t an_seen(const an_network *net);
+int an_iteration(const an_network *net);
+/* device buffer of a layer: which = 0 output, 1 delta, 2 weights,
+ * 3 weight_updates, 4 biases, 5 bias_updates, 6 scales, 7 scale_updates,
+ * 8 rolling_mean, 9 rolling_variance, 10 mean, 11 variance, 12 x (pre-BN),
+ * 14 indexes (int32), 15 loss; *count = elements (0 if absent)              */
+void *an_layer_buffer(an_network *net, int layer, int which, size_t *count);
+/* total GFLOP of one training step's conv GEMMs (fwd + wgrad + dgrad where
+ * the layer has an input gradient)                                          */
+double an_step_conv_gflop(const an_network *net);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,217 @@
+/*
+ * aetcnn_ops.h -- C-ABI of the MI355X (gfx950) HIP kernels for one CNN
+ * training step of aet-cnn.  Plain pointers and sizes only; every pointer
+ * argument named like a tensor is DEVICE memory unless stated otherwise.
+ *
+ * Each entry point replaces one operation of the reference's CPU path
+ * (paths relative to /root/reference/src/com/ai/dnn/) with CPU-path
+ * semantics; the reference's own GPU ("mtcs") path differs from its CPU path
+ * (biased BN variance, other eps, 0.99 rolling momentum, beta gradient) and
+ * is NOT what these functions compute.
+ *
+ * Conventions
+ *  - tensors are fp32 NCHW, batch outermost: ((b*C + c)*H + h)*W + w
+ *  - `stream` is a hipStream_t passed as void*; NULL = the null stream
+ *  - functions return 0 on success or a negative ACH_E* code; nothing is
+ *    synchronised unless the name says so
+ *  - functions that need scratch take (ws, ws_bytes) and have a matching
+ *    *_workspace() query; kernels never allocate
+ */
+#ifndef AETCNN_OPS_H
+#define AETCNN_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ACH_OK 0
+#define ACH_EINVAL (-1)     /* bad argument / shape                        */
+#define ACH_EWORKSPACE (-2) /* workspace missing or too small               */
+#define ACH_EHIP (-3)       /* HIP runtime error (ach_last_hip_error())     */
+#define ACH_EUNSUPPORTED (-4)
+
+/* Activation ids = the reference's ActivationType order (Activation.h). */
+#define ACH_LOGISTIC 0
+#define ACH_RELU 1
+#define ACH_LINEAR 3
+#define ACH_LEAKY 7
+
+typedef void *ach_stream_t;
+
+/* ---- runtime plumbing (the reference's MtcsMem / MtcsStream roles:
+ *      mtcs/MtcsTool.c:22-30, mtcs/MtcsData.c:20-28) ----------------------- */
+const char *ach_version(void);
+int ach_device_count(void);
+int ach_set_device(int dev);
+const char *ach_last_hip_error(void);
+int ach_malloc(void **ptr, size_t bytes);
+int ach_free(void *ptr);
+int ach_host_alloc(void **ptr, size_t bytes); /* pinned host memory */
+int ach_host_free(void *ptr);
+int ach_memcpy_h2d(void *dst, const void *src, size_t bytes, ach_stream_t stream);
+int ach_memcpy_d2h(void *dst, const void *src, size_t bytes, ach_stream_t stream);
+int ach_memcpy_d2d(void *dst, const void *src, size_t bytes, ach_stream_t stream);
+int ach_stream_create(ach_stream_t *stream);
+int ach_stream_destroy(ach_stream_t stream);
+int ach_stream_sync(ach_stream_t stream);
+int ach_device_sync(void);
+/* events for timing (hipEvent_t as void*) */
+int ach_event_create(void **ev);
+int ach_event_destroy(void *ev);
+int ach_event_record(void *ev, ach_stream_t stream);
+int ach_event_elapsed_ms(void *start, void *stop, float *ms); /* syncs stop */
+
+/* ---- BLAS-1 helpers (mtcs/MtcsTool.c:33-132; NData.setZero NData.c:232) */
+int ach_fill(float *x, size_t n, float value, ach_stream_t stream);
+int ach_axpy(size_t n, float alpha, const float *x, float *y, ach_stream_t stream);
+int ach_scal(size_t n, float alpha, float *x, ach_stream_t stream);
+
+/* ---- GEMM (Gemm.gemm, Gemm.c:116-144; Gemm.h:12-16) --------------------
+ * Row-major C = ALPHA*op(A)*op(B) + BETA*C on fp32 MFMA.                  */
+int ach_gemm(int TA, int TB, int M, int N, int K, float ALPHA,
+             const float *A, int lda, const float *B, int ldb,
+             float BETA, float *C, int ldc, ach_stream_t stream);
+
+/* ---- im2col / col2im for one image (Im2Col.c:65-103, 155-192) ---------- */
+int ach_im2col(const float *im, int channels, int height, int width,
+               int kh, int kw, int ph, int pw, int sh, int sw,
+               float *col, ach_stream_t stream);
+/* col2im zeroes `im` first, as the reference does (Im2Col.c:162)          */
+int ach_col2im(const float *col, int channels, int height, int width,
+               int kh, int kw, int ph, int pw, int sh, int sw,
+               float *im, ach_stream_t stream);
+
+/* ---- convolution (ConvolutionalLayer.c:684-803, 906-947) ---------------- */
+typedef struct {
+    int batch, c, h, w;   /* input  [batch][c][h][w]                     */
+    int n;                /* filters (output channels)                   */
+    int size, stride, pad;/* square kernel, stride, padding (groups = 1) */
+} ach_conv_desc;
+
+int ach_conv_out_h(const ach_conv_desc *d);
+int ach_conv_out_w(const ach_conv_desc *d);
+/* y = W * im2col(x), overwriting y        (ConvolutionalLayer.c:689,716-803) */
+size_t ach_conv_fwd_workspace(const ach_conv_desc *d);
+int ach_conv_fwd(const ach_conv_desc *d, const float *x, const float *w, float *y,
+                 void *ws, size_t ws_bytes, ach_stream_t stream);
+/* dx = col2im(W^T * dy), overwriting dx   (ConvolutionalLayer.c:933-945)   */
+size_t ach_conv_bwd_data_workspace(const ach_conv_desc *d);
+int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, float *dx,
+                      void *ws, size_t ws_bytes, ach_stream_t stream);
+/* dw += sum_b dy_b * im2col(x_b)^T        (ConvolutionalLayer.c:913-929)   */
+size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d);
+int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
+                        void *ws, size_t ws_bytes, ach_stream_t stream);
+
+/* ---- bias (IOData.addBias IOData.c:43-55; BiasData.calcGrad BiasData.c:40-57) */
+int ach_add_bias(float *out, const float *biases, int batch, int n, int spatial,
+                 ach_stream_t stream);
+size_t ach_bias_grad_workspace(int batch, int n, int spatial);
+int ach_bias_grad(float *bias_updates, const float *delta, int batch, int n, int spatial,
+                  void *ws, size_t ws_bytes, ach_stream_t stream);
+
+/* ---- batch-norm, training mode ------------------------------------------
+ * Forward (forwardNormCPU NLayer.c:141-162 = NormData.calcVarianceAndMean
+ * NormData.c:141-186, scalAxpyRollMeanAndRollVariance :224-229, normalize
+ * :244-282).  `out` holds the conv output on entry; on return x = copy of it,
+ * x_norm (optional, may be NULL) = (x-mean)/(sqrt(var)+1e-6), and
+ * out = act(x_norm*scales + biases) where act is ACH_LINEAR for the plain op
+ * or ACH_LEAKY / ACH_RELU to fuse the layer's activation (Activation.c:160).
+ * mean/variance (unbiased) and rolling_mean/rolling_variance (.9/.1) are
+ * updated.  `x` may equal NULL only if x_norm is also NULL and the caller
+ * keeps the pre-BN tensor itself (pass it as `out` != x is required).        */
+size_t ach_bn_workspace(int batch, int c, int spatial);
+int ach_bn_train_fwd(float *out, int batch, int c, int spatial,
+                     const float *scales, const float *biases,
+                     float *mean, float *variance,
+                     float *rolling_mean, float *rolling_variance,
+                     float *x, float *x_norm, int activation,
+                     void *ws, size_t ws_bytes, ach_stream_t stream);
+/* Same, reading the pre-BN tensor from `x` and writing only `out`
+ * (x is not copied): the layout the network driver uses.                   */
+int ach_bn_train_fwd_from_x(const float *x, float *out, int batch, int c, int spatial,
+                            const float *scales, const float *biases,
+                            float *mean, float *variance,
+                            float *rolling_mean, float *rolling_variance,
+                            int activation, void *ws, size_t ws_bytes,
+                            ach_stream_t stream);
+/* Backward (backwardNormCPU NLayer.c:246-278): scale_updates += sum(d*x_norm);
+ * d *= scales; mean_delta, variance_delta; d <- normalize_delta.  No beta
+ * gradient (the CPU path computes none).  If activation is ACH_LEAKY/RELU the
+ * activation gradient (ConvolutionalLayer.c:898, Activation.c:233-239) is
+ * applied to `delta` first, its sign taken from the recomputed BN output.
+ * x_norm may be NULL (recomputed from x).  mean_delta/variance_delta may be
+ * NULL.                                                                     */
+int ach_bn_bwd(float *delta, int batch, int c, int spatial,
+               const float *x, const float *x_norm,
+               const float *mean, const float *variance,
+               const float *scales, const float *biases, float *scale_updates,
+               float *mean_delta, float *variance_delta, int activation,
+               void *ws, size_t ws_bytes, ach_stream_t stream);
+
+/* ---- activations (Activation.c:160-179 activate, :233-239 gradientArray) */
+int ach_activate(float *x, size_t n, int activation, ach_stream_t stream);
+int ach_gradient(const float *y, size_t n, int activation, float *delta,
+                 ach_stream_t stream);
+
+/* ---- max-pool (MaxPoolLayer.c:237-272 forward, :318-331 backward) --------
+ * out size = (in + padding - size)/stride + 1, window offset -padding/2,
+ * -FLT_MAX init, strict '>' (first max in row-major scan wins); indexes are
+ * global flat input indices.  Backward adds into delta_in in ascending
+ * output order, bit-identical to the reference's scatter loop.            */
+int ach_maxpool_out(int in, int size, int stride, int padding);
+int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w,
+                    int size, int stride, int padding,
+                    float *out, int32_t *indexes, ach_stream_t stream);
+int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
+                    int batch, int c, int h, int w, int size, int stride, int padding,
+                    float *delta_in, ach_stream_t stream);
+
+/* ---- global average pool (AvgPoolLayer.c:29-46, 73-88) ----------------- */
+int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out,
+                    ach_stream_t stream);
+int ach_avgpool_bwd(const float *delta_out, int batch, int c, int spatial,
+                    float *delta_in, ach_stream_t stream);
+
+/* ---- softmax + cross-entropy (SoftMaxLayer.c:47-119) ---------------------
+ * output = softmax(in/temperature) per (image, group); if truth != NULL:
+ * error = t ? -log(p) : 0, delta = t - p, *cost (device float) = sum(error).
+ * Backward is ach_axpy(n, 1, delta, delta_prev) (SoftMaxLayer.c:313).      */
+size_t ach_softmax_workspace(int batch, int groups);
+int ach_softmax_xent(const float *in, int batch, int inputs, int groups,
+                     float temperature, const float *truth,
+                     float *output, float *delta, float *error, float *cost,
+                     void *ws, size_t ws_bytes, ach_stream_t stream);
+
+/* ---- dropout (DropoutLayer.c:55-86) ---------------------------------------
+ * r = u(seed, iter, layer, i) from a counter-based generator (SplitMix64
+ * finaliser, top 24 bits); r < p -> 0 else x * 1/(1-p).  Same mask forward
+ * and backward; nothing is stored.                                          */
+float ach_dropout_uniform(uint64_t seed, uint32_t iter, uint32_t layer, uint32_t i);
+int ach_dropout_fwd(float *x, size_t n, float probability, uint64_t seed,
+                    uint32_t iter, uint32_t layer, ach_stream_t stream);
+int ach_dropout_bwd(float *delta, size_t n, float probability, uint64_t seed,
+                    uint32_t iter, uint32_t layer, ach_stream_t stream);
+
+/* ---- SGD momentum / weight-decay update ----------------------------------
+ * ConvolutionalLayer.update (ConvolutionalLayer.c:959-980):
+ *   dW += -decay*batch*W; W += (lr/batch)*dW; dW *= momentum;
+ *   b  += (lr/batch)*db;  db *= momentum;  (scales likewise, no decay)
+ * scales/scale_updates may be NULL.                                        */
+int ach_conv_update(size_t nweights, float *weights, float *weight_updates,
+                    size_t n, float *biases, float *bias_updates,
+                    float *scales, float *scale_updates,
+                    int batch, float learning_rate, float momentum, float decay,
+                    ach_stream_t stream);
+/* One flat buffer: v += decay_coef*w; w += lr_coef*v; v *= momentum, with
+ * decay_coef = -decay*batch (0 for no decay), lr_coef = lr/batch.          */
+int ach_sgd_update(size_t n, float *w, float *v, float decay_coef, float lr_coef,
+                   float momentum, ach_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,355 @@
+"""Per-operator parity: HIP kernels (through the C-ABI of libach.so) against
+the CPU oracle on identical seeded inputs.
+
+Bars: integer outputs (argmax indices, dropout masks, im2col copies) and
+elementwise ops with identical arithmetic are bit-exact; reductions and GEMMs
+are within 1e-4 normwise relative error (the tolerance the reference's own
+GPU-vs-CPU compare blocks use, DnnUtils.c:377-392)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import aetcnn
+from aetcnn import DeviceArray as D, check
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def dev(a):
+    return D.from_numpy(np.ascontiguousarray(a))
+
+
+def conv_desc(B, Cc, H, W, F, k, s, p):
+    return aetcnn.ConvDesc(B, Cc, H, W, F, k, s, p)
+
+
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("TA,TB", [(0, 0), (1, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(67, 45, 33), (256, 300, 129), (10, 128, 512), (1, 1, 1)])
+def test_gemm(gpu, oracle, TA, TB, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 3 + K + TA * 2 + TB)
+    A = rng.standard_normal((K, M) if TA else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if TB else (K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    lda, ldb = A.shape[1], B.shape[1]
+    for alpha, beta in [(1.0, 1.0), (0.5, 0.0), (1.0, 0.25)]:
+        ref = oracle.gemm(TA, TB, M, N, K, alpha, A, lda, B, ldb, beta, C0, N)
+        dA, dB, dC = dev(A), dev(B), dev(C0)
+        check(gpu.ach_gemm(TA, TB, M, N, K, alpha, dA.ptr, lda, dB.ptr, ldb, beta, dC.ptr, N, None))
+        got = dC.numpy()
+        assert rel_err(got, ref) < 1e-5, (alpha, beta)
+
+
+@pytest.mark.parametrize("Cc,H,W,k,p,s", [(3, 7, 9, 3, 1, 1), (4, 12, 12, 5, 2, 2),
+                                          (2, 35, 35, 11, 0, 4), (6, 6, 6, 6, 0, 1),
+                                          (5, 8, 8, 1, 0, 1)])
+def test_im2col_col2im_bit_exact(gpu, oracle, Cc, H, W, k, p, s):
+    rng = np.random.default_rng(Cc * H + k)
+    im = rng.standard_normal((Cc, H, W)).astype(np.float32)
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    col_ref = np.zeros(Cc * k * k * OH * OW, np.float32)
+    oracle.lib().or_im2col(oracle.P(im), Cc, H, W, k, k, p, p, s, s, 1, 1, oracle.P(col_ref))
+    dim, dcol = dev(im), D(col_ref.shape)
+    check(gpu.ach_im2col(dim.ptr, Cc, H, W, k, k, p, p, s, s, dcol.ptr, None))
+    assert np.array_equal(dcol.numpy(), col_ref)
+    col = rng.standard_normal(col_ref.shape).astype(np.float32)
+    im_ref = np.zeros_like(im)
+    oracle.lib().or_col2im(oracle.P(col), Cc, H, W, k, k, p, p, s, s, 1, 1, oracle.P(im_ref))
+    dcol2, dim2 = dev(col), dev(np.full_like(im, 7.0))  # col2im must overwrite
+    check(gpu.ach_col2im(dcol2.ptr, Cc, H, W, k, k, p, p, s, s, dim2.ptr, None))
+    assert np.array_equal(dim2.numpy(), im_ref)
+
+
+CONV_SHAPES = [
+    # (B, C, H, W, F, k, s, p)
+    (2, 3, 32, 32, 128, 3, 1, 1),
+    (2, 128, 32, 32, 128, 3, 1, 1),
+    (2, 128, 16, 16, 256, 3, 1, 1),
+    (2, 256, 16, 16, 256, 3, 1, 1),
+    (2, 256, 8, 8, 512, 3, 1, 1),
+    (2, 512, 8, 8, 512, 3, 1, 1),
+    (2, 512, 8, 8, 10, 1, 1, 0),
+    (3, 5, 9, 7, 10, 3, 1, 1),
+    (2, 16, 13, 13, 24, 5, 1, 2),
+    (2, 3, 35, 35, 8, 11, 4, 0),
+    (4, 32, 6, 6, 40, 6, 1, 0),
+    (5, 7, 1, 1, 9, 1, 1, 0),
+]
+
+
+def _conv_inputs(shape, seed):
+    B, Cc, H, W, F, k, s, p = shape
+    rng = np.random.default_rng(seed)
+    x = rng.uniform(-1, 1, (B, Cc, H, W)).astype(np.float32)
+    w = (rng.standard_normal((F, Cc, k, k)) * 0.05).astype(np.float32)
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    dy = rng.uniform(-1, 1, (B, F, OH, OW)).astype(np.float32)
+    return x, w, dy
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv_fwd(gpu, oracle, shape):
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, _ = _conv_inputs(shape, 1)
+    ref = oracle.conv_forward(x, w, F, k, s, p)
+    d = conv_desc(*shape)
+    dx, dw, dy = dev(x), dev(w), D(ref.shape)
+    check(gpu.ach_fill(dy.ptr, ref.size, 123.0, None))  # must be overwritten
+    ws = gpu.ach_conv_fwd_workspace(C.byref(d))
+    dws = D(max(ws, 4) // 4)
+    check(gpu.ach_conv_fwd(C.byref(d), dx.ptr, dw.ptr, dy.ptr, dws.ptr, ws, None))
+    assert rel_err(dy.numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv_bwd_data(gpu, oracle, shape):
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, dy = _conv_inputs(shape, 2)
+    _, ref = oracle.conv_backward(x, dy, w, k, s, p)
+    d = conv_desc(*shape)
+    ddy, dw, ddx = dev(dy), dev(w), dev(np.full(x.shape, 5.0, np.float32))
+    ws = gpu.ach_conv_bwd_data_workspace(C.byref(d))
+    dws = D(max(ws, 4) // 4)
+    check(gpu.ach_conv_bwd_data(C.byref(d), ddy.ptr, dw.ptr, ddx.ptr, dws.ptr, ws, None))
+    assert rel_err(ddx.numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_conv_bwd_filter(gpu, oracle, shape):
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, dy = _conv_inputs(shape, 3)
+    dw0 = (np.random.default_rng(9).standard_normal(w.shape) * 0.1).astype(np.float32)
+    ref, _ = oracle.conv_backward(x, dy, w, k, s, p, dw0=dw0, want_dx=False)
+    d = conv_desc(*shape)
+    dx, ddy, ddw = dev(x), dev(dy), dev(dw0)
+    ws = gpu.ach_conv_bwd_filter_workspace(C.byref(d))
+    dws = D(max(ws, 4) // 4)
+    check(gpu.ach_conv_bwd_filter(C.byref(d), dx.ptr, ddy.ptr, ddw.ptr, dws.ptr, ws, None))
+    assert rel_err(ddw.numpy(), ref) < TOL
+
+
+def test_conv_bwd_filter_full_batch_split_k(gpu, oracle):
+    """B=16 forces split-K with several partials; compare to the oracle."""
+    shape = (16, 64, 16, 16, 64, 3, 1, 1)
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, dy = _conv_inputs(shape, 4)
+    ref, _ = oracle.conv_backward(x, dy, w, k, s, p, want_dx=False)
+    d = conv_desc(*shape)
+    assert gpu.ach_conv_bwd_filter_workspace(C.byref(d)) > 0
+    dx, ddy, ddw = dev(x), dev(dy), dev(np.zeros_like(w))
+    ws = gpu.ach_conv_bwd_filter_workspace(C.byref(d))
+    dws = D(ws // 4)
+    check(gpu.ach_conv_bwd_filter(C.byref(d), dx.ptr, ddy.ptr, ddw.ptr, dws.ptr, ws, None))
+    got = ddw.numpy()
+    assert rel_err(got, ref) < TOL
+    # deterministic: a second run from zero gives identical bits
+    ddw.zero()
+    check(gpu.ach_conv_bwd_filter(C.byref(d), dx.ptr, ddy.ptr, ddw.ptr, dws.ptr, ws, None))
+    assert np.array_equal(ddw.numpy(), got)
+
+
+def test_conv_workspace_errors(gpu):
+    d = conv_desc(16, 64, 16, 16, 64, 3, 1, 1)
+    x, dy, dw = D((16, 64, 16, 16)), D((16, 64, 16, 16)), D((64, 64, 3, 3))
+    assert gpu.ach_conv_bwd_filter(C.byref(d), x.ptr, dy.ptr, dw.ptr, None, 0, None) == \
+        aetcnn.ACH_EWORKSPACE
+    bad = conv_desc(0, 64, 16, 16, 64, 3, 1, 1)
+    assert gpu.ach_conv_fwd(C.byref(bad), x.ptr, dw.ptr, dy.ptr, None, 0, None) == aetcnn.ACH_EINVAL
+
+
+# ---------------------------------------------------------------------------
+def _bn_inputs(B, Cc, H, W, seed):
+    rng = np.random.default_rng(seed)
+    out = (rng.standard_normal((B, Cc, H, W)) * 1.3 + 0.2).astype(np.float32)
+    scales = rng.uniform(0.5, 1.5, Cc).astype(np.float32)
+    biases = rng.uniform(-0.2, 0.2, Cc).astype(np.float32)
+    rm = rng.uniform(-0.1, 0.1, Cc).astype(np.float32)
+    rv = rng.uniform(0.5, 1.5, Cc).astype(np.float32)
+    return out, scales, biases, rm, rv
+
+
+@pytest.mark.parametrize("B,Cc,H,W", [(8, 16, 32, 32), (4, 24, 13, 13), (128, 32, 8, 8),
+                                      (3, 5, 1, 1)])
+@pytest.mark.parametrize("act", [aetcnn.LINEAR, aetcnn.LEAKY])
+def test_bn_train_fwd(gpu, oracle, B, Cc, H, W, act):
+    out, sc, bi, rm, rv = _bn_inputs(B, Cc, H, W, B + Cc + act)
+    ref = oracle.bn_forward(out, sc, bi, rm, rv)
+    ref_out = oracle.activate(ref["out"], act)
+    d_out, d_x, d_xn = dev(out), D(out.shape), D(out.shape)
+    d_sc, d_bi, d_m, d_v, d_rm, d_rv = dev(sc), dev(bi), D(Cc), D(Cc), dev(rm), dev(rv)
+    ws = gpu.ach_bn_workspace(B, Cc, H * W)
+    d_ws = D(ws // 4 + 1)
+    check(gpu.ach_bn_train_fwd(d_out.ptr, B, Cc, H * W, d_sc.ptr, d_bi.ptr, d_m.ptr, d_v.ptr,
+                               d_rm.ptr, d_rv.ptr, d_x.ptr, d_xn.ptr, act, d_ws.ptr, ws, None))
+    assert np.array_equal(d_x.numpy(), out)
+    assert rel_err(d_m.numpy(), ref["mean"]) < 1e-5
+    assert rel_err(d_v.numpy(), ref["var"]) < 1e-5
+    assert rel_err(d_rm.numpy(), ref["rm"]) < 1e-5
+    assert rel_err(d_rv.numpy(), ref["rv"]) < 1e-5
+    assert rel_err(d_xn.numpy(), ref["xn"]) < TOL
+    assert rel_err(d_out.numpy(), ref_out) < TOL
+    # from_x variant writes only out
+    d_out2 = D(out.shape)
+    d_rm2, d_rv2 = dev(rm), dev(rv)
+    check(gpu.ach_bn_train_fwd_from_x(d_x.ptr, d_out2.ptr, B, Cc, H * W, d_sc.ptr, d_bi.ptr,
+                                      d_m.ptr, d_v.ptr, d_rm2.ptr, d_rv2.ptr, act, d_ws.ptr, ws,
+                                      None))
+    assert np.array_equal(d_out2.numpy(), d_out.numpy())
+
+
+@pytest.mark.parametrize("B,Cc,H,W", [(8, 16, 32, 32), (4, 24, 13, 13), (128, 32, 8, 8)])
+@pytest.mark.parametrize("act", [aetcnn.LINEAR, aetcnn.LEAKY, aetcnn.RELU])
+def test_bn_bwd(gpu, oracle, B, Cc, H, W, act):
+    out, sc, bi, rm, rv = _bn_inputs(B, Cc, H, W, 7 * B + Cc + act)
+    f = oracle.bn_forward(out, sc, bi, rm, rv)
+    y = oracle.activate(f["out"], act)
+    rng = np.random.default_rng(B * Cc + act)
+    delta = rng.standard_normal(out.shape).astype(np.float32)
+    su0 = rng.standard_normal(Cc).astype(np.float32) * 0.1
+    d_after_act = oracle.gradient(y, act, delta)
+    ref = oracle.bn_backward(d_after_act, f["x"], f["xn"], f["mean"], f["var"], sc, su0)
+    d_delta, d_x = dev(delta), dev(f["x"])
+    d_m, d_v, d_sc, d_bi, d_su = dev(f["mean"]), dev(f["var"]), dev(sc), dev(bi), dev(su0)
+    d_md, d_vd = D(Cc), D(Cc)
+    ws = gpu.ach_bn_workspace(B, Cc, H * W)
+    d_ws = D(ws // 4 + 1)
+    check(gpu.ach_bn_bwd(d_delta.ptr, B, Cc, H * W, d_x.ptr, None, d_m.ptr, d_v.ptr, d_sc.ptr,
+                         d_bi.ptr, d_su.ptr, d_md.ptr, d_vd.ptr, act, d_ws.ptr, ws, None))
+    assert rel_err(d_su.numpy(), ref["scale_updates"]) < TOL
+    assert rel_err(d_md.numpy(), ref["mean_delta"]) < TOL
+    assert rel_err(d_vd.numpy(), ref["var_delta"]) < TOL
+    assert rel_err(d_delta.numpy(), ref["delta"]) < TOL
+
+
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("act", [aetcnn.LEAKY, aetcnn.RELU, aetcnn.LINEAR, aetcnn.LOGISTIC])
+def test_activation_bit_exact(gpu, oracle, act):
+    rng = np.random.default_rng(act)
+    x = rng.standard_normal(100003).astype(np.float32) * 3
+    x[:5] = [0.0, -0.0, 1e-38, -1e-38, 2.5]
+    ref = oracle.activate(x, act)
+    d = dev(x)
+    check(gpu.ach_activate(d.ptr, x.size, act, None))
+    got = d.numpy()
+    if act == aetcnn.LOGISTIC:
+        assert rel_err(got, ref) < 1e-6
+    else:
+        assert np.array_equal(got, ref)
+    delta = rng.standard_normal(x.size).astype(np.float32)
+    gref = oracle.gradient(ref, act, delta)
+    dd = dev(delta)
+    check(gpu.ach_gradient(dev(ref).ptr, x.size, act, dd.ptr, None))
+    assert np.array_equal(dd.numpy(), gref)
+
+
+@pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [
+    (4, 3, 32, 32, 2, 2, 1),      # darknet default padding = size-1
+    (2, 5, 55, 55, 3, 2, 0),      # AlexNet overlapping 3x3/2
+    (2, 4, 13, 13, 3, 2, 2),
+    (3, 2, 7, 9, 2, 1, 1),
+    (2, 3, 16, 16, 2, 2, 0),
+])
+def test_maxpool_bit_exact(gpu, oracle, B, Cc, H, W, size, stride, pad):
+    rng = np.random.default_rng(H * W + size)
+    # small integers produce many ties: first max in scan order must win
+    x = rng.integers(-3, 4, (B, Cc, H, W)).astype(np.float32)
+    out, idx = oracle.maxpool_forward(x, size, stride, pad)
+    dx, dout, didx = dev(x), D(out.shape), D(out.shape, np.int32)
+    check(gpu.ach_maxpool_fwd(dx.ptr, B, Cc, H, W, size, stride, pad, dout.ptr, didx.ptr, None))
+    assert np.array_equal(dout.numpy(), out)
+    assert np.array_equal(didx.numpy(), idx)
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    din0 = rng.standard_normal(x.shape).astype(np.float32)
+    ref = oracle.maxpool_backward(g, idx, din0)
+    ddin = dev(din0)
+    check(gpu.ach_maxpool_bwd(dev(g).ptr, didx.ptr, B, Cc, H, W, size, stride, pad, ddin.ptr,
+                              None))
+    assert np.array_equal(ddin.numpy(), ref)
+
+
+def test_avgpool_bit_exact(gpu, oracle):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((128, 10, 8, 8)).astype(np.float32)
+    ref = oracle.avgpool_forward(x)
+    dout = D(ref.shape)
+    check(gpu.ach_avgpool_fwd(dev(x).ptr, 128, 10, 64, dout.ptr, None))
+    assert np.array_equal(dout.numpy(), ref)
+    g = rng.standard_normal(ref.shape).astype(np.float32)
+    din0 = rng.standard_normal(x.shape).astype(np.float32)
+    refb = oracle.avgpool_backward(g, x.shape, din0)
+    ddin = dev(din0)
+    check(gpu.ach_avgpool_bwd(dev(g).ptr, 128, 10, 64, ddin.ptr, None))
+    assert np.array_equal(ddin.numpy(), refb)
+
+
+@pytest.mark.parametrize("B,n,groups", [(128, 10, 1), (512, 1000, 1), (7, 12, 3)])
+def test_softmax_xent(gpu, oracle, B, n, groups):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((B, n)) * 3).astype(np.float32)
+    labels = rng.integers(0, n // groups, (B, groups))
+    truth = np.zeros((B, n), np.float32)
+    for b in range(B):
+        for g in range(groups):
+            truth[b, g * (n // groups) + labels[b, g]] = 1
+    out, delta, err, cost = oracle.softmax_xent(x, truth, groups)
+    dout, ddelta, derr, dcost = D(x.shape), D(x.shape), D(x.shape), D(1)
+    ws = gpu.ach_softmax_workspace(B, groups)
+    dws = D(ws // 4 + 1)
+    check(gpu.ach_softmax_xent(dev(x).ptr, B, n, groups, 1.0, dev(truth).ptr, dout.ptr,
+                               ddelta.ptr, derr.ptr, dcost.ptr, dws.ptr, ws, None))
+    got = dout.numpy()
+    assert rel_err(got, out) < 1e-6
+    assert rel_err(ddelta.numpy(), delta) < 1e-6
+    assert rel_err(derr.numpy(), err) < 1e-6
+    assert abs(dcost.numpy()[0] - cost) <= 1e-5 * abs(cost)
+    # label predictions bit-exact
+    assert np.array_equal(got.reshape(B * groups, -1).argmax(1),
+                          out.reshape(B * groups, -1).argmax(1))
+
+
+def test_dropout_mask_bit_exact(gpu, oracle):
+    n = 1 << 20
+    for (p, seed, it, layer) in [(0.5, 1, 0, 7), (0.2, 12345, 99, 3), (0.0, 5, 1, 1)]:
+        ref = oracle.dropout_mask_scale(n, p, seed, it, layer)
+        d = dev(np.ones(n, np.float32))
+        check(gpu.ach_dropout_fwd(d.ptr, n, p, seed, it, layer, None))
+        assert np.array_equal(d.numpy(), ref)
+        check(gpu.ach_dropout_bwd(d.ptr, n, p, seed, it, layer, None))
+        assert np.array_equal(d.numpy(), oracle.dropout_mask_scale(n, p, seed, it, layer) * ref)
+    assert gpu.ach_dropout_uniform(3, 4, 5, 6) == oracle.lib().or_dropout_uniform(3, 4, 5, 6)
+
+
+def test_conv_update(gpu, oracle):
+    rng = np.random.default_rng(11)
+    nw, n = 10007, 64
+    w, dw = rng.standard_normal(nw).astype(np.float32), rng.standard_normal(nw).astype(np.float32)
+    b, db = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    s, ds = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    ref = oracle.conv_update(w, dw, b, db, s, ds, 128, 0.1, 0.9, 5e-4)
+    arrs = [dev(a) for a in (w, dw, b, db, s, ds)]
+    check(gpu.ach_conv_update(nw, arrs[0].ptr, arrs[1].ptr, n, arrs[2].ptr, arrs[3].ptr,
+                              arrs[4].ptr, arrs[5].ptr, 128, 0.1, 0.9, 5e-4, None))
+    for a, r in zip(arrs, ref):
+        assert rel_err(a.numpy(), r) < 1e-6
+
+
+def test_bias_ops(gpu, oracle):
+    rng = np.random.default_rng(12)
+    B, n, sp = 16, 10, 64
+    out = rng.standard_normal((B, n, sp)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    ref = out.copy()
+    oracle.lib().or_add_bias(oracle.P(ref), oracle.P(bias), B, n, sp)
+    d = dev(out)
+    check(gpu.ach_add_bias(d.ptr, dev(bias).ptr, B, n, sp, None))
+    assert np.array_equal(d.numpy(), ref)
+    upd = rng.standard_normal(n).astype(np.float32)
+    refu = upd.copy()
+    oracle.lib().or_bias_grad(oracle.P(refu), oracle.P(out), B, n, sp)
+    du = dev(upd)
+    check(gpu.ach_bias_grad(du.ptr, dev(out).ptr, B, n, sp, None, 0, None))
+    assert rel_err(du.numpy(), refu) < 1e-5
