@@ -125,6 +125,8 @@ _NET = {
     "an_forward": (_i, [_vp, _i]),
     "an_backward": (_i, [_vp]),
     "an_update": (_i, [_vp]),
+    "an_layer_forward": (_i, [_vp, _i, _i]),
+    "an_layer_backward": (_i, [_vp, _i]),
     "an_n_layers": (_i, [_vp]),
     "an_batch": (_i, [_vp]),
     "an_input": (_vp, [_vp]),
@@ -337,6 +339,12 @@ class Network:
     def update(self):
         check(self.lib.an_update(self.h), "an_update")
 
+    def layer_forward(self, i, train=1):
+        check(self.lib.an_layer_forward(self.h, i, train), "an_layer_forward")
+
+    def layer_backward(self, i):
+        check(self.lib.an_layer_backward(self.h, i), "an_layer_backward")
+
     def buffer(self, layer: int, which: int) -> Optional[np.ndarray]:
         n = _sz()
         p = self.lib.an_layer_buffer(self.h, layer, which, C.byref(n))
@@ -350,7 +358,7 @@ class Network:
     def set_buffer(self, layer: int, which: int, values: np.ndarray):
         n = _sz()
         p = self.lib.an_layer_buffer(self.h, layer, which, C.byref(n))
-        v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+        v = np.ascontiguousarray(values, dtype=np.int32 if which == 14 else np.float32).ravel()
         assert p and v.size == n.value, (layer, which, v.size, n.value)
         check(ops().ach_memcpy_h2d(p, v.ctypes.data, v.nbytes, self.stream), "h2d")
 

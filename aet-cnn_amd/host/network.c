@@ -618,24 +618,48 @@ int an_forward(an_network *net, int train)
     return ACH_OK;
 }
 
+static an_state backward_state(an_network *net, int i)
+{
+    an_state st = base_state(net);
+    st.index = i;
+    if (i > 0) {
+        st.input = net->layers[i - 1]->output;
+        st.delta = net->layers[i - 1]->delta;
+    }
+    return st;
+}
+
 /* NNetwork.backward (NNetwork.c:627-654).                                 */
 int an_backward(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
-    an_state st = base_state(net);
     for (int i = net->n - 1; i >= 0; --i) {
-        st.index = i;
-        if (i == 0) {
-            st.input = net->input;
-            st.delta = NULL;
-        } else {
-            st.input = net->layers[i - 1]->output;
-            st.delta = net->layers[i - 1]->delta;
-        }
         an_layer *l = net->layers[i];
-        AN_CHECK(l->backward(net, l, st));
+        AN_CHECK(l->backward(net, l, backward_state(net, i)));
     }
     return ACH_OK;
+}
+
+/* One layer of the loops above, with the same NetworkState: the
+ * reference's per-layer NLayer.forward / backward entry points.           */
+int an_layer_forward(an_network *net, int i, int train)
+{
+    an_layer *l = an_get_layer(net, i);
+    if (!l || !net->finalized) return ACH_EINVAL;
+    an_state st = base_state(net);
+    st.train = train;
+    st.index = i;
+    if (i > 0) st.input = net->layers[i - 1]->output;
+    if (train && l->zero_delta && !l->shares_prev)
+        AN_CHECK(ach_fill(l->delta, (size_t)l->batch * l->outputs, 0.f, net->stream));
+    return l->forward(net, l, st);
+}
+
+int an_layer_backward(an_network *net, int i)
+{
+    an_layer *l = an_get_layer(net, i);
+    if (!l || !net->finalized) return ACH_EINVAL;
+    return l->backward(net, l, backward_state(net, i));
 }
 
 /* NNetwork.updateCPU (NNetwork.c:667-680) with the constant rate policy:

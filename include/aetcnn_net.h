@@ -129,6 +129,10 @@ int an_train(an_network *net, const float *host_input, const float *host_truth, 
 int an_forward(an_network *net, int train);
 int an_backward(an_network *net);
 int an_update(an_network *net);
+/* one layer with the NetworkState the loops above would give it
+ * (NLayer.forward / NLayer.backward, NLayer.h:159-166)                     */
+int an_layer_forward(an_network *net, int layer, int train);
+int an_layer_backward(an_network *net, int layer);
 
 /* ---- introspection (tests, checkpoints) ------------------------------------ */
 int an_n_layers(const an_network *net);

@@ -665,6 +665,8 @@ struct or_net {
     float *workspace;
     size_t workspace_size;
     float *input; /* host copy of the current input (layer 0 reads it) */
+    float *truth; /* host copy of the current one-hot truth */
+    int has_truth;
 };
 
 or_net *or_net_create(int batch, int h, int w, int c)
@@ -837,6 +839,7 @@ int or_net_finalize(or_net *net)
     net->workspace_size = ws;
     net->workspace = fzalloc(ws);
     net->input = fzalloc((size_t)net->batch * net->h * net->w * net->c);
+    net->truth = fzalloc((size_t)net->batch * net->layers[net->n - 1].outputs);
     return 0;
 }
 
@@ -857,6 +860,7 @@ void or_net_free(or_net *net)
     free(net->layers);
     free(net->workspace);
     free(net->input);
+    free(net->truth);
     free(net);
 }
 
@@ -948,32 +952,53 @@ static void layer_backward(or_net *net, or_layer *l, or_state st)
     }
 }
 
-float or_net_forward_backward(or_net *net, const float *input, const float *truth)
+void or_net_load(or_net *net, const float *input, const float *truth)
 {
     size_t in_n = (size_t)net->batch * net->h * net->w * net->c;
     memcpy(net->input, input, in_n * sizeof(float));
-    or_state st = {truth, net->input, NULL, 1, 0};
-    /* NNetwork.forward, NNetwork.c:382-396: zero each delta, then forward */
-    for (int i = 0; i < net->n; ++i) {
-        or_layer *l = &net->layers[i];
-        st.index = i;
-        if (l->delta) memset(l->delta, 0, sizeof(float) * (size_t)l->batch * l->outputs);
-        layer_forward(net, l, st);
-        st.input = l->output;
+    if (truth) {
+        const or_layer *last = &net->layers[net->n - 1];
+        size_t tn = (size_t)net->batch * last->outputs;
+        memcpy(net->truth, truth, tn * sizeof(float));
+        net->has_truth = 1;
+    } else {
+        net->has_truth = 0;
     }
-    /* NNetwork.backward, NNetwork.c:627-654 */
-    for (int i = net->n - 1; i >= 0; --i) {
-        or_state bs = st;
-        bs.index = i;
-        if (i == 0) {
-            bs.input = net->input;
-            bs.delta = NULL;
-        } else {
-            bs.input = net->layers[i - 1].output;
-            bs.delta = net->layers[i - 1].delta;
-        }
-        layer_backward(net, &net->layers[i], bs);
+}
+
+static or_state fwd_state(or_net *net, int i, int train)
+{
+    or_state st = {net->has_truth ? net->truth : NULL, net->input, NULL, train, i};
+    if (i > 0) st.input = net->layers[i - 1].output;
+    return st;
+}
+
+static or_state bwd_state(or_net *net, int i)
+{
+    or_state st = {net->has_truth ? net->truth : NULL, net->input, NULL, 1, i};
+    if (i > 0) {
+        st.input = net->layers[i - 1].output;
+        st.delta = net->layers[i - 1].delta;
     }
+    return st;
+}
+
+/* One layer of NNetwork.forward (NNetwork.c:385-395): zero its delta, run. */
+void or_net_layer_forward(or_net *net, int i, int train)
+{
+    or_layer *l = &net->layers[i];
+    if (train && l->delta) memset(l->delta, 0, sizeof(float) * (size_t)l->batch * l->outputs);
+    layer_forward(net, l, fwd_state(net, i, train));
+}
+
+/* One layer of NNetwork.backward (NNetwork.c:631-652). */
+void or_net_layer_backward(or_net *net, int i)
+{
+    layer_backward(net, &net->layers[i], bwd_state(net, i));
+}
+
+float or_net_cost(or_net *net)
+{
     /* getNetworkCost (NNetwork.c:611-624) then sum/(subdivisions*batch) */
     float sum = 0;
     int count = 0;
@@ -984,6 +1009,14 @@ float or_net_forward_backward(or_net *net, const float *input, const float *trut
         }
     float cost = count ? sum / count : 0;
     return cost / net->batch;
+}
+
+float or_net_forward_backward(or_net *net, const float *input, const float *truth)
+{
+    or_net_load(net, input, truth);
+    for (int i = 0; i < net->n; ++i) or_net_layer_forward(net, i, 1);
+    for (int i = net->n - 1; i >= 0; --i) or_net_layer_backward(net, i);
+    return or_net_cost(net);
 }
 
 void or_net_update(or_net *net)

@@ -160,6 +160,12 @@ float or_net_train(or_net *net, const float *input, const float *truth);
 /* forward + backward only (no update)                                       */
 float or_net_forward_backward(or_net *net, const float *input, const float *truth);
 void or_net_update(or_net *net);
+/* per-layer steps with the network's own state (NetworkState of
+ * NNetwork.forward/backward): load one batch, then run layer i             */
+void or_net_load(or_net *net, const float *input, const float *truth);
+void or_net_layer_forward(or_net *net, int i, int train);
+void or_net_layer_backward(or_net *net, int i);
+float or_net_cost(or_net *net);
 
 /* introspection for tests */
 int  or_net_n_layers(const or_net *net);

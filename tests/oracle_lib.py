@@ -66,6 +66,10 @@ _SIGS = {
     "or_net_train": (_f, [_vp, _vp, _vp]),
     "or_net_forward_backward": (_f, [_vp, _vp, _vp]),
     "or_net_update": (None, [_vp]),
+    "or_net_load": (None, [_vp, _vp, _vp]),
+    "or_net_layer_forward": (None, [_vp, _i, _i]),
+    "or_net_layer_backward": (None, [_vp, _i]),
+    "or_net_cost": (_f, [_vp]),
     "or_net_n_layers": (_i, [_vp]),
     "or_net_buffer": (_vp, [_vp, _i, _i, C.POINTER(_sz)]),
     "or_net_layer_info": (None, [_vp, _i, C.POINTER(_i)]),
@@ -281,6 +285,18 @@ class OracleNet:
     def update(self):
         self.L.or_net_update(self.h)
 
+    def load(self, x, truth):
+        self.L.or_net_load(self.h, P(f32(x)), P(f32(truth)) if truth is not None else None)
+
+    def layer_forward(self, i, train=1):
+        self.L.or_net_layer_forward(self.h, i, train)
+
+    def layer_backward(self, i):
+        self.L.or_net_layer_backward(self.h, i)
+
+    def cost(self):
+        return self.L.or_net_cost(self.h)
+
     def n_layers(self):
         return self.L.or_net_n_layers(self.h)
 
@@ -296,7 +312,7 @@ class OracleNet:
     def set_buffer(self, layer, which, values):
         n = _sz()
         p = self.L.or_net_buffer(self.h, layer, which, C.byref(n))
-        v = f32(values).ravel()
+        v = np.ascontiguousarray(values, np.int32 if which == 14 else np.float32).ravel()
         assert p and v.size == n.value
         C.memmove(p, v.ctypes.data, v.nbytes)
 

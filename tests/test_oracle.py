@@ -1,0 +1,380 @@
+"""Pins the CPU oracle (oracle/liboracle.so) against what the mathematics
+fixes, independently of how the oracle is written: double-precision brute
+force, adjoint identities, closed forms, textbook gradients, finite
+differences and published known-answer values.  The reference ships no
+golden vectors (it has no tests), so these checks are the pin.  CPU only."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from conftest import rel_err
+
+LEAKY, RELU, LINEAR = 7, 1, 3
+
+
+from refs64 import conv_ref, dgrad_ref, wgrad_ref  # noqa: E402
+
+
+# ---- GEMM --------------------------------------------------------------------
+@pytest.mark.parametrize("TA,TB", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_vs_float64(TA, TB):
+    rng = np.random.default_rng(TA * 2 + TB)
+    M, N, K = 13, 17, 19
+    A = rng.standard_normal((K, M) if TA else (M, K)).astype(np.float32)
+    B = rng.standard_normal((N, K) if TB else (K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    got = O.gemm(TA, TB, M, N, K, 0.75, A, A.shape[1], B, B.shape[1], 0.5, C0, N)
+    a = A.T if TA else A
+    b = B.T if TB else B
+    ref = 0.75 * a.astype(np.float64) @ b.astype(np.float64) + 0.5 * C0
+    assert rel_err(got, ref) < 1e-6
+
+
+def test_gemm_parallel_is_bit_identical():
+    rng = np.random.default_rng(3)
+    M, N, K = 64, 100, 300
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    C0 = np.zeros((M, N), np.float32)
+    O.lib().or_set_gemm_parallel(0)
+    a = O.gemm(0, 0, M, N, K, 1, A, K, B, N, 1, C0, N)
+    O.lib().or_set_gemm_parallel(1)
+    b = O.gemm(0, 0, M, N, K, 1, A, K, B, N, 1, C0, N)
+    O.lib().or_set_gemm_parallel(0)
+    assert np.array_equal(a, b)
+
+
+# ---- im2col / col2im -----------------------------------------------------------
+@pytest.mark.parametrize("Cc,H,W,k,p,s", [(2, 5, 6, 3, 1, 1), (3, 9, 9, 5, 2, 2), (1, 11, 11, 11, 0, 4)])
+def test_im2col_index_map_and_col2im_adjoint(Cc, H, W, k, p, s):
+    rng = np.random.default_rng(k)
+    im = rng.standard_normal((Cc, H, W)).astype(np.float32)
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    col = np.zeros(Cc * k * k * OH * OW, np.float32)
+    O.lib().or_im2col(O.P(im), Cc, H, W, k, k, p, p, s, s, 1, 1, O.P(col))
+    col = col.reshape(Cc, k, k, OH, OW)
+    for c in range(Cc):
+        for ki in range(k):
+            for kj in range(k):
+                for oh in range(OH):
+                    for ow in range(OW):
+                        ih, iw = oh * s - p + ki, ow * s - p + kj
+                        v = im[c, ih, iw] if 0 <= ih < H and 0 <= iw < W else 0.0
+                        assert col[c, ki, kj, oh, ow] == v
+    # col2im is the adjoint of im2col: <im2col(x), y> == <x, col2im(y)>
+    y = rng.standard_normal(col.size).astype(np.float32)
+    back = np.full((Cc, H, W), 9.0, np.float32)  # must be zeroed first
+    O.lib().or_col2im(O.P(y), Cc, H, W, k, k, p, p, s, s, 1, 1, O.P(back))
+    lhs = float(np.dot(col.ravel().astype(np.float64), y.astype(np.float64)))
+    rhs = float(np.dot(im.ravel().astype(np.float64), back.ravel().astype(np.float64)))
+    assert abs(lhs - rhs) <= 1e-5 * max(1.0, abs(lhs))
+
+
+# ---- convolution ---------------------------------------------------------------
+SHAPES = [(2, 3, 8, 8, 4, 3, 1, 1), (1, 4, 7, 9, 5, 5, 2, 2), (2, 2, 12, 12, 3, 11, 4, 0),
+          (3, 6, 4, 4, 7, 1, 1, 0), (2, 5, 6, 6, 8, 6, 1, 0)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_conv_forward_vs_direct(shape):
+    B, Cc, H, W, F, k, s, p = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.uniform(-1, 1, (B, Cc, H, W)).astype(np.float32)
+    w = rng.standard_normal((F, Cc, k, k)).astype(np.float32)
+    assert rel_err(O.conv_forward(x, w, F, k, s, p), conv_ref(x, w, s, p)) < 1e-6
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_conv_backward_vs_direct_and_adjoint(shape):
+    B, Cc, H, W, F, k, s, p = shape
+    rng = np.random.default_rng(sum(shape) + 1)
+    x = rng.uniform(-1, 1, (B, Cc, H, W)).astype(np.float32)
+    w = rng.standard_normal((F, Cc, k, k)).astype(np.float32)
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    dy = rng.standard_normal((B, F, OH, OW)).astype(np.float32)
+    dw0 = rng.standard_normal(w.shape).astype(np.float32)
+    dw, dx = O.conv_backward(x, dy, w, k, s, p, dw0=dw0)
+    assert rel_err(dw, dw0 + wgrad_ref(x, dy, k, s, p)) < 1e-6  # accumulates (beta = 1)
+    assert rel_err(dx, dgrad_ref(dy, w, x.shape, s, p)) < 1e-6
+    # adjoint identities: <conv(x,W), dy> = <x, dgrad(dy)> = <W, wgrad(x,dy)>
+    y = conv_ref(x, w, s, p)
+    ip = float((y * dy).sum())
+    assert abs(ip - float((x.astype(np.float64) * dx).sum())) <= 1e-5 * abs(ip) + 1e-5
+    assert abs(ip - float((w.astype(np.float64) * (dw - dw0)).sum())) <= 1e-4 * abs(ip) + 1e-4
+
+
+# ---- bias ------------------------------------------------------------------------
+def test_bias_add_and_grad():
+    rng = np.random.default_rng(4)
+    out = rng.standard_normal((3, 4, 5)).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    ref = out + b[None, :, None]
+    got = out.copy()
+    O.lib().or_add_bias(O.P(got), O.P(b), 3, 4, 5)
+    assert np.array_equal(got, ref)
+    upd = np.ones(4, np.float32)
+    O.lib().or_bias_grad(O.P(upd), O.P(out), 3, 4, 5)
+    assert rel_err(upd, 1 + out.astype(np.float64).sum(axis=(0, 2))) < 1e-6
+
+
+# ---- batch-norm ------------------------------------------------------------------
+def test_bn_forward_closed_form():
+    rng = np.random.default_rng(5)
+    B, Cc, H, W = 6, 3, 5, 4
+    out = (rng.standard_normal((B, Cc, H, W)) * 2 + 0.5).astype(np.float32)
+    sc = rng.uniform(0.5, 2, Cc).astype(np.float32)
+    bi = rng.standard_normal(Cc).astype(np.float32)
+    rm0 = rng.standard_normal(Cc).astype(np.float32)
+    rv0 = rng.uniform(0.5, 2, Cc).astype(np.float32)
+    r = O.bn_forward(out, sc, bi, rm0, rv0)
+    x64 = out.astype(np.float64)
+    mean = x64.mean(axis=(0, 2, 3))
+    var = x64.var(axis=(0, 2, 3), ddof=1)  # unbiased (NormData.c:176)
+    assert rel_err(r["mean"], mean) < 1e-6
+    assert rel_err(r["var"], var) < 1e-5
+    assert rel_err(r["rm"], 0.9 * rm0 + 0.1 * mean) < 1e-6
+    assert rel_err(r["rv"], 0.9 * rv0 + 0.1 * var) < 1e-6
+    xn = (x64 - mean[None, :, None, None]) / (np.sqrt(var) + 1e-6)[None, :, None, None]
+    assert np.array_equal(r["x"], out)
+    assert rel_err(r["xn"], xn) < 1e-5
+    assert rel_err(r["out"], xn * sc[None, :, None, None] + bi[None, :, None, None]) < 1e-5
+    assert r["nan"] == 0
+
+
+def test_bn_backward_textbook_gradient_and_fd():
+    """dgamma = sum(delta*xn) exactly; delta' matches the textbook batch-norm
+    input gradient of y = (x-mu)/sqrt(var_N + 1e-5) (biased var in the
+    derivative, as the reference's /N terms), and a finite-difference check
+    of that forward."""
+    rng = np.random.default_rng(6)
+    B, Cc, H, W = 4, 3, 6, 5
+    N = B * H * W
+    out = (rng.standard_normal((B, Cc, H, W)) * 1.5 + 0.3).astype(np.float32)
+    sc = rng.uniform(0.5, 2, Cc).astype(np.float32)
+    f = O.bn_forward(out, sc, np.zeros(Cc, np.float32))
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    r = O.bn_backward(g, f["x"], f["xn"], f["mean"], f["var"], sc)
+    assert rel_err(r["scale_updates"], (g.astype(np.float64) * f["xn"]).sum(axis=(0, 2, 3))) < 1e-6
+    # textbook: for y = xhat with xhat = (x-mu)/s, s = sqrt(v + eps),
+    # dL/dx = (1/s)(dyh - mean(dyh) - (x-mu)/s^2 * mean(dyh*(x-mu))), dyh = gamma*g
+    x = out.astype(np.float64)
+    mu = f["mean"].astype(np.float64)[None, :, None, None]
+    v = f["var"].astype(np.float64)[None, :, None, None]
+    s = np.sqrt(v + 1e-5)
+    dyh = g * sc[None, :, None, None].astype(np.float64)
+    xc = x - mu
+    ref = (dyh - dyh.mean(axis=(0, 2, 3), keepdims=True)
+           - xc / s ** 2 * (dyh * xc).mean(axis=(0, 2, 3), keepdims=True)) / s
+    assert rel_err(r["delta"], ref) < 1e-4
+    # finite differences of L(x) = sum(gamma*g*(x-mu)/sqrt(var_N(x)+1e-5)),
+    # var_N with denominator N (the derivative the reference's /N terms take)
+    def L(xx):
+        m = xx.mean(axis=(0, 2, 3), keepdims=True)
+        vn = ((xx - m) ** 2).mean(axis=(0, 2, 3), keepdims=True)
+        return float((dyh * (xx - m) / np.sqrt(vn + 1e-5)).sum())
+    for idx in [(0, 0, 0, 0), (1, 2, 3, 4), (3, 1, 5, 2)]:
+        e = np.zeros_like(x)
+        e[idx] = 1e-5
+        fd = (L(x + e) - L(x - e)) / 2e-5
+        # unbiased vs biased variance differ by N/(N-1): allow that much
+        assert abs(fd - r["delta"][idx]) <= 5e-2 * abs(fd) / N * 10 + 2e-3 * max(1, abs(fd))
+
+
+# ---- activations -------------------------------------------------------------------
+def test_activations_exact():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(10001) * 3).astype(np.float32)
+    x[:3] = [0.0, -0.0, -1e-30]
+    leaky = np.where(x > 0, x, (0.1 * x.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(O.activate(x, LEAKY), leaky)
+    assert np.array_equal(O.activate(x, RELU), x * (x > 0))
+    assert np.array_equal(O.activate(x, LINEAR), x)
+    d = rng.standard_normal(x.size).astype(np.float32)
+    assert np.array_equal(O.gradient(leaky, LEAKY, d), d * np.where(leaky > 0, 1, np.float32(0.1)))
+    assert np.array_equal(O.gradient(x, RELU, d), d * (x > 0))
+
+
+# ---- pooling -------------------------------------------------------------------------
+@pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [(2, 2, 6, 6, 2, 2, 1), (1, 2, 9, 9, 3, 2, 0),
+                                                       (1, 1, 5, 7, 3, 2, 2)])
+def test_maxpool_brute_force(B, Cc, H, W, size, stride, pad):
+    rng = np.random.default_rng(H + size)
+    x = rng.integers(-2, 3, (B, Cc, H, W)).astype(np.float32)  # ties
+    out, idx = O.maxpool_forward(x, size, stride, pad)
+    OH, OW = out.shape[2:]
+    off = -(pad // 2)
+    flat = x.ravel()
+    for b in range(B):
+        for c in range(Cc):
+            for i in range(OH):
+                for j in range(OW):
+                    best, bi = -np.finfo(np.float32).max, -1
+                    for n in range(size):
+                        for m in range(size):
+                            h, w = off + i * stride + n, off + j * stride + m
+                            if 0 <= h < H and 0 <= w < W:
+                                k = ((b * Cc + c) * H + h) * W + w
+                                if flat[k] > best:  # strict: first max wins
+                                    best, bi = flat[k], k
+                    assert out[b, c, i, j] == best and idx[b, c, i, j] == bi
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    d0 = rng.standard_normal(x.shape).astype(np.float32)
+    ref = d0.ravel().copy()
+    np.add.at(ref, idx.ravel(), g.ravel())  # sequential, ascending output order
+    assert np.array_equal(O.maxpool_backward(g, idx, d0).ravel(), ref)
+
+
+def test_avgpool_closed_form():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((3, 4, 5, 5)).astype(np.float32)
+    assert rel_err(O.avgpool_forward(x), x.astype(np.float64).mean(axis=(2, 3))) < 1e-6
+    g = rng.standard_normal((3, 4)).astype(np.float32)
+    d = O.avgpool_backward(g, x.shape)
+    assert rel_err(d, np.broadcast_to(g[:, :, None, None] / 25.0, x.shape)) < 1e-6
+
+
+# ---- softmax + cross-entropy -----------------------------------------------------------
+def test_softmax_xent_closed_form():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((5, 7)) * 4).astype(np.float32)
+    t = np.zeros_like(x)
+    t[np.arange(5), rng.integers(0, 7, 5)] = 1
+    out, delta, err, cost = O.softmax_xent(x, t)
+    x64 = x.astype(np.float64)
+    p = np.exp(x64 - x64.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    assert rel_err(out, p) < 1e-6
+    assert np.allclose(out.sum(1), 1, atol=1e-6)
+    assert rel_err(delta, t - p) < 1e-6
+    assert rel_err(err, np.where(t > 0, -np.log(p), 0)) < 1e-6
+    assert abs(cost - float(-(t * np.log(p)).sum())) < 1e-5 * abs(cost)
+    d0 = rng.standard_normal(x.shape).astype(np.float32)
+    d1 = d0.copy()
+    O.lib().or_softmax_backward(O.P(delta), delta.size, O.P(d1))
+    assert np.array_equal(d1, d0 + delta)
+
+
+# ---- dropout -------------------------------------------------------------------------------
+def test_dropout_uniform_known_answer():
+    # u(seed, 0, 0, 0) is the SplitMix64 finaliser of the seed; SplitMix64's
+    # first output for state 0 is 0xE220A8397B1DCDAF (finaliser of the golden
+    # gamma 0x9E3779B97F4A7C15), so u(gamma,0,0,0) = top 24 bits / 2^24.
+    u = O.lib().or_dropout_uniform(0x9E3779B97F4A7C15, 0, 0, 0)
+    assert u == (0xE220A8397B1DCDAF >> 40) / float(1 << 24)
+
+
+def test_dropout_statistics_and_determinism():
+    n = 1 << 20
+    for p in (0.5, 0.2):
+        m = O.dropout_mask_scale(n, p, 99, 3, 4)
+        keep = m != 0
+        assert abs((1 - keep.mean()) - p) < 3e-3
+        assert np.all(m[keep] == np.float32(1.0 / (1.0 - p)))
+        assert np.array_equal(m, O.dropout_mask_scale(n, p, 99, 3, 4))
+        assert not np.array_equal(keep, O.dropout_mask_scale(n, p, 99, 4, 4) != 0)
+        assert not np.array_equal(keep, O.dropout_mask_scale(n, p, 99, 3, 5) != 0)
+
+
+# ---- SGD update ------------------------------------------------------------------------------
+def test_sgd_update_closed_form_three_steps():
+    rng = np.random.default_rng(10)
+    nw, n = 50, 6
+    w, v = rng.standard_normal(nw), rng.standard_normal(nw)
+    b, vb = rng.standard_normal(n), rng.standard_normal(n)
+    s, vs = rng.standard_normal(n), rng.standard_normal(n)
+    W, V, Bb, VB, S, VS = (a.astype(np.float32) for a in (w, v, b, vb, s, vs))
+    lr, mom, decay, batch = 0.1, 0.9, 5e-4, 128
+    for _ in range(3):
+        W, V, Bb, VB, S, VS = O.conv_update(W, V, Bb, VB, S, VS, batch, lr, mom, decay)
+        v = v - decay * batch * w
+        w = w + lr / batch * v
+        v = v * mom
+        b = b + lr / batch * vb
+        vb = vb * mom
+        s = s + lr / batch * vs
+        vs = vs * mom
+    for got, ref in ((W, w), (V, v), (Bb, b), (VB, vb), (S, s), (VS, vs)):
+        assert rel_err(got, ref) < 1e-6
+
+
+def test_weight_init_glibc_rand_known_answer():
+    # glibc: srand(1); rand() == 1804289383 (the reference inits weights from
+    # this default stream, WeightData.c:161 via DnnUtils.c:207)
+    O.lib().or_rand_seed(1)
+    u = O.lib().or_rand_uniform(-1.0, 1.0)
+    assert u == np.float32(np.float32(1804289383) / np.float32(2147483647) * np.float32(2) - 1)
+
+
+# ---- whole network glue ---------------------------------------------------------------------
+def _tiny_nobn(onet):
+    onet.conv(4, 3, 1, 1, LEAKY, 0)
+    onet.maxpool(2, 2, 1)
+    onet.conv(5, 1, 1, 0, LINEAR, 0)
+    onet.avgpool()
+    onet.softmax()
+
+
+def test_network_gradient_finite_difference():
+    """The network's weight_updates are -dL/dW summed over the batch
+    (delta = t - p convention), with L = sum of cross-entropies."""
+    B, H, W, Cc = 3, 6, 6, 2
+    rng = np.random.default_rng(11)
+    x = rng.random((B, Cc, H, W)).astype(np.float32)
+    t = np.zeros((B, 5), np.float32)
+    t[np.arange(B), rng.integers(0, 5, B)] = 1
+    O.lib().or_rand_seed(3)
+    net = O.OracleNet(B, H, W, Cc)
+    _tiny_nobn(net)
+    net.finalize()
+    loss = net.forward_backward(x, t)
+    g0 = net.buffer(0, 3).copy()  # weight_updates of layer 0
+    w0 = net.buffer(0, 2).copy()
+
+    def total_loss(w):
+        O.lib().or_rand_seed(3)
+        n2 = O.OracleNet(B, H, W, Cc)
+        _tiny_nobn(n2)
+        n2.finalize()
+        n2.set_buffer(0, 2, w)
+        val = n2.forward_backward(x, t) * B
+        n2.close()
+        return val
+
+    assert abs(total_loss(w0) - loss * B) < 1e-5
+    for k in (0, 7, 20):
+        e = np.zeros_like(w0)
+        e[k] = 2e-3
+        fd = (total_loss(w0 + e) - total_loss(w0 - e)) / 4e-3
+        assert abs(-fd - g0[k]) <= 3e-3 * max(1.0, abs(fd)), (k, fd, g0[k])
+
+
+def test_network_forward_composes_ops():
+    """or_net forward == the op functions composed by hand (pins the layer
+    loop, dropout sharing and the loss = cost/batch convention)."""
+    B, H, W, Cc = 4, 8, 8, 3
+    rng = np.random.default_rng(12)
+    x = rng.random((B, Cc, H, W)).astype(np.float32)
+    t = np.zeros((B, 6), np.float32)
+    t[np.arange(B), rng.integers(0, 6, B)] = 1
+    O.lib().or_rand_seed(5)
+    net = O.OracleNet(B, H, W, Cc)
+    net.conv(5, 3, 1, 1, LEAKY, 1)
+    net.maxpool(2, 2, 1)
+    net.dropout(0.5)
+    net.conv(6, 1, 1, 0, LINEAR, 0)
+    net.avgpool()
+    net.softmax()
+    net.dropout_seed(77)
+    net.finalize()
+    w0, w3 = net.buffer(0, 2).reshape(5, 3, 3, 3), net.buffer(3, 2).reshape(6, 5, 1, 1)
+    loss = net.forward_backward(x, t)
+    y = O.conv_forward(x, w0, 5, 3, 1, 1)
+    f = O.bn_forward(y, np.ones(5, np.float32), np.zeros(5, np.float32))
+    a = O.activate(f["out"], LEAKY)
+    mp, idx = O.maxpool_forward(a, 2, 2, 1)
+    mp = mp * O.dropout_mask_scale(mp.size, 0.5, 77, 0, 2).reshape(mp.shape)
+    z = O.conv_forward(mp, w3, 6, 1, 1, 0)
+    av = O.avgpool_forward(z)
+    _, _, _, cost = O.softmax_xent(av, t)
+    assert abs(loss - cost / B) < 1e-6
+    assert np.array_equal(net.buffer(1, 14).reshape(idx.shape), idx)
