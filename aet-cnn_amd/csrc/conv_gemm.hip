@@ -14,22 +14,45 @@
 //   wgrad   : M = filters, N = C*k*k, K = batch*OH*OW, deterministic split-K
 //             (fixed-order reduction, no float atomics)
 //
-// Tiling: 256 threads = 4 wave64s in a 2x2 grid; block tile 128x128x16; each
-// wave owns a 64x64 sub-tile = 2x2 v_mfma_f32_32x32x2f32 accumulators (64
-// VGPRs).  Global loads for tile k+1 are issued into registers before the
-// MFMAs of tile k, then written to the other half of a double-buffered LDS
-// stage, so one barrier per k-tile suffices.
+// Kernel shape: 256 threads = 4 wave64s; block tile BM x 128 x BK; each wave
+// owns a (BM/WM) x (128/WN) sub-tile of v_mfma_f32_32x32x2f32 accumulators.
+// Operands are fetched with buffer loads whose out-of-range offsets return
+// zero in hardware, so padding, ragged K and partial tiles cost no branches.
+// Loads for k-tile t+1 are issued into registers before the MFMAs of tile t
+// and then written to the other half of a double-buffered LDS stage (one
+// barrier per k-tile).  For 3x3 filters the k-tile is 18 = two input
+// channels, which makes the im2col (ki, kj) of every loaded row a
+// compile-time constant.  Workgroups are remapped so that the M-tiles
+// sharing an N-tile (the same input patch) run on the same XCD and share its
+// L2.
 #include "common.hpp"
 
 namespace ach {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int GBM = 128, GBN = 128, GBK = 16, GNT = 256;
-constexpr int LDP = 4;                 // LDS row padding (floats)
-constexpr int LDA = GBM + LDP, LDB = GBN + LDP;
-constexpr int RA = GBM * GBK / GNT;    // A elements per thread per k-tile (8)
-constexpr int RB = GBN * GBK / GNT;    // B elements per thread per k-tile (8)
+constexpr int GNT = 256;     // threads per workgroup
+constexpr int GBN = 128;     // N tile
+constexpr int LDP = 4;       // LDS row padding (floats)
+constexpr unsigned kOOB = 0x80000000u;  // buffer offset that reads as 0
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, unsigned bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// element offset -> byte offset, or the out-of-range offset when invalid
+__device__ __forceinline__ int boff(bool ok, int elem)
+{
+    return ok ? elem * 4 : (int)kOOB;
+}
+
+// the builtin returns the loaded dword as an integer: reinterpret its bits
+__device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, int byte_off)
+{
+    return __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
 
 struct ConvGeom {
     int B, C, H, W;    // input
@@ -37,87 +60,310 @@ struct ConvGeom {
     int OH, OW;
 };
 
-// ---------------------------------------------------------------------------
-// Thread->element maps for one k-tile.  "KC" = contiguous along k (operand
-// stored with k fastest in global memory), "MC" = contiguous along m or n.
-//   KC: thread t covers k = k0 + t%16 and rows r0 + t/16 + 16*i, i < 8
-//   MC: thread t covers row r0 + t%128 and k = k0 + t/128 + 2*i, i < 8
-__device__ __forceinline__ void lds_store_kc(float (*S)[LDA], int tid, const float *r)
-{
-    const int kc = tid % GBK, rr = tid / GBK;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) S[kc][rr + 16 * i] = r[i];
-}
+// ===========================================================================
+// Operand loaders.  Each provides, for its k-tile width BK:
+//   RA / RB          elements per thread per k-tile
+//   init(m0|n0,tid)  loop-invariant per-thread state
+//   load(k0, ke, r)  global -> registers for k in [k0, k0+BK) clipped to ke
+//   store(S, r)      registers -> LDS stage S[BK][BM or BN + LDP]
+// ===========================================================================
 
-__device__ __forceinline__ void lds_store_mc(float (*S)[LDA], int tid, const float *r)
-{
-    const int rc = tid % GBM, kr = tid / GBM;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) S[kr + 2 * i][rc] = r[i];
-}
-
-// ---------------------------------------------------------------------------
-// Forward implicit GEMM.  A = weights [F][C*k*k] row-major, B = im2col(x).
-template <int KS_T>
-struct FwdProblem {
-    static constexpr bool A_KC = true, B_KC = false;
-    const float *__restrict__ x;
-    const float *__restrict__ w;
-    float *__restrict__ y;
-    ConvGeom g;
-    int M, N, K;
-
-    __device__ __forceinline__ int ks() const { return KS_T ? KS_T : g.KS; }
-    __device__ __forceinline__ void krange(int, int &kb, int &ke) const { kb = 0; ke = K; }
-
-    struct AState { int mr, kc; };
-    __device__ __forceinline__ void a_init(AState &s, int m0, int tid) const
+// A = weights [M][K] row-major (k contiguous).  Linear map over the tile:
+// element e = tid + 256*i -> (row e / BK, col e % BK).
+template <int BM, int BK>
+struct AWeights {
+    static constexpr int RA = (BM * BK + GNT - 1) / GNT;
+    __amdgpu_buffer_rsrc_t rs;
+    int M, K;
+    int off[RA];   // row*K + col, or -1
+    int col[RA];
+    int row[RA];
+    __device__ __forceinline__ void init(const float *w, int M_, int K_, int m0, int tid)
     {
-        s.mr = m0 + tid / GBK;
-        s.kc = tid % GBK;
-    }
-    __device__ __forceinline__ void a_load(const AState &s, int k0, int ke, float *r) const
-    {
-        const int k = k0 + s.kc;
-        const bool kok = k < ke;
+        M = M_;
+        K = K_;
+        rs = make_rsrc(w, (unsigned)((size_t)M_ * K_ * 4));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int m = s.mr + 16 * i;
-            r[i] = (kok && m < M) ? w[(size_t)m * K + k] : 0.f;
+        for (int i = 0; i < RA; ++i) {
+            const int e = tid + GNT * i;
+            const int r = e / BK, c = e - (e / BK) * BK;
+            row[i] = r;
+            col[i] = c;
+            const bool ok = e < BM * BK && m0 + r < M_;
+            off[i] = ok ? (m0 + r) * K_ + c : -1;
         }
     }
-
-    struct BState { int ok, xoff, ihb, iwb, kr; };
-    __device__ __forceinline__ void b_init(BState &s, int n0, int tid) const
+    __device__ __forceinline__ void load(int k0, int ke, float *ra) const
     {
+#pragma unroll
+        for (int i = 0; i < RA; ++i)
+            ra[i] = bload(rs, boff(off[i] >= 0 && k0 + col[i] < ke, off[i] + k0));
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
+    {
+#pragma unroll
+        for (int i = 0; i < RA; ++i)
+            if (GNT * i + (int)threadIdx.x < BM * BK) S[col[i]][row[i]] = ra[i];
+    }
+};
+
+// B for the forward pass with a 3x3 kernel and BK = 18 (two input channels):
+// thread -> column n = n0 + tid%128 and channel half kr = tid/128; its 9
+// rows are (ki, kj) = (i/3, i%3), i = 0..8, all compile-time.
+struct BIm2col3 {
+    static constexpr int BK = 18, RB = 9;
+    __amdgpu_buffer_rsrc_t rs;
+    int base;      // b*C*H*W + (oh*S-P)*W + (ow*S-P) + kr*H*W
+    int HW, W, K, kr;
+    unsigned valid; // bit i: (ki,kj) in bounds for this column
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
+                                         int tid)
+    {
+        rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
         const int n = n0 + tid % GBN;
-        s.kr = tid / GBN;
-        s.ok = n < N;
+        kr = tid / GBN;
+        HW = g.H * g.W;
+        W = g.W;
+        K = g.C * 9;
         const int ohw = g.OH * g.OW;
-        const int nn = s.ok ? n : 0;
+        const bool nok = n < N;
+        const int nn = nok ? n : 0;
         const int b = nn / ohw, p = nn - b * ohw;
         const int oh = p / g.OW, ow = p - oh * g.OW;
-        s.xoff = b * g.C * g.H * g.W;
-        s.ihb = oh * g.S - g.P;
-        s.iwb = ow * g.S - g.P;
-    }
-    __device__ __forceinline__ void b_load(const BState &s, int k0, int ke, float *r) const
-    {
-        const int KS = ks(), KK = KS * KS;
+        const int ihb = oh * g.S - g.P, iwb = ow * g.S - g.P;
+        base = b * g.C * HW + ihb * g.W + iwb + kr * HW;
+        valid = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int k = k0 + s.kr + 2 * i;
-            float v = 0.f;
-            if (s.ok && k < ke) {
-                const int c = k / KK, t = k - c * KK;
-                const int ki = t / KS, kj = t - ki * KS;
-                const int ih = s.ihb + ki, iw = s.iwb + kj;
-                if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-                    v = x[s.xoff + (c * g.H + ih) * g.W + iw];
-            }
-            r[i] = v;
+        for (int i = 0; i < 9; ++i) {
+            const int ih = ihb + i / 3, iw = iwb + i % 3;
+            if (nok && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
+                valid |= 1u << i;
         }
     }
+    __device__ __forceinline__ void load(int k0, int ke, float *rb) const
+    {
+        // rows k0 + kr*9 + i all belong to channel c = k0/9 + kr
+        const bool cok = k0 + kr * 9 < ke;
+        const int cb = base + (k0 / 9) * HW;
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            rb[i] = bload(rs, boff(cok && ((valid >> i) & 1u), cb + (i / 3) * W + (i % 3)));
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
+    {
+        const int nc = threadIdx.x % GBN;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) S[kr * 9 + i][nc] = rb[i];
+    }
+};
+
+// B for the forward pass with any kernel size, BK = 16: thread -> column
+// n0 + tid%128, rows tid/128 + 2*i.
+template <int KS_T>
+struct BIm2colAny {
+    static constexpr int BK = 16, RB = 8;
+    __amdgpu_buffer_rsrc_t rs;
+    int xoff, ihb, iwb, kr, ok, H, W, KS;
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
+                                         int tid)
+    {
+        rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
+        const int n = n0 + tid % GBN;
+        kr = tid / GBN;
+        ok = n < N;
+        H = g.H;
+        W = g.W;
+        KS = KS_T ? KS_T : g.KS;
+        const int ohw = g.OH * g.OW;
+        const int nn = ok ? n : 0;
+        const int b = nn / ohw, p = nn - b * ohw;
+        const int oh = p / g.OW, ow = p - oh * g.OW;
+        xoff = b * g.C * g.H * g.W;
+        ihb = oh * g.S - g.P;
+        iwb = ow * g.S - g.P;
+    }
+    __device__ __forceinline__ void load(int k0, int ke, float *rb) const
+    {
+        const int ks = KS_T ? KS_T : KS, kk2 = ks * ks;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = k0 + kr + 2 * i;
+            const int c = k / kk2, t = k - c * kk2;
+            const int ki = t / ks, kj = t - ki * ks;
+            const int ih = ihb + ki, iw = iwb + kj;
+            const bool v = ok && k < ke && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+            rb[i] = bload(rs, boff(v, xoff + (c * H + ih) * W + iw));
+        }
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
+    {
+        const int nc = threadIdx.x % GBN;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) S[kr + 2 * i][nc] = rb[i];
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Weight gradient, BK = 16.  k = b*OHW + p runs over the batch and the
+// output plane.  A[m][k] = dy[b][m][p]; B[k][n] = x[b][c][oh*S-P+ki][ow*S-P+kj]
+// with n = c*KK + ki*KS + kj.  Thread -> k = k0 + tid%16 and rows
+// tid/16 + 16*i (i < BM/16 for A, < 8 for B); the (c, ki, kj) of its 8 B rows
+// are loop-invariant and precomputed.
+template <int BM>
+struct AWgrad {
+    static constexpr int BK = 16, RA = BM / 16;
+    __amdgpu_buffer_rsrc_t rs;
+    int kc, ohw, MO;   // MO = M*ohw
+    int moff[RA];      // m*ohw or -1
+    __device__ __forceinline__ void init(const float *dy, const ConvGeom &g, int M, int m0,
+                                         int tid)
+    {
+        ohw = g.OH * g.OW;
+        rs = make_rsrc(dy, (unsigned)((size_t)g.B * M * ohw * 4));
+        kc = tid % 16;
+        MO = M * ohw;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) {
+            const int m = m0 + tid / 16 + 16 * i;
+            moff[i] = m < M ? m * ohw : -1;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int ke, float *ra) const
+    {
+        const int k = k0 + kc;
+        const bool kok = k < ke;
+        const int kk = kok ? k : 0;
+        const int b = kk / ohw, p = kk - b * ohw;
+        const int base = b * MO + p;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) ra[i] = bload(rs, boff(kok && moff[i] >= 0, base + moff[i]));
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
+    {
+        const int r = threadIdx.x / 16;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) S[kc][r + 16 * i] = ra[i];
+    }
+};
+
+template <int KS_T>
+struct BWgrad {
+    static constexpr int BK = 16, RB = 8;
+    __amdgpu_buffer_rsrc_t rs;
+    int kc, ohw, OW, S, P, H, W, CHW;
+    int coff[8];       // c*H*W + ki*W + kj, or -1 when n >= N
+    int kij[8];        // ki | kj << 16
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
+                                         int tid)
+    {
+        rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
+        kc = tid % 16;
+        ohw = g.OH * g.OW;
+        OW = g.OW;
+        S = g.S;
+        P = g.P;
+        H = g.H;
+        W = g.W;
+        CHW = g.C * g.H * g.W;
+        const int ks = KS_T ? KS_T : g.KS, kk2 = ks * ks;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int n = n0 + tid / 16 + 16 * i;
+            const int c = n / kk2, t = n - c * kk2;
+            const int ki = t / ks, kj = t - ki * ks;
+            coff[i] = n < N ? c * g.H * g.W + ki * g.W + kj : -1;
+            kij[i] = ki | (kj << 16);
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int ke, float *rb) const
+    {
+        const int k = k0 + kc;
+        const bool kok = k < ke;
+        const int kk = kok ? k : 0;
+        const int b = kk / ohw, p = kk - b * ohw;
+        const int oh = p / OW, ow = p - oh * OW;
+        const int ihb = oh * S - P, iwb = ow * S - P;
+        const int base = b * CHW + ihb * W + iwb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int ih = ihb + (kij[i] & 0xffff), iw = iwb + (kij[i] >> 16);
+            const bool v = kok && coff[i] >= 0 && (unsigned)ih < (unsigned)H &&
+                           (unsigned)iw < (unsigned)W;
+            rb[i] = bload(rs, boff(v, base + coff[i]));
+        }
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S_)[LD], const float *rb) const
+    {
+        const int r = threadIdx.x / 16;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) S_[kc][r + 16 * i] = rb[i];
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Plain row-major GEMM operands (Gemm.c:116-144), BK = 16.
+template <bool T, int BR>
+struct PlainOperand {
+    // element (r, k) of op(X) where X is [R][K] (T = 0) or [K][R] (T = 1);
+    // thread map: T = 0 -> k fastest (k = tid%16), T = 1 -> r fastest.
+    static constexpr int BK = 16, RN = BR * BK / GNT, RA = RN, RB = RN;
+    __amdgpu_buffer_rsrc_t rs;
+    int R, K, ld, r0;
+    __device__ __forceinline__ void init(const float *X, int R_, int K_, int ld_, size_t bytes,
+                                         int r0_)
+    {
+        rs = make_rsrc(X, (unsigned)bytes);
+        R = R_;
+        K = K_;
+        ld = ld_;
+        r0 = r0_;
+    }
+    __device__ __forceinline__ void coords(int i, int k0, int &r, int &k) const
+    {
+        if (!T) { r = r0 + (int)threadIdx.x / BK + (GNT / BK) * i; k = k0 + (int)threadIdx.x % BK; }
+        else { r = r0 + (int)threadIdx.x % BR; k = k0 + (int)threadIdx.x / BR + (GNT / BR) * i; }
+    }
+    __device__ __forceinline__ void load(int k0, int ke, float *v) const
+    {
+#pragma unroll
+        for (int i = 0; i < RN; ++i) {
+            int r, k;
+            coords(i, k0, r, k);
+            v[i] = bload(rs, boff(r < R && k < ke, T ? k * ld + r : r * ld + k));
+        }
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *v) const
+    {
+#pragma unroll
+        for (int i = 0; i < RN; ++i) {
+            int r, k;
+            coords(i, 0, r, k);
+            S[k][r - r0] = v[i];
+        }
+    }
+};
+
+// ===========================================================================
+// Problems: operand loaders + k range + epilogue.
+// ===========================================================================
+template <int BM_, class BL>
+struct FwdProblem {
+    static constexpr int BM = BM_, BK = BL::BK;
+    using AL = AWeights<BM, BK>;
+    using BLd = BL;
+    const float *x, *w;
+    float *y;
+    ConvGeom g;
+    int M, N, K;
+    __device__ __forceinline__ void krange(int, int &kb, int &ke) const { kb = 0; ke = K; }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(w, M, K, m0, tid); }
+    __device__ __forceinline__ void init_b(BL &b, int n0, int tid) const { b.init(x, g, N, n0, tid); }
     __device__ __forceinline__ void store(int m, int n, float v, int) const
     {
         if (m >= M || n >= N) return;
@@ -127,78 +373,22 @@ struct FwdProblem {
     }
 };
 
-// ---------------------------------------------------------------------------
-// Weight-gradient GEMM.  A = dy viewed as [F][B*OH*OW] (k = b*OHW + p),
-// B[k][n] = im2col(x)[n][p] of image b, n = c*k*k + ki*k + kj.
-template <int KS_T>
+template <int BM_, int KS_T>
 struct WgradProblem {
-    static constexpr bool A_KC = true, B_KC = true;
-    const float *__restrict__ x;
-    const float *__restrict__ dy;
-    float *__restrict__ dw;     // [F][C*k*k], accumulated (+=) when splits == 1
-    float *__restrict__ part;   // [splits][M][N] partials when splits > 1
+    static constexpr int BM = BM_, BK = 16;
+    using AL = AWgrad<BM>;
+    using BLd = BWgrad<KS_T>;
+    const float *x, *dy;
+    float *dw, *part;
     ConvGeom g;
     int M, N, K, kchunk, splits;
-
-    __device__ __forceinline__ int ks() const { return KS_T ? KS_T : g.KS; }
     __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
     {
         kb = z * kchunk;
         ke = min(K, kb + kchunk);
     }
-
-    struct AState { int mr, kc; };
-    __device__ __forceinline__ void a_init(AState &s, int m0, int tid) const
-    {
-        s.mr = m0 + tid / GBK;
-        s.kc = tid % GBK;
-    }
-    __device__ __forceinline__ void a_load(const AState &s, int k0, int ke, float *r) const
-    {
-        const int k = k0 + s.kc;
-        const int ohw = g.OH * g.OW;
-        const bool kok = k < ke;
-        const int kk = kok ? k : 0;
-        const int b = kk / ohw, p = kk - b * ohw;
-        const size_t base = (size_t)b * M * ohw + p;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int m = s.mr + 16 * i;
-            r[i] = (kok && m < M) ? dy[base + (size_t)m * ohw] : 0.f;
-        }
-    }
-
-    struct BState { int nr, kc; };
-    __device__ __forceinline__ void b_init(BState &s, int n0, int tid) const
-    {
-        s.nr = n0 + tid / GBK;
-        s.kc = tid % GBK;
-    }
-    __device__ __forceinline__ void b_load(const BState &s, int k0, int ke, float *r) const
-    {
-        const int KS = ks(), KK = KS * KS;
-        const int k = k0 + s.kc;
-        const int ohw = g.OH * g.OW;
-        const bool kok = k < ke;
-        const int kk = kok ? k : 0;
-        const int b = kk / ohw, p = kk - b * ohw;
-        const int oh = p / g.OW, ow = p - oh * g.OW;
-        const int ihb = oh * g.S - g.P, iwb = ow * g.S - g.P;
-        const float *xb = x + (size_t)b * g.C * g.H * g.W;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int n = s.nr + 16 * i;
-            float v = 0.f;
-            if (kok && n < N) {
-                const int c = n / KK, t = n - c * KK;
-                const int ki = t / KS, kj = t - ki * KS;
-                const int ih = ihb + ki, iw = iwb + kj;
-                if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-                    v = xb[(c * g.H + ih) * g.W + iw];
-            }
-            r[i] = v;
-        }
-    }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(dy, g, M, m0, tid); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int tid) const { b.init(x, g, N, n0, tid); }
     __device__ __forceinline__ void store(int m, int n, float v, int z) const
     {
         if (m >= M || n >= N) return;
@@ -209,58 +399,19 @@ struct WgradProblem {
     }
 };
 
-// ---------------------------------------------------------------------------
-// Plain row-major GEMM (Gemm.c:116-144): C = alpha*op(A)op(B) + beta*C.
 template <bool TA, bool TB>
 struct GemmProblem {
-    static constexpr bool A_KC = !TA, B_KC = TB;
-    const float *__restrict__ A;
-    const float *__restrict__ Bm;
-    float *__restrict__ C;
+    static constexpr int BM = 128, BK = 16;
+    using AL = PlainOperand<TA, 128>;
+    using BLd = PlainOperand<!TB, GBN>;
+    const float *A, *Bm;
+    float *C;
     int M, N, K, lda, ldb, ldc;
+    size_t abytes, bbytes;
     float alpha, beta;
-
     __device__ __forceinline__ void krange(int, int &kb, int &ke) const { kb = 0; ke = K; }
-    __device__ __forceinline__ float a_at(int m, int k) const
-    {
-        return TA ? A[(size_t)k * lda + m] : A[(size_t)m * lda + k];
-    }
-    __device__ __forceinline__ float b_at(int k, int n) const
-    {
-        return TB ? Bm[(size_t)n * ldb + k] : Bm[(size_t)k * ldb + n];
-    }
-    struct AState { int r, c; };
-    __device__ __forceinline__ void a_init(AState &s, int m0, int tid) const
-    {
-        if (A_KC) { s.r = m0 + tid / GBK; s.c = tid % GBK; }
-        else { s.r = m0 + tid % GBM; s.c = tid / GBM; }
-    }
-    __device__ __forceinline__ void a_load(const AState &s, int k0, int ke, float *r) const
-    {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int m, k;
-            if (A_KC) { m = s.r + 16 * i; k = k0 + s.c; }
-            else { m = s.r; k = k0 + s.c + 2 * i; }
-            r[i] = (m < M && k < ke) ? a_at(m, k) : 0.f;
-        }
-    }
-    struct BState { int r, c; };
-    __device__ __forceinline__ void b_init(BState &s, int n0, int tid) const
-    {
-        if (B_KC) { s.r = n0 + tid / GBK; s.c = tid % GBK; }
-        else { s.r = n0 + tid % GBN; s.c = tid / GBN; }
-    }
-    __device__ __forceinline__ void b_load(const BState &s, int k0, int ke, float *r) const
-    {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            int n, k;
-            if (B_KC) { n = s.r + 16 * i; k = k0 + s.c; }
-            else { n = s.r; k = k0 + s.c + 2 * i; }
-            r[i] = (n < N && k < ke) ? b_at(k, n) : 0.f;
-        }
-    }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int) const { a.init(A, M, K, lda, abytes, m0); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int) const { b.init(Bm, N, K, ldb, bbytes, n0); }
     __device__ __forceinline__ void store(int m, int n, float v, int) const
     {
         if (m >= M || n >= N) return;
@@ -269,41 +420,50 @@ struct GemmProblem {
     }
 };
 
-// ---------------------------------------------------------------------------
+// ===========================================================================
 template <class P>
-__global__ void __launch_bounds__(GNT) k_mfma_gemm(P p)
+__global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 {
-    __shared__ float As[2][GBK][LDA];
-    __shared__ float Bs[2][GBK][LDB];
+    constexpr int BM = P::BM, BK = P::BK;
+    constexpr int WM = BM >= 64 ? 2 : 1, WN = 4 / WM;        // wave grid
+    constexpr int TM = BM / WM / 32, TN = GBN / WN / 32;     // MFMA tiles per wave
+    constexpr int LA = BM + LDP, LB = GBN + LDP;
+    __shared__ float As[2][BK][LA];
+    __shared__ float Bs[2][BK][LB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM, z = blockIdx.z;
+    const int wm = wave / WN, wn = wave % WN;
+
+    // XCD-aware tile order: the 8 XCDs take workgroups round-robin, so give
+    // XCD x the contiguous tile range [x*T/8, (x+1)*T/8) with M fastest.
+    const int nblk = mt * nt;
+    int lin = blockIdx.x;
+    if ((nblk & 7) == 0) lin = (lin & 7) * (nblk >> 3) + (lin >> 3);
+    const int m0 = (lin % mt) * BM, n0 = (lin / mt) * GBN, z = blockIdx.y;
 
     int kb, ke;
     p.krange(z, kb, ke);
+    typename P::AL al;
+    typename P::BLd bl;
+    p.init_a(al, m0, tid);
+    p.init_b(bl, n0, tid);
 
-    typename P::AState as;
-    typename P::BState bs;
-    p.a_init(as, m0, tid);
-    p.b_init(bs, n0, tid);
-
-    v16f acc[2][2];
+    v16f acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    float ra[RA], rb[RB];
-    const int nkt = (ke - kb + GBK - 1) / GBK;
+    float ra[P::AL::RA], rb[P::BLd::RB];
+    const int nkt = (ke - kb + BK - 1) / BK;
     if (nkt > 0) {
-        p.a_load(as, kb, ke, ra);
-        p.b_load(bs, kb, ke, rb);
-        if (P::A_KC) lds_store_kc(As[0], tid, ra); else lds_store_mc(As[0], tid, ra);
-        if (P::B_KC) lds_store_kc(Bs[0], tid, rb); else lds_store_mc(Bs[0], tid, rb);
+        al.load(kb, ke, ra);
+        bl.load(kb, ke, rb);
+        al.template store<LA>(As[0], ra);
+        bl.template store<LB>(Bs[0], rb);
     }
     __syncthreads();
 
@@ -312,24 +472,26 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p)
         const int cur = kt & 1;
         const bool more = kt + 1 < nkt;
         if (more) {
-            const int k0 = kb + (kt + 1) * GBK;
-            p.a_load(as, k0, ke, ra);
-            p.b_load(bs, k0, ke, rb);
+            const int k0 = kb + (kt + 1) * BK;
+            al.load(k0, ke, ra);
+            bl.load(k0, ke, rb);
         }
 #pragma unroll
-        for (int kk = 0; kk < GBK; kk += 2) {
-            const float a0 = As[cur][kk + lrow][wm * 64 + lcol];
-            const float a1 = As[cur][kk + lrow][wm * 64 + 32 + lcol];
-            const float b0 = Bs[cur][kk + lrow][wn * 64 + lcol];
-            const float b1 = Bs[cur][kk + lrow][wn * 64 + 32 + lcol];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[i] = As[cur][kk + lrow][wm * (BM / WM) + i * 32 + lcol];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = Bs[cur][kk + lrow][wn * (GBN / WN) + j * 32 + lcol];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (more) {
-            if (P::A_KC) lds_store_kc(As[cur ^ 1], tid, ra); else lds_store_mc(As[cur ^ 1], tid, ra);
-            if (P::B_KC) lds_store_kc(Bs[cur ^ 1], tid, rb); else lds_store_mc(Bs[cur ^ 1], tid, rb);
+            al.template store<LA>(As[cur ^ 1], ra);
+            bl.template store<LB>(Bs[cur ^ 1], rb);
         }
         __syncthreads();
     }
@@ -337,13 +499,13 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p)
     // D layout of v_mfma_f32_32x32x2f32: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + lcol;
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + wn * (GBN / WN) + j * 32 + lcol;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lrow + (r & 3);
+                const int m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * lrow + (r & 3);
                 p.store(m, n, acc[i][j][r], z);
             }
         }
@@ -383,9 +545,9 @@ __global__ void k_flip_weights(const float *__restrict__ w, float *__restrict__ 
 template <class P>
 static int launch_gemm(const P &p, int M, int N, int splits, hipStream_t st)
 {
-    dim3 grid((N + GBN - 1) / GBN, (M + GBM - 1) / GBM, splits);
-    if (grid.y > 65535u || splits > 65535) return ACH_EINVAL;
-    hipLaunchKernelGGL(k_mfma_gemm<P>, grid, dim3(GNT), 0, st, p);
+    const int mt = (M + P::BM - 1) / P::BM, nt = (N + GBN - 1) / GBN;
+    if ((long long)mt * nt > 0x7fffffffLL || splits > 65535) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_mfma_gemm<P>, dim3(mt * nt, splits), dim3(GNT), 0, st, p, mt, nt);
     return check_launch();
 }
 
@@ -406,44 +568,74 @@ static ConvGeom geom(const ach_conv_desc *d)
     return g;
 }
 
+// Buffer loads address bytes with 32-bit offsets: every operand must stay
+// below 2 GiB.
 static bool fits_int(const ach_conv_desc *d)
 {
     const ConvGeom g = geom(d);
+    const double lim = 536870911.0;  // floats in 2 GiB - 4 bytes
     const double in = (double)g.B * g.C * g.H * g.W;
     const double out = (double)g.B * g.F * g.OH * g.OW;
-    return in < 2147483647.0 && out < 2147483647.0 &&
-           (double)g.F * g.C * g.KS * g.KS < 2147483647.0;
+    return in <= lim && out <= lim && (double)g.F * g.C * g.KS * g.KS <= lim;
+}
+
+template <int BM>
+static int fwd_bm(const ConvGeom &g, const float *x, const float *w, float *y, hipStream_t st)
+{
+    const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
+    if (g.KS == 3) {
+        FwdProblem<BM, BIm2col3> p{x, w, y, g, M, N, K};
+        return launch_gemm(p, M, N, 1, st);
+    }
+    if (g.KS == 1) {
+        FwdProblem<BM, BIm2colAny<1>> p{x, w, y, g, M, N, K};
+        return launch_gemm(p, M, N, 1, st);
+    }
+    FwdProblem<BM, BIm2colAny<0>> p{x, w, y, g, M, N, K};
+    return launch_gemm(p, M, N, 1, st);
 }
 
 static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, hipStream_t st)
 {
-    const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
-#define ACH_FWD(KS_)                                                        \
-    {                                                                       \
-        FwdProblem<KS_> p{x, w, y, g, M, N, K};                             \
-        return launch_gemm(p, M, N, 1, st);                                 \
-    }
-    if (g.KS == 3) ACH_FWD(3)
-    if (g.KS == 1) ACH_FWD(1)
-    ACH_FWD(0)
-#undef ACH_FWD
+    if (g.F <= 32) return fwd_bm<32>(g, x, w, y, st);
+    if (g.F <= 64) return fwd_bm<64>(g, x, w, y, st);
+    return fwd_bm<128>(g, x, w, y, st);
 }
 
 // Split count for wgrad: aim for >= ~1024 workgroups over 256 CUs, K chunks a
 // multiple of the k-tile.
-static void wgrad_split(const ConvGeom &g, int &splits, int &kchunk)
+static void wgrad_split(const ConvGeom &g, int bm, int &splits, int &kchunk)
 {
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
-    const int tiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    const int tiles = ((M + bm - 1) / bm) * ((N + GBN - 1) / GBN);
     int s = (1024 + tiles - 1) / tiles;
-    const int max_s = (K + 4 * GBK - 1) / (4 * GBK);  // >= 4 k-tiles per split
+    const int max_s = (K + 4 * 16 - 1) / (4 * 16);  // >= 4 k-tiles per split
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
     if (s > 256) s = 256;
     int chunk = (K + s - 1) / s;
-    chunk = (chunk + GBK - 1) / GBK * GBK;
+    chunk = (chunk + 15) / 16 * 16;
     splits = (K + chunk - 1) / chunk;
     kchunk = chunk;
+}
+
+static int wgrad_bm(const ConvGeom &g) { return g.F <= 32 ? 32 : (g.F <= 64 ? 64 : 128); }
+
+template <int BM>
+static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, float *dw,
+                        float *part, int splits, int kchunk, hipStream_t st)
+{
+    const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
+    if (g.KS == 3) {
+        WgradProblem<BM, 3> p{x, dy, dw, part, g, M, N, K, kchunk, splits};
+        return launch_gemm(p, M, N, splits, st);
+    }
+    if (g.KS == 1) {
+        WgradProblem<BM, 1> p{x, dy, dw, part, g, M, N, K, kchunk, splits};
+        return launch_gemm(p, M, N, splits, st);
+    }
+    WgradProblem<BM, 0> p{x, dy, dw, part, g, M, N, K, kchunk, splits};
+    return launch_gemm(p, M, N, splits, st);
 }
 
 }  // namespace ach
@@ -460,7 +652,8 @@ size_t ach_conv_fwd_workspace(const ach_conv_desc *) { return 0; }
 int ach_conv_fwd(const ach_conv_desc *d, const float *x, const float *w, float *y,
                  void *, size_t, ach_stream_t stream)
 {
-    if (!conv_ok(d) || !x || !w || !y || !fits_int(d)) return ACH_EINVAL;
+    if (!conv_ok(d) || !x || !w || !y) return ACH_EINVAL;
+    if (!fits_int(d)) return ACH_EUNSUPPORTED;
     return fwd_impl(geom(d), x, w, y, as_stream(stream));
 }
 
@@ -477,7 +670,8 @@ size_t ach_conv_bwd_data_workspace(const ach_conv_desc *d)
 int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, float *dx,
                       void *ws, size_t ws_bytes, ach_stream_t stream)
 {
-    if (!conv_ok(d) || !dy || !w || !dx || !fits_int(d)) return ACH_EINVAL;
+    if (!conv_ok(d) || !dy || !w || !dx) return ACH_EINVAL;
+    if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const size_t need = ach_conv_bwd_data_workspace(d);
     if (!ws || ws_bytes < need) return ACH_EWORKSPACE;
     const ConvGeom g = geom(d);
@@ -515,7 +709,7 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
     int splits, kchunk;
-    wgrad_split(g, splits, kchunk);
+    wgrad_split(g, wgrad_bm(g), splits, kchunk);
     if (splits <= 1) return 0;
     return (size_t)splits * g.F * g.C * g.KS * g.KS * sizeof(float);
 }
@@ -523,27 +717,22 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)
 int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
                         void *ws, size_t ws_bytes, ach_stream_t stream)
 {
-    if (!conv_ok(d) || !x || !dy || !dw || !fits_int(d)) return ACH_EINVAL;
+    if (!conv_ok(d) || !x || !dy || !dw) return ACH_EINVAL;
+    if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
+    const int bm = wgrad_bm(g);
     int splits, kchunk;
-    wgrad_split(g, splits, kchunk);
+    wgrad_split(g, bm, splits, kchunk);
     const size_t need = ach_conv_bwd_filter_workspace(d);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
     hipStream_t st = as_stream(stream);
-    const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
     float *part = (float *)ws;
     int rc;
-#define ACH_WG(KS_)                                                         \
-    {                                                                       \
-        WgradProblem<KS_> p{x, dy, dw, part, g, M, N, K, kchunk, splits};   \
-        rc = launch_gemm(p, M, N, splits, st);                              \
-    }
-    if (g.KS == 3) ACH_WG(3)
-    else if (g.KS == 1) ACH_WG(1)
-    else ACH_WG(0)
-#undef ACH_WG
+    if (bm == 32) rc = wgrad_launch<32>(g, x, dy, dw, part, splits, kchunk, st);
+    else if (bm == 64) rc = wgrad_launch<64>(g, x, dy, dw, part, splits, kchunk, st);
+    else rc = wgrad_launch<128>(g, x, dy, dw, part, splits, kchunk, st);
     if (rc || splits == 1) return rc;
-    const size_t mn = (size_t)M * N;
+    const size_t mn = (size_t)g.F * g.C * g.KS * g.KS;
     hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(mn, 256)), dim3(256), 0, st, part, dw,
                        mn, splits);
     return check_launch();
@@ -555,11 +744,13 @@ int ach_gemm(int TA, int TB, int M, int N, int K, float ALPHA, const float *A, i
     if (M < 0 || N < 0 || K < 0 || !C) return ACH_EINVAL;
     if (M == 0 || N == 0) return ACH_OK;
     if (K > 0 && (!A || !B)) return ACH_EINVAL;
+    const size_t abytes = (size_t)(TA ? K : M) * lda * 4, bbytes = (size_t)(TB ? N : K) * ldb * 4;
+    if (abytes >= 0x80000000ull || bbytes >= 0x80000000ull) return ACH_EUNSUPPORTED;
     hipStream_t st = as_stream(stream);
-#define ACH_GM(ta, tb)                                                              \
-    {                                                                               \
-        GemmProblem<ta, tb> p{A, B, C, M, N, K, lda, ldb, ldc, ALPHA, BETA};        \
-        return launch_gemm(p, M, N, 1, st);                                         \
+#define ACH_GM(ta, tb)                                                                      \
+    {                                                                                       \
+        GemmProblem<ta, tb> p{A, B, C, M, N, K, lda, ldb, ldc, abytes, bbytes, ALPHA, BETA}; \
+        return launch_gemm(p, M, N, 1, st);                                                 \
     }
     if (!TA && !TB) ACH_GM(false, false)
     if (TA && !TB) ACH_GM(true, false)
