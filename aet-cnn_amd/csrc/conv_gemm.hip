@@ -35,6 +35,10 @@ constexpr int GNT = 256;     // threads per workgroup
 constexpr int GBN = 128;     // N tile
 constexpr int LDP = 4;       // LDS row padding (floats)
 constexpr unsigned kOOB = 0x80000000u;  // buffer offset that reads as 0
+#ifndef ACH_WGRAD_BK
+#define ACH_WGRAD_BK 16
+#endif
+constexpr int WGRAD_BK = ACH_WGRAD_BK;  // k-tile of the weight-gradient GEMM
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, unsigned bytes)
 {
@@ -68,43 +72,38 @@ struct ConvGeom {
 //   store(S, r)      registers -> LDS stage S[BK][BM or BN + LDP]
 // ===========================================================================
 
-// A = weights [M][K] row-major (k contiguous).  Linear map over the tile:
-// element e = tid + 256*i -> (row e / BK, col e % BK).
+// A = weights stored k-major, Wt[K][M] (m contiguous): thread -> column
+// m0 + tid%BM, rows tid/BM + (256/BM)*i.  Loads are coalesced along m and
+// the LDS stores hit consecutive banks.
 template <int BM, int BK>
-struct AWeights {
-    static constexpr int RA = (BM * BK + GNT - 1) / GNT;
+struct AWeightsT {
+    static constexpr int RPI = GNT / BM;                 // rows per step
+    static constexpr int RA = (BK + RPI - 1) / RPI, PAD = LDP;
     __amdgpu_buffer_rsrc_t rs;
-    int M, K;
-    int off[RA];   // row*K + col, or -1
-    int col[RA];
-    int row[RA];
-    __device__ __forceinline__ void init(const float *w, int M_, int K_, int m0, int tid)
+    int M, mok, kr, col;
+    __device__ __forceinline__ void init(const float *wt, int M_, int K_, int m0, int tid)
     {
         M = M_;
-        K = K_;
-        rs = make_rsrc(w, (unsigned)((size_t)M_ * K_ * 4));
-#pragma unroll
-        for (int i = 0; i < RA; ++i) {
-            const int e = tid + GNT * i;
-            const int r = e / BK, c = e - (e / BK) * BK;
-            row[i] = r;
-            col[i] = c;
-            const bool ok = e < BM * BK && m0 + r < M_;
-            off[i] = ok ? (m0 + r) * K_ + c : -1;
-        }
+        rs = make_rsrc(wt, (unsigned)((size_t)M_ * K_ * 4));
+        col = m0 + tid % BM;
+        kr = tid / BM;
+        mok = col < M_;
     }
     __device__ __forceinline__ void load(int k0, int ke, float *ra) const
     {
 #pragma unroll
-        for (int i = 0; i < RA; ++i)
-            ra[i] = bload(rs, boff(off[i] >= 0 && k0 + col[i] < ke, off[i] + k0));
+        for (int i = 0; i < RA; ++i) {
+            const int k = k0 + kr + RPI * i;
+            ra[i] = bload(rs, boff(mok && k < ke && kr + RPI * i < BK, k * M + col));
+        }
     }
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
     {
+        const int mc = threadIdx.x % BM;
 #pragma unroll
         for (int i = 0; i < RA; ++i)
-            if (GNT * i + (int)threadIdx.x < BM * BK) S[col[i]][row[i]] = ra[i];
+            if (kr + RPI * i < BK) S[kr + RPI * i][mc] = ra[i];
     }
 };
 
@@ -112,7 +111,7 @@ struct AWeights {
 // thread -> column n = n0 + tid%128 and channel half kr = tid/128; its 9
 // rows are (ki, kj) = (i/3, i%3), i = 0..8, all compile-time.
 struct BIm2col3 {
-    static constexpr int BK = 18, RB = 9;
+    static constexpr int BK = 18, RB = 9, PAD = LDP;
     __amdgpu_buffer_rsrc_t rs;
     int base;      // b*C*H*W + (oh*S-P)*W + (ow*S-P) + kr*H*W
     int HW, W, K, kr;
@@ -163,7 +162,7 @@ struct BIm2col3 {
 // n0 + tid%128, rows tid/128 + 2*i.
 template <int KS_T>
 struct BIm2colAny {
-    static constexpr int BK = 16, RB = 8;
+    static constexpr int BK = 16, RB = 8, PAD = LDP;
     __amdgpu_buffer_rsrc_t rs;
     int xoff, ihb, iwb, kr, ok, H, W, KS;
     __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
@@ -207,27 +206,56 @@ struct BIm2colAny {
 };
 
 // ---------------------------------------------------------------------------
-// Weight gradient, BK = 16.  k = b*OHW + p runs over the batch and the
-// output plane.  A[m][k] = dy[b][m][p]; B[k][n] = x[b][c][oh*S-P+ki][ow*S-P+kj]
-// with n = c*KK + ki*KS + kj.  Thread -> k = k0 + tid%16 and rows
-// tid/16 + 16*i (i < BM/16 for A, < 8 for B); the (c, ki, kj) of its 8 B rows
-// are loop-invariant and precomputed.
-template <int BM>
+// Unsigned division by a runtime constant d: q = (mulhi(n, mul) + n) >> shift
+// with shift = ceil(log2 d), mul = floor(2^32 (2^shift - d) / d) + 1
+// (Granlund & Montgomery 1994), exact for n < 2^31.
+struct FastDiv {
+    unsigned mul, shift, d;
+};
+
+static FastDiv make_fastdiv(unsigned d)
+{
+    FastDiv f;
+    unsigned l = 0;
+    while ((1ull << l) < d) ++l;
+    f.mul = (unsigned)((((1ull << 32) * ((1ull << l) - d)) / d) + 1);
+    f.shift = l;
+    f.d = d;
+    return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv &f)
+{
+    return (int)((__umulhi((unsigned)n, f.mul) + (unsigned)n) >> f.shift);
+}
+
+// Weight gradient.  k = b*OHW + p runs over the batch and the output plane.
+// A[m][k] = dy[b][m][p]; B[k][n] = x[b][c][oh*S-P+ki][ow*S-P+kj] with
+// n = c*KK + ki*KS + kj.  Thread -> k = k0 + tid%BK and rows
+// tid/BK + (256/BK)*i; both operands are read in BK-long runs along k, and
+// the (c, ki, kj) of a thread's B rows are loop-invariant and precomputed.
+struct WgradDivs {
+    FastDiv ohw, ow;
+};
+
+template <int BM, int BK_>
 struct AWgrad {
-    static constexpr int BK = 16, RA = BM / 16;
+    static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = 1;
     __amdgpu_buffer_rsrc_t rs;
-    int kc, ohw, MO;   // MO = M*ohw
+    int kc, MO;        // MO = M*ohw
     int moff[RA];      // m*ohw or -1
-    __device__ __forceinline__ void init(const float *dy, const ConvGeom &g, int M, int m0,
-                                         int tid)
+    FastDiv dohw;
+    __device__ __forceinline__ void init(const float *dy, const ConvGeom &g, const WgradDivs &dv,
+                                         int M, int m0, int tid)
     {
-        ohw = g.OH * g.OW;
+        const int ohw = g.OH * g.OW;
         rs = make_rsrc(dy, (unsigned)((size_t)g.B * M * ohw * 4));
-        kc = tid % 16;
+        kc = tid % BK;
         MO = M * ohw;
+        dohw = dv.ohw;
 #pragma unroll
         for (int i = 0; i < RA; ++i) {
-            const int m = m0 + tid / 16 + 16 * i;
+            const int m = m0 + tid / BK + RPI * i;
             moff[i] = m < M ? m * ohw : -1;
         }
     }
@@ -236,7 +264,7 @@ struct AWgrad {
         const int k = k0 + kc;
         const bool kok = k < ke;
         const int kk = kok ? k : 0;
-        const int b = kk / ohw, p = kk - b * ohw;
+        const int b = fdiv(kk, dohw), p = kk - b * (int)dohw.d;
         const int base = b * MO + p;
 #pragma unroll
         for (int i = 0; i < RA; ++i) ra[i] = bload(rs, boff(kok && moff[i] >= 0, base + moff[i]));
@@ -244,26 +272,27 @@ struct AWgrad {
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
     {
-        const int r = threadIdx.x / 16;
+        const int r = threadIdx.x / BK;
 #pragma unroll
-        for (int i = 0; i < RA; ++i) S[kc][r + 16 * i] = ra[i];
+        for (int i = 0; i < RA; ++i) S[kc][r + RPI * i] = ra[i];
     }
 };
 
-template <int KS_T>
+template <int BN, int BK_, int KS_T>
 struct BWgrad {
-    static constexpr int BK = 16, RB = 8;
+    static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = 1;
     __amdgpu_buffer_rsrc_t rs;
-    int kc, ohw, OW, S, P, H, W, CHW;
-    int coff[8];       // c*H*W + ki*W + kj, or -1 when n >= N
-    int kij[8];        // ki | kj << 16
-    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
-                                         int tid)
+    int kc, S, P, H, W, CHW;
+    FastDiv dohw, dow;
+    int coff[RB];      // c*H*W + ki*W + kj, or -1 when n >= N
+    int kij[RB];       // ki | kj << 16
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, const WgradDivs &dv,
+                                         int N, int n0, int tid)
     {
         rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
-        kc = tid % 16;
-        ohw = g.OH * g.OW;
-        OW = g.OW;
+        kc = tid % BK;
+        dohw = dv.ohw;
+        dow = dv.ow;
         S = g.S;
         P = g.P;
         H = g.H;
@@ -271,8 +300,8 @@ struct BWgrad {
         CHW = g.C * g.H * g.W;
         const int ks = KS_T ? KS_T : g.KS, kk2 = ks * ks;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int n = n0 + tid / 16 + 16 * i;
+        for (int i = 0; i < RB; ++i) {
+            const int n = n0 + tid / BK + RPI * i;
             const int c = n / kk2, t = n - c * kk2;
             const int ki = t / ks, kj = t - ki * ks;
             coff[i] = n < N ? c * g.H * g.W + ki * g.W + kj : -1;
@@ -284,12 +313,12 @@ struct BWgrad {
         const int k = k0 + kc;
         const bool kok = k < ke;
         const int kk = kok ? k : 0;
-        const int b = kk / ohw, p = kk - b * ohw;
-        const int oh = p / OW, ow = p - oh * OW;
+        const int b = fdiv(kk, dohw), p = kk - b * (int)dohw.d;
+        const int oh = fdiv(p, dow), ow = p - oh * (int)dow.d;
         const int ihb = oh * S - P, iwb = ow * S - P;
         const int base = b * CHW + ihb * W + iwb;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < RB; ++i) {
             const int ih = ihb + (kij[i] & 0xffff), iw = iwb + (kij[i] >> 16);
             const bool v = kok && coff[i] >= 0 && (unsigned)ih < (unsigned)H &&
                            (unsigned)iw < (unsigned)W;
@@ -299,9 +328,9 @@ struct BWgrad {
     template <int LD>
     __device__ __forceinline__ void store(float (*S_)[LD], const float *rb) const
     {
-        const int r = threadIdx.x / 16;
+        const int r = threadIdx.x / BK;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) S_[kc][r + 16 * i] = rb[i];
+        for (int i = 0; i < RB; ++i) S_[kc][r + RPI * i] = rb[i];
     }
 };
 
@@ -311,7 +340,7 @@ template <bool T, int BR>
 struct PlainOperand {
     // element (r, k) of op(X) where X is [R][K] (T = 0) or [K][R] (T = 1);
     // thread map: T = 0 -> k fastest (k = tid%16), T = 1 -> r fastest.
-    static constexpr int BK = 16, RN = BR * BK / GNT, RA = RN, RB = RN;
+    static constexpr int BK = 16, RN = BR * BK / GNT, RA = RN, RB = RN, PAD = T ? LDP : 1;
     __amdgpu_buffer_rsrc_t rs;
     int R, K, ld, r0;
     __device__ __forceinline__ void init(const float *X, int R_, int K_, int ld_, size_t bytes,
@@ -352,34 +381,16 @@ struct PlainOperand {
 // ===========================================================================
 // Problems: operand loaders + k range + epilogue.
 // ===========================================================================
+// Forward: y[b][m][p] = sum_k Wt[k][m] * im2col(x)[k][b*OHW+p].  With
+// splits > 1 each z-slice of K writes part[z][m][n] and a fixed-order
+// reduction produces y (used when the tile grid alone cannot fill the GPU).
 template <int BM_, class BL>
 struct FwdProblem {
-    static constexpr int BM = BM_, BK = BL::BK;
-    using AL = AWeights<BM, BK>;
+    static constexpr int BM = BM_, BN = 128, BK = BL::BK;
+    using AL = AWeightsT<BM, BK>;  // w points at the k-major copy Wt[K][M]
     using BLd = BL;
     const float *x, *w;
-    float *y;
-    ConvGeom g;
-    int M, N, K;
-    __device__ __forceinline__ void krange(int, int &kb, int &ke) const { kb = 0; ke = K; }
-    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(w, M, K, m0, tid); }
-    __device__ __forceinline__ void init_b(BL &b, int n0, int tid) const { b.init(x, g, N, n0, tid); }
-    __device__ __forceinline__ void store(int m, int n, float v, int) const
-    {
-        if (m >= M || n >= N) return;
-        const int ohw = g.OH * g.OW;
-        const int b = n / ohw, p = n - b * ohw;
-        y[((size_t)b * M + m) * ohw + p] = v;
-    }
-};
-
-template <int BM_, int KS_T>
-struct WgradProblem {
-    static constexpr int BM = BM_, BK = 16;
-    using AL = AWgrad<BM>;
-    using BLd = BWgrad<KS_T>;
-    const float *x, *dy;
-    float *dw, *part;
+    float *y, *part;
     ConvGeom g;
     int M, N, K, kchunk, splits;
     __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
@@ -387,8 +398,38 @@ struct WgradProblem {
         kb = z * kchunk;
         ke = min(K, kb + kchunk);
     }
-    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(dy, g, M, m0, tid); }
-    __device__ __forceinline__ void init_b(BLd &b, int n0, int tid) const { b.init(x, g, N, n0, tid); }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(w, M, K, m0, tid); }
+    __device__ __forceinline__ void init_b(BL &b, int n0, int tid) const { b.init(x, g, N, n0, tid); }
+    __device__ __forceinline__ void store(int m, int n, float v, int z) const
+    {
+        if (m >= M || n >= N) return;
+        if (splits > 1) {
+            part[((size_t)z * M + m) * N + n] = v;
+            return;
+        }
+        const int ohw = g.OH * g.OW;
+        const int b = n / ohw, p = n - b * ohw;
+        y[((size_t)b * M + m) * ohw + p] = v;
+    }
+};
+
+template <int BM_, int BN_, int KS_T>
+struct WgradProblem {
+    static constexpr int BM = BM_, BN = BN_, BK = WGRAD_BK;
+    using AL = AWgrad<BM, BK>;
+    using BLd = BWgrad<BN, BK, KS_T>;
+    const float *x, *dy;
+    float *dw, *part;
+    ConvGeom g;
+    WgradDivs dv;
+    int M, N, K, kchunk, splits;
+    __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
+    {
+        kb = z * kchunk;
+        ke = min(K, kb + kchunk);
+    }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(dy, g, dv, M, m0, tid); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int tid) const { b.init(x, g, dv, N, n0, tid); }
     __device__ __forceinline__ void store(int m, int n, float v, int z) const
     {
         if (m >= M || n >= N) return;
@@ -401,9 +442,9 @@ struct WgradProblem {
 
 template <bool TA, bool TB>
 struct GemmProblem {
-    static constexpr int BM = 128, BK = 16;
+    static constexpr int BM = 128, BN = 128, BK = 16;
     using AL = PlainOperand<TA, 128>;
-    using BLd = PlainOperand<!TB, GBN>;
+    using BLd = PlainOperand<!TB, 128>;
     const float *A, *Bm;
     float *C;
     int M, N, K, lda, ldb, ldc;
@@ -424,10 +465,12 @@ struct GemmProblem {
 template <class P>
 __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 {
-    constexpr int BM = P::BM, BK = P::BK;
-    constexpr int WM = BM >= 64 ? 2 : 1, WN = 4 / WM;        // wave grid
-    constexpr int TM = BM / WM / 32, TN = GBN / WN / 32;     // MFMA tiles per wave
-    constexpr int LA = BM + LDP, LB = GBN + LDP;
+    constexpr int BM = P::BM, BN = P::BN, BK = P::BK;
+    // wave grid: 2x2 for 64+ x 128 tiles, 1x4 for 32-row, 4x1 for 32-column
+    constexpr int WM = BN <= 32 ? 4 : (BM >= 64 ? 2 : 1), WN = 4 / WM;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
+    static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
+    constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
     __shared__ float As[2][BK][LA];
     __shared__ float Bs[2][BK][LB];
 
@@ -440,7 +483,7 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     const int nblk = mt * nt;
     int lin = blockIdx.x;
     if ((nblk & 7) == 0) lin = (lin & 7) * (nblk >> 3) + (lin >> 3);
-    const int m0 = (lin % mt) * BM, n0 = (lin / mt) * GBN, z = blockIdx.y;
+    const int m0 = (lin % mt) * BM, n0 = (lin / mt) * BN, z = blockIdx.y;
 
     int kb, ke;
     p.krange(z, kb, ke);
@@ -482,7 +525,7 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 #pragma unroll
             for (int i = 0; i < TM; ++i) a[i] = As[cur][kk + lrow][wm * (BM / WM) + i * 32 + lcol];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = Bs[cur][kk + lrow][wn * (GBN / WN) + j * 32 + lcol];
+            for (int j = 0; j < TN; ++j) b[j] = Bs[cur][kk + lrow][wn * (BN / WN) + j * 32 + lcol];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -502,7 +545,7 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn * (GBN / WN) + j * 32 + lcol;
+            const int n = n0 + wn * (BN / WN) + j * 32 + lcol;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * lrow + (r & 3);
@@ -523,21 +566,56 @@ __global__ void k_splitk_reduce(const float *__restrict__ part, float *__restric
     }
 }
 
-// Wflip[c][f][a][b] = W[f][c][k-1-a][k-1-b]: turns stride-1 dgrad into a
-// forward convolution of dy with C output channels.
-__global__ void k_flip_weights(const float *__restrict__ w, float *__restrict__ wf,
-                               int F, int C, int KS)
+// First level for many splits: tmp[c][i] = sum of part[z][i] over the
+// SPLIT_GROUP consecutive z of group c (z ascending); the second level is
+// k_splitk_reduce over the groups.  Keeps every output's sum order fixed.
+constexpr int SPLIT_GROUP = 32;
+__global__ void k_splitk_group(const float *__restrict__ part, float *__restrict__ tmp, size_t mn,
+                               int splits)
 {
-    const int KK = KS * KS;
+    const int c = blockIdx.y;
+    const int z0 = c * SPLIT_GROUP, z1 = min(splits, z0 + SPLIT_GROUP);
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < mn;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float s = 0.f;
+        for (int z = z0; z < z1; ++z) s += part[(size_t)z * mn + i];
+        tmp[(size_t)c * mn + i] = s;
+    }
+}
+
+// Wt[k][m] = W[m][k]: the k-major copy of the filter the forward GEMM reads
+// (32x32 tiles through LDS so both sides stay coalesced).
+__global__ void __launch_bounds__(256) k_weights_kmajor(const float *__restrict__ w,
+                                                        float *__restrict__ wt, int M, int K)
+{
+    __shared__ float t[32][33];
+    const int k0 = blockIdx.x * 32, m0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int r = ty; r < 32; r += 8) {
+        const int m = m0 + r, k = k0 + tx;
+        t[r][tx] = (m < M && k < K) ? w[(size_t)m * K + k] : 0.f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int k = k0 + r, m = m0 + tx;
+        if (k < K && m < M) wt[(size_t)k * M + m] = t[tx][r];
+    }
+}
+
+// Flipped, transposed filter for stride-1 dgrad, k-major:
+// Wft[(f*KK + t)*C + c] = W[f][c][KK-1-t], i.e. the forward filter of a
+// convolution of dy (F input channels) producing C channels with pad k-1-p.
+__global__ void k_weights_flip_kmajor(const float *__restrict__ w, float *__restrict__ wft,
+                                      int F, int C, int KK)
+{
     const size_t total = (size_t)F * C * KK;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
          i += (size_t)gridDim.x * blockDim.x) {
-        const int t = (int)(i % KK);
-        const size_t fc = i / KK;
-        const int f = (int)(fc % F);
-        const int c = (int)(fc / F);
-        const int a = t / KS, b = t - a * KS;
-        wf[i] = w[((size_t)f * C + c) * KK + (KS - 1 - a) * KS + (KS - 1 - b)];
+        const int c = (int)(i % C);
+        const size_t ft = i / C;
+        const int t = (int)(ft % KK);
+        const int f = (int)(ft / KK);
+        wft[i] = w[((size_t)f * C + c) * KK + (KK - 1 - t)];
     }
 }
 
@@ -545,7 +623,7 @@ __global__ void k_flip_weights(const float *__restrict__ w, float *__restrict__ 
 template <class P>
 static int launch_gemm(const P &p, int M, int N, int splits, hipStream_t st)
 {
-    const int mt = (M + P::BM - 1) / P::BM, nt = (N + GBN - 1) / GBN;
+    const int mt = (M + P::BM - 1) / P::BM, nt = (N + P::BN - 1) / P::BN;
     if ((long long)mt * nt > 0x7fffffffLL || splits > 65535) return ACH_EINVAL;
     hipLaunchKernelGGL(k_mfma_gemm<P>, dim3(mt * nt, splits), dim3(GNT), 0, st, p, mt, nt);
     return check_launch();
@@ -579,62 +657,143 @@ static bool fits_int(const ach_conv_desc *d)
     return in <= lim && out <= lim && (double)g.F * g.C * g.KS * g.KS <= lim;
 }
 
+// y[b][m][p] = sum_z part[z][m][b*OHW+p], z ascending (fixed order).
+__global__ void k_splitk_to_nchw(const float *__restrict__ part, float *__restrict__ y, int M,
+                                 int N, int ohw, int splits)
+{
+    const size_t mn = (size_t)M * N;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < mn;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int p = (int)(i % ohw);
+        const size_t bm = i / ohw;
+        const int m = (int)(bm % M);
+        const int b = (int)(bm / M);
+        const size_t n = (size_t)b * ohw + p;
+        float s = 0.f;
+        for (int z = 0; z < splits; ++z) s += part[((size_t)z * M + m) * N + n];
+        y[i] = s;
+    }
+}
+
+// Forward tiling plan: BM from the filter count; K split into `splits`
+// slices (a multiple of the k-tile each) when the tile grid alone gives
+// fewer than ~2 workgroups per CU.  Depends only on the shape, so results are
+// reproducible run to run.
+struct FwdPlan {
+    int bm, bk, splits, kchunk;
+};
+
+static FwdPlan fwd_plan(const ConvGeom &g)
+{
+    FwdPlan pl;
+    const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
+    pl.bm = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
+    pl.bk = g.KS == 3 ? 18 : 16;
+    const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + 127) / 128);
+    const int ktiles = (K + pl.bk - 1) / pl.bk;
+    int s = 1;
+    if (tiles < 512) {
+        s = (512 + tiles - 1) / tiles;
+        if (s > 32) s = 32;
+        if (s > ktiles / 8) s = ktiles / 8;  // keep >= 8 k-tiles per slice
+        if (s < 1) s = 1;
+    }
+    pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
+    pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
+    return pl;
+}
+
+static size_t fwd_part_bytes(const ConvGeom &g)
+{
+    const FwdPlan pl = fwd_plan(g);
+    if (pl.splits <= 1) return 0;
+    return (size_t)pl.splits * g.F * g.B * g.OH * g.OW * sizeof(float);
+}
+
 template <int BM>
-static int fwd_bm(const ConvGeom &g, const float *x, const float *w, float *y, hipStream_t st)
+static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const float *w,
+                  float *y, float *part, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
     if (g.KS == 3) {
-        FwdProblem<BM, BIm2col3> p{x, w, y, g, M, N, K};
-        return launch_gemm(p, M, N, 1, st);
+        FwdProblem<BM, BIm2col3> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        return launch_gemm(p, M, N, pl.splits, st);
     }
     if (g.KS == 1) {
-        FwdProblem<BM, BIm2colAny<1>> p{x, w, y, g, M, N, K};
-        return launch_gemm(p, M, N, 1, st);
+        FwdProblem<BM, BIm2colAny<1>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        return launch_gemm(p, M, N, pl.splits, st);
     }
-    FwdProblem<BM, BIm2colAny<0>> p{x, w, y, g, M, N, K};
-    return launch_gemm(p, M, N, 1, st);
+    FwdProblem<BM, BIm2colAny<0>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+    return launch_gemm(p, M, N, pl.splits, st);
 }
 
-static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, hipStream_t st)
+// w: k-major filter Wt[K][M]; part: fwd_part_bytes(g) of scratch (or NULL
+// when no split is planned)
+static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, float *part,
+                    hipStream_t st)
 {
-    if (g.F <= 32) return fwd_bm<32>(g, x, w, y, st);
-    if (g.F <= 64) return fwd_bm<64>(g, x, w, y, st);
-    return fwd_bm<128>(g, x, w, y, st);
+    const FwdPlan pl = fwd_plan(g);
+    int rc;
+    if (pl.bm == 32) rc = fwd_bm<32>(g, pl, x, w, y, part, st);
+    else if (pl.bm == 64) rc = fwd_bm<64>(g, pl, x, w, y, part, st);
+    else rc = fwd_bm<128>(g, pl, x, w, y, part, st);
+    if (rc || pl.splits == 1) return rc;
+    const int M = g.F, N = g.B * g.OH * g.OW;
+    const size_t mn = (size_t)M * N;
+    hipLaunchKernelGGL(k_splitk_to_nchw, dim3(grid_for(mn, 256)), dim3(256), 0, st, part, y, M, N,
+                       g.OH * g.OW, pl.splits);
+    return check_launch();
 }
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Split count for wgrad: aim for >= ~1024 workgroups over 256 CUs, K chunks a
 // multiple of the k-tile.
-static void wgrad_split(const ConvGeom &g, int bm, int &splits, int &kchunk)
+static void wgrad_split(const ConvGeom &g, int bm, int bn, int &splits, int &kchunk)
 {
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
-    const int tiles = ((M + bm - 1) / bm) * ((N + GBN - 1) / GBN);
+    const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int bk = WGRAD_BK;
     int s = (1024 + tiles - 1) / tiles;
-    const int max_s = (K + 4 * 16 - 1) / (4 * 16);  // >= 4 k-tiles per split
+    const int max_s = (K + 4 * bk - 1) / (4 * bk);  // >= 4 k-tiles per split
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
-    if (s > 256) s = 256;
+    if (s > 1024) s = 1024;
     int chunk = (K + s - 1) / s;
-    chunk = (chunk + 15) / 16 * 16;
+    chunk = (chunk + bk - 1) / bk * bk;
     splits = (K + chunk - 1) / chunk;
     kchunk = chunk;
 }
 
-static int wgrad_bm(const ConvGeom &g) { return g.F <= 32 ? 32 : (g.F <= 64 ? 64 : 128); }
+// wgrad tile: 32-column tiles when C*k*k <= 32 (e.g. the 3-channel first
+// layer, N = 27), otherwise BM from the filter count x 128.
+static int wgrad_bm(const ConvGeom &g)
+{
+    if (g.C * g.KS * g.KS <= 32 && g.F > 64) return 128;
+    return g.F <= 32 ? 32 : (g.F <= 64 ? 64 : 128);
+}
+static int wgrad_bn(const ConvGeom &g)
+{
+    return (g.C * g.KS * g.KS <= 32 && g.F > 64) ? 32 : 128;
+}
 
-template <int BM>
+template <int BM, int BN>
 static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, float *dw,
                         float *part, int splits, int kchunk, hipStream_t st)
 {
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
+    WgradDivs dv;
+    dv.ohw = make_fastdiv((unsigned)(g.OH * g.OW));
+    dv.ow = make_fastdiv((unsigned)g.OW);
     if (g.KS == 3) {
-        WgradProblem<BM, 3> p{x, dy, dw, part, g, M, N, K, kchunk, splits};
+        WgradProblem<BM, BN, 3> p{x, dy, dw, part, g, dv, M, N, K, kchunk, splits};
         return launch_gemm(p, M, N, splits, st);
     }
     if (g.KS == 1) {
-        WgradProblem<BM, 1> p{x, dy, dw, part, g, M, N, K, kchunk, splits};
+        WgradProblem<BM, BN, 1> p{x, dy, dw, part, g, dv, M, N, K, kchunk, splits};
         return launch_gemm(p, M, N, splits, st);
     }
-    WgradProblem<BM, 0> p{x, dy, dw, part, g, M, N, K, kchunk, splits};
+    WgradProblem<BM, BN, 0> p{x, dy, dw, part, g, dv, M, N, K, kchunk, splits};
     return launch_gemm(p, M, N, splits, st);
 }
 
@@ -647,14 +806,41 @@ extern "C" {
 int ach_conv_out_h(const ach_conv_desc *d) { return conv_ok(d) ? geom(d).OH : -1; }
 int ach_conv_out_w(const ach_conv_desc *d) { return conv_ok(d) ? geom(d).OW : -1; }
 
-size_t ach_conv_fwd_workspace(const ach_conv_desc *) { return 0; }
+// Workspace of the forward pass: the k-major copy of the filter, then the
+// split-K partials when the plan splits K.
+size_t ach_conv_fwd_workspace(const ach_conv_desc *d)
+{
+    if (!conv_ok(d)) return 0;
+    const ConvGeom g = geom(d);
+    return align256((size_t)g.F * g.C * g.KS * g.KS * sizeof(float)) + fwd_part_bytes(g);
+}
 
 int ach_conv_fwd(const ach_conv_desc *d, const float *x, const float *w, float *y,
-                 void *, size_t, ach_stream_t stream)
+                 void *ws, size_t ws_bytes, ach_stream_t stream)
 {
     if (!conv_ok(d) || !x || !w || !y) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
-    return fwd_impl(geom(d), x, w, y, as_stream(stream));
+    if (!ws || ws_bytes < ach_conv_fwd_workspace(d)) return ACH_EWORKSPACE;
+    const ConvGeom g = geom(d);
+    hipStream_t st = as_stream(stream);
+    const int M = g.F, K = g.C * g.KS * g.KS;
+    float *wt = (float *)ws;
+    float *part = (float *)((char *)ws + align256((size_t)M * K * sizeof(float)));
+    hipLaunchKernelGGL(k_weights_kmajor, dim3((K + 31) / 32, (M + 31) / 32), dim3(256), 0, st, w,
+                       wt, M, K);
+    int rc = check_launch();
+    if (rc) return rc;
+    return fwd_impl(g, x, wt, y, part, st);
+}
+
+// geometry of stride-1 dgrad seen as a forward convolution of dy
+static ConvGeom dgrad_as_fwd(const ConvGeom &g)
+{
+    ConvGeom t;
+    t.B = g.B; t.C = g.F; t.H = g.OH; t.W = g.OW;
+    t.F = g.C; t.KS = g.KS; t.S = 1; t.P = g.KS - 1 - g.P;
+    t.OH = g.H; t.OW = g.W;
+    return t;
 }
 
 size_t ach_conv_bwd_data_workspace(const ach_conv_desc *d)
@@ -662,7 +848,7 @@ size_t ach_conv_bwd_data_workspace(const ach_conv_desc *d)
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
     size_t wf = (size_t)g.F * g.C * g.KS * g.KS * sizeof(float);
-    if (g.S == 1 && g.P <= g.KS - 1) return wf;
+    if (g.S == 1 && g.P <= g.KS - 1) return align256(wf) + fwd_part_bytes(dgrad_as_fwd(g));
     // strided fallback: one image's column buffer
     return (size_t)g.C * g.KS * g.KS * g.OH * g.OW * sizeof(float);
 }
@@ -679,15 +865,12 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
     if (g.S == 1 && g.P <= g.KS - 1) {
         float *wf = (float *)ws;
         const size_t tot = (size_t)g.F * g.C * g.KS * g.KS;
-        hipLaunchKernelGGL(k_flip_weights, dim3(grid_for(tot, 256)), dim3(256), 0, st, w, wf,
-                           g.F, g.C, g.KS);
+        hipLaunchKernelGGL(k_weights_flip_kmajor, dim3(grid_for(tot, 256)), dim3(256), 0, st, w,
+                           wf, g.F, g.C, g.KS * g.KS);
         int rc = check_launch();
         if (rc) return rc;
-        ConvGeom t;
-        t.B = g.B; t.C = g.F; t.H = g.OH; t.W = g.OW;
-        t.F = g.C; t.KS = g.KS; t.S = 1; t.P = g.KS - 1 - g.P;
-        t.OH = g.H; t.OW = g.W;
-        return fwd_impl(t, dy, wf, dx, st);
+        float *part = (float *)((char *)ws + align256(tot * sizeof(float)));
+        return fwd_impl(dgrad_as_fwd(g), dy, wf, dx, part, st);
     }
     // Strided convolution: the reference's per-image TN GEMM + col2im
     // (ConvolutionalLayer.c:933-945).  Not on any benchmark path.
@@ -709,9 +892,10 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
     int splits, kchunk;
-    wgrad_split(g, wgrad_bm(g), splits, kchunk);
+    wgrad_split(g, wgrad_bm(g), wgrad_bn(g), splits, kchunk);
     if (splits <= 1) return 0;
-    return (size_t)splits * g.F * g.C * g.KS * g.KS * sizeof(float);
+    const int groups = splits > 2 * SPLIT_GROUP ? (splits + SPLIT_GROUP - 1) / SPLIT_GROUP : 0;
+    return (size_t)(splits + groups) * g.F * g.C * g.KS * g.KS * sizeof(float);
 }
 
 int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
@@ -720,19 +904,31 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
     if (!conv_ok(d) || !x || !dy || !dw) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
-    const int bm = wgrad_bm(g);
+    const int bm = wgrad_bm(g), bn = wgrad_bn(g);
     int splits, kchunk;
-    wgrad_split(g, bm, splits, kchunk);
+    wgrad_split(g, bm, bn, splits, kchunk);
     const size_t need = ach_conv_bwd_filter_workspace(d);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
     hipStream_t st = as_stream(stream);
     float *part = (float *)ws;
     int rc;
-    if (bm == 32) rc = wgrad_launch<32>(g, x, dy, dw, part, splits, kchunk, st);
-    else if (bm == 64) rc = wgrad_launch<64>(g, x, dy, dw, part, splits, kchunk, st);
-    else rc = wgrad_launch<128>(g, x, dy, dw, part, splits, kchunk, st);
+    if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st);
+    else if (bm == 32) rc = wgrad_launch<32, 128>(g, x, dy, dw, part, splits, kchunk, st);
+    else if (bm == 64) rc = wgrad_launch<64, 128>(g, x, dy, dw, part, splits, kchunk, st);
+    else rc = wgrad_launch<128, 128>(g, x, dy, dw, part, splits, kchunk, st);
     if (rc || splits == 1) return rc;
     const size_t mn = (size_t)g.F * g.C * g.KS * g.KS;
+    if (splits > 2 * SPLIT_GROUP) {
+        const int groups = (splits + SPLIT_GROUP - 1) / SPLIT_GROUP;
+        float *tmp = part + (size_t)splits * mn;
+        hipLaunchKernelGGL(k_splitk_group, dim3(grid_for(mn, 256, 1024), groups), dim3(256), 0, st,
+                           part, tmp, mn, splits);
+        rc = check_launch();
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(mn, 256)), dim3(256), 0, st, tmp, dw,
+                           mn, groups);
+        return check_launch();
+    }
     hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(mn, 256)), dim3(256), 0, st, part, dw,
                        mn, splits);
     return check_launch();

@@ -109,7 +109,8 @@ def sweep_phase(aetcnn, batch, reps):
         dx = D((batch, ci, hw, hw))
         dw = D((co, ci, k, k))
         dw.zero()
-        wsz = max(ops.ach_conv_bwd_data_workspace(C.byref(d)),
+        wsz = max(ops.ach_conv_fwd_workspace(C.byref(d)),
+                  ops.ach_conv_bwd_data_workspace(C.byref(d)),
                   ops.ach_conv_bwd_filter_workspace(C.byref(d)), 256)
         ws = D(wsz // 4)
         flop = 2.0 * batch * co * oh * oh * ci * k * k
