@@ -128,6 +128,8 @@ _NET = {
     "an_layer_forward": (_i, [_vp, _i, _i]),
     "an_layer_backward": (_i, [_vp, _i]),
     "an_n_layers": (_i, [_vp]),
+    "an_get_layer": (_vp, [_vp, _i]),
+    "an_layer_shape": (_i, [_vp, _i, C.POINTER(_i)]),
     "an_batch": (_i, [_vp]),
     "an_input": (_vp, [_vp]),
     "an_truth": (_vp, [_vp]),
@@ -308,6 +310,12 @@ class Network:
 
     def n_layers(self):
         return self.lib.an_n_layers(self.h)
+
+    def shape(self, i):
+        """[type, out_c, out_h, out_w, c, h, w, batch] of layer i (host only)."""
+        a = (_i * 8)()
+        check(self.lib.an_layer_shape(self.h, i, a), "an_layer_shape")
+        return list(a)
 
     def set_input(self, x: np.ndarray, truth: Optional[np.ndarray]):
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -720,6 +720,21 @@ an_layer *an_get_layer(an_network *net, int i)
 {
     return (net && i >= 0 && i < net->n) ? net->layers[i] : NULL;
 }
+int an_layer_shape(const an_network *net, int i, int *out)
+{
+    if (!net || i < 0 || i >= net->n || !out) return ACH_EINVAL;
+    const an_layer *l = net->layers[i];
+    out[0] = (int)l->type;
+    out[1] = l->out_c;
+    out[2] = l->out_h;
+    out[3] = l->out_w;
+    out[4] = l->c;
+    out[5] = l->h;
+    out[6] = l->w;
+    out[7] = l->batch;
+    return ACH_OK;
+}
+
 int an_batch(const an_network *net) { return net->batch; }
 float *an_input(an_network *net) { return net->input; }
 float *an_truth(an_network *net) { return net->truth; }

@@ -30,6 +30,10 @@ SWEEP = [  # config 1: (C_in, C_out, H, k, pad)
     (256, 512, 8, 3, 1), (512, 512, 8, 3, 1), (512, 10, 8, 1, 0),
 ]
 ROOFLINE_SHAPE = (256, 256, 16, 3, 1)  # dominant kernel probe: conv fwd GEMM
+# HBM bytes per launch of the probe kernel, from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE runs scaled by a 256 MiB copy dispatch (profiles/
+# conv_fwd_gemm_darknet_b128.md): 52.8 MB read + 33.6 MB written.
+ROOFLINE_TRAFFIC_BYTES = 86.4e6
 
 
 def log(msg):
@@ -98,7 +102,6 @@ def sweep_phase(aetcnn, batch, reps):
     rng = np.random.default_rng(0)
     rows = []
     tot_flop = tot_ms = 0.0
-    probe = None
     for (ci, co, hw, k, p) in SWEEP:
         d = aetcnn.ConvDesc(batch, ci, hw, hw, co, k, 1, p)
         oh = (hw + 2 * p - k) + 1
@@ -133,14 +136,56 @@ def sweep_phase(aetcnn, batch, reps):
         rows.append(row)
         tot_flop += 3 * flop
         tot_ms += sum(t)
-        if (ci, co, hw, k, p) == ROOFLINE_SHAPE:
-            probe = dict(kernel="k_mfma_gemm<FwdProblem<3>> (conv fwd implicit GEMM)",
-                         shape=row["shape"] + f" b{batch}", flop=flop, ms=t[0])
         log(f"sweep {row['shape']}: fwd/dgrad/wgrad {row['tflops']} TFLOP/s")
         for a in (x, w, y, dy, dx, dw, ws):
             a.free()
     ops.ach_stream_destroy(stream)
-    return rows, tot_flop / (tot_ms * 1e-3) / 1e12, probe
+    return rows, tot_flop / (tot_ms * 1e-3) / 1e12
+
+
+def roofline_phase(aetcnn, batch, reps):
+    """The dominant kernel of the training step -- the implicit-GEMM conv
+    forward (also used for the stride-1 input gradient) -- on one config-3 /
+    config-1 layer, launched `reps` times back to back on its own stream with
+    HIP events around the run.  Each ach_conv_fwd call is the filter
+    transpose (k_weights_kmajor, ~1% of the time) plus the GEMM; the average
+    here therefore slightly over-states the GEMM's own duration."""
+    ops = aetcnn.ops()
+    D = aetcnn.DeviceArray
+    ci, co, hw, k, p = ROOFLINE_SHAPE
+    stream = C.c_void_p()
+    aetcnn.check(ops.ach_stream_create(C.byref(stream)), "stream")
+    d = aetcnn.ConvDesc(batch, ci, hw, hw, co, k, 1, p)
+    rng = np.random.default_rng(1)
+    x = D.from_numpy(rng.uniform(-1, 1, (batch, ci, hw, hw)).astype(np.float32))
+    w = D.from_numpy((rng.standard_normal((co, ci, k, k)) * 0.05).astype(np.float32))
+    y = D((batch, co, hw, hw))
+    wsz = ops.ach_conv_fwd_workspace(C.byref(d))
+    ws = D(wsz // 4 + 64)
+
+    def fwd():
+        aetcnn.check(ops.ach_conv_fwd(C.byref(d), x.ptr, w.ptr, y.ptr, ws.ptr, wsz, stream))
+
+    ms = time_launch(ops, stream, fwd, reps)
+    flop = 2.0 * batch * co * hw * hw * ci * k * k
+    for a in (x, w, y, ws):
+        a.free()
+    ops.ach_stream_destroy(stream)
+    return dict(kernel="k_mfma_gemm<FwdProblem<128, BIm2col3>> (conv fwd / dgrad implicit GEMM)",
+                shape=f"{ci}->{co}@{hw}x{hw} k{k} b{batch}", flop=flop, ms=ms, reps=reps)
+
+
+def copy_calibration_phase(aetcnn, nfloats=1 << 26):
+    """One ach_scal over a 256 MiB buffer (reads and writes exactly 256 MiB):
+    the reference dispatch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE
+    counters to bytes."""
+    ops = aetcnn.ops()
+    buf = aetcnn.DeviceArray(nfloats)
+    buf.zero()
+    aetcnn.check(ops.ach_scal(nfloats, 1.0, buf.ptr, None), "scal")
+    aetcnn.check(ops.ach_device_sync(), "sync")
+    buf.free()
+    return nfloats * 4
 
 
 def cpu_phase(configs, name, batch, steps):
@@ -176,6 +221,7 @@ def main():
     ap.add_argument("--config", default="darknet", choices=["darknet", "tiny", "alexnet"])
     ap.add_argument("--sweep-reps", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=3)
@@ -202,18 +248,22 @@ def main():
     log(f"{ms_step:.3f} ms/step ({tr['gpu_ms'] / args.steps:.3f} GPU ms), {ips:.1f} img/s, "
         f"conv {step_tflops:.2f} TFLOP/s, loss {tr['first_loss']:.4f} -> {tr['loss']:.4f}")
 
-    sweep_rows, sweep_tflops, probe = [], None, None
+    sweep_rows, sweep_tflops = [], None
     if not args.no_sweep:
-        sweep_rows, sweep_tflops, probe = sweep_phase(aetcnn, 128, args.sweep_reps)
+        sweep_rows, sweep_tflops = sweep_phase(aetcnn, 128, args.sweep_reps)
         log(f"conv sweep fwd+dgrad+wgrad: {sweep_tflops:.2f} TFLOP/s")
+    probe = roofline_phase(aetcnn, 128, args.roofline_reps)
+    copy_calibration_phase(aetcnn)
+    log(f"roofline probe {probe['shape']}: {probe['ms']:.4f} ms/launch over {probe['reps']}")
 
     roofline = None
     if probe:
         ach = probe["flop"] / (probe["ms"] * 1e-3) / 1e12
         roofline = dict(bound="mfma", achieved=round(ach, 3), peak=MFMA_FP32_PEAK_TFLOPS,
                         unit="TFLOP/s", frac=round(ach / MFMA_FP32_PEAK_TFLOPS, 4),
-                        traffic=None, kernel=probe["kernel"], shape=probe["shape"],
-                        avg_launch_ms=round(probe["ms"], 5),
+                        traffic=ROOFLINE_TRAFFIC_BYTES, kernel=probe["kernel"],
+                        shape=probe["shape"],
+                        avg_launch_ms=round(probe["ms"], 5), launches=probe["reps"],
                         flop_per_launch=probe["flop"])
 
     cpu = None

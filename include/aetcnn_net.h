@@ -137,6 +137,9 @@ int an_layer_backward(an_network *net, int layer);
 /* ---- introspection (tests, checkpoints) ------------------------------------ */
 int an_n_layers(const an_network *net);
 an_layer *an_get_layer(an_network *net, int i);
+/* out[8] = {type, out_c, out_h, out_w, c, h, w, batch}; host-only, valid
+ * before an_finalize                                                        */
+int an_layer_shape(const an_network *net, int i, int *out8);
 int an_batch(const an_network *net);
 /* device pointers of the network's input and truth buffers                 */
 float *an_input(an_network *net);

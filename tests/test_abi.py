@@ -1,0 +1,144 @@
+"""The C-ABI libraries load and export every declared symbol; host-side
+logic (shapes, workspace plans, cfg parsing errors, counter-based RNG,
+bench argument handling) checked without a GPU."""
+import ctypes as C
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import aetcnn
+from aetcnn import configs
+from conftest import ROOT
+
+HEADERS = {
+    "aetcnn_ops.h": "libach.so",
+    "aetcnn_net.h": "libaetcnn.so",
+}
+
+
+def declared(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:ach|an)_[A-Za-z0-9_]+)\s*\(", text)))
+
+
+@pytest.mark.parametrize("header", sorted(HEADERS))
+def test_library_exports_every_declared_symbol(header):
+    lib = C.CDLL(os.path.join(aetcnn.LIB_DIR, HEADERS[header]))
+    names = declared(header)
+    assert len(names) > 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_bindings_cover_headers():
+    ops_decl = set(declared("aetcnn_ops.h"))
+    net_decl = set(declared("aetcnn_net.h"))
+    assert ops_decl <= set(aetcnn.op_symbols()), ops_decl - set(aetcnn.op_symbols())
+    assert net_decl <= set(aetcnn.net_symbols()), net_decl - set(aetcnn.net_symbols())
+    aetcnn.ops()
+    aetcnn.net_lib()
+
+
+def test_conv_shape_and_workspace_queries():
+    ops = aetcnn.ops()
+    d = aetcnn.ConvDesc(128, 3, 227, 227, 96, 11, 4, 0)
+    assert ops.ach_conv_out_h(C.byref(d)) == 55 and ops.ach_conv_out_w(C.byref(d)) == 55
+    assert ops.ach_conv_fwd_workspace(C.byref(d)) >= 96 * 3 * 121 * 4
+    bad = aetcnn.ConvDesc(1, 3, 2, 2, 4, 5, 1, 0)  # kernel larger than padded input
+    assert ops.ach_conv_out_h(C.byref(bad)) == -1
+    # split-K partial buffers appear only when the tile grid is small
+    small = aetcnn.ConvDesc(128, 512, 8, 8, 512, 3, 1, 1)
+    big = aetcnn.ConvDesc(128, 128, 32, 32, 128, 3, 1, 1)
+    assert ops.ach_conv_fwd_workspace(C.byref(small)) > 512 * 512 * 9 * 4
+    assert ops.ach_conv_fwd_workspace(C.byref(big)) < 128 * 128 * 9 * 4 + 512
+    assert ops.ach_conv_bwd_filter_workspace(C.byref(big)) > 0
+    assert ops.ach_maxpool_out(32, 2, 2, 1) == 16  # darknet default padding = size-1
+    assert ops.ach_maxpool_out(55, 3, 2, 0) == 27
+
+
+def test_dropout_generator_matches_oracle(oracle):
+    ops = aetcnn.ops()
+    for args in [(1, 0, 0, 0), (0x5EED, 7, 3, 12345), (2**63, 2**31, 17, 2**32 - 1)]:
+        assert ops.ach_dropout_uniform(*args) == oracle.lib().or_dropout_uniform(*args)
+
+
+def test_network_shapes_match_oracle(oracle):
+    for name, batch in [("tiny", 4), ("darknet", 2), ("alexnet", 2)]:
+        net = aetcnn.Network(*configs.dims(name, batch))
+        configs.build(net, name)
+        onet = oracle.OracleNet(*configs.dims(name, batch))
+        configs.build(onet, name)
+        assert net.n_layers() == onet.n_layers()
+        for i in range(net.n_layers()):
+            assert net.shape(i) == onet.info(i), (name, i)
+        net.close()
+        onet.close()
+    # AlexNet-style with padding=0 pools: 55 -> 27 -> 13 -> 6, FC input 9216
+    net = aetcnn.Network(*configs.dims("alexnet", 1))
+    configs.build(net, "alexnet")
+    assert net.shape(7)[1:4] == [256, 6, 6]
+    net.close()
+
+
+def test_layer_constructors_reject_bad_shapes():
+    lib = aetcnn.net_lib()
+    h = lib.an_network_create(2, 4, 4, 3)
+    assert lib.an_add_convolutional(h, 8, 7, 1, 0, aetcnn.LEAKY, 1) < 0   # 7x7 on 4x4
+    assert lib.an_add_convolutional(h, 8, 3, 1, 1, 5, 1) == aetcnn.ACH_EUNSUPPORTED
+    assert lib.an_add_dropout(h, 1.5) < 0
+    assert lib.an_add_convolutional(h, 8, 3, 1, 1, aetcnn.LEAKY, 1) == 0
+    assert lib.an_add_softmax(h, 3, 1.0) < 0                              # 128 % 3 != 0
+    lib.an_free(h)
+    assert lib.an_network_create(0, 4, 4, 3) is None
+
+
+def test_cfg_parser_error_paths(tmp_path):
+    lib = aetcnn.net_lib()
+    assert lib.an_parse_cfg(str(tmp_path / "missing.cfg").encode()) is None
+    p = tmp_path / "nonet.cfg"
+    p.write_text("[convolutional]\nfilters=4\n")
+    assert lib.an_parse_cfg(str(p).encode()) is None
+    p.write_text("[net]\nbatch=2\nheight=8\nwidth=8\nchannels=3\n[yolo]\n")
+    assert lib.an_parse_cfg(str(p).encode()) is None
+    p.write_text("[net]\nbatch=2\nheight=8\nwidth=8\nchannels=3\n"
+                 "[convolutional]\nfilters=4\nsize=3\nxnor=1\n")
+    assert lib.an_parse_cfg(str(p).encode()) is None
+
+
+def test_cfg_files_describe_the_configs():
+    """The shipped .cfg files parse into the same layer sequence as the
+    programmatic configs (checked through the darknet key semantics)."""
+    for name in ("tiny", "darknet", "alexnet"):
+        text = open(os.path.join(ROOT, "aet-cnn_amd", "cfg", f"{name}.cfg")).read()
+        sections = re.findall(r"^\[(\w+)\]", text, flags=re.M)
+        kinds = [l[0] for l in configs.CONFIGS[name]["layers"]]
+        assert sections[0] == "net"
+        assert [s.replace("convolutional", "conv") for s in sections[1:]] == kinds, name
+
+
+def test_step_flops_match_survey():
+    # config 3 step ~813.8 GF, config 0 ~1.15 GF, config 4 ~845 GF
+    assert abs(configs.step_gflop("darknet") - 813.8) < 1.0
+    assert abs(configs.step_gflop("tiny") - 1.15) < 0.05
+    assert abs(configs.step_gflop("alexnet") - 845) / 845 < 0.02
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_finalize_without_device_fails_loudly():
+    if aetcnn.gpu_available():
+        pytest.skip("a device is present")
+    net = aetcnn.Network(2, 8, 8, 3)
+    net.conv(4, 3, 1, 1, aetcnn.LEAKY, 1)
+    net.softmax()
+    with pytest.raises(aetcnn.HipError):
+        net.finalize()

@@ -378,3 +378,20 @@ def test_network_forward_composes_ops():
     _, _, _, cost = O.softmax_xent(av, t)
     assert abs(loss - cost / B) < 1e-6
     assert np.array_equal(net.buffer(1, 14).reshape(idx.shape), idx)
+
+
+def test_bn_inference_normalize_closed_form():
+    """NormData.normalizeByRoll (NormData.c:291-326): rolling statistics,
+    inv = 1/(sqrt(rolling_var)+1e-6)."""
+    rng = np.random.default_rng(13)
+    out = rng.standard_normal((3, 4, 5, 2)).astype(np.float32)
+    rm = rng.standard_normal(4).astype(np.float32)
+    rv = rng.uniform(0.5, 2, 4).astype(np.float32)
+    sc = rng.uniform(0.5, 2, 4).astype(np.float32)
+    bi = rng.standard_normal(4).astype(np.float32)
+    got = out.copy()
+    O.lib().or_bn_normalize_roll(O.P(got), 3, 4, 10, O.P(rm), O.P(rv), O.P(sc), O.P(bi))
+    x = out.astype(np.float64)
+    ref = ((x - rm[None, :, None, None]) / (np.sqrt(rv.astype(np.float64)) + 1e-6)[None, :, None, None]
+           * sc[None, :, None, None] + bi[None, :, None, None])
+    assert rel_err(got, ref) < 1e-6
