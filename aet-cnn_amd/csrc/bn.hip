@@ -9,19 +9,26 @@
 //   DeltaData.calcMean/calcVariance/normalize DeltaData.c:23-80 (eps 1e-5,
 //   double sub-expressions); no beta gradient.
 //
-// Each direction is a per-channel reduction pass (grid = channels x batch
-// chunks, double accumulation, one partial per block, no atomics), a one-
-// thread-per-channel finalize that combines the partials in a fixed order,
-// and one coalesced elementwise pass (float4 when H*W % 4 == 0).  The
-// activation that follows BN in a conv layer can be fused into the forward
-// apply and its gradient into both backward passes; the gradient's sign is
-// taken from the recomputed BN output (same float ops as the forward), so
-// the activated tensor does not have to be re-read.
+// Each direction is two launches:
+//   reduce : grid = channels x batch chunks; each block sums its chunk of one
+//            channel in double and writes one partial (no atomics);
+//   apply  : grid = element chunks x channels, so the channel is uniform per
+//            block; wave 0 first combines the channel's partials (the same
+//            fixed-order reduction in every block, so every block derives
+//            bit-identical statistics), block 0 of the channel stores the
+//            per-channel results, and the block then makes one coalesced
+//            elementwise pass (float4 when H*W % 4 == 0).
+// Element positions are walked incrementally (no per-element division).
+// The activation that follows BN in a conv layer can be fused into the
+// forward apply and its gradient into both backward passes; the gradient's
+// sign is taken from the recomputed BN output (same float ops as the
+// forward), so the activated tensor does not have to be re-read.
 #include "common.hpp"
 
 namespace ach {
 
-constexpr int BN_NT = 256;
+constexpr int BN_NT = 256;  // threads per block
+constexpr int BN_U = 4;     // elements (float or float4) per thread in apply
 
 static int bn_chunks(int batch, int c)
 {
@@ -30,6 +37,44 @@ static int bn_chunks(int batch, int c)
     if (nch < 1) nch = 1;
     return nch;
 }
+
+template <bool VEC> struct Elem;
+template <> struct Elem<true> {
+    typedef float4 T;
+    static constexpr int N = 4;
+};
+template <> struct Elem<false> {
+    typedef float T;
+    static constexpr int N = 1;
+};
+
+template <class T> __device__ __forceinline__ float &comp(T &v, int k)
+{
+    return reinterpret_cast<float *>(&v)[k];
+}
+
+// Walks positions i, i + BN_NT, ... of a channel's [batch][hwv] range:
+// element (b, q) lives at ((b*C + c)*hwv + q).
+struct Walk {
+    int b, q, db, dq, hwv;
+    __device__ __forceinline__ Walk(int i, int hwv_) : hwv(hwv_)
+    {
+        b = i / hwv;
+        q = i - b * hwv;
+        db = BN_NT / hwv;
+        dq = BN_NT - db * hwv;
+    }
+    __device__ __forceinline__ void step()
+    {
+        q += dq;
+        b += db;
+        if (q >= hwv) {
+            q -= hwv;
+            ++b;
+        }
+    }
+    __device__ __forceinline__ int at(int C, int c) const { return (b * C + c) * hwv + q; }
+};
 
 template <int NV>
 __device__ __forceinline__ double block_sum(double v, double *sh)
@@ -45,33 +90,44 @@ __device__ __forceinline__ double block_sum(double v, double *sh)
     return t;  // valid in thread 0
 }
 
+// Sum of partial j of channel c over the nch chunks, by one wave: lane l
+// adds chunks l, l+64, ... in order, then a fixed xor tree.  Every block of
+// the apply pass runs the same code on the same data, so all get the same
+// bits.
+__device__ __forceinline__ double chunk_sum(const double *__restrict__ part, int nch, int C, int c,
+                                            int stride, int j)
+{
+    const int lane = threadIdx.x & 63;
+    double s = 0;
+    for (int ch = lane; ch < nch; ch += 64) s += part[((size_t)ch * C + c) * stride + j];
+    return wave_sum(s);
+}
+
 // ---- forward statistics: partial[ch][c] = {sum x, sum x^2} -----------------
+template <bool VEC>
 __global__ void __launch_bounds__(BN_NT) k_bn_stats(const float *__restrict__ x, int batch,
-                                                    int C, int HW, int per,
+                                                    int C, int hwv, int per,
                                                     double *__restrict__ part)
 {
+    typedef typename Elem<VEC>::T T;
     __shared__ double sh[BN_NT / 64];
     const int c = blockIdx.x, ch = blockIdx.y;
     const int b0 = ch * per, b1 = min(batch, b0 + per);
+    const int tot = (b1 - b0) * hwv;
+    const T *xv = reinterpret_cast<const T *>(x);
     double s1 = 0, s2 = 0;
-    if ((HW & 3) == 0) {
-        const int hw4 = HW >> 2;
-        const int tot = (b1 - b0) * hw4;
-        for (int i = threadIdx.x; i < tot; i += BN_NT) {
-            const int bb = b0 + i / hw4, q = i - (i / hw4) * hw4;
-            const float4 v = reinterpret_cast<const float4 *>(x + ((size_t)bb * C + c) * HW)[q];
-            s1 += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
-            s2 += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) +
-                  (double)(v.w * v.w);
+    Walk wk(threadIdx.x, hwv);
+    wk.b += b0;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < tot; i += BN_NT) {
+        T v = xv[wk.at(C, c)];
+#pragma unroll
+        for (int k = 0; k < Elem<VEC>::N; ++k) {
+            const float e = comp(v, k);
+            s1 += (double)e;
+            s2 += (double)(e * e);
         }
-    } else {
-        const int tot = (b1 - b0) * HW;
-        for (int i = threadIdx.x; i < tot; i += BN_NT) {
-            const int bb = b0 + i / HW, q = i - (i / HW) * HW;
-            const float v = x[((size_t)bb * C + c) * HW + q];
-            s1 += v;
-            s2 += (double)(v * v);
-        }
+        wk.step();
     }
     const double t1 = block_sum<BN_NT / 64>(s1, sh);
     const double t2 = block_sum<BN_NT / 64>(s2, sh);
@@ -81,88 +137,91 @@ __global__ void __launch_bounds__(BN_NT) k_bn_stats(const float *__restrict__ x,
     }
 }
 
-// ---- forward finalize: mean, unbiased variance, rolling stats, inv --------
-__global__ void k_bn_finalize(const double *__restrict__ part, int nch, int C, int batch,
-                              int HW, float *__restrict__ mean, float *__restrict__ variance,
-                              float *__restrict__ rmean, float *__restrict__ rvar,
-                              float *__restrict__ inv)
+// NormData.c:170-185 in float: mean = (sum x) * (1/N);
+// var = (t1 + t2*mean + mean*mean*batch*spatial) * (1/(N-1)), t2 = sum(-2x)
+__device__ __forceinline__ void bn_moments(double S1, double S2, int batch, int HW, float &m,
+                                           float &v)
 {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C) return;
-    double S1 = 0, S2 = 0;
-    for (int ch = 0; ch < nch; ++ch) {
-        S1 += part[((size_t)ch * C + c) * 2 + 0];
-        S2 += part[((size_t)ch * C + c) * 2 + 1];
-    }
-    // NormData.c:170-185 in float: mean = (sum x) * (1/N);
-    // var = (t1 + t2*mean + mean*mean*batch*spatial) * (1/(N-1)), t2 = sum(-2x)
     const int N = batch * HW;
     const float scale = (float)(1. / N);
-    const float m = (float)S1 * scale;
+    m = (float)S1 * scale;
     const float t1 = (float)S2, t2 = (float)(-2.0 * S1);
     float mm = m * m;
     mm = mm * (float)batch;
     mm = mm * (float)HW;
-    float v = t1 + t2 * m + mm;
+    v = t1 + t2 * m + mm;
     v *= (float)(1. / (N - 1));
-    mean[c] = m;
-    variance[c] = v;
-    if (rmean) {
-        const float keep = .9f, take = .1f;
-        rmean[c] = rmean[c] * keep;
-        rmean[c] += take * m;
-        rvar[c] = rvar[c] * keep;
-        rvar[c] += take * v;
-    }
-    inv[c] = (float)(1.0 / (sqrt((double)v) + (double)1e-6f));
 }
 
-__global__ void k_bn_inv(const float *__restrict__ variance, int C, float *__restrict__ inv)
+// NormData.c:251-262: 1/(sqrt(var) + .000001f) in double, rounded to float
+__device__ __forceinline__ float bn_inv(float v)
 {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c < C) inv[c] = (float)(1.0 / (sqrt((double)variance[c]) + (double)1e-6f));
+    return (float)(1.0 / (sqrt((double)v) + (double)1e-6f));
 }
 
-// ---- forward apply ----------------------------------------------------------
+// ---- forward apply ------------------------------------------------------------
+// Wave 0 turns the partials into mean / variance / inv; block 0 of the
+// channel writes mean, variance and the rolling statistics.  Then
 // src: pre-BN tensor; xcopy (optional) gets a copy; xnorm (optional);
 // out = act(xnorm*scale + bias).
-__global__ void __launch_bounds__(256) k_bn_apply(const float *src, float *xcopy,
-                                                  float *xnorm, float *out,
-                                                  size_t total, int C, int HW,
-                                                  const float *__restrict__ mean,
-                                                  const float *__restrict__ inv,
-                                                  const float *__restrict__ scales,
-                                                  const float *__restrict__ biases, int act)
+template <bool VEC>
+__global__ void __launch_bounds__(BN_NT) k_bn_apply(
+    const float *src, float *xcopy, float *xnorm, float *out, int batch, int C, int HW, int hwv,
+    const double *__restrict__ part, int nch, float *__restrict__ mean,
+    float *__restrict__ variance, float *__restrict__ rmean, float *__restrict__ rvar,
+    const float *__restrict__ scales, const float *__restrict__ biases, int act)
 {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    if ((HW & 3) == 0) {
-        const size_t tot4 = total >> 2;
-        const int hw4 = HW >> 2;
-        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < tot4; i += stride) {
-            const int c = (int)((i / hw4) % C);
-            const float mu = mean[c], iv = inv[c], s = scales[c], bb = biases[c];
-            float4 v = reinterpret_cast<const float4 *>(src)[i];
-            if (xcopy) reinterpret_cast<float4 *>(xcopy)[i] = v;
-            float4 n;
-            n.x = (v.x - mu) * iv; n.y = (v.y - mu) * iv;
-            n.z = (v.z - mu) * iv; n.w = (v.w - mu) * iv;
-            if (xnorm) reinterpret_cast<float4 *>(xnorm)[i] = n;
-            float4 o;
-            o.x = act_forward(__fmaf_rn(n.x, s, bb), act);
-            o.y = act_forward(__fmaf_rn(n.y, s, bb), act);
-            o.z = act_forward(__fmaf_rn(n.z, s, bb), act);
-            o.w = act_forward(__fmaf_rn(n.w, s, bb), act);
-            reinterpret_cast<float4 *>(out)[i] = o;
+    typedef typename Elem<VEC>::T T;
+    __shared__ float sp[2];
+    const int c = blockIdx.y;
+    if (threadIdx.x < 64) {
+        const double S1 = chunk_sum(part, nch, C, c, 2, 0);
+        const double S2 = chunk_sum(part, nch, C, c, 2, 1);
+        if (threadIdx.x == 0) {
+            float m, v;
+            bn_moments(S1, S2, batch, HW, m, v);
+            if (blockIdx.x == 0) {
+                mean[c] = m;
+                variance[c] = v;
+                if (rmean) {
+                    const float keep = .9f, take = .1f;
+                    float r = rmean[c] * keep;
+                    rmean[c] = r + take * m;
+                    r = rvar[c] * keep;
+                    rvar[c] = r + take * v;
+                }
+            }
+            sp[0] = m;
+            sp[1] = bn_inv(v);
         }
-    } else {
-        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += stride) {
-            const int c = (int)((i / HW) % C);
-            const float v = src[i];
-            if (xcopy) xcopy[i] = v;
-            const float n = (v - mean[c]) * inv[c];
-            if (xnorm) xnorm[i] = n;
-            out[i] = act_forward(__fmaf_rn(n, scales[c], biases[c]), act);
-        }
+    }
+    __syncthreads();
+    const float mu = sp[0], iv = sp[1], s = scales[c], bb = biases[c];
+    const int tot = batch * hwv;
+    const int i0 = blockIdx.x * (BN_NT * BN_U) + threadIdx.x;
+    Walk wk(i0, hwv);
+    int at[BN_U];
+    T v[BN_U];
+#pragma unroll
+    for (int u = 0; u < BN_U; ++u) {
+        at[u] = i0 + u * BN_NT < tot ? wk.at(C, c) : -1;
+        wk.step();
+    }
+#pragma unroll
+    for (int u = 0; u < BN_U; ++u)
+        if (at[u] >= 0) v[u] = reinterpret_cast<const T *>(src)[at[u]];
+#pragma unroll
+    for (int u = 0; u < BN_U; ++u) {
+        if (at[u] < 0) continue;
+        if (xcopy) reinterpret_cast<T *>(xcopy)[at[u]] = v[u];
+        T n, o;
+#pragma unroll
+        for (int k = 0; k < Elem<VEC>::N; ++k) comp(n, k) = (comp(v[u], k) - mu) * iv;
+        if (xnorm) reinterpret_cast<T *>(xnorm)[at[u]] = n;
+#pragma unroll
+        for (int k = 0; k < Elem<VEC>::N; ++k)
+            comp(o, k) = act_forward(__fmaf_rn(comp(n, k), s, bb), act);
+        reinterpret_cast<T *>(out)[at[u]] = o;
     }
 }
 
@@ -181,29 +240,42 @@ __device__ __forceinline__ float bwd_grad(float d, float xv, float mu, float iv,
 }
 
 // partial[ch][c] = {sum g*xn, sum g*s, sum (g*s)*(x-mean)}
+template <bool VEC>
 __global__ void __launch_bounds__(BN_NT) k_bn_bwd_reduce(
     const float *__restrict__ delta, const float *__restrict__ x,
-    const float *__restrict__ xnorm, int batch, int C, int HW, int per,
-    const float *__restrict__ mean, const float *__restrict__ inv,
+    const float *__restrict__ xnorm, int batch, int C, int hwv, int per,
+    const float *__restrict__ mean, const float *__restrict__ variance,
     const float *__restrict__ scales, const float *__restrict__ biases, int act,
     double *__restrict__ part)
 {
+    typedef typename Elem<VEC>::T T;
     __shared__ double sh[BN_NT / 64];
     const int c = blockIdx.x, ch = blockIdx.y;
     const int b0 = ch * per, b1 = min(batch, b0 + per);
-    const float mu = mean[c], iv = inv[c], s = scales[c], bb = biases ? biases[c] : 0.f;
+    const float mu = mean[c], iv = bn_inv(variance[c]), s = scales[c];
+    const float bb = biases ? biases[c] : 0.f;
     double g1 = 0, g2 = 0, g3 = 0;
-    const int tot = (b1 - b0) * HW;
+    const int tot = (b1 - b0) * hwv;
+    Walk wk(threadIdx.x, hwv);
+    wk.b += b0;
+#pragma unroll 2
     for (int i = threadIdx.x; i < tot; i += BN_NT) {
-        const int b = b0 + i / HW, q = i - (i / HW) * HW;
-        const size_t idx = ((size_t)b * C + c) * HW + q;
-        const float xv = x[idx];
-        const float g = bwd_grad(delta[idx], xv, mu, iv, s, bb, act);
-        const float xn = xnorm ? xnorm[idx] : (xv - mu) * iv;
-        const float gs = g * s;
-        g1 += (double)(g * xn);
-        g2 += (double)gs;
-        g3 += (double)(gs * (xv - mu));
+        const int at = wk.at(C, c);
+        T xv = reinterpret_cast<const T *>(x)[at];
+        T dv = reinterpret_cast<const T *>(delta)[at];
+        T nv;
+        if (xnorm) nv = reinterpret_cast<const T *>(xnorm)[at];
+#pragma unroll
+        for (int k = 0; k < Elem<VEC>::N; ++k) {
+            const float xe = comp(xv, k);
+            const float g = bwd_grad(comp(dv, k), xe, mu, iv, s, bb, act);
+            const float xn = xnorm ? comp(nv, k) : (xe - mu) * iv;
+            const float gs = g * s;
+            g1 += (double)(g * xn);
+            g2 += (double)gs;
+            g3 += (double)(gs * (xe - mu));
+        }
+        wk.step();
     }
     const double t1 = block_sum<BN_NT / 64>(g1, sh);
     const double t2 = block_sum<BN_NT / 64>(g2, sh);
@@ -214,85 +286,113 @@ __global__ void __launch_bounds__(BN_NT) k_bn_bwd_reduce(
     }
 }
 
-// coef[c] = {1/sqrt(var+1e-5), 2*variance_delta/N, mean_delta/N}
-__global__ void k_bn_bwd_finalize(const double *__restrict__ part, int nch, int C, int N,
-                                  const float *__restrict__ variance,
-                                  float *__restrict__ scale_updates,
-                                  float *__restrict__ mean_delta,
-                                  float *__restrict__ variance_delta,
-                                  double *__restrict__ coef)
+// Wave 0 combines the partials into
+//   scale_updates += G1; mean_delta = G2 * (-1/sqrt(var+1e-5));
+//   variance_delta = G3 * (-.5 * pow(var+1e-5, -1.5))     (DeltaData.c:23-58)
+// (stored by block 0 of the channel), then every element gets
+//   d = d*s * 1/sqrt(v+1e-5) + vd*2*(x-mu)/N + md/N   in double (DeltaData.c:64-80).
+template <bool VEC>
+__global__ void __launch_bounds__(BN_NT) k_bn_bwd_apply(
+    float *__restrict__ delta, const float *__restrict__ x, int batch, int C, int HW, int hwv,
+    const double *__restrict__ part, int nch, const float *__restrict__ mean,
+    const float *__restrict__ variance, const float *__restrict__ scales,
+    const float *__restrict__ biases, int act, float *__restrict__ scale_updates,
+    float *__restrict__ mean_delta, float *__restrict__ variance_delta)
 {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= C) return;
-    double G1 = 0, G2 = 0, G3 = 0;
-    for (int ch = 0; ch < nch; ++ch) {
-        const double *p = part + ((size_t)ch * C + c) * 3;
-        G1 += p[0]; G2 += p[1]; G3 += p[2];
+    typedef typename Elem<VEC>::T T;
+    __shared__ double coef[3];
+    const int c = blockIdx.y;
+    if (threadIdx.x < 64) {
+        const double G1 = chunk_sum(part, nch, C, c, 3, 0);
+        const double G2 = chunk_sum(part, nch, C, c, 3, 1);
+        const double G3 = chunk_sum(part, nch, C, c, 3, 2);
+        if (threadIdx.x == 0) {
+            const int N = batch * HW;
+            const float ve = variance[c] + 1e-5f;
+            // DeltaData.c:36  mean *= (-1./sqrt(var + 1e-5f))
+            const float md = (float)((double)(float)G2 * (-1. / sqrt((double)ve)));
+            // DeltaData.c:56  variance *= -.5 * pow(var + 1e-5f, -1.5f)
+            const float vd =
+                (float)((double)(float)G3 * (-.5 * pow((double)ve, (double)(-1.5f))));
+            if (blockIdx.x == 0) {
+                scale_updates[c] += (float)G1;
+                if (mean_delta) mean_delta[c] = md;
+                if (variance_delta) variance_delta[c] = vd;
+            }
+            coef[0] = 1. / sqrt((double)ve);
+            coef[1] = (double)vd * 2. / (double)N;
+            coef[2] = (double)(md / (float)N);
+        }
     }
-    scale_updates[c] += (float)G1;
-    const float ve = variance[c] + 1e-5f;
-    // DeltaData.c:36  mean *= (-1./sqrt(var + 1e-5f))
-    const float md = (float)((double)(float)G2 * (-1. / sqrt((double)ve)));
-    // DeltaData.c:56  variance *= -.5 * pow(var + 1e-5f, -1.5f)
-    const float vd = (float)((double)(float)G3 * (-.5 * pow((double)ve, (double)(-1.5f))));
-    if (mean_delta) mean_delta[c] = md;
-    if (variance_delta) variance_delta[c] = vd;
-    coef[(size_t)c * 3 + 0] = 1. / sqrt((double)ve);
-    coef[(size_t)c * 3 + 1] = (double)vd * 2. / (double)N;
-    coef[(size_t)c * 3 + 2] = (double)(md / (float)N);
-}
-
-// DeltaData.c:64-80: d = d*1/sqrt(v+1e-5) + vd*2*(x-mu)/N + md/N (double)
-__global__ void __launch_bounds__(256) k_bn_bwd_apply(
-    float *__restrict__ delta, const float *__restrict__ x, size_t total, int C, int HW,
-    const float *__restrict__ mean, const float *__restrict__ inv,
-    const float *__restrict__ scales, const float *__restrict__ biases, int act,
-    const double *__restrict__ coef)
-{
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int c = (int)((i / HW) % C);
-        const float mu = mean[c], s = scales[c];
-        const float xv = x[i];
-        const float g = bwd_grad(delta[i], xv, mu, inv[c], s, biases ? biases[c] : 0.f, act);
-        const float gs = g * s;
-        const double *k = coef + (size_t)c * 3;
-        delta[i] = (float)((double)gs * k[0] + k[1] * (double)(xv - mu) + k[2]);
+    __syncthreads();
+    const double k0 = coef[0], k1 = coef[1], k2 = coef[2];
+    const float mu = mean[c], iv = bn_inv(variance[c]), s = scales[c];
+    const float bb = biases ? biases[c] : 0.f;
+    const int tot = batch * hwv;
+    const int i0 = blockIdx.x * (BN_NT * BN_U) + threadIdx.x;
+    Walk wk(i0, hwv);
+    int at[BN_U];
+    T dv[BN_U], xv[BN_U];
+#pragma unroll
+    for (int u = 0; u < BN_U; ++u) {
+        at[u] = i0 + u * BN_NT < tot ? wk.at(C, c) : -1;
+        wk.step();
+    }
+#pragma unroll
+    for (int u = 0; u < BN_U; ++u)
+        if (at[u] >= 0) {
+            dv[u] = reinterpret_cast<const T *>(delta)[at[u]];
+            xv[u] = reinterpret_cast<const T *>(x)[at[u]];
+        }
+#pragma unroll
+    for (int u = 0; u < BN_U; ++u) {
+        if (at[u] < 0) continue;
+        T o;
+#pragma unroll
+        for (int k = 0; k < Elem<VEC>::N; ++k) {
+            const float xe = comp(xv[u], k);
+            const float g = bwd_grad(comp(dv[u], k), xe, mu, iv, s, bb, act);
+            const float gs = g * s;
+            comp(o, k) = (float)((double)gs * k0 + k1 * (double)(xe - mu) + k2);
+        }
+        reinterpret_cast<T *>(delta)[at[u]] = o;
     }
 }
-
-struct BnWs {
-    double *part;
-    double *coef;
-    float *inv;
-};
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static size_t bn_ws_bytes(int batch, int c)
 {
-    const int nch = bn_chunks(batch, c);
-    return align256((size_t)nch * c * 3 * sizeof(double)) + align256((size_t)c * 3 * sizeof(double)) +
-           align256((size_t)c * sizeof(float));
+    return align256((size_t)bn_chunks(batch, c) * c * 3 * sizeof(double));
 }
 
-static BnWs bn_ws(void *ws, int batch, int c)
-{
-    const int nch = bn_chunks(batch, c);
-    char *p = (char *)ws;
-    BnWs w;
-    w.part = (double *)p;
-    p += align256((size_t)nch * c * 3 * sizeof(double));
-    w.coef = (double *)p;
-    p += align256((size_t)c * 3 * sizeof(double));
-    w.inv = (float *)p;
-    return w;
-}
-
+// element counts stay below 2^31 (32-bit element indexing)
 static bool bn_args_ok(int batch, int c, int spatial)
 {
-    return batch > 0 && c > 0 && spatial > 0 && (double)batch * c * spatial < 4.0e18 &&
-           (double)batch * spatial > 1.0;
+    return batch > 0 && c > 0 && spatial > 0 && (double)batch * c * spatial < 2147483647.0 &&
+           (double)batch * spatial > 1.0 && c <= 65535;
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+struct BnPlan {
+    bool vec;
+    int hwv, nch, per;
+    dim3 reduce_grid, apply_grid;
+};
+
+static BnPlan bn_plan(int batch, int C, int HW, bool vec_ok)
+{
+    BnPlan p;
+    p.vec = vec_ok && (HW & 3) == 0;
+    p.hwv = p.vec ? HW / 4 : HW;
+    const int nch = bn_chunks(batch, C);
+    p.per = (batch + nch - 1) / nch;
+    p.nch = (batch + p.per - 1) / p.per;
+    p.reduce_grid = dim3(C, p.nch);
+    const int tot = batch * p.hwv;
+    p.apply_grid = dim3((tot + BN_NT * BN_U - 1) / (BN_NT * BN_U), C);
+    return p;
 }
 
 static int bn_fwd(const float *src, float *xcopy, float *xnorm, float *out, int batch, int C,
@@ -304,22 +404,26 @@ static int bn_fwd(const float *src, float *xcopy, float *xnorm, float *out, int 
         return ACH_EINVAL;
     if ((rmean == nullptr) != (rvar == nullptr)) return ACH_EINVAL;
     if (!ws || ws_bytes < bn_ws_bytes(batch, C)) return ACH_EWORKSPACE;
-    const BnWs w = bn_ws(ws, batch, C);
-    const int nch = bn_chunks(batch, C);
-    const int per = (batch + nch - 1) / nch;
-    const int nch_eff = (batch + per - 1) / per;
-    hipLaunchKernelGGL(k_bn_stats, dim3(C, nch_eff), dim3(BN_NT), 0, st, src, batch, C, HW, per,
-                       w.part);
+    double *part = (double *)ws;
+    const BnPlan p = bn_plan(batch, C, HW,
+                             aligned16(src) && aligned16(out) && aligned16(xcopy) &&
+                                 aligned16(xnorm));
+    if (p.vec)
+        hipLaunchKernelGGL(k_bn_stats<true>, p.reduce_grid, dim3(BN_NT), 0, st, src, batch, C,
+                           p.hwv, p.per, part);
+    else
+        hipLaunchKernelGGL(k_bn_stats<false>, p.reduce_grid, dim3(BN_NT), 0, st, src, batch, C,
+                           p.hwv, p.per, part);
     int rc = check_launch();
     if (rc) return rc;
-    hipLaunchKernelGGL(k_bn_finalize, dim3((C + 63) / 64), dim3(64), 0, st, w.part, nch_eff, C,
-                       batch, HW, mean, variance, rmean, rvar, w.inv);
-    rc = check_launch();
-    if (rc) return rc;
-    const size_t total = (size_t)batch * C * HW;
-    const size_t work = (HW & 3) == 0 ? total / 4 : total;
-    hipLaunchKernelGGL(k_bn_apply, dim3(grid_for(work, 256, 256u * 32u)), dim3(256), 0, st, src,
-                       xcopy, xnorm, out, total, C, HW, mean, w.inv, scales, biases, act);
+    if (p.vec)
+        hipLaunchKernelGGL(k_bn_apply<true>, p.apply_grid, dim3(BN_NT), 0, st, src, xcopy, xnorm,
+                           out, batch, C, HW, p.hwv, part, p.nch, mean, variance, rmean, rvar,
+                           scales, biases, act);
+    else
+        hipLaunchKernelGGL(k_bn_apply<false>, p.apply_grid, dim3(BN_NT), 0, st, src, xcopy,
+                           xnorm, out, batch, C, HW, p.hwv, part, p.nch, mean, variance, rmean,
+                           rvar, scales, biases, act);
     return check_launch();
 }
 
@@ -369,27 +473,27 @@ int ach_bn_bwd(float *delta, int batch, int C, int HW, const float *x, const flo
     if (!fused && activation != ACH_LINEAR) return ACH_EUNSUPPORTED;
     if (!ws || ws_bytes < bn_ws_bytes(batch, C)) return ACH_EWORKSPACE;
     hipStream_t st = as_stream(stream);
-    const BnWs w = bn_ws(ws, batch, C);
-    const int nch = bn_chunks(batch, C);
-    const int per = (batch + nch - 1) / nch;
-    const int nch_eff = (batch + per - 1) / per;
-    // inv = 1/(sqrt(var)+1e-6) exactly as the forward computed it
-    hipLaunchKernelGGL(k_bn_inv, dim3((C + 63) / 64), dim3(64), 0, st, variance, C, w.inv);
+    double *part = (double *)ws;
+    const BnPlan p = bn_plan(batch, C, HW, aligned16(delta) && aligned16(x) && aligned16(x_norm));
+    const int act = fused ? activation : ACH_LINEAR;
+    if (p.vec)
+        hipLaunchKernelGGL(k_bn_bwd_reduce<true>, p.reduce_grid, dim3(BN_NT), 0, st, delta, x,
+                           x_norm, batch, C, p.hwv, p.per, mean, variance, scales, biases, act,
+                           part);
+    else
+        hipLaunchKernelGGL(k_bn_bwd_reduce<false>, p.reduce_grid, dim3(BN_NT), 0, st, delta, x,
+                           x_norm, batch, C, p.hwv, p.per, mean, variance, scales, biases, act,
+                           part);
     int rc = check_launch();
     if (rc) return rc;
-    const int act = fused ? activation : ACH_LINEAR;
-    hipLaunchKernelGGL(k_bn_bwd_reduce, dim3(C, nch_eff), dim3(BN_NT), 0, st, delta, x, x_norm,
-                       batch, C, HW, per, mean, w.inv, scales, biases, act, w.part);
-    rc = check_launch();
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_bn_bwd_finalize, dim3((C + 63) / 64), dim3(64), 0, st, w.part, nch_eff,
-                       C, batch * HW, variance, scale_updates, mean_delta, variance_delta,
-                       w.coef);
-    rc = check_launch();
-    if (rc) return rc;
-    const size_t total = (size_t)batch * C * HW;
-    hipLaunchKernelGGL(k_bn_bwd_apply, dim3(grid_for(total, 256, 256u * 32u)), dim3(256), 0, st,
-                       delta, x, total, C, HW, mean, w.inv, scales, biases, act, w.coef);
+    if (p.vec)
+        hipLaunchKernelGGL(k_bn_bwd_apply<true>, p.apply_grid, dim3(BN_NT), 0, st, delta, x,
+                           batch, C, HW, p.hwv, part, p.nch, mean, variance, scales, biases, act,
+                           scale_updates, mean_delta, variance_delta);
+    else
+        hipLaunchKernelGGL(k_bn_bwd_apply<false>, p.apply_grid, dim3(BN_NT), 0, st, delta, x,
+                           batch, C, HW, p.hwv, part, p.nch, mean, variance, scales, biases, act,
+                           scale_updates, mean_delta, variance_delta);
     return check_launch();
 }
 

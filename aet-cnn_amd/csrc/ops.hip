@@ -132,38 +132,68 @@ __global__ void __launch_bounds__(256) k_bias_grad(float *updates, const float *
 }
 
 // ---- activations ---------------------------------------------------------------
+// float4 body when x is 16-byte aligned, scalar tail
 __global__ void k_activate(float *x, size_t n, int act)
 {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x)
-        x[i] = act_forward(x[i], act);
+    const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t done = 0;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        float4 *x4 = reinterpret_cast<float4 *>(x);
+        const size_t n4 = n >> 2;
+        for (size_t i = gid; i < n4; i += stride) {
+            float4 v = x4[i];
+            v.x = act_forward(v.x, act); v.y = act_forward(v.y, act);
+            v.z = act_forward(v.z, act); v.w = act_forward(v.w, act);
+            x4[i] = v;
+        }
+        done = n4 << 2;
+    }
+    for (size_t i = done + gid; i < n; i += stride) x[i] = act_forward(x[i], act);
 }
 
 __global__ void k_gradient(const float *__restrict__ y, size_t n, int act, float *d)
 {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x)
-        d[i] *= act_gradient(y[i], act);
+    const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t done = 0;
+    if (((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(d)) & 15) == 0) {
+        const float4 *y4 = reinterpret_cast<const float4 *>(y);
+        float4 *d4 = reinterpret_cast<float4 *>(d);
+        const size_t n4 = n >> 2;
+        for (size_t i = gid; i < n4; i += stride) {
+            const float4 v = y4[i];
+            float4 g = d4[i];
+            g.x *= act_gradient(v.x, act); g.y *= act_gradient(v.y, act);
+            g.z *= act_gradient(v.z, act); g.w *= act_gradient(v.w, act);
+            d4[i] = g;
+        }
+        done = n4 << 2;
+    }
+    for (size_t i = done + gid; i < n; i += stride) d[i] *= act_gradient(y[i], act);
 }
 
 // ---- max-pool --------------------------------------------------------------------
+// Input element counts are below 2^31 (the indexes are int32), so all index
+// arithmetic is 32-bit.
 __global__ void k_maxpool_fwd(const float *__restrict__ in, int batch, int C, int H, int W,
                               int size, int stride, int pad, int OH, int OW,
                               float *__restrict__ out, int32_t *__restrict__ idx)
 {
-    const size_t total = (size_t)batch * C * OH * OW;
+    const unsigned total = (unsigned)batch * C * OH * OW;
     const int off = -pad / 2;
-    for (size_t o = blockIdx.x * (size_t)blockDim.x + threadIdx.x; o < total;
-         o += (size_t)gridDim.x * blockDim.x) {
+    for (unsigned o = blockIdx.x * blockDim.x + threadIdx.x; o < total;
+         o += gridDim.x * blockDim.x) {
         const int j = (int)(o % OW);
-        const int i = (int)((o / OW) % OH);
-        const size_t bc = o / ((size_t)OW * OH);
+        const unsigned r = o / OW;
+        const int i = (int)(r % OH);
+        const int bc = (int)(r / OH);
         float mx = -FLT_MAX;
         int mi = -1;
         for (int n = 0; n < size; ++n)
             for (int m = 0; m < size; ++m) {
                 const int ch = off + i * stride + n, cw = off + j * stride + m;
-                const int index = cw + W * (ch + H * (int)bc);
+                const int index = cw + W * (ch + H * bc);
                 const bool valid = ch >= 0 && ch < H && cw >= 0 && cw < W;
                 const float v = valid ? in[index] : -FLT_MAX;
                 mi = (v > mx) ? index : mi;
@@ -174,34 +204,110 @@ __global__ void k_maxpool_fwd(const float *__restrict__ in, int batch, int C, in
     }
 }
 
+// 2x2 windows, stride 2, no offset, every window inside the image, W % 4 == 0
+// (the darknet default padding = 1 on even sizes): a thread reads a 2x4 input
+// block as two float4 and writes two adjacent outputs.  Same scan order and
+// strict '>' as the generic kernel.
+__device__ __forceinline__ void max4(float a, float b, float c, float d, int ia, int W,
+                                     float &mx, int &mi)
+{
+    mx = -FLT_MAX;
+    mi = -1;
+    if (a > mx) { mx = a; mi = ia; }
+    if (b > mx) { mx = b; mi = ia + 1; }
+    if (c > mx) { mx = c; mi = ia + W; }
+    if (d > mx) { mx = d; mi = ia + W + 1; }
+}
+
+__global__ void __launch_bounds__(256) k_maxpool2_fwd(const float *__restrict__ in, int H, int W,
+                                                      unsigned pairs, float *__restrict__ out,
+                                                      int32_t *__restrict__ idx)
+{
+    const int OW2 = W >> 2, OH = H >> 1;
+    for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < pairs;
+         t += gridDim.x * blockDim.x) {
+        const int jp = (int)(t % OW2);
+        const unsigned r = t / OW2;
+        const int i = (int)(r % OH);
+        const int bc = (int)(r / OH);
+        const int i0 = (bc * H + 2 * i) * W + 4 * jp;
+        const float4 a = *reinterpret_cast<const float4 *>(in + i0);
+        const float4 b = *reinterpret_cast<const float4 *>(in + i0 + W);
+        float2 o;
+        int2 ix;
+        max4(a.x, a.y, b.x, b.y, i0, W, o.x, ix.x);
+        max4(a.z, a.w, b.z, b.w, i0 + 2, W, o.y, ix.y);
+        reinterpret_cast<float2 *>(out)[t] = o;
+        if (idx) reinterpret_cast<int2 *>(idx)[t] = ix;
+    }
+}
+
 __device__ __forceinline__ int floor_div(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 
 // Gather: each input pixel visits, in ascending output order, the outputs
-// whose window holds it and adds the ones whose argmax is this pixel.
+// whose window holds it and adds the ones whose argmax is this pixel.  With
+// accumulate == 0 the sum starts from +0 instead of delta_in (the value the
+// reference's zeroed delta holds), and delta_in is not read.
 __global__ void k_maxpool_bwd(const float *__restrict__ dout, const int32_t *__restrict__ idx,
                               int batch, int C, int H, int W, int size, int stride, int pad,
-                              int OH, int OW, float *din)
+                              int OH, int OW, float *din, int accumulate)
 {
-    const size_t total = (size_t)batch * C * H * W;
+    const unsigned total = (unsigned)batch * C * H * W;
     const int off = -pad / 2;
-    for (size_t p = blockIdx.x * (size_t)blockDim.x + threadIdx.x; p < total;
-         p += (size_t)gridDim.x * blockDim.x) {
+    for (unsigned p = blockIdx.x * blockDim.x + threadIdx.x; p < total;
+         p += gridDim.x * blockDim.x) {
         const int w = (int)(p % W);
-        const int h = (int)((p / W) % H);
-        const size_t bc = p / ((size_t)W * H);
+        const unsigned r = p / W;
+        const int h = (int)(r % H);
+        const int bc = (int)(r / H);
         // output row i covers rows off + i*stride .. + size-1
         int i0 = floor_div(h - off - size, stride) + 1, i1 = floor_div(h - off, stride);
         int j0 = floor_div(w - off - size, stride) + 1, j1 = floor_div(w - off, stride);
         i0 = max(i0, 0); j0 = max(j0, 0);
         i1 = min(i1, OH - 1); j1 = min(j1, OW - 1);
-        float v = din[p];
-        const size_t obase = bc * OH * OW;
+        float v = accumulate ? din[p] : 0.f;
+        const int obase = bc * OH * OW;
         for (int i = i0; i <= i1; ++i)
             for (int j = j0; j <= j1; ++j) {
-                const size_t o = obase + (size_t)i * OW + j;
+                const int o = obase + i * OW + j;
                 if (idx[o] == (int32_t)p) v += dout[o];
             }
         din[p] = v;
+    }
+}
+
+// Backward of k_maxpool2_fwd: every input pixel lies in exactly one window.
+__device__ __forceinline__ float pick(float v, int p, int ix, float d)
+{
+    return ix == p ? v + d : v;
+}
+
+__global__ void __launch_bounds__(256) k_maxpool2_bwd(const float *__restrict__ dout,
+                                                      const int32_t *__restrict__ idx, int H,
+                                                      int W, unsigned pairs, float *din,
+                                                      int accumulate)
+{
+    const int OW2 = W >> 2, OH = H >> 1;
+    for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < pairs;
+         t += gridDim.x * blockDim.x) {
+        const int jp = (int)(t % OW2);
+        const unsigned r = t / OW2;
+        const int i = (int)(r % OH);
+        const int bc = (int)(r / OH);
+        const int i0 = (bc * H + 2 * i) * W + 4 * jp;
+        const float2 d = reinterpret_cast<const float2 *>(dout)[t];
+        const int2 ix = reinterpret_cast<const int2 *>(idx)[t];
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (accumulate) {
+            a = *reinterpret_cast<const float4 *>(din + i0);
+            b = *reinterpret_cast<const float4 *>(din + i0 + W);
+        }
+        a.x = pick(a.x, i0, ix.x, d.x);         a.y = pick(a.y, i0 + 1, ix.x, d.x);
+        b.x = pick(b.x, i0 + W, ix.x, d.x);     b.y = pick(b.y, i0 + W + 1, ix.x, d.x);
+        a.z = pick(a.z, i0 + 2, ix.y, d.y);     a.w = pick(a.w, i0 + 3, ix.y, d.y);
+        b.z = pick(b.z, i0 + W + 2, ix.y, d.y); b.w = pick(b.w, i0 + W + 3, ix.y, d.y);
+        *reinterpret_cast<float4 *>(din + i0) = a;
+        *reinterpret_cast<float4 *>(din + i0 + W) = b;
     }
 }
 
@@ -527,11 +633,28 @@ static bool pool_ok(int batch, int c, int h, int w, int size, int stride, int pa
     return ach_maxpool_out(h, size, stride, pad) > 0 && ach_maxpool_out(w, size, stride, pad) > 0;
 }
 
+// the 2x2 / stride-2 fast path applies when the window offset is 0 and
+// every window lies inside the image
+static bool pool2_fast(const void *a, const void *b, int h, int w, int size, int stride, int pad,
+                       int OH, int OW)
+{
+    return size == 2 && stride == 2 && pad / 2 == 0 && (h & 1) == 0 && (w & 3) == 0 &&
+           OH == h / 2 && OW == w / 2 &&
+           ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+}
+
 int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, int stride,
                     int pad, float *out, int32_t *idx, ach_stream_t s)
 {
     if (!in || !out || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
+    if (pool2_fast(in, out, h, w, size, stride, pad, OH, OW) &&
+        (reinterpret_cast<uintptr_t>(idx) & 7) == 0) {
+        const unsigned pairs = (unsigned)((size_t)batch * c * OH * OW / 2);
+        hipLaunchKernelGGL(k_maxpool2_fwd, dim3(grid_for(pairs, 256, 256u * 64u)), dim3(256), 0,
+                           as_stream(s), in, h, w, pairs, out, idx);
+        return check_launch();
+    }
     const size_t tot = (size_t)batch * c * OH * OW;
     hipLaunchKernelGGL(k_maxpool_fwd, dim3(grid_for(tot, 256, 256u * 64u)), dim3(256), 0,
                        as_stream(s), in, batch, c, h, w, size, stride, pad, OH, OW, out, idx);
@@ -539,13 +662,22 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
 }
 
 int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
-                    int size, int stride, int pad, float *din, ach_stream_t s)
+                    int size, int stride, int pad, float *din, int accumulate, ach_stream_t s)
 {
     if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
+    const int acc = accumulate ? 1 : 0;
+    if (pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
+        (reinterpret_cast<uintptr_t>(idx) & 7) == 0) {
+        const unsigned pairs = (unsigned)((size_t)batch * c * OH * OW / 2);
+        hipLaunchKernelGGL(k_maxpool2_bwd, dim3(grid_for(pairs, 256, 256u * 64u)), dim3(256), 0,
+                           as_stream(s), dout, idx, h, w, pairs, din, acc);
+        return check_launch();
+    }
     const size_t tot = (size_t)batch * c * h * w;
     hipLaunchKernelGGL(k_maxpool_bwd, dim3(grid_for(tot, 256, 256u * 64u)), dim3(256), 0,
-                       as_stream(s), dout, idx, batch, c, h, w, size, stride, pad, OH, OW, din);
+                       as_stream(s), dout, idx, batch, c, h, w, size, stride, pad, OH, OW, din,
+                       acc);
     return check_launch();
 }
 

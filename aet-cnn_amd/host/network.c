@@ -246,8 +246,10 @@ static int maxpool_forward(an_network *net, an_layer *l, an_state st)
 static int maxpool_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
+    /* the only contribution to the previous delta, which the reference
+     * zeroes in forward: write the sums instead of adding to zeros */
     return ach_maxpool_bwd(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size, l->stride,
-                           l->pad, st.delta, net->stream);
+                           l->pad, st.delta, 0, net->stream);
 }
 
 int an_add_maxpool(an_network *net, int size, int stride, int padding)
@@ -476,10 +478,12 @@ int an_finalize(an_network *net)
     an_layer *last = net->layers[net->n - 1];
     net->classes = last->outputs;
     /* deltas the next layer accumulates into (+=) must start at zero:
-     * maxpool / avgpool / softmax backward add into their input delta.    */
+     * avgpool / softmax backward add into their input delta.  Max-pool
+     * backward writes its input delta outright (accumulate = 0), which is
+     * the same as adding to the zeroed buffer.                             */
     for (int i = 1; i < net->n; ++i) {
         an_layer *l = net->layers[i];
-        if (l->type == AN_MAXPOOL || l->type == AN_AVGPOOL || l->type == AN_SOFTMAX) {
+        if (l->type == AN_AVGPOOL || l->type == AN_SOFTMAX) {
             int j = i - 1;
             while (j > 0 && net->layers[j]->shares_prev) --j;
             net->layers[j]->zero_delta = 1;

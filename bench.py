@@ -175,6 +175,91 @@ def roofline_phase(aetcnn, batch, reps):
                 shape=f"{ci}->{co}@{hw}x{hw} k{k} b{batch}", flop=flop, ms=ms, reps=reps)
 
 
+BW_SHAPE = (512, 128, 32, 32)  # config 2: x ~ N(0,1), S = 256 MiB per tensor
+SGD_PARAMS = 60_000_000        # config 2: SGD over a 60 M-parameter flat buffer
+
+
+def bandwidth_phase(aetcnn, reps):
+    """Config 2: the HBM-bound ops on [512][128][32][32] fp32.  Each op is
+    launched `reps` times back to back on its own stream between HIP events;
+    algorithmic bytes are the minimum traffic the semantics require (BN
+    forward 3S with the pre-BN tensor kept, BN backward 5S with x_norm
+    recomputed, leaky 2S / 3S, 2x2 max-pool 1.5S each way, SGD 16 bytes per
+    parameter); softmax + cross-entropy on 512 x 1000 is reported in us."""
+    ops = aetcnn.ops()
+    D = aetcnn.DeviceArray
+    B, Cc, H, W = BW_SHAPE
+    n = B * Cc * H * W
+    S = 4.0 * n
+    HW = H * W
+    stream = C.c_void_p()
+    aetcnn.check(ops.ach_stream_create(C.byref(stream)), "stream")
+    rng = np.random.default_rng(2)
+    x = D.from_numpy(rng.standard_normal(n, dtype=np.float32))
+    delta0 = rng.standard_normal(n, dtype=np.float32)
+    delta = D.from_numpy(delta0)
+    out = D(n)
+    chan = [D.from_numpy(np.full(Cc, v, np.float32)) for v in (1.0, 0.0, 0, 0, 0, 0, 0)]
+    scales, biases, mean, var, rmean, rvar, supd = chan
+    wsz = ops.ach_bn_workspace(B, Cc, HW)
+    ws = D(wsz // 4 + 64)
+    OH, OW = H // 2, W // 2
+    pout = D(B * Cc * OH * OW)
+    pidx = D(B * Cc * OH * OW, np.int32)
+    pdelta = D.from_numpy(rng.standard_normal(B * Cc * OH * OW, dtype=np.float32))
+    LEAKY, LINEAR = aetcnn.LEAKY, aetcnn.LINEAR
+    rows = []
+
+    def run(name, fn, nbytes):
+        ms = time_launch(ops, stream, fn, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append(dict(op=name, ms=round(ms, 5), algorithmic_bytes=nbytes,
+                         gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
+
+    chk = aetcnn.check
+    run("bn_fwd (stats + normalize, pre-BN tensor kept)",
+        lambda: chk(ops.ach_bn_train_fwd_from_x(x.ptr, out.ptr, B, Cc, HW, scales.ptr, biases.ptr,
+                                                mean.ptr, var.ptr, rmean.ptr, rvar.ptr, LINEAR,
+                                                ws.ptr, wsz, stream)), 3 * S)
+    run("bn_bwd (x_norm recomputed)",
+        lambda: chk(ops.ach_bn_bwd(delta.ptr, B, Cc, HW, x.ptr, None, mean.ptr, var.ptr,
+                                   scales.ptr, biases.ptr, supd.ptr, None, None, LINEAR, ws.ptr,
+                                   wsz, stream)), 5 * S)
+    run("leaky_fwd", lambda: chk(ops.ach_activate(out.ptr, n, LEAKY, stream)), 2 * S)
+    run("leaky_bwd", lambda: chk(ops.ach_gradient(x.ptr, n, LEAKY, delta.ptr, stream)), 3 * S)
+    run("maxpool2x2_fwd",
+        lambda: chk(ops.ach_maxpool_fwd(x.ptr, B, Cc, H, W, 2, 2, 1, pout.ptr, pidx.ptr,
+                                        stream)), 1.5 * S)
+    run("maxpool2x2_bwd",
+        lambda: chk(ops.ach_maxpool_bwd(pdelta.ptr, pidx.ptr, B, Cc, H, W, 2, 2, 1, delta.ptr,
+                                        0, stream)), 1.5 * S)
+    for a in (x, delta, out, ws, pout, pidx, pdelta, *chan):
+        a.free()
+    P = SGD_PARAMS
+    w = D.from_numpy(rng.standard_normal(P, dtype=np.float32) * 0.05)
+    v = D.from_numpy(rng.standard_normal(P, dtype=np.float32) * 0.01)
+    run("sgd_update (60 M params)",
+        lambda: chk(ops.ach_sgd_update(P, w.ptr, v.ptr, -5e-4 * 512, 0.1 / 512, 0.9, stream)),
+        16.0 * P)
+    w.free()
+    v.free()
+    SB, SK = 512, 1000
+    logits = D.from_numpy(rng.standard_normal(SB * SK, dtype=np.float32))
+    truth = np.zeros((SB, SK), np.float32)
+    truth[np.arange(SB), rng.integers(0, SK, SB)] = 1
+    dtruth = D.from_numpy(truth)
+    prob, sdelta, err, cost = D(SB * SK), D(SB * SK), D(SB * SK), D(4)
+    sws = ops.ach_softmax_workspace(SB, 1)
+    swsb = D(sws // 4 + 64)
+    ms = time_launch(ops, stream, lambda: chk(ops.ach_softmax_xent(
+        logits.ptr, SB, SK, 1, 1.0, dtruth.ptr, prob.ptr, sdelta.ptr, err.ptr, cost.ptr,
+        swsb.ptr, sws, stream)), reps)
+    for a in (logits, dtruth, prob, sdelta, err, cost, swsb):
+        a.free()
+    ops.ach_stream_destroy(stream)
+    return rows, round(ms * 1e3, 2)
+
+
 def copy_calibration_phase(aetcnn, nfloats=1 << 26):
     """One ach_scal over a 256 MiB buffer (reads and writes exactly 256 MiB):
     the reference dispatch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE
@@ -222,6 +307,8 @@ def main():
     ap.add_argument("--sweep-reps", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=20)
+    ap.add_argument("--no-bandwidth", action="store_true")
+    ap.add_argument("--bandwidth-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=3)
@@ -252,6 +339,13 @@ def main():
     if not args.no_sweep:
         sweep_rows, sweep_tflops = sweep_phase(aetcnn, 128, args.sweep_reps)
         log(f"conv sweep fwd+dgrad+wgrad: {sweep_tflops:.2f} TFLOP/s")
+    bw_rows, softmax_us = [], None
+    if not args.no_bandwidth:
+        bw_rows, softmax_us = bandwidth_phase(aetcnn, args.bandwidth_reps)
+        for r in bw_rows:
+            log(f"bandwidth {r['op']}: {r['ms']:.4f} ms, {r['gbs']:.0f} GB/s "
+                f"({100 * r['frac']:.1f}% of HBM)")
+        log(f"softmax+xent 512x1000: {softmax_us} us")
     probe = roofline_phase(aetcnn, 128, args.roofline_reps)
     copy_calibration_phase(aetcnn)
     log(f"roofline probe {probe['shape']}: {probe['ms']:.4f} ms/launch over {probe['reps']}")
@@ -295,6 +389,8 @@ def main():
         "conv_sweep_tflops": None if sweep_tflops is None else round(sweep_tflops, 3),
         "conv_sweep": sweep_rows,
         "loss_first_last": [round(tr["first_loss"], 5), round(tr["loss"], 5)],
+        "bandwidth_ops": {"shape": "x[512][128][32][32] fp32 (config 2)", "ops": bw_rows,
+                          "softmax_xent_512x1000_us": softmax_us},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

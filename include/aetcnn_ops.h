@@ -161,14 +161,18 @@ int ach_gradient(const float *y, size_t n, int activation, float *delta,
  * out size = (in + padding - size)/stride + 1, window offset -padding/2,
  * -FLT_MAX init, strict '>' (first max in row-major scan wins); indexes are
  * global flat input indices.  Backward adds into delta_in in ascending
- * output order, bit-identical to the reference's scatter loop.            */
+ * output order, bit-identical to the reference's scatter loop.  With
+ * accumulate = 0 the sums start from +0 instead of delta_in's contents (the
+ * reference's delta is zeroed in forward, NNetwork.c:388-391), so a caller
+ * whose delta_in is all zeros may skip that zeroing; delta_in is then only
+ * written.                                                                 */
 int ach_maxpool_out(int in, int size, int stride, int padding);
 int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w,
                     int size, int stride, int padding,
                     float *out, int32_t *indexes, ach_stream_t stream);
 int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
                     int batch, int c, int h, int w, int size, int stride, int padding,
-                    float *delta_in, ach_stream_t stream);
+                    float *delta_in, int accumulate, ach_stream_t stream);
 
 /* ---- global average pool (AvgPoolLayer.c:29-46, 73-88) ----------------- */
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out,

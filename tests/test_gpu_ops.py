@@ -269,6 +269,8 @@ def test_activation_bit_exact(gpu, oracle, act):
     (2, 4, 13, 13, 3, 2, 2),
     (3, 2, 7, 9, 2, 1, 1),
     (2, 3, 16, 16, 2, 2, 0),
+    (2, 3, 8, 12, 2, 2, 1),       # 2x2/2 fast path, non-square
+    (1, 2, 6, 6, 2, 2, 1),        # W % 4 != 0: generic kernel
 ])
 def test_maxpool_bit_exact(gpu, oracle, B, Cc, H, W, size, stride, pad):
     rng = np.random.default_rng(H * W + size)
@@ -280,12 +282,21 @@ def test_maxpool_bit_exact(gpu, oracle, B, Cc, H, W, size, stride, pad):
     assert np.array_equal(dout.numpy(), out)
     assert np.array_equal(didx.numpy(), idx)
     g = rng.standard_normal(out.shape).astype(np.float32)
+    g.reshape(-1)[::7] = -0.0  # +0 + -0 must give +0, as on the zeroed reference delta
     din0 = rng.standard_normal(x.shape).astype(np.float32)
     ref = oracle.maxpool_backward(g, idx, din0)
     ddin = dev(din0)
-    check(gpu.ach_maxpool_bwd(dev(g).ptr, didx.ptr, B, Cc, H, W, size, stride, pad, ddin.ptr,
+    dg = dev(g)
+    check(gpu.ach_maxpool_bwd(dg.ptr, didx.ptr, B, Cc, H, W, size, stride, pad, ddin.ptr, 1,
                               None))
     assert np.array_equal(ddin.numpy(), ref)
+    # accumulate = 0: delta_in is written, never read (NaN contents ignored)
+    ref0 = oracle.maxpool_backward(g, idx, np.zeros_like(x))
+    ddin0 = dev(np.full(x.shape, np.nan, np.float32))
+    check(gpu.ach_maxpool_bwd(dg.ptr, didx.ptr, B, Cc, H, W, size, stride, pad, ddin0.ptr, 0,
+                              None))
+    got0 = ddin0.numpy()
+    assert np.array_equal(got0.view(np.uint32), ref0.view(np.uint32))
 
 
 def test_avgpool_bit_exact(gpu, oracle):
