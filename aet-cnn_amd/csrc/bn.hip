@@ -118,16 +118,23 @@ __global__ void __launch_bounds__(BN_NT) k_bn_stats(const float *__restrict__ x,
     double s1 = 0, s2 = 0;
     Walk wk(threadIdx.x, hwv);
     wk.b += b0;
-#pragma unroll 4
-    for (int i = threadIdx.x; i < tot; i += BN_NT) {
-        T v = xv[wk.at(C, c)];
+    for (int i = threadIdx.x; i < tot; i += BN_NT * BN_U) {
+        T v[BN_U];
 #pragma unroll
-        for (int k = 0; k < Elem<VEC>::N; ++k) {
-            const float e = comp(v, k);
-            s1 += (double)e;
-            s2 += (double)(e * e);
+        for (int u = 0; u < BN_U; ++u) {
+            if (i + u * BN_NT < tot) v[u] = xv[wk.at(C, c)];
+            wk.step();
         }
-        wk.step();
+#pragma unroll
+        for (int u = 0; u < BN_U; ++u) {
+            if (i + u * BN_NT >= tot) continue;
+#pragma unroll
+            for (int k = 0; k < Elem<VEC>::N; ++k) {
+                const float e = comp(v[u], k);
+                s1 += (double)e;
+                s2 += (double)(e * e);
+            }
+        }
     }
     const double t1 = block_sum<BN_NT / 64>(s1, sh);
     const double t2 = block_sum<BN_NT / 64>(s2, sh);
@@ -167,7 +174,7 @@ __device__ __forceinline__ float bn_inv(float v)
 template <bool VEC>
 __global__ void __launch_bounds__(BN_NT) k_bn_apply(
     const float *src, float *xcopy, float *xnorm, float *out, int batch, int C, int HW, int hwv,
-    const double *__restrict__ part, int nch, float *__restrict__ mean,
+    int per, const double *__restrict__ part, int nch, float *__restrict__ mean,
     float *__restrict__ variance, float *__restrict__ rmean, float *__restrict__ rvar,
     const float *__restrict__ scales, const float *__restrict__ biases, int act)
 {
@@ -197,31 +204,32 @@ __global__ void __launch_bounds__(BN_NT) k_bn_apply(
     }
     __syncthreads();
     const float mu = sp[0], iv = sp[1], s = scales[c], bb = biases[c];
-    const int tot = batch * hwv;
-    const int i0 = blockIdx.x * (BN_NT * BN_U) + threadIdx.x;
-    Walk wk(i0, hwv);
-    int at[BN_U];
-    T v[BN_U];
+    const int r0 = blockIdx.x * per, r1 = min(batch * hwv, r0 + per);
+    Walk wk(r0 + threadIdx.x, hwv);
+    for (int i = r0 + threadIdx.x; i < r1; i += BN_NT * BN_U) {
+        int at[BN_U];
+        T v[BN_U];
 #pragma unroll
-    for (int u = 0; u < BN_U; ++u) {
-        at[u] = i0 + u * BN_NT < tot ? wk.at(C, c) : -1;
-        wk.step();
-    }
+        for (int u = 0; u < BN_U; ++u) {
+            at[u] = i + u * BN_NT < r1 ? wk.at(C, c) : -1;
+            wk.step();
+        }
 #pragma unroll
-    for (int u = 0; u < BN_U; ++u)
-        if (at[u] >= 0) v[u] = reinterpret_cast<const T *>(src)[at[u]];
+        for (int u = 0; u < BN_U; ++u)
+            if (at[u] >= 0) v[u] = reinterpret_cast<const T *>(src)[at[u]];
 #pragma unroll
-    for (int u = 0; u < BN_U; ++u) {
-        if (at[u] < 0) continue;
-        if (xcopy) reinterpret_cast<T *>(xcopy)[at[u]] = v[u];
-        T n, o;
+        for (int u = 0; u < BN_U; ++u) {
+            if (at[u] < 0) continue;
+            if (xcopy) reinterpret_cast<T *>(xcopy)[at[u]] = v[u];
+            T n, o;
 #pragma unroll
-        for (int k = 0; k < Elem<VEC>::N; ++k) comp(n, k) = (comp(v[u], k) - mu) * iv;
-        if (xnorm) reinterpret_cast<T *>(xnorm)[at[u]] = n;
+            for (int k = 0; k < Elem<VEC>::N; ++k) comp(n, k) = (comp(v[u], k) - mu) * iv;
+            if (xnorm) reinterpret_cast<T *>(xnorm)[at[u]] = n;
 #pragma unroll
-        for (int k = 0; k < Elem<VEC>::N; ++k)
-            comp(o, k) = act_forward(__fmaf_rn(comp(n, k), s, bb), act);
-        reinterpret_cast<T *>(out)[at[u]] = o;
+            for (int k = 0; k < Elem<VEC>::N; ++k)
+                comp(o, k) = act_forward(__fmaf_rn(comp(n, k), s, bb), act);
+            reinterpret_cast<T *>(out)[at[u]] = o;
+        }
     }
 }
 
@@ -258,24 +266,33 @@ __global__ void __launch_bounds__(BN_NT) k_bn_bwd_reduce(
     const int tot = (b1 - b0) * hwv;
     Walk wk(threadIdx.x, hwv);
     wk.b += b0;
-#pragma unroll 2
-    for (int i = threadIdx.x; i < tot; i += BN_NT) {
-        const int at = wk.at(C, c);
-        T xv = reinterpret_cast<const T *>(x)[at];
-        T dv = reinterpret_cast<const T *>(delta)[at];
-        T nv;
-        if (xnorm) nv = reinterpret_cast<const T *>(xnorm)[at];
+    constexpr int RU = BN_U / 2;  // two or three streams per element: half the batch
+    for (int i = threadIdx.x; i < tot; i += BN_NT * RU) {
+        T xv[RU], dv[RU], nv[RU];
 #pragma unroll
-        for (int k = 0; k < Elem<VEC>::N; ++k) {
-            const float xe = comp(xv, k);
-            const float g = bwd_grad(comp(dv, k), xe, mu, iv, s, bb, act);
-            const float xn = xnorm ? comp(nv, k) : (xe - mu) * iv;
-            const float gs = g * s;
-            g1 += (double)(g * xn);
-            g2 += (double)gs;
-            g3 += (double)(gs * (xe - mu));
+        for (int u = 0; u < RU; ++u) {
+            if (i + u * BN_NT < tot) {
+                const int at = wk.at(C, c);
+                xv[u] = reinterpret_cast<const T *>(x)[at];
+                dv[u] = reinterpret_cast<const T *>(delta)[at];
+                if (xnorm) nv[u] = reinterpret_cast<const T *>(xnorm)[at];
+            }
+            wk.step();
         }
-        wk.step();
+#pragma unroll
+        for (int u = 0; u < RU; ++u) {
+            if (i + u * BN_NT >= tot) continue;
+#pragma unroll
+            for (int k = 0; k < Elem<VEC>::N; ++k) {
+                const float xe = comp(xv[u], k);
+                const float g = bwd_grad(comp(dv[u], k), xe, mu, iv, s, bb, act);
+                const float xn = xnorm ? comp(nv[u], k) : (xe - mu) * iv;
+                const float gs = g * s;
+                g1 += (double)(g * xn);
+                g2 += (double)gs;
+                g3 += (double)(gs * (xe - mu));
+            }
+        }
     }
     const double t1 = block_sum<BN_NT / 64>(g1, sh);
     const double t2 = block_sum<BN_NT / 64>(g2, sh);
@@ -294,7 +311,7 @@ __global__ void __launch_bounds__(BN_NT) k_bn_bwd_reduce(
 template <bool VEC>
 __global__ void __launch_bounds__(BN_NT) k_bn_bwd_apply(
     float *__restrict__ delta, const float *__restrict__ x, int batch, int C, int HW, int hwv,
-    const double *__restrict__ part, int nch, const float *__restrict__ mean,
+    int per, const double *__restrict__ part, int nch, const float *__restrict__ mean,
     const float *__restrict__ variance, const float *__restrict__ scales,
     const float *__restrict__ biases, int act, float *__restrict__ scale_updates,
     float *__restrict__ mean_delta, float *__restrict__ variance_delta)
@@ -328,34 +345,35 @@ __global__ void __launch_bounds__(BN_NT) k_bn_bwd_apply(
     const double k0 = coef[0], k1 = coef[1], k2 = coef[2];
     const float mu = mean[c], iv = bn_inv(variance[c]), s = scales[c];
     const float bb = biases ? biases[c] : 0.f;
-    const int tot = batch * hwv;
-    const int i0 = blockIdx.x * (BN_NT * BN_U) + threadIdx.x;
-    Walk wk(i0, hwv);
-    int at[BN_U];
-    T dv[BN_U], xv[BN_U];
+    const int r0 = blockIdx.x * per, r1 = min(batch * hwv, r0 + per);
+    Walk wk(r0 + threadIdx.x, hwv);
+    for (int i = r0 + threadIdx.x; i < r1; i += BN_NT * BN_U) {
+        int at[BN_U];
+        T dv[BN_U], xv[BN_U];
 #pragma unroll
-    for (int u = 0; u < BN_U; ++u) {
-        at[u] = i0 + u * BN_NT < tot ? wk.at(C, c) : -1;
-        wk.step();
-    }
-#pragma unroll
-    for (int u = 0; u < BN_U; ++u)
-        if (at[u] >= 0) {
-            dv[u] = reinterpret_cast<const T *>(delta)[at[u]];
-            xv[u] = reinterpret_cast<const T *>(x)[at[u]];
+        for (int u = 0; u < BN_U; ++u) {
+            at[u] = i + u * BN_NT < r1 ? wk.at(C, c) : -1;
+            wk.step();
         }
 #pragma unroll
-    for (int u = 0; u < BN_U; ++u) {
-        if (at[u] < 0) continue;
-        T o;
+        for (int u = 0; u < BN_U; ++u)
+            if (at[u] >= 0) {
+                dv[u] = reinterpret_cast<const T *>(delta)[at[u]];
+                xv[u] = reinterpret_cast<const T *>(x)[at[u]];
+            }
 #pragma unroll
-        for (int k = 0; k < Elem<VEC>::N; ++k) {
-            const float xe = comp(xv[u], k);
-            const float g = bwd_grad(comp(dv[u], k), xe, mu, iv, s, bb, act);
-            const float gs = g * s;
-            comp(o, k) = (float)((double)gs * k0 + k1 * (double)(xe - mu) + k2);
+        for (int u = 0; u < BN_U; ++u) {
+            if (at[u] < 0) continue;
+            T o;
+#pragma unroll
+            for (int k = 0; k < Elem<VEC>::N; ++k) {
+                const float xe = comp(xv[u], k);
+                const float g = bwd_grad(comp(dv[u], k), xe, mu, iv, s, bb, act);
+                const float gs = g * s;
+                comp(o, k) = (float)((double)gs * k0 + k1 * (double)(xe - mu) + k2);
+            }
+            reinterpret_cast<T *>(delta)[at[u]] = o;
         }
-        reinterpret_cast<T *>(delta)[at[u]] = o;
     }
 }
 
@@ -377,7 +395,7 @@ static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 struct BnPlan {
     bool vec;
-    int hwv, nch, per;
+    int hwv, nch, per, apply_per;
     dim3 reduce_grid, apply_grid;
 };
 
@@ -390,8 +408,15 @@ static BnPlan bn_plan(int batch, int C, int HW, bool vec_ok)
     p.per = (batch + nch - 1) / nch;
     p.nch = (batch + p.per - 1) / p.per;
     p.reduce_grid = dim3(C, p.nch);
-    const int tot = batch * p.hwv;
-    p.apply_grid = dim3((tot + BN_NT * BN_U - 1) / (BN_NT * BN_U), C);
+    // apply: about 4096 blocks in all (a block's channel statistics are
+    // derived once, then it streams a contiguous share of the channel)
+    const int tot = batch * p.hwv, step = BN_NT * BN_U;
+    const int need = (tot + step - 1) / step;
+    int chunks = (4096 + C - 1) / C;
+    if (chunks > need) chunks = need;
+    if (chunks < 1) chunks = 1;
+    p.apply_per = ((tot + chunks - 1) / chunks + step - 1) / step * step;
+    p.apply_grid = dim3((tot + p.apply_per - 1) / p.apply_per, C);
     return p;
 }
 
@@ -418,12 +443,12 @@ static int bn_fwd(const float *src, float *xcopy, float *xnorm, float *out, int 
     if (rc) return rc;
     if (p.vec)
         hipLaunchKernelGGL(k_bn_apply<true>, p.apply_grid, dim3(BN_NT), 0, st, src, xcopy, xnorm,
-                           out, batch, C, HW, p.hwv, part, p.nch, mean, variance, rmean, rvar,
-                           scales, biases, act);
+                           out, batch, C, HW, p.hwv, p.apply_per, part, p.nch, mean, variance,
+                           rmean, rvar, scales, biases, act);
     else
         hipLaunchKernelGGL(k_bn_apply<false>, p.apply_grid, dim3(BN_NT), 0, st, src, xcopy,
-                           xnorm, out, batch, C, HW, p.hwv, part, p.nch, mean, variance, rmean,
-                           rvar, scales, biases, act);
+                           xnorm, out, batch, C, HW, p.hwv, p.apply_per, part, p.nch, mean,
+                           variance, rmean, rvar, scales, biases, act);
     return check_launch();
 }
 
@@ -488,12 +513,12 @@ int ach_bn_bwd(float *delta, int batch, int C, int HW, const float *x, const flo
     if (rc) return rc;
     if (p.vec)
         hipLaunchKernelGGL(k_bn_bwd_apply<true>, p.apply_grid, dim3(BN_NT), 0, st, delta, x,
-                           batch, C, HW, p.hwv, part, p.nch, mean, variance, scales, biases, act,
-                           scale_updates, mean_delta, variance_delta);
+                           batch, C, HW, p.hwv, p.apply_per, part, p.nch, mean, variance, scales,
+                           biases, act, scale_updates, mean_delta, variance_delta);
     else
         hipLaunchKernelGGL(k_bn_bwd_apply<false>, p.apply_grid, dim3(BN_NT), 0, st, delta, x,
-                           batch, C, HW, p.hwv, part, p.nch, mean, variance, scales, biases, act,
-                           scale_updates, mean_delta, variance_delta);
+                           batch, C, HW, p.hwv, p.apply_per, part, p.nch, mean, variance, scales,
+                           biases, act, scale_updates, mean_delta, variance_delta);
     return check_launch();
 }
 

@@ -519,18 +519,32 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
             al.load(k0, ke, ra);
             bl.load(k0, ke, rb);
         }
+        // fragments of k-step kk+2 are read from LDS while the MFMAs of
+        // k-step kk issue, so the LDS latency hides behind the matrix pipe
+        float a[2][TM], b[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[0][i] = As[cur][lrow][wm * (BM / WM) + i * 32 + lcol];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[0][j] = Bs[cur][lrow][wn * (BN / WN) + j * 32 + lcol];
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
-            float a[TM], b[TN];
+            const int s = (kk >> 1) & 1;
+            if (kk + 2 < BK) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) a[i] = As[cur][kk + lrow][wm * (BM / WM) + i * 32 + lcol];
+                for (int i = 0; i < TM; ++i)
+                    a[s ^ 1][i] = As[cur][kk + 2 + lrow][wm * (BM / WM) + i * 32 + lcol];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = Bs[cur][kk + lrow][wn * (BN / WN) + j * 32 + lcol];
+                for (int j = 0; j < TN; ++j)
+                    b[s ^ 1][j] = Bs[cur][kk + 2 + lrow][wn * (BN / WN) + j * 32 + lcol];
+            }
+            // keep the scheduler from sinking those reads below the MFMAs
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][i], b[s][j], acc[i][j],
+                                                                     0, 0, 0);
         }
         if (more) {
             al.template store<LA>(As[cur ^ 1], ra);

@@ -132,7 +132,12 @@ __global__ void __launch_bounds__(256) k_bias_grad(float *updates, const float *
 }
 
 // ---- activations ---------------------------------------------------------------
-// float4 body when x is 16-byte aligned, scalar tail
+// Streaming elementwise kernels: one float4 per thread per grid-stride step
+// (float4 body when the pointers are 16-byte aligned, scalar tail), launched
+// with one thread per float4 up to 2^20 blocks -- measured on MI355X as the
+// fastest shape for two-input streams.
+static unsigned grid_stream(size_t n) { return grid_for((n + 3) / 4, 256, 1u << 20); }
+
 __global__ void k_activate(float *x, size_t n, int act)
 {
     const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
@@ -389,42 +394,68 @@ __global__ void __launch_bounds__(256) k_sum_rows(const float *__restrict__ row_
 }
 
 // ---- dropout -------------------------------------------------------------------------
+__device__ __forceinline__ float drop1(float v, float r, float p, float scale)
+{
+    return (r < p) ? 0.f : v * scale;
+}
+
 __global__ void k_dropout(float *x, size_t n, float p, float scale, uint64_t seed,
                           uint32_t iter, uint32_t layer)
 {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const float r = dropout_uniform(seed, iter, layer, (uint32_t)i);
-        x[i] = (r < p) ? 0.f : x[i] * scale;
+    const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t done = 0;
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        float4 *x4 = reinterpret_cast<float4 *>(x);
+        const size_t n4 = n >> 2;
+        for (size_t i = gid; i < n4; i += stride) {
+            float4 v = x4[i];
+            const uint32_t e = (uint32_t)(i << 2);
+            v.x = drop1(v.x, dropout_uniform(seed, iter, layer, e), p, scale);
+            v.y = drop1(v.y, dropout_uniform(seed, iter, layer, e + 1), p, scale);
+            v.z = drop1(v.z, dropout_uniform(seed, iter, layer, e + 2), p, scale);
+            v.w = drop1(v.w, dropout_uniform(seed, iter, layer, e + 3), p, scale);
+            x4[i] = v;
+        }
+        done = n4 << 2;
     }
+    for (size_t i = done + gid; i < n; i += stride)
+        x[i] = drop1(x[i], dropout_uniform(seed, iter, layer, (uint32_t)i), p, scale);
 }
 
 // ---- SGD ---------------------------------------------------------------------------------
 // v += decay_coef*w; w += lr_coef*v; v *= momentum  (WeightData.c:45-78)
+__device__ __forceinline__ void sgd1(float &a, float &u, float dc, float lc, float mom)
+{
+    u += dc * a;
+    a += lc * u;
+    u *= mom;
+}
+
 __global__ void k_sgd(size_t n, float *__restrict__ w, float *__restrict__ v, float dc,
                       float lc, float mom)
 {
+    const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
-    const size_t n4 = n >> 2;
-    float4 *w4 = reinterpret_cast<float4 *>(w);
-    float4 *v4 = reinterpret_cast<float4 *>(v);
-    const bool vec = ((((uintptr_t)w) | ((uintptr_t)v)) & 15) == 0;
     size_t done = 0;
-    if (vec) {
-        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+    if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(v)) & 15) == 0) {
+        float4 *w4 = reinterpret_cast<float4 *>(w);
+        float4 *v4 = reinterpret_cast<float4 *>(v);
+        const size_t n4 = n >> 2;
+        for (size_t i = gid; i < n4; i += stride) {
             float4 a = w4[i], u = v4[i];
-            u.x += dc * a.x; u.y += dc * a.y; u.z += dc * a.z; u.w += dc * a.w;
-            a.x += lc * u.x; a.y += lc * u.y; a.z += lc * u.z; a.w += lc * u.w;
-            u.x *= mom; u.y *= mom; u.z *= mom; u.w *= mom;
+            sgd1(a.x, u.x, dc, lc, mom); sgd1(a.y, u.y, dc, lc, mom);
+            sgd1(a.z, u.z, dc, lc, mom); sgd1(a.w, u.w, dc, lc, mom);
             w4[i] = a;
             v4[i] = u;
         }
-        done = n4 * 4;
+        done = n4 << 2;
     }
-    for (size_t i = done + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        float u = v[i] + dc * w[i];
-        w[i] += lc * u;
-        v[i] = u * mom;
+    for (size_t i = done + gid; i < n; i += stride) {
+        float a = w[i], u = v[i];
+        sgd1(a, u, dc, lc, mom);
+        w[i] = a;
+        v[i] = u;
     }
 }
 
@@ -604,7 +635,7 @@ int ach_activate(float *x, size_t n, int act, ach_stream_t s)
     if (act == ACH_LINEAR || n == 0) return ACH_OK;  // IOData.c:68-69: LINEAR is skipped
     if (!x) return ACH_EINVAL;
     if (act != ACH_LEAKY && act != ACH_RELU && act != ACH_LOGISTIC) return ACH_EUNSUPPORTED;
-    hipLaunchKernelGGL(k_activate, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), x, n, act);
+    hipLaunchKernelGGL(k_activate, dim3(grid_stream(n)), dim3(256), 0, as_stream(s), x, n, act);
     return check_launch();
 }
 
@@ -614,7 +645,7 @@ int ach_gradient(const float *y, size_t n, int act, float *d, ach_stream_t s)
     if (!y || !d) return ACH_EINVAL;
     if (act == ACH_LINEAR) return ACH_OK;  // linear_gradient == 1
     if (act != ACH_LEAKY && act != ACH_RELU && act != ACH_LOGISTIC) return ACH_EUNSUPPORTED;
-    hipLaunchKernelGGL(k_gradient, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), y, n, act,
+    hipLaunchKernelGGL(k_gradient, dim3(grid_stream(n)), dim3(256), 0, as_stream(s), y, n, act,
                        d);
     return check_launch();
 }
@@ -733,7 +764,7 @@ int ach_dropout_fwd(float *x, size_t n, float p, uint64_t seed, uint32_t iter, u
     if (n == 0) return ACH_OK;
     if (!x || !(p >= 0.f && p < 1.f) || n > 0xffffffffull) return ACH_EINVAL;
     const float scale = (float)(1. / (1.0 - p));
-    hipLaunchKernelGGL(k_dropout, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(s), x, n, p,
+    hipLaunchKernelGGL(k_dropout, dim3(grid_stream(n)), dim3(256), 0, as_stream(s), x, n, p,
                        scale, seed, iter, layer);
     return check_launch();
 }
@@ -748,7 +779,7 @@ int ach_sgd_update(size_t n, float *w, float *v, float dc, float lc, float mom, 
 {
     if (n == 0) return ACH_OK;
     if (!w || !v) return ACH_EINVAL;
-    hipLaunchKernelGGL(k_sgd, dim3(grid_for((n + 3) / 4, 256, 256u * 32u)), dim3(256), 0,
+    hipLaunchKernelGGL(k_sgd, dim3(grid_stream(n)), dim3(256), 0,
                        as_stream(s), n, w, v, dc, lc, mom);
     return check_launch();
 }

@@ -89,6 +89,29 @@ def time_launch(ops, stream, fn, reps):
     return ms.value / reps
 
 
+def time_launch_cold(ops, stream, fn, reps, flush):
+    """Average time of fn() with the caches flushed before every launch: each
+    launch is bracketed by its own events, and flush() (an untimed pass over
+    a buffer larger than the 256 MB last-level cache) runs in between."""
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    ops.ach_event_create(C.byref(e0))
+    ops.ach_event_create(C.byref(e1))
+    fn()  # warm
+    tot = 0.0
+    for _ in range(reps):
+        flush()
+        ops.ach_event_record(e0, stream)
+        fn()
+        ops.ach_event_record(e1, stream)
+        aetcnn_check(ops.ach_stream_sync(stream), "sync")
+        ms = C.c_float()
+        aetcnn_check(ops.ach_event_elapsed_ms(e0, e1, C.byref(ms)), "event")
+        tot += ms.value
+    ops.ach_event_destroy(e0)
+    ops.ach_event_destroy(e1)
+    return tot / reps
+
+
 def aetcnn_check(rc, what):
     import aetcnn
     aetcnn.check(rc, what)
@@ -185,7 +208,9 @@ def bandwidth_phase(aetcnn, reps):
     algorithmic bytes are the minimum traffic the semantics require (BN
     forward 3S with the pre-BN tensor kept, BN backward 5S with x_norm
     recomputed, leaky 2S / 3S, 2x2 max-pool 1.5S each way, SGD 16 bytes per
-    parameter); softmax + cross-entropy on 512 x 1000 is reported in us."""
+    parameter); softmax + cross-entropy on 512 x 1000 is reported in us.
+    A 1 GiB buffer is read before every timed launch so that no operand
+    starts in the 256 MB last-level (Infinity) cache."""
     ops = aetcnn.ops()
     D = aetcnn.DeviceArray
     B, Cc, H, W = BW_SHAPE
@@ -209,9 +234,21 @@ def bandwidth_phase(aetcnn, reps):
     pdelta = D.from_numpy(rng.standard_normal(B * Cc * OH * OW, dtype=np.float32))
     LEAKY, LINEAR = aetcnn.LEAKY, aetcnn.LINEAR
     rows = []
+    # cache flush: a read-only reduction over 1 GiB (a write pass would leave
+    # dirty lines whose write-back then competes with the timed launch)
+    flush_n = 1 << 28
+    flush_buf = D(flush_n)
+    flush_buf.zero()
+    flush_out = D(1024)
+    fws = ops.ach_bias_grad_workspace(256, 1024, 1024)
+    flush_ws = D(max(fws, 256) // 4 + 64)
+
+    def flush():
+        aetcnn.check(ops.ach_bias_grad(flush_out.ptr, flush_buf.ptr, 256, 1024, 1024,
+                                       flush_ws.ptr, max(fws, 256), stream), "flush")
 
     def run(name, fn, nbytes):
-        ms = time_launch(ops, stream, fn, reps)
+        ms = time_launch_cold(ops, stream, fn, reps, flush)
         gbs = nbytes / (ms * 1e-3) / 1e9
         rows.append(dict(op=name, ms=round(ms, 5), algorithmic_bytes=nbytes,
                          gbs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4)))
@@ -251,10 +288,10 @@ def bandwidth_phase(aetcnn, reps):
     prob, sdelta, err, cost = D(SB * SK), D(SB * SK), D(SB * SK), D(4)
     sws = ops.ach_softmax_workspace(SB, 1)
     swsb = D(sws // 4 + 64)
-    ms = time_launch(ops, stream, lambda: chk(ops.ach_softmax_xent(
+    ms = time_launch_cold(ops, stream, lambda: chk(ops.ach_softmax_xent(
         logits.ptr, SB, SK, 1, 1.0, dtruth.ptr, prob.ptr, sdelta.ptr, err.ptr, cost.ptr,
-        swsb.ptr, sws, stream)), reps)
-    for a in (logits, dtruth, prob, sdelta, err, cost, swsb):
+        swsb.ptr, sws, stream)), reps, flush)
+    for a in (logits, dtruth, prob, sdelta, err, cost, swsb, flush_buf, flush_out, flush_ws):
         a.free()
     ops.ach_stream_destroy(stream)
     return rows, round(ms * 1e3, 2)
@@ -308,6 +345,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--no-bandwidth", action="store_true")
+    ap.add_argument("--bandwidth-only", action="store_true",
+                    help="run only the config-2 bandwidth ops and print their rows")
     ap.add_argument("--bandwidth-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
@@ -326,6 +365,11 @@ def main():
         print("bench.py: no HIP device", file=sys.stderr)
         sys.exit(1)
     aetcnn.check(ops.ach_set_device(0), "set_device")
+
+    if args.bandwidth_only:
+        rows, softmax_us = bandwidth_phase(aetcnn, args.bandwidth_reps)
+        print(json.dumps({"bandwidth_ops": rows, "softmax_xent_512x1000_us": softmax_us}))
+        return
 
     log(f"training phase: {args.config} b128, warmup {args.warmup}, steps {args.steps}")
     tr = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None)
