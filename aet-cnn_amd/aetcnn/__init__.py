@@ -116,6 +116,8 @@ _NET = {
     "an_finalize": (_i, [_vp]),
     "an_free": (None, [_vp]),
     "an_parse_cfg": (_vp, [C.c_char_p]),
+    "an_save_weights": (_i, [_vp, C.c_char_p]),
+    "an_load_weights": (_i, [_vp, C.c_char_p]),
     "an_stream": (_vp, [_vp]),
     "an_set_input": (_i, [_vp, _vp, _vp]),
     "an_set_input_device": (_i, [_vp, _vp, _vp]),
@@ -372,6 +374,20 @@ class Network:
 
     def conv_gflop(self) -> float:
         return self.lib.an_step_conv_gflop(self.h)
+
+    def save_weights(self, path: str):
+        """darknet .weights file (NNetwork.saveWeightsUpto, NNetwork.c:113-146)"""
+        check(self.lib.an_save_weights(self.h, os.fsencode(path)), "an_save_weights")
+
+    def load_weights(self, path: str):
+        """darknet .weights file (NNetwork.loadWeights, NNetwork.c:64-110)"""
+        check(self.lib.an_load_weights(self.h, os.fsencode(path)), "an_load_weights")
+
+    def seen(self) -> int:
+        return self.lib.an_seen(self.h)
+
+    def iteration(self) -> int:
+        return self.lib.an_iteration(self.h)
 
     def close(self):
         if self.h:

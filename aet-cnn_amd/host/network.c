@@ -788,3 +788,119 @@ double an_step_conv_gflop(const an_network *net)
     }
     return tot / 1e9;
 }
+
+/* ======================================================================== */
+/* Darknet .weights files (NNetwork.loadWeights / saveWeightsUpto,
+ * NNetwork.c:64-151; per layer ConvolutionalLayer.saveWeights / loadWeights,
+ * ConvolutionalLayer.c:422-486).  Little-endian:
+ *   int32 major = 0, minor = 2, revision = 5; uint64 seen;
+ *   for each convolutional layer in order:
+ *     biases[n], (batch_normalize: scales[n], rolling_mean[n],
+ *     rolling_variance[n]), weights[nweights]  (float32 each)
+ * seen = iteration * batch * subdivisions (subdivisions = 1 here).        */
+
+/* one conv layer's parameter arrays in file order */
+static int conv_param_arrays(an_layer *l, float **ptr, size_t *cnt)
+{
+    int k = 0;
+    ptr[k] = l->biases; cnt[k++] = (size_t)l->n;
+    if (l->batch_normalize) {
+        ptr[k] = l->scales; cnt[k++] = (size_t)l->n;
+        ptr[k] = l->rolling_mean; cnt[k++] = (size_t)l->n;
+        ptr[k] = l->rolling_variance; cnt[k++] = (size_t)l->n;
+    }
+    ptr[k] = l->weights; cnt[k++] = (size_t)l->nweights;
+    return k;
+}
+
+int an_save_weights(an_network *net, const char *path)
+{
+    if (!net || !net->finalized || !path) return ACH_EINVAL;
+    FILE *fp = fopen(path, "wb");
+    if (!fp) {
+        fprintf(stderr, "an_save_weights: cannot open %s\n", path);
+        return ACH_EINVAL;
+    }
+    const int32_t hdr[3] = {0, 2, 5};
+    const uint64_t seen = (uint64_t)net->cur_iteration * (uint64_t)net->batch;
+    int rc = ACH_OK;
+    if (fwrite(hdr, sizeof(int32_t), 3, fp) != 3 || fwrite(&seen, sizeof(seen), 1, fp) != 1)
+        rc = ACH_EINVAL;
+    float *host = NULL;
+    size_t host_cap = 0;
+    for (int i = 0; i < net->n && rc == ACH_OK; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        float *ptr[5];
+        size_t cnt[5];
+        const int na = conv_param_arrays(l, ptr, cnt);
+        for (int a = 0; a < na && rc == ACH_OK; ++a) {
+            if (cnt[a] > host_cap) {
+                float *nh = (float *)realloc(host, cnt[a] * sizeof(float));
+                if (!nh) { rc = ACH_EINVAL; break; }
+                host = nh;
+                host_cap = cnt[a];
+            }
+            rc = ach_memcpy_d2h(host, ptr[a], cnt[a] * sizeof(float), net->stream);
+            if (rc == ACH_OK && fwrite(host, sizeof(float), cnt[a], fp) != cnt[a])
+                rc = ACH_EINVAL;
+        }
+    }
+    free(host);
+    if (fclose(fp) != 0 && rc == ACH_OK) rc = ACH_EINVAL;
+    return rc;
+}
+
+/* Reads as the reference does: a version >= 0.2 header carries a 64-bit
+ * seen (older files none); layers are filled in order until the file ends,
+ * a short array keeps the values it read (the rest unchanged) with a
+ * warning.  Sets seen and the iteration (seen / batch).                     */
+int an_load_weights(an_network *net, const char *path)
+{
+    if (!net || !net->finalized || !path) return ACH_EINVAL;
+    FILE *fp = fopen(path, "rb");
+    if (!fp) {
+        fprintf(stderr, "an_load_weights: cannot open %s\n", path);
+        return ACH_EINVAL;
+    }
+    int32_t hdr[3];
+    if (fread(hdr, sizeof(int32_t), 3, fp) != 3) {
+        fclose(fp);
+        return ACH_EINVAL;
+    }
+    if (hdr[0] * 10 + hdr[1] >= 2) {
+        uint64_t seen = 0;
+        if (fread(&seen, sizeof(seen), 1, fp) != 1) {
+            fclose(fp);
+            return ACH_EINVAL;
+        }
+        net->seen = seen;
+    }
+    net->cur_iteration = (int)(net->seen / (uint64_t)net->batch);
+    int rc = ACH_OK;
+    float *host = NULL;
+    size_t host_cap = 0;
+    for (int i = 0; i < net->n && rc == ACH_OK && !feof(fp); ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        float *ptr[5];
+        size_t cnt[5];
+        const int na = conv_param_arrays(l, ptr, cnt);
+        for (int a = 0; a < na && rc == ACH_OK; ++a) {
+            if (cnt[a] > host_cap) {
+                float *nh = (float *)realloc(host, cnt[a] * sizeof(float));
+                if (!nh) { rc = ACH_EINVAL; break; }
+                host = nh;
+                host_cap = cnt[a];
+            }
+            const size_t got = fread(host, sizeof(float), cnt[a], fp);
+            if (got > 0 && got < cnt[a])
+                fprintf(stderr, "an_load_weights: unexpected end of weights file at layer %d\n",
+                        i);
+            if (got > 0) rc = ach_memcpy_h2d(ptr[a], host, got * sizeof(float), net->stream);
+        }
+    }
+    free(host);
+    fclose(fp);
+    return rc;
+}

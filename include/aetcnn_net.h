@@ -112,6 +112,15 @@ void an_free(an_network *net);
  * NULL on error (message on stderr).  The network is finalized.            */
 an_network *an_parse_cfg(const char *path);
 
+/* ---- darknet .weights files (NNetwork.c:64-151, ConvolutionalLayer.c:422-486)
+ * header int32 {0, 2, 5} + uint64 seen, then per convolutional layer:
+ * biases, [scales, rolling_mean, rolling_variance if batch_normalize],
+ * weights (float32).  Load accepts older headers without seen and stops
+ * quietly at end of file, as the reference does; it sets seen and the
+ * iteration.  The network must be finalized.                              */
+int an_save_weights(an_network *net, const char *path);
+int an_load_weights(an_network *net, const char *path);
+
 /* ---- training ------------------------------------------------------------- */
 ach_stream_t an_stream(an_network *net);
 /* copy one batch from host buffers into the network's input/truth        */
