@@ -17,7 +17,7 @@ from typing import Optional
 import numpy as np
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_DIR = os.path.join(PKG_DIR, "lib")
+LIB_DIR = os.environ.get("AETCNN_LIB_DIR") or os.path.join(PKG_DIR, "lib")
 
 ACH_OK = 0
 ACH_EINVAL = -1

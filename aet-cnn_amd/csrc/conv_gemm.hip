@@ -107,11 +107,17 @@ struct AWeightsT {
     }
 };
 
-// B for the forward pass with a 3x3 kernel and BK = 18 (two input channels):
-// thread -> column n = n0 + tid%128 and channel half kr = tid/128; its 9
-// rows are (ki, kj) = (i/3, i%3), i = 0..8, all compile-time.
+// B for the forward pass with a 3x3 kernel and BK = 9*CH (CH input channels
+// per k-tile): thread -> column n = n0 + tid%128 and channel group
+// kr = tid/128 (channels kr*CH/2 .. +CH/2-1 of the tile); the 9 rows of a
+// channel are (ki, kj) = (i/3, i%3), i = 0..8, all compile-time.
+#ifndef ACH_FWD_CH
+#define ACH_FWD_CH 2
+#endif
 struct BIm2col3 {
-    static constexpr int BK = 18, RB = 9, PAD = LDP;
+    static constexpr int CH = ACH_FWD_CH, HC = CH / 2;
+    static_assert(CH % 2 == 0, "channel groups split over two thread halves");
+    static constexpr int BK = 9 * CH, RB = 9 * HC, PAD = LDP;
     __amdgpu_buffer_rsrc_t rs;
     int base;      // b*C*H*W + (oh*S-P)*W + (ow*S-P) + kr*H*W
     int HW, W, K, kr;
@@ -131,7 +137,7 @@ struct BIm2col3 {
         const int b = nn / ohw, p = nn - b * ohw;
         const int oh = p / g.OW, ow = p - oh * g.OW;
         const int ihb = oh * g.S - g.P, iwb = ow * g.S - g.P;
-        base = b * g.C * HW + ihb * g.W + iwb + kr * HW;
+        base = b * g.C * HW + ihb * g.W + iwb + kr * HC * HW;
         valid = 0;
 #pragma unroll
         for (int i = 0; i < 9; ++i) {
@@ -142,19 +148,25 @@ struct BIm2col3 {
     }
     __device__ __forceinline__ void load(int k0, int ke, float *rb) const
     {
-        // rows k0 + kr*9 + i all belong to channel c = k0/9 + kr
-        const bool cok = k0 + kr * 9 < ke;
-        const int cb = base + (k0 / 9) * HW;
+        // rows k0 + (kr*HC + j)*9 + i belong to channel k0/9 + kr*HC + j
 #pragma unroll
-        for (int i = 0; i < 9; ++i)
-            rb[i] = bload(rs, boff(cok && ((valid >> i) & 1u), cb + (i / 3) * W + (i % 3)));
+        for (int j = 0; j < HC; ++j) {
+            const bool cok = k0 + (kr * HC + j) * 9 < ke;
+            const int cb = base + (k0 / 9 + j) * HW;
+#pragma unroll
+            for (int i = 0; i < 9; ++i)
+                rb[j * 9 + i] =
+                    bload(rs, boff(cok && ((valid >> i) & 1u), cb + (i / 3) * W + (i % 3)));
+        }
     }
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
     {
         const int nc = threadIdx.x % GBN;
 #pragma unroll
-        for (int i = 0; i < 9; ++i) S[kr * 9 + i][nc] = rb[i];
+        for (int j = 0; j < HC; ++j)
+#pragma unroll
+            for (int i = 0; i < 9; ++i) S[(kr * HC + j) * 9 + i][nc] = rb[j * 9 + i];
     }
 };
 
@@ -702,7 +714,10 @@ static FwdPlan fwd_plan(const ConvGeom &g)
     FwdPlan pl;
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
     pl.bm = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
-    pl.bk = g.KS == 3 ? 18 : 16;
+    // 3x3 layers with a multiple of 256 filters: 256 x 128 tiles (each wave
+    // 128 x 64), measured 2-5% faster on the 256- and 512-filter layers
+    if (M % 256 == 0 && g.KS == 3) pl.bm = 256;
+    pl.bk = g.KS == 3 ? BIm2col3::BK : 16;
     const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + 127) / 128);
     const int ktiles = (K + pl.bk - 1) / pl.bk;
     int s = 1;
@@ -750,6 +765,7 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
     int rc;
     if (pl.bm == 32) rc = fwd_bm<32>(g, pl, x, w, y, part, st);
     else if (pl.bm == 64) rc = fwd_bm<64>(g, pl, x, w, y, part, st);
+    else if (pl.bm == 256) rc = fwd_bm<256>(g, pl, x, w, y, part, st);
     else rc = fwd_bm<128>(g, pl, x, w, y, part, st);
     if (rc || pl.splits == 1) return rc;
     const int M = g.F, N = g.B * g.OH * g.OW;

@@ -30,10 +30,12 @@ SWEEP = [  # config 1: (C_in, C_out, H, k, pad)
     (256, 512, 8, 3, 1), (512, 512, 8, 3, 1), (512, 10, 8, 1, 0),
 ]
 ROOFLINE_SHAPE = (256, 256, 16, 3, 1)  # dominant kernel probe: conv fwd GEMM
-# HBM bytes per launch of the probe kernel, from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE runs scaled by a 256 MiB copy dispatch (profiles/
-# conv_fwd_gemm_darknet_b128.md): 52.8 MB read + 33.6 MB written.
-ROOFLINE_TRAFFIC_BYTES = 86.4e6
+# HBM bytes per probe call (filter transpose + split-K GEMM + split-K
+# reduction), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs scaled by a
+# 256 MiB copy dispatch (profiles/conv_fwd_gemm_darknet_b128.md):
+# GEMM 53.1 MB read + 67.1 MB written, reduction 67.2 + 33.6 MB,
+# transpose 2.4 + 2.4 MB.
+ROOFLINE_TRAFFIC_BYTES = 225.6e6
 
 
 def log(msg):
@@ -171,8 +173,10 @@ def roofline_phase(aetcnn, batch, reps):
     forward (also used for the stride-1 input gradient) -- on one config-3 /
     config-1 layer, launched `reps` times back to back on its own stream with
     HIP events around the run.  Each ach_conv_fwd call is the filter
-    transpose (k_weights_kmajor, ~1% of the time) plus the GEMM; the average
-    here therefore slightly over-states the GEMM's own duration."""
+    transpose (k_weights_kmajor, ~1% of the time), the GEMM (256 x 128
+    tiles, K split in two halves because the 256-tile grid is small) and the
+    fixed-order split-K reduction into NCHW (~6%); the average here is the
+    whole call, so it under-states the GEMM's own rate."""
     ops = aetcnn.ops()
     D = aetcnn.DeviceArray
     ci, co, hw, k, p = ROOFLINE_SHAPE
@@ -194,7 +198,7 @@ def roofline_phase(aetcnn, batch, reps):
     for a in (x, w, y, ws):
         a.free()
     ops.ach_stream_destroy(stream)
-    return dict(kernel="k_mfma_gemm<FwdProblem<128, BIm2col3>> (conv fwd / dgrad implicit GEMM)",
+    return dict(kernel="k_mfma_gemm<FwdProblem<256, BIm2col3>> (conv fwd / dgrad implicit GEMM)",
                 shape=f"{ci}->{co}@{hw}x{hw} k{k} b{batch}", flop=flop, ms=ms, reps=reps)
 
 
@@ -347,10 +351,13 @@ def main():
     ap.add_argument("--no-bandwidth", action="store_true")
     ap.add_argument("--bandwidth-only", action="store_true",
                     help="run only the config-2 bandwidth ops and print their rows")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the roofline probe and the copy calibration dispatch "
+                         "(for rocprofv3 counter passes)")
     ap.add_argument("--bandwidth-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-batch", type=int, default=8)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-batch", type=int, default=128)
+    ap.add_argument("--cpu-steps", type=int, default=4)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -366,6 +373,12 @@ def main():
         sys.exit(1)
     aetcnn.check(ops.ach_set_device(0), "set_device")
 
+    if args.roofline_only:
+        probe = roofline_phase(aetcnn, 128, args.roofline_reps)
+        copy_calibration_phase(aetcnn)
+        print(json.dumps({"roofline_probe_ms": probe["ms"], "kernel": probe["kernel"],
+                          "shape": probe["shape"]}))
+        return
     if args.bandwidth_only:
         rows, softmax_us = bandwidth_phase(aetcnn, args.bandwidth_reps)
         print(json.dumps({"bandwidth_ops": rows, "softmax_xent_512x1000_us": softmax_us}))
