@@ -85,6 +85,7 @@ _OPS = {
                               _vp, _sz, _vp]),
     "ach_bn_train_fwd_from_x": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                                      _vp, _sz, _vp]),
+    "ach_bn_infer": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]),
     "ach_bn_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                         _vp, _sz, _vp]),
     "ach_activate": (_i, [_vp, _sz, _i, _vp]),
@@ -125,6 +126,8 @@ _NET = {
     "an_get_loss": (_i, [_vp, C.POINTER(_f)]),
     "an_train": (_i, [_vp, _vp, _vp, C.POINTER(_f)]),
     "an_forward": (_i, [_vp, _i]),
+    "an_predict": (_i, [_vp, _vp, _vp]),
+    "an_top_k": (None, [_vp, _i, _i, _vp]),
     "an_backward": (_i, [_vp]),
     "an_update": (_i, [_vp]),
     "an_layer_forward": (_i, [_vp, _i, _i]),
@@ -335,6 +338,13 @@ class Network:
     def train_step(self):
         check(self.lib.an_train_step(self.h), "an_train_step")
 
+    def predict(self, x: np.ndarray) -> np.ndarray:
+        """NNetwork.predict: inference forward, returns [batch][classes]"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty((self.batch, self.lib.an_classes(self.h)), np.float32)
+        check(self.lib.an_predict(self.h, x.ctypes.data, out.ctypes.data), "an_predict")
+        return out
+
     def loss(self) -> float:
         v = _f()
         check(self.lib.an_get_loss(self.h, C.byref(v)), "an_get_loss")
@@ -399,3 +409,12 @@ class Network:
             self.close()
         except Exception:
             pass
+
+
+def top_k(a: np.ndarray, k: int) -> np.ndarray:
+    """DnnUtils.topK through the C host library: indices of the k largest
+    values, largest first (ties as the reference's insertion leaves them)."""
+    a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+    idx = np.empty(k, np.int32)
+    net_lib().an_top_k(a.ctypes.data, a.size, k, idx.ctypes.data)
+    return idx

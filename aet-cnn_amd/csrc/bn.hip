@@ -166,44 +166,14 @@ __device__ __forceinline__ float bn_inv(float v)
     return (float)(1.0 / (sqrt((double)v) + (double)1e-6f));
 }
 
-// ---- forward apply ------------------------------------------------------------
-// Wave 0 turns the partials into mean / variance / inv; block 0 of the
-// channel writes mean, variance and the rolling statistics.  Then
-// src: pre-BN tensor; xcopy (optional) gets a copy; xnorm (optional);
-// out = act(xnorm*scale + bias).
+// One block's share [per*blockIdx.x, +per) of channel c's [batch][hwv]
+// range: out = act(((src - mu) * iv) * s + bb); xcopy / xnorm optional.
 template <bool VEC>
-__global__ void __launch_bounds__(BN_NT) k_bn_apply(
-    const float *src, float *xcopy, float *xnorm, float *out, int batch, int C, int HW, int hwv,
-    int per, const double *__restrict__ part, int nch, float *__restrict__ mean,
-    float *__restrict__ variance, float *__restrict__ rmean, float *__restrict__ rvar,
-    const float *__restrict__ scales, const float *__restrict__ biases, int act)
+__device__ __forceinline__ void bn_stream(const float *src, float *xcopy, float *xnorm,
+                                          float *out, int batch, int C, int hwv, int per, int c,
+                                          float mu, float iv, float s, float bb, int act)
 {
     typedef typename Elem<VEC>::T T;
-    __shared__ float sp[2];
-    const int c = blockIdx.y;
-    if (threadIdx.x < 64) {
-        const double S1 = chunk_sum(part, nch, C, c, 2, 0);
-        const double S2 = chunk_sum(part, nch, C, c, 2, 1);
-        if (threadIdx.x == 0) {
-            float m, v;
-            bn_moments(S1, S2, batch, HW, m, v);
-            if (blockIdx.x == 0) {
-                mean[c] = m;
-                variance[c] = v;
-                if (rmean) {
-                    const float keep = .9f, take = .1f;
-                    float r = rmean[c] * keep;
-                    rmean[c] = r + take * m;
-                    r = rvar[c] * keep;
-                    rvar[c] = r + take * v;
-                }
-            }
-            sp[0] = m;
-            sp[1] = bn_inv(v);
-        }
-    }
-    __syncthreads();
-    const float mu = sp[0], iv = sp[1], s = scales[c], bb = biases[c];
     const int r0 = blockIdx.x * per, r1 = min(batch * hwv, r0 + per);
     Walk wk(r0 + threadIdx.x, hwv);
     for (int i = r0 + threadIdx.x; i < r1; i += BN_NT * BN_U) {
@@ -231,6 +201,60 @@ __global__ void __launch_bounds__(BN_NT) k_bn_apply(
             reinterpret_cast<T *>(out)[at[u]] = o;
         }
     }
+}
+
+// ---- forward apply ------------------------------------------------------------
+// Wave 0 turns the partials into mean / variance / inv; block 0 of the
+// channel writes mean, variance and the rolling statistics.  Then
+// src: pre-BN tensor; xcopy (optional) gets a copy; xnorm (optional);
+// out = act(xnorm*scale + bias).
+template <bool VEC>
+__global__ void __launch_bounds__(BN_NT) k_bn_apply(
+    const float *src, float *xcopy, float *xnorm, float *out, int batch, int C, int HW, int hwv,
+    int per, const double *__restrict__ part, int nch, float *__restrict__ mean,
+    float *__restrict__ variance, float *__restrict__ rmean, float *__restrict__ rvar,
+    const float *__restrict__ scales, const float *__restrict__ biases, int act)
+{
+    __shared__ float sp[2];
+    const int c = blockIdx.y;
+    if (threadIdx.x < 64) {
+        const double S1 = chunk_sum(part, nch, C, c, 2, 0);
+        const double S2 = chunk_sum(part, nch, C, c, 2, 1);
+        if (threadIdx.x == 0) {
+            float m, v;
+            bn_moments(S1, S2, batch, HW, m, v);
+            if (blockIdx.x == 0) {
+                mean[c] = m;
+                variance[c] = v;
+                if (rmean) {
+                    const float keep = .9f, take = .1f;
+                    float r = rmean[c] * keep;
+                    rmean[c] = r + take * m;
+                    r = rvar[c] * keep;
+                    rvar[c] = r + take * v;
+                }
+            }
+            sp[0] = m;
+            sp[1] = bn_inv(v);
+        }
+    }
+    __syncthreads();
+    bn_stream<VEC>(src, xcopy, xnorm, out, batch, C, hwv, per, c, sp[0], sp[1], scales[c],
+                   biases[c], act);
+}
+
+// ---- inference ------------------------------------------------------------------
+// NormData.normalizeByRoll (NormData.c:291-326): the rolling statistics
+// replace the batch statistics, inv = 1/(sqrt(rolling_var) + 1e-6) in double.
+template <bool VEC>
+__global__ void __launch_bounds__(BN_NT) k_bn_infer(
+    const float *src, float *out, int batch, int C, int hwv, int per,
+    const float *__restrict__ rmean, const float *__restrict__ rvar,
+    const float *__restrict__ scales, const float *__restrict__ biases, int act)
+{
+    const int c = blockIdx.y;
+    bn_stream<VEC>(src, nullptr, nullptr, out, batch, C, hwv, per, c, rmean[c], bn_inv(rvar[c]),
+                   scales[c], biases[c], act);
 }
 
 // ---- backward ---------------------------------------------------------------
@@ -482,6 +506,26 @@ int ach_bn_train_fwd_from_x(const float *x, float *out, int batch, int c, int sp
     if (!x || x == out) return ACH_EINVAL;
     return bn_fwd(x, nullptr, nullptr, out, batch, c, spatial, scales, biases, mean, variance,
                   rolling_mean, rolling_variance, activation, ws, ws_bytes, as_stream(stream));
+}
+
+int ach_bn_infer(const float *x, float *out, int batch, int c, int spatial,
+                 const float *scales, const float *biases, const float *rolling_mean,
+                 const float *rolling_variance, int activation, ach_stream_t stream)
+{
+    if (!bn_args_ok(batch, c, spatial) || !x || !out || !scales || !biases || !rolling_mean ||
+        !rolling_variance)
+        return ACH_EINVAL;
+    const BnPlan p = bn_plan(batch, c, spatial, aligned16(x) && aligned16(out));
+    hipStream_t st = as_stream(stream);
+    if (p.vec)
+        hipLaunchKernelGGL(k_bn_infer<true>, p.apply_grid, dim3(BN_NT), 0, st, x, out, batch, c,
+                           p.hwv, p.apply_per, rolling_mean, rolling_variance, scales, biases,
+                           activation);
+    else
+        hipLaunchKernelGGL(k_bn_infer<false>, p.apply_grid, dim3(BN_NT), 0, st, x, out, batch, c,
+                           p.hwv, p.apply_per, rolling_mean, rolling_variance, scales, biases,
+                           activation);
+    return check_launch();
 }
 
 int ach_bn_bwd(float *delta, int batch, int C, int HW, const float *x, const float *x_norm,

@@ -141,10 +141,14 @@ static int conv_forward(an_network *net, an_layer *l, an_state st)
         AN_CHECK(ach_conv_fwd(&d, st.input, l->weights, l->x, st.workspace,
                               st.workspace_bytes, s));
         const int act = fusable(l->activation) ? l->activation : ACH_LINEAR;
-        AN_CHECK(ach_bn_train_fwd_from_x(l->x, l->output, l->batch, l->n, spatial, l->scales,
-                                         l->biases, l->mean, l->variance, l->rolling_mean,
-                                         l->rolling_variance, act, st.workspace,
-                                         st.workspace_bytes, s));
+        if (st.train)
+            AN_CHECK(ach_bn_train_fwd_from_x(l->x, l->output, l->batch, l->n, spatial,
+                                             l->scales, l->biases, l->mean, l->variance,
+                                             l->rolling_mean, l->rolling_variance, act,
+                                             st.workspace, st.workspace_bytes, s));
+        else /* forwardNormCPU test branch: normalizeByRoll (NormData.c:291-326) */
+            AN_CHECK(ach_bn_infer(l->x, l->output, l->batch, l->n, spatial, l->scales,
+                                  l->biases, l->rolling_mean, l->rolling_variance, act, s));
         if (!fusable(l->activation))
             AN_CHECK(ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s));
         return ACH_OK;
@@ -611,6 +615,7 @@ int an_forward(an_network *net, int train)
     if (!net || !net->finalized) return ACH_EINVAL;
     an_state st = base_state(net);
     st.train = train;
+    if (!train) st.truth = NULL; /* NNetwork.predict: state.truth = 0 */
     if (train && net->zero_floats)
         AN_CHECK(ach_fill(net->zero_region, net->zero_floats, 0.f, net->stream));
     for (int i = 0; i < net->n; ++i) {
@@ -679,6 +684,38 @@ int an_update(an_network *net)
                             net->stream));
     return ach_sgd_update(net->nbias_total, net->bflat, net->bvflat, 0.f, a2, net->momentum,
                           net->stream);
+}
+
+/* NNetwork.predict (NNetwork.c:411-422): forward with train = 0 (BN on the
+ * rolling statistics, dropout off, no truth) on a host batch; the output of
+ * the last layer (NNetwork.getOutput, NNetwork.c:400-407; this build has no
+ * cost layers), batch x outputs floats, is copied to host_output.          */
+int an_predict(an_network *net, const float *host_input, float *host_output)
+{
+    if (!net || !net->finalized || !host_input || !host_output) return ACH_EINVAL;
+    AN_CHECK(an_set_input(net, host_input, NULL));
+    AN_CHECK(an_forward(net, 0));
+    const an_layer *last = net->layers[net->n - 1];
+    return ach_memcpy_d2h(host_output, last->output,
+                          sizeof(float) * (size_t)last->batch * last->outputs, net->stream);
+}
+
+/* DnnUtils.topK (DnnUtils.c:463-477): indices of the k largest of a[0..n),
+ * largest first (insertion with strict '>', so equal values keep the order
+ * in which the insertion left them, as in the reference).                  */
+void an_top_k(const float *a, int n, int k, int *index)
+{
+    for (int j = 0; j < k; ++j) index[j] = -1;
+    for (int i = 0; i < n; ++i) {
+        int curr = i;
+        for (int j = 0; j < k; ++j) {
+            if (index[j] < 0 || a[curr] > a[index[j]]) {
+                const int t = curr;
+                curr = index[j];
+                index[j] = t;
+            }
+        }
+    }
 }
 
 int an_train_step(an_network *net)

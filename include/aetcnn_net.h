@@ -136,6 +136,14 @@ int an_get_loss(an_network *net, float *loss);
 /* host-buffer convenience: set_input + train_step + get_loss               */
 int an_train(an_network *net, const float *host_input, const float *host_truth, float *loss);
 int an_forward(an_network *net, int train);
+/* NNetwork.predict (NNetwork.c:411-422): inference forward on a host batch
+ * (batch-norm on the rolling statistics, dropout off, no truth); copies the
+ * last layer's output, batch x outputs floats, to host_output.              */
+int an_predict(an_network *net, const float *host_input, float *host_output);
+/* DnnUtils.topK (DnnUtils.c:463-477): the k largest of a[0..n), largest
+ * first (ties ordered as the reference's strict-'>' insertion leaves them);
+ * host-only                                                                 */
+void an_top_k(const float *a, int n, int k, int *index);
 int an_backward(an_network *net);
 int an_update(an_network *net);
 /* one layer with the NetworkState the loops above would give it

@@ -138,6 +138,13 @@ int ach_bn_train_fwd_from_x(const float *x, float *out, int batch, int c, int sp
                             float *rolling_mean, float *rolling_variance,
                             int activation, void *ws, size_t ws_bytes,
                             ach_stream_t stream);
+/* Inference (forwardNormCPU test branch, NLayer.c:155-160 ->
+ * NormData.normalizeByRoll, NormData.c:291-326): out = act(((x - rolling_mean)
+ * * inv) * scales + biases), inv = 1/(sqrt(rolling_variance) + 1e-6) in
+ * double; statistics are not updated.  x may equal out.                    */
+int ach_bn_infer(const float *x, float *out, int batch, int c, int spatial,
+                 const float *scales, const float *biases, const float *rolling_mean,
+                 const float *rolling_variance, int activation, ach_stream_t stream);
 /* Backward (backwardNormCPU NLayer.c:246-278): scale_updates += sum(d*x_norm);
  * d *= scales; mean_delta, variance_delta; d <- normalize_delta.  No beta
  * gradient (the CPU path computes none).  If activation is ACH_LEAKY/RELU the

@@ -877,7 +877,14 @@ static void conv_forward(or_net *net, or_layer *l, or_state st)
     or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad};
     const int spatial = l->out_h * l->out_w;
     or_conv_forward(&s, st.input, l->weights, l->output, net->workspace);
-    if (l->batch_normalize) {
+    if (l->batch_normalize && !st.train) {
+        /* forwardNormCPU, NLayer.c:141-162 (inference branch): normalizeByRoll
+         * copies the pre-BN tensor to x, then normalizes with the rolling
+         * statistics (NormData.c:291-326) */
+        memcpy(l->x, l->output, sizeof(float) * (size_t)l->batch * l->outputs);
+        or_bn_normalize_roll(l->output, l->batch, l->n, spatial, l->rolling_mean,
+                             l->rolling_variance, l->scales, l->biases);
+    } else if (l->batch_normalize) {
         /* forwardNormCPU, NLayer.c:141-162 (train branch) */
         or_bn_mean_var(l->output, l->batch, l->n, spatial, l->mean, l->variance);
         or_bn_roll(l->n, l->mean, l->variance, l->rolling_mean, l->rolling_variance);
@@ -1030,6 +1037,17 @@ void or_net_update(or_net *net)
                        l->bias_updates, l->scales, l->scale_updates, net->batch,
                        net->learning_rate, net->momentum, net->decay);
     }
+}
+
+/* NNetwork.predict (NNetwork.c:411-422): forward with train = 0 and no
+ * truth, then the output of the last non-cost layer (NNetwork.c:400-407),
+ * batch x outputs floats, is copied to `output`.                          */
+void or_net_predict(or_net *net, const float *input, float *output)
+{
+    or_net_load(net, input, NULL);
+    for (int i = 0; i < net->n; ++i) layer_forward(net, &net->layers[i], fwd_state(net, i, 0));
+    const or_layer *last = &net->layers[net->n - 1];
+    memcpy(output, last->output, sizeof(float) * (size_t)last->batch * last->outputs);
 }
 
 float or_net_train(or_net *net, const float *input, const float *truth)

@@ -160,6 +160,9 @@ float or_net_train(or_net *net, const float *input, const float *truth);
 /* forward + backward only (no update)                                       */
 float or_net_forward_backward(or_net *net, const float *input, const float *truth);
 void or_net_update(or_net *net);
+/* NNetwork.predict (NNetwork.c:411-422): inference forward (BN with rolling
+ * statistics, dropout off, no truth); output = last layer's output          */
+void or_net_predict(or_net *net, const float *input, float *output);
 /* per-layer steps with the network's own state (NetworkState of
  * NNetwork.forward/backward): load one batch, then run layer i             */
 void or_net_load(or_net *net, const float *input, const float *truth);

@@ -66,6 +66,7 @@ _SIGS = {
     "or_net_train": (_f, [_vp, _vp, _vp]),
     "or_net_forward_backward": (_f, [_vp, _vp, _vp]),
     "or_net_update": (None, [_vp]),
+    "or_net_predict": (None, [_vp, _vp, _vp]),
     "or_net_load": (None, [_vp, _vp, _vp]),
     "or_net_layer_forward": (None, [_vp, _i, _i]),
     "or_net_layer_backward": (None, [_vp, _i]),
@@ -153,6 +154,16 @@ def bn_forward(out, scales, biases, rolling_mean=None, rolling_var=None):
     bad = lib().or_bn_normalize(P(out), B, Cc, sp, P(mean), P(var), P(f32(scales)), P(f32(biases)),
                                 P(x), P(xn))
     return dict(out=out, mean=mean, var=var, rm=rm, rv=rv, x=x, xn=xn, nan=bad)
+
+
+def bn_normalize_roll(out, rolling_mean, rolling_var, scales, biases):
+    """NormData.normalizeByRoll (inference batch-norm)"""
+    out = f32(out).copy()
+    B, Cc = out.shape[0], out.shape[1]
+    sp = int(np.prod(out.shape[2:]))
+    lib().or_bn_normalize_roll(P(out), B, Cc, sp, P(f32(rolling_mean)), P(f32(rolling_var)),
+                               P(f32(scales)), P(f32(biases)))
+    return out
 
 
 def bn_backward(delta, x, xn, mean, var, scales, scale_updates=None):
@@ -284,6 +295,13 @@ class OracleNet:
 
     def update(self):
         self.L.or_net_update(self.h)
+
+    def predict(self, x):
+        n = self.n_layers()
+        classes = int(np.prod(self.info(n - 1)[1:4]))
+        out = np.empty((self.batch, classes), np.float32)
+        self.L.or_net_predict(self.h, P(f32(x)), P(out))
+        return out
 
     def load(self, x, truth):
         self.L.or_net_load(self.h, P(f32(x)), P(f32(truth)) if truth is not None else None)

@@ -142,3 +142,18 @@ def test_finalize_without_device_fails_loudly():
     net.softmax()
     with pytest.raises(aetcnn.HipError):
         net.finalize()
+
+
+def test_top_k_matches_reference_ranking():
+    """an_top_k (DnnUtils.topK, DnnUtils.c:463-477): the k largest, largest
+    first.  Distinct values: exactly the descending order.  With ties the
+    values are still the k largest, non-increasing, with distinct indices
+    (their relative order is the reference's insertion order)."""
+    rng = np.random.default_rng(4)
+    for n, k in [(10, 1), (10, 5), (1000, 5), (7, 7)]:
+        a = rng.standard_normal(n).astype(np.float32)
+        assert list(aetcnn.top_k(a, k)) == list(np.argsort(-a, kind="stable")[:k]), (n, k)
+        t = rng.integers(0, 6, n).astype(np.float32)  # many ties
+        idx = aetcnn.top_k(t, k)
+        assert len(set(idx.tolist())) == k and idx.min() >= 0
+        assert np.array_equal(t[idx], np.sort(t)[::-1][:k]), (n, k)

@@ -209,3 +209,35 @@ def test_alexnet_step(gpu, oracle):
         l_gpu = net.train(x, truth)
         l_ref = onet.train(x, truth)
         assert abs(l_gpu - l_ref) <= 1e-3 * max(1, abs(l_ref)), (step, l_gpu, l_ref)
+
+
+@pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8)])
+def test_predict_matches_oracle(gpu, oracle, name, batch):
+    """NNetwork.predict (inference: BN on rolling statistics, dropout off):
+    after the oracle trains 3 steps, its parameters and rolling statistics are
+    loaded into the GPU network; class probabilities within 1e-4 and the
+    predicted labels (argmax) identical wherever the top two differ by more
+    than 1e-5."""
+    oracle.lib().or_set_gemm_parallel(1)
+    net, onet = make_pair(oracle, name, batch)
+    for step in range(3):
+        x, truth, _ = configs.synthetic_batch(name, 300 + step, batch)
+        onet.train(x, truth)
+    for i in conv_layers(onet):
+        for code in (2, 4, 6, 8, 9):  # weights, biases, scales, rolling mean / variance
+            v = onet.buffer(i, code)
+            if v is not None and v.size:
+                net.set_buffer(i, code, v)
+    x, _, _ = configs.synthetic_batch(name, 400, batch)
+    p_ref = onet.predict(x)
+    p_gpu = net.predict(x)
+    assert rel_err(p_gpu, p_ref) < TOL
+    top2 = np.sort(p_ref, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 1e-5
+    assert np.array_equal(p_gpu.argmax(1)[clear], p_ref.argmax(1)[clear])
+    for r in range(batch):
+        assert aetcnn.top_k(p_gpu[r], 1)[0] == p_gpu[r].argmax()
+    # inference leaves the training state alone
+    assert net.iteration() == 0
+    net.close()
+    onet.close()

@@ -215,6 +215,24 @@ def test_bn_train_fwd(gpu, oracle, B, Cc, H, W, act):
     assert np.array_equal(d_out2.numpy(), d_out.numpy())
 
 
+@pytest.mark.parametrize("B,Cc,H,W", [(8, 16, 32, 32), (4, 24, 13, 13), (3, 5, 1, 1)])
+@pytest.mark.parametrize("act", [aetcnn.LINEAR, aetcnn.LEAKY, aetcnn.RELU])
+def test_bn_infer(gpu, oracle, B, Cc, H, W, act):
+    """ach_bn_infer vs NormData.normalizeByRoll + activation; in place too."""
+    out, sc, bi, rm, rv = _bn_inputs(B, Cc, H, W, 3 * B + Cc + act)
+    ref = oracle.activate(oracle.bn_normalize_roll(out, rm, rv, sc, bi), act)
+    d_x, d_out = dev(out), D(out.shape)
+    d_sc, d_bi, d_rm, d_rv = dev(sc), dev(bi), dev(rm), dev(rv)
+    check(gpu.ach_bn_infer(d_x.ptr, d_out.ptr, B, Cc, H * W, d_sc.ptr, d_bi.ptr, d_rm.ptr,
+                           d_rv.ptr, act, None))
+    assert rel_err(d_out.numpy(), ref) < 1e-6
+    assert np.array_equal(d_x.numpy(), out)
+    check(gpu.ach_bn_infer(d_x.ptr, d_x.ptr, B, Cc, H * W, d_sc.ptr, d_bi.ptr, d_rm.ptr,
+                           d_rv.ptr, act, None))
+    assert np.array_equal(d_x.numpy(), d_out.numpy())
+    assert np.array_equal(d_rm.numpy(), rm) and np.array_equal(d_rv.numpy(), rv)
+
+
 @pytest.mark.parametrize("B,Cc,H,W", [(8, 16, 32, 32), (4, 24, 13, 13), (128, 32, 8, 8)])
 @pytest.mark.parametrize("act", [aetcnn.LINEAR, aetcnn.LEAKY, aetcnn.RELU])
 def test_bn_bwd(gpu, oracle, B, Cc, H, W, act):

@@ -395,3 +395,47 @@ def test_bn_inference_normalize_closed_form():
     ref = ((x - rm[None, :, None, None]) / (np.sqrt(rv.astype(np.float64)) + 1e-6)[None, :, None, None]
            * sc[None, :, None, None] + bi[None, :, None, None])
     assert rel_err(got, ref) < 1e-6
+
+
+def test_oracle_predict_composes_inference_ops():
+    """or_net_predict (NNetwork.predict, NNetwork.c:411-422) after two training
+    steps equals the hand composition of the oracle's inference ops: conv,
+    batch-norm on the rolling statistics, leaky, max-pool, 1x1 conv + bias,
+    global avg-pool, softmax without truth -- and leaves the state alone."""
+    from aetcnn import configs
+    L = O.lib()
+    L.or_rand_seed(3)
+    B, h, w, c = configs.dims("tiny", 4)
+    net = O.OracleNet(B, h, w, c)
+    configs.build(net, "tiny")
+    net.finalize()
+    for s in range(2):
+        x, truth, _ = configs.synthetic_batch("tiny", 20 + s, B)
+        net.train(x, truth)
+    before = {(i, k): net.buffer(i, k).copy() for i in (0, 2, 4) for k in (2, 4, 8, 9)
+              if net.buffer(i, k) is not None}
+    x, _, _ = configs.synthetic_batch("tiny", 99, B)
+    got = net.predict(x)
+    a = x
+    for i, layer in enumerate(configs.CONFIGS["tiny"]["layers"]):
+        kind = layer[0]
+        if kind == "conv":
+            F, k, st, pad, act, bn = layer[1:]
+            a = O.conv_forward(a, net.buffer(i, 2).reshape(F, -1, k, k), F, k, st, pad)
+            if bn:
+                a = O.bn_normalize_roll(a, net.buffer(i, 8), net.buffer(i, 9),
+                                        net.buffer(i, 6), net.buffer(i, 4))
+            else:
+                a = a + net.buffer(i, 4)[None, :, None, None]
+            a = O.activate(a, act)
+        elif kind == "maxpool":
+            a, _ = O.maxpool_forward(a, *layer[1:])
+        elif kind == "avgpool":
+            a = O.avgpool_forward(a)
+        elif kind == "softmax":
+            a, _, _, _ = O.softmax_xent(a.reshape(B, -1), None)
+    assert np.array_equal(got, a.reshape(got.shape))
+    assert np.allclose(got.sum(axis=1), 1.0, atol=1e-5)
+    for key, v in before.items():
+        assert np.array_equal(net.buffer(*key), v), key
+    net.close()
