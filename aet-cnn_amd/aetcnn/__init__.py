@@ -54,6 +54,9 @@ _OPS = {
     "ach_host_free": (_i, [_vp]),
     "ach_memcpy_h2d": (_i, [_vp, _vp, _sz, _vp]),
     "ach_memcpy_d2h": (_i, [_vp, _vp, _sz, _vp]),
+    "ach_memcpy_h2d_async": (_i, [_vp, _vp, _sz, _vp]),
+    "ach_event_sync": (_i, [_vp]),
+    "ach_stream_wait_event": (_i, [_vp, _vp]),
     "ach_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
     "ach_stream_create": (_i, [C.POINTER(_vp)]),
     "ach_stream_destroy": (_i, [_vp]),
@@ -127,6 +130,12 @@ _NET = {
     "an_train": (_i, [_vp, _vp, _vp, C.POINTER(_f)]),
     "an_forward": (_i, [_vp, _i]),
     "an_predict": (_i, [_vp, _vp, _vp]),
+    "an_feeder_create_cifar": (_vp, [_vp, _vp, _i, _i, _u64, _i, _f]),
+    "an_feeder_create_synthetic": (_vp, [_vp, _i, _u64]),
+    "an_feeder_next": (_i, [_vp]),
+    "an_feeder_served": (_u64, [_vp]),
+    "an_feeder_sample": (_u64, [_u64, _u64, _i, _i]),
+    "an_feeder_free": (None, [_vp]),
     "an_top_k": (None, [_vp, _i, _i, _vp]),
     "an_backward": (_i, [_vp]),
     "an_update": (_i, [_vp]),
@@ -418,3 +427,40 @@ def top_k(a: np.ndarray, k: int) -> np.ndarray:
     idx = np.empty(k, np.int32)
     net_lib().an_top_k(a.ctypes.data, a.size, k, idx.ctypes.data)
     return idx
+
+
+class Feeder:
+    """Input pipeline (an_feeder_*): worker threads fill pinned host batches,
+    next() makes the next one the network's input (copy overlapped with the
+    previous step)."""
+
+    def __init__(self, net: "Network", cifar_files=None, threads: int = 8, seed: int = 0,
+                 flip: bool = False, label_smooth_eps: float = 0.0):
+        self.lib = net_lib()
+        self.net = net
+        if cifar_files:
+            arr = (C.c_char_p * len(cifar_files))(*[os.fsencode(p) for p in cifar_files])
+            self._files = arr
+            self.h = self.lib.an_feeder_create_cifar(net.h, arr, len(cifar_files), threads, seed,
+                                                     int(flip), label_smooth_eps)
+        else:
+            self.h = self.lib.an_feeder_create_synthetic(net.h, threads, seed)
+        if not self.h:
+            raise HipError("an_feeder_create failed (see stderr)")
+
+    def next(self):
+        check(self.lib.an_feeder_next(self.h), "an_feeder_next")
+
+    def served(self) -> int:
+        return self.lib.an_feeder_served(self.h)
+
+    def close(self):
+        if self.h:
+            self.lib.an_feeder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

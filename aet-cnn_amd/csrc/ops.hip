@@ -513,6 +513,13 @@ int ach_memcpy_d2h(void *dst, const void *src, size_t bytes, ach_stream_t s)
     return check(hipStreamSynchronize(as_stream(s)));
 }
 
+int ach_memcpy_h2d_async(void *dst, const void *src, size_t bytes, ach_stream_t s)
+{
+    if (!bytes) return ACH_OK;
+    if (!dst || !src) return ACH_EINVAL;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(s)));
+}
+
 int ach_memcpy_d2d(void *dst, const void *src, size_t bytes, ach_stream_t s)
 {
     if (!bytes) return ACH_OK;
@@ -548,6 +555,18 @@ int ach_event_record(void *ev, ach_stream_t s)
 {
     if (!ev) return ACH_EINVAL;
     return check(hipEventRecord((hipEvent_t)ev, as_stream(s)));
+}
+
+int ach_event_sync(void *ev)
+{
+    if (!ev) return ACH_EINVAL;
+    return check(hipEventSynchronize((hipEvent_t)ev));
+}
+
+int ach_stream_wait_event(ach_stream_t s, void *ev)
+{
+    if (!ev) return ACH_EINVAL;
+    return check(hipStreamWaitEvent(as_stream(s), (hipEvent_t)ev, 0));
 }
 
 int ach_event_elapsed_ms(void *a, void *b, float *ms)

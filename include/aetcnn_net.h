@@ -121,6 +121,29 @@ an_network *an_parse_cfg(const char *path);
 int an_save_weights(an_network *net, const char *path);
 int an_load_weights(an_network *net, const char *path);
 
+/* ---- input pipeline (ImageData.c:20-224, DstbCompute.c:60-216) ------------
+ * Worker threads fill two pinned host batches; an_feeder_next copies the next
+ * one to the device on the feeder's own stream (overlapping the previous
+ * training step), orders the network's stream after it and makes it the
+ * network's input and truth.  Image i of batch k is drawn from a counter-
+ * based hash of (seed, k, i): an_feeder_sample(seed, k, i, 0) % records is
+ * its record, bit 0 of an_feeder_sample(seed, k, i, 1) its horizontal flip
+ * (when enabled).  Truth is one-hot with label smoothing (fillTruthSmooth,
+ * ImageData.c:77-103).  The CIFAR source reads CIFAR-10 binary batches
+ * (1 label byte + 3x32x32 planar RGB bytes per record; pixels / 255) and
+ * needs a 3x32x32 network input; the synthetic source draws pixels uniform
+ * in [0,1) (an_feeder_sample(seed, k, i*inputs + j, 2) >> 40 / 2^24) and
+ * labels an_feeder_sample(seed, k, i, 3) % classes.  Free the feeder before
+ * the network.                                                             */
+typedef struct an_feeder an_feeder;
+an_feeder *an_feeder_create_cifar(an_network *net, const char *const *files, int nfiles,
+                                  int threads, uint64_t seed, int flip, float label_smooth_eps);
+an_feeder *an_feeder_create_synthetic(an_network *net, int threads, uint64_t seed);
+int an_feeder_next(an_feeder *f);
+uint64_t an_feeder_served(const an_feeder *f);
+uint64_t an_feeder_sample(uint64_t seed, uint64_t batch_no, int image, int what);
+void an_feeder_free(an_feeder *f);
+
 /* ---- training ------------------------------------------------------------- */
 ach_stream_t an_stream(an_network *net);
 /* copy one batch from host buffers into the network's input/truth        */

@@ -54,6 +54,8 @@ int ach_host_free(void *ptr);
 int ach_memcpy_h2d(void *dst, const void *src, size_t bytes, ach_stream_t stream);
 int ach_memcpy_d2h(void *dst, const void *src, size_t bytes, ach_stream_t stream);
 int ach_memcpy_d2d(void *dst, const void *src, size_t bytes, ach_stream_t stream);
+/* enqueue only (no synchronisation); truly asynchronous from pinned memory */
+int ach_memcpy_h2d_async(void *dst, const void *src, size_t bytes, ach_stream_t stream);
 int ach_stream_create(ach_stream_t *stream);
 int ach_stream_destroy(ach_stream_t stream);
 int ach_stream_sync(ach_stream_t stream);
@@ -63,6 +65,8 @@ int ach_event_create(void **ev);
 int ach_event_destroy(void *ev);
 int ach_event_record(void *ev, ach_stream_t stream);
 int ach_event_elapsed_ms(void *start, void *stop, float *ms); /* syncs stop */
+int ach_event_sync(void *ev);                         /* host waits for ev */
+int ach_stream_wait_event(ach_stream_t stream, void *ev); /* stream waits for ev */
 
 /* ---- BLAS-1 helpers (mtcs/MtcsTool.c:33-132; NData.setZero NData.c:232) */
 int ach_fill(float *x, size_t n, float value, ach_stream_t stream);
