@@ -39,6 +39,12 @@ constexpr unsigned kOOB = 0x80000000u;  // buffer offset that reads as 0
 #define ACH_WGRAD_BK 16
 #endif
 constexpr int WGRAD_BK = ACH_WGRAD_BK;  // k-tile of the weight-gradient GEMM
+#ifndef ACH_WGRAD_TARGET
+#define ACH_WGRAD_TARGET 2048  // weight-gradient workgroups aimed for (tiles x splits)
+#endif
+#ifndef ACH_WGRAD_BN
+#define ACH_WGRAD_BN 64        // weight-gradient N tile for layers with > 64 filters
+#endif
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, unsigned bytes)
 {
@@ -784,7 +790,7 @@ static void wgrad_split(const ConvGeom &g, int bm, int bn, int &splits, int &kch
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
     const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int bk = WGRAD_BK;
-    int s = (1024 + tiles - 1) / tiles;
+    int s = (ACH_WGRAD_TARGET + tiles - 1) / tiles;
     const int max_s = (K + 4 * bk - 1) / (4 * bk);  // >= 4 k-tiles per split
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
@@ -804,7 +810,8 @@ static int wgrad_bm(const ConvGeom &g)
 }
 static int wgrad_bn(const ConvGeom &g)
 {
-    return (g.C * g.KS * g.KS <= 32 && g.F > 64) ? 32 : 128;
+    if (g.C * g.KS * g.KS <= 32 && g.F > 64) return 32;
+    return g.F > 64 ? ACH_WGRAD_BN : 128;
 }
 
 template <int BM, int BN>
@@ -943,6 +950,9 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
     float *part = (float *)ws;
     int rc;
     if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st);
+#if ACH_WGRAD_BN == 64
+    else if (bn == 64) rc = wgrad_launch<128, 64>(g, x, dy, dw, part, splits, kchunk, st);
+#endif
     else if (bm == 32) rc = wgrad_launch<32, 128>(g, x, dy, dw, part, splits, kchunk, st);
     else if (bm == 64) rc = wgrad_launch<64, 128>(g, x, dy, dw, part, splits, kchunk, st);
     else rc = wgrad_launch<128, 128>(g, x, dy, dw, part, splits, kchunk, st);

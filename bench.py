@@ -75,6 +75,36 @@ def train_phase(aetcnn, configs, name, steps, warmup, batch):
                 gflop_step=gflop, batch=B)
 
 
+def fed_phase(aetcnn, configs, name, steps, warmup, threads):
+    """The same training step fed by the input pipeline (an_feeder, synthetic
+    source, `threads` host workers): a fresh batch per step, its host-to-device
+    copy overlapped with the previous step.  PCIe-inclusive; not `value`."""
+    lib = aetcnn.net_lib()
+    lib.an_rand_seed(1)
+    B, h, w, c = configs.dims(name)
+    net = aetcnn.Network(B, h, w, c)
+    configs.build(net, name)
+    net.finalize()
+    feeder = aetcnn.Feeder(net, threads=threads, seed=3)
+    ops = aetcnn.ops()
+    for _ in range(warmup):
+        feeder.next()
+        net.train_step()
+    ops.ach_device_sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        feeder.next()
+        net.train_step()
+    aetcnn.check(ops.ach_device_sync(), "sync")
+    dt = time.perf_counter() - t0
+    loss = net.loss()
+    feeder.close()
+    net.close()
+    return dict(images_per_s=round(B * steps / dt, 1), ms_per_step=round(dt * 1e3 / steps, 4),
+                threads=threads, loss=round(loss, 5),
+                source="synthetic, a fresh batch per step through pinned double buffers")
+
+
 def time_launch(ops, stream, fn, reps):
     e0, e1 = C.c_void_p(), C.c_void_p()
     ops.ach_event_create(C.byref(e0))
@@ -349,6 +379,8 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--no-bandwidth", action="store_true")
+    ap.add_argument("--no-fed", action="store_true",
+                    help="skip the input-pipeline (PCIe-inclusive) training measurement")
     ap.add_argument("--bandwidth-only", action="store_true",
                     help="run only the config-2 bandwidth ops and print their rows")
     ap.add_argument("--roofline-only", action="store_true",
@@ -391,6 +423,12 @@ def main():
     step_tflops = tr["gflop_step"] / (ms_step * 1e-3) / 1e3
     log(f"{ms_step:.3f} ms/step ({tr['gpu_ms'] / args.steps:.3f} GPU ms), {ips:.1f} img/s, "
         f"conv {step_tflops:.2f} TFLOP/s, loss {tr['first_loss']:.4f} -> {tr['loss']:.4f}")
+
+    fed = None
+    if not args.no_fed:
+        fed = fed_phase(aetcnn, configs, args.config, args.steps, args.warmup, 8)
+        log(f"fed by the input pipeline: {fed['ms_per_step']:.3f} ms/step, "
+            f"{fed['images_per_s']:.1f} img/s")
 
     sweep_rows, sweep_tflops = [], None
     if not args.no_sweep:
@@ -446,6 +484,7 @@ def main():
         "conv_sweep_tflops": None if sweep_tflops is None else round(sweep_tflops, 3),
         "conv_sweep": sweep_rows,
         "loss_first_last": [round(tr["first_loss"], 5), round(tr["loss"], 5)],
+        "input_pipeline": fed,
         "bandwidth_ops": {"shape": "x[512][128][32][32] fp32 (config 2)", "ops": bw_rows,
                           "softmax_xent_512x1000_us": softmax_us},
         "roofline": roofline,
