@@ -64,10 +64,34 @@ __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, int byte_off)
     return __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
 }
 
+// Unsigned division by a runtime constant d: q = (mulhi(n, mul) + n) >> shift
+// with shift = ceil(log2 d), mul = floor(2^32 (2^shift - d) / d) + 1
+// (Granlund & Montgomery 1994), exact for n < 2^31.
+struct FastDiv {
+    unsigned mul, shift, d;
+};
+
+static FastDiv make_fastdiv(unsigned d)
+{
+    FastDiv f;
+    unsigned l = 0;
+    while ((1ull << l) < d) ++l;
+    f.mul = (unsigned)((((1ull << 32) * ((1ull << l) - d)) / d) + 1);
+    f.shift = l;
+    f.d = d;
+    return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv &f)
+{
+    return (int)((__umulhi((unsigned)n, f.mul) + (unsigned)n) >> f.shift);
+}
+
 struct ConvGeom {
     int B, C, H, W;    // input
     int F, KS, S, P;   // filters, kernel, stride, pad
     int OH, OW;
+    FastDiv dkk, dks;  // division by KS*KS and by KS
 };
 
 // ===========================================================================
@@ -183,6 +207,7 @@ struct BIm2colAny {
     static constexpr int BK = 16, RB = 8, PAD = LDP;
     __amdgpu_buffer_rsrc_t rs;
     int xoff, ihb, iwb, kr, ok, H, W, KS;
+    FastDiv dkk, dks;
     __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
                                          int tid)
     {
@@ -193,6 +218,8 @@ struct BIm2colAny {
         H = g.H;
         W = g.W;
         KS = KS_T ? KS_T : g.KS;
+        dkk = g.dkk;
+        dks = g.dks;
         const int ohw = g.OH * g.OW;
         const int nn = ok ? n : 0;
         const int b = nn / ohw, p = nn - b * ohw;
@@ -207,8 +234,15 @@ struct BIm2colAny {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int k = k0 + kr + 2 * i;
-            const int c = k / kk2, t = k - c * kk2;
-            const int ki = t / ks, kj = t - ki * ks;
+            int c, ki;
+            if (KS_T) {
+                c = k / kk2;
+                ki = (k - c * kk2) / ks;
+            } else {  // runtime kernel size: magic-number division
+                c = fdiv(k, dkk);
+                ki = fdiv(k - c * kk2, dks);
+            }
+            const int t = k - c * kk2, kj = t - ki * ks;
             const int ih = ihb + ki, iw = iwb + kj;
             const bool v = ok && k < ke && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
             rb[i] = bload(rs, boff(v, xoff + (c * H + ih) * W + iw));
@@ -223,29 +257,6 @@ struct BIm2colAny {
     }
 };
 
-// ---------------------------------------------------------------------------
-// Unsigned division by a runtime constant d: q = (mulhi(n, mul) + n) >> shift
-// with shift = ceil(log2 d), mul = floor(2^32 (2^shift - d) / d) + 1
-// (Granlund & Montgomery 1994), exact for n < 2^31.
-struct FastDiv {
-    unsigned mul, shift, d;
-};
-
-static FastDiv make_fastdiv(unsigned d)
-{
-    FastDiv f;
-    unsigned l = 0;
-    while ((1ull << l) < d) ++l;
-    f.mul = (unsigned)((((1ull << 32) * ((1ull << l) - d)) / d) + 1);
-    f.shift = l;
-    f.d = d;
-    return f;
-}
-
-__device__ __forceinline__ int fdiv(int n, const FastDiv &f)
-{
-    return (int)((__umulhi((unsigned)n, f.mul) + (unsigned)n) >> f.shift);
-}
 
 // Weight gradient.  k = b*OHW + p runs over the batch and the output plane.
 // A[m][k] = dy[b][m][p]; B[k][n] = x[b][c][oh*S-P+ki][ow*S-P+kj] with
@@ -675,6 +686,8 @@ static ConvGeom geom(const ach_conv_desc *d)
     g.F = d->n; g.KS = d->size; g.S = d->stride; g.P = d->pad;
     g.OH = (d->h + 2 * d->pad - d->size) / d->stride + 1;
     g.OW = (d->w + 2 * d->pad - d->size) / d->stride + 1;
+    g.dkk = make_fastdiv((unsigned)(d->size * d->size));
+    g.dks = make_fastdiv((unsigned)d->size);
     return g;
 }
 
@@ -877,6 +890,7 @@ static ConvGeom dgrad_as_fwd(const ConvGeom &g)
     t.B = g.B; t.C = g.F; t.H = g.OH; t.W = g.OW;
     t.F = g.C; t.KS = g.KS; t.S = 1; t.P = g.KS - 1 - g.P;
     t.OH = g.H; t.OW = g.W;
+    t.dkk = g.dkk; t.dks = g.dks;
     return t;
 }
 

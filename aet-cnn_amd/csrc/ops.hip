@@ -114,21 +114,44 @@ __global__ void k_add_bias(float *out, const float *__restrict__ b, size_t total
 }
 
 // one block per channel; double accumulation; updates[c] += sum
-__global__ void __launch_bounds__(256) k_bias_grad(float *updates, const float *__restrict__ d,
-                                                   int batch, int n, int spatial)
+// Bias gradient (BiasData.calcGrad, BiasData.c:40-57): dbias[c] += sum over
+// images and positions of delta.  Two passes so that every CU works: blocks
+// of (channel, image chunk) write double partial sums, then one thread per
+// channel adds them in chunk order (fixed order, no atomics).
+constexpr int BIAS_IMGS = 8;  // images per partial-sum block
+
+__global__ void __launch_bounds__(256) k_bias_part(const float *__restrict__ d, int batch, int n,
+                                                   int spatial, double *__restrict__ part)
 {
     __shared__ double sh[4];
-    const int c = blockIdx.x;
+    const int c = blockIdx.x, ch = blockIdx.y;
+    const int b0 = ch * BIAS_IMGS, b1 = min(batch, b0 + BIAS_IMGS);
     double s = 0;
-    const int tot = batch * spatial;
-    for (int i = threadIdx.x; i < tot; i += 256) {
-        const int b = i / spatial, q = i - b * spatial;
-        s += d[((size_t)b * n + c) * spatial + q];
+    for (int b = b0; b < b1; ++b) {
+        const float *p = d + ((size_t)b * n + c) * spatial;
+        if ((spatial & 3) == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(p);
+            for (int q = threadIdx.x; q < (spatial >> 2); q += 256) {
+                const float4 v = p4[q];
+                s += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
+            }
+        } else {
+            for (int q = threadIdx.x; q < spatial; q += 256) s += p[q];
+        }
     }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) updates[c] += (float)(sh[0] + sh[1] + sh[2] + sh[3]);
+    if (threadIdx.x == 0) part[(size_t)ch * n + c] = sh[0] + sh[1] + sh[2] + sh[3];
+}
+
+__global__ void k_bias_final(const double *__restrict__ part, int nch, int n, float *updates)
+{
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n) return;
+    double s = 0;
+    for (int ch = 0; ch < nch; ++ch) s += part[(size_t)ch * n + c];
+    updates[c] += (float)s;
 }
 
 // ---- activations ---------------------------------------------------------------
@@ -181,32 +204,32 @@ __global__ void k_gradient(const float *__restrict__ y, size_t n, int act, float
 // ---- max-pool --------------------------------------------------------------------
 // Input element counts are below 2^31 (the indexes are int32), so all index
 // arithmetic is 32-bit.
-__global__ void k_maxpool_fwd(const float *__restrict__ in, int batch, int C, int H, int W,
-                              int size, int stride, int pad, int OH, int OW,
-                              float *__restrict__ out, int32_t *__restrict__ idx)
+template <int SIZE, int STRIDE>
+__global__ void __launch_bounds__(256) k_maxpool_fwd(const float *__restrict__ in, int total,
+                                                     int H, int W, int size_, int stride_,
+                                                     int pad, int OH, int OW,
+                                                     float *__restrict__ out,
+                                                     int32_t *__restrict__ idx)
 {
-    const unsigned total = (unsigned)batch * C * OH * OW;
+    const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
     const int off = -pad / 2;
-    for (unsigned o = blockIdx.x * blockDim.x + threadIdx.x; o < total;
-         o += gridDim.x * blockDim.x) {
-        const int j = (int)(o % OW);
-        const unsigned r = o / OW;
-        const int i = (int)(r % OH);
-        const int bc = (int)(r / OH);
-        float mx = -FLT_MAX;
-        int mi = -1;
-        for (int n = 0; n < size; ++n)
-            for (int m = 0; m < size; ++m) {
-                const int ch = off + i * stride + n, cw = off + j * stride + m;
-                const int index = cw + W * (ch + H * bc);
-                const bool valid = ch >= 0 && ch < H && cw >= 0 && cw < W;
-                const float v = valid ? in[index] : -FLT_MAX;
-                mi = (v > mx) ? index : mi;
-                mx = (v > mx) ? v : mx;
-            }
-        out[o] = mx;
-        if (idx) idx[o] = mi;
-    }
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    if (o >= total) return;
+    const int r = o / OW, j = o - r * OW;
+    const int bc = r / OH, i = r - bc * OH;
+    float mx = -FLT_MAX;
+    int mi = -1;
+    for (int n = 0; n < size; ++n)
+        for (int m = 0; m < size; ++m) {
+            const int ch = off + i * stride + n, cw = off + j * stride + m;
+            const int index = cw + W * (ch + H * bc);
+            const bool valid = ch >= 0 && ch < H && cw >= 0 && cw < W;
+            const float v = valid ? in[index] : -FLT_MAX;
+            mi = (v > mx) ? index : mi;
+            mx = (v > mx) ? v : mx;
+        }
+    out[o] = mx;
+    if (idx) idx[o] = mi;
 }
 
 // 2x2 windows, stride 2, no offset, every window inside the image, W % 4 == 0
@@ -252,33 +275,36 @@ __device__ __forceinline__ int floor_div(int a, int b) { return a >= 0 ? a / b :
 // Gather: each input pixel visits, in ascending output order, the outputs
 // whose window holds it and adds the ones whose argmax is this pixel.  With
 // accumulate == 0 the sum starts from +0 instead of delta_in (the value the
-// reference's zeroed delta holds), and delta_in is not read.
-__global__ void k_maxpool_bwd(const float *__restrict__ dout, const int32_t *__restrict__ idx,
-                              int batch, int C, int H, int W, int size, int stride, int pad,
-                              int OH, int OW, float *din, int accumulate)
+// reference's zeroed delta holds), and delta_in is not read.  One thread per
+// input pixel; SIZE / STRIDE are compile-time for the common windows (0 =
+// taken from the arguments), which turns the window-range divisions into
+// shifts.
+template <int SIZE, int STRIDE>
+__global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ dout,
+                                                     const int32_t *__restrict__ idx, int total,
+                                                     int H, int W, int size_, int stride_,
+                                                     int pad, int OH, int OW, float *din,
+                                                     int accumulate)
 {
-    const unsigned total = (unsigned)batch * C * H * W;
+    const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= total) return;
+    const int row = p / W, w = p - row * W;  // row = bc*H + h
+    const int bc = row / H, h = row - bc * H;
     const int off = -pad / 2;
-    for (unsigned p = blockIdx.x * blockDim.x + threadIdx.x; p < total;
-         p += gridDim.x * blockDim.x) {
-        const int w = (int)(p % W);
-        const unsigned r = p / W;
-        const int h = (int)(r % H);
-        const int bc = (int)(r / H);
-        // output row i covers rows off + i*stride .. + size-1
-        int i0 = floor_div(h - off - size, stride) + 1, i1 = floor_div(h - off, stride);
-        int j0 = floor_div(w - off - size, stride) + 1, j1 = floor_div(w - off, stride);
-        i0 = max(i0, 0); j0 = max(j0, 0);
-        i1 = min(i1, OH - 1); j1 = min(j1, OW - 1);
-        float v = accumulate ? din[p] : 0.f;
-        const int obase = bc * OH * OW;
-        for (int i = i0; i <= i1; ++i)
-            for (int j = j0; j <= j1; ++j) {
-                const int o = obase + i * OW + j;
-                if (idx[o] == (int32_t)p) v += dout[o];
-            }
-        din[p] = v;
-    }
+    // output row i covers rows off + i*stride .. + size-1
+    const int i0 = max(floor_div(h - off - size, stride) + 1, 0);
+    const int i1 = min(floor_div(h - off, stride), OH - 1);
+    const int j0 = max(floor_div(w - off - size, stride) + 1, 0);
+    const int j1 = min(floor_div(w - off, stride), OW - 1);
+    float v = accumulate ? din[p] : 0.f;
+    const int obase = bc * OH * OW;
+    for (int i = i0; i <= i1; ++i)
+        for (int j = j0; j <= j1; ++j) {
+            const int o = obase + i * OW + j;
+            if (idx[o] == (int32_t)p) v += dout[o];
+        }
+    din[p] = v;
 }
 
 // Backward of k_maxpool2_fwd: every input pixel lies in exactly one window.
@@ -638,14 +664,26 @@ int ach_add_bias(float *out, const float *b, int batch, int n, int spatial, ach_
     return check_launch();
 }
 
-size_t ach_bias_grad_workspace(int, int, int) { return 0; }
-
-int ach_bias_grad(float *updates, const float *delta, int batch, int n, int spatial, void *,
-                  size_t, ach_stream_t s)
+size_t ach_bias_grad_workspace(int batch, int n, int)
 {
-    if (!updates || !delta || batch <= 0 || n <= 0 || spatial <= 0) return ACH_EINVAL;
-    hipLaunchKernelGGL(k_bias_grad, dim3(n), dim3(256), 0, as_stream(s), updates, delta, batch,
-                       n, spatial);
+    if (batch <= 0 || n <= 0) return 0;
+    const size_t nch = (size_t)(batch + BIAS_IMGS - 1) / BIAS_IMGS;
+    return (nch * n * sizeof(double) + 255) & ~(size_t)255;
+}
+
+int ach_bias_grad(float *updates, const float *delta, int batch, int n, int spatial, void *ws,
+                  size_t ws_bytes, ach_stream_t s)
+{
+    if (!updates || !delta || batch <= 0 || n <= 0 || spatial <= 0 || n > 65535) return ACH_EINVAL;
+    if (!ws || ws_bytes < ach_bias_grad_workspace(batch, n, spatial)) return ACH_EWORKSPACE;
+    const int nch = (batch + BIAS_IMGS - 1) / BIAS_IMGS;
+    double *part = (double *)ws;
+    hipLaunchKernelGGL(k_bias_part, dim3(n, nch), dim3(256), 0, as_stream(s), delta, batch, n,
+                       spatial, part);
+    int rc = check_launch();
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_bias_final, dim3((n + 63) / 64), dim3(64), 0, as_stream(s), part, nch, n,
+                       updates);
     return check_launch();
 }
 
@@ -705,9 +743,17 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
                            as_stream(s), in, h, w, pairs, out, idx);
         return check_launch();
     }
-    const size_t tot = (size_t)batch * c * OH * OW;
-    hipLaunchKernelGGL(k_maxpool_fwd, dim3(grid_for(tot, 256, 256u * 64u)), dim3(256), 0,
-                       as_stream(s), in, batch, c, h, w, size, stride, pad, OH, OW, out, idx);
+    const int total = batch * c * OH * OW;
+    const dim3 grid((total + 255) / 256);
+    if (size == 3 && stride == 2)
+        hipLaunchKernelGGL((k_maxpool_fwd<3, 2>), grid, dim3(256), 0, as_stream(s), in, total, h,
+                           w, size, stride, pad, OH, OW, out, idx);
+    else if (size == 2 && stride == 2)
+        hipLaunchKernelGGL((k_maxpool_fwd<2, 2>), grid, dim3(256), 0, as_stream(s), in, total, h,
+                           w, size, stride, pad, OH, OW, out, idx);
+    else
+        hipLaunchKernelGGL((k_maxpool_fwd<0, 0>), grid, dim3(256), 0, as_stream(s), in, total, h,
+                           w, size, stride, pad, OH, OW, out, idx);
     return check_launch();
 }
 
@@ -724,10 +770,17 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
                            as_stream(s), dout, idx, h, w, pairs, din, acc);
         return check_launch();
     }
-    const size_t tot = (size_t)batch * c * h * w;
-    hipLaunchKernelGGL(k_maxpool_bwd, dim3(grid_for(tot, 256, 256u * 64u)), dim3(256), 0,
-                       as_stream(s), dout, idx, batch, c, h, w, size, stride, pad, OH, OW, din,
-                       acc);
+    const int total = batch * c * h * w;  // < 2^31: pool_ok
+    const dim3 grid((total + 255) / 256);
+    if (size == 3 && stride == 2)
+        hipLaunchKernelGGL((k_maxpool_bwd<3, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
+                           total, h, w, size, stride, pad, OH, OW, din, acc);
+    else if (size == 2 && stride == 2)
+        hipLaunchKernelGGL((k_maxpool_bwd<2, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
+                           total, h, w, size, stride, pad, OH, OW, din, acc);
+    else
+        hipLaunchKernelGGL((k_maxpool_bwd<0, 0>), grid, dim3(256), 0, as_stream(s), dout, idx,
+                           total, h, w, size, stride, pad, OH, OW, din, acc);
     return check_launch();
 }
 

@@ -413,10 +413,9 @@ static size_t layer_ws(const an_layer *l, int batch)
                c = ach_conv_bwd_filter_workspace(&d);
         ws = a > b ? a : b;
         ws = ws > c ? ws : c;
-        if (l->batch_normalize) {
-            size_t n = ach_bn_workspace(batch, l->n, l->out_h * l->out_w);
-            ws = ws > n ? ws : n;
-        }
+        size_t n = l->batch_normalize ? ach_bn_workspace(batch, l->n, l->out_h * l->out_w)
+                                      : ach_bias_grad_workspace(batch, l->n, l->out_h * l->out_w);
+        ws = ws > n ? ws : n;
     } else if (l->type == AN_SOFTMAX) {
         ws = ach_softmax_workspace(batch, l->groups);
     }

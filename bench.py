@@ -344,12 +344,15 @@ def copy_calibration_phase(aetcnn, nfloats=1 << 26):
     return nfloats * 4
 
 
-def cpu_phase(configs, name, batch, steps):
+def cpu_phase(configs, name, batch, steps, parallel=True):
     """The oracle (CPU restatement of the reference CPU path) on a bounded
-    sample: `steps` training steps of the same network at a small batch."""
+    sample: `steps` training steps of the same network.  parallel=True is the
+    "oracle-parallel" mode (row-parallel GEMM over OpenMP threads, results
+    bit-identical to serial); parallel=False is "reference-faithful" (the
+    GEMM single-threaded as in the reference, Gemm.c:133)."""
     import oracle_lib
     L = oracle_lib.lib()
-    L.or_set_gemm_parallel(1)
+    L.or_set_gemm_parallel(1 if parallel else 0)
     L.or_rand_seed(1)
     B, h, w, c = configs.dims(name, batch)
     onet = oracle_lib.OracleNet(B, h, w, c)
@@ -361,12 +364,14 @@ def cpu_phase(configs, name, batch, steps):
     for _ in range(steps):
         onet.train(x, truth)
     dt = time.perf_counter() - t0
-    threads = L.or_max_threads()
+    threads = L.or_max_threads() if parallel else 1
     onet.close()
+    how = (f"row-parallel GEMM on {threads} OpenMP threads" if parallel
+           else "single-threaded GEMM (reference-faithful)")
     return dict(value=round(B * steps / dt, 3), unit="images/s", cores=int(threads),
                 kind="port",
                 sample=f"oracle {name} net, batch {B}, {steps} timed steps after 1 warm-up, "
-                       f"row-parallel GEMM on {threads} OpenMP threads ({dt:.1f} s)")
+                       f"{how} ({dt:.1f} s)")
 
 
 def main():
@@ -455,12 +460,14 @@ def main():
                         avg_launch_ms=round(probe["ms"], 5), launches=probe["reps"],
                         flop_per_launch=probe["flop"])
 
-    cpu = None
+    cpu = cpu_serial = None
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         try:
             cpu = cpu_phase(configs, args.config, args.cpu_batch, args.cpu_steps)
             log(f"cpu baseline: {cpu['value']} img/s on {cpu['cores']} threads")
+            cpu_serial = cpu_phase(configs, args.config, 16, 1, parallel=False)
+            log(f"cpu baseline (reference-faithful): {cpu_serial['value']} img/s")
         except Exception as e:  # the oracle is optional on the box
             log(f"cpu baseline skipped: {e}")
 
@@ -489,6 +496,7 @@ def main():
                           "softmax_xent_512x1000_us": softmax_us},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_reference_faithful": cpu_serial,
     }
     print(json.dumps(out), flush=True)
 

@@ -113,6 +113,8 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
 /* ---- bias (IOData.addBias IOData.c:43-55; BiasData.calcGrad BiasData.c:40-57) */
 int ach_add_bias(float *out, const float *biases, int batch, int n, int spatial,
                  ach_stream_t stream);
+/* bias_updates[c] += sum of delta over images and positions; the workspace
+ * (ach_bias_grad_workspace bytes) holds double partial sums per image chunk */
 size_t ach_bias_grad_workspace(int batch, int n, int spatial);
 int ach_bias_grad(float *bias_updates, const float *delta, int batch, int n, int spatial,
                   void *ws, size_t ws_bytes, ach_stream_t stream);

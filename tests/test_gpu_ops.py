@@ -397,5 +397,7 @@ def test_bias_ops(gpu, oracle):
     refu = upd.copy()
     oracle.lib().or_bias_grad(oracle.P(refu), oracle.P(out), B, n, sp)
     du = dev(upd)
-    check(gpu.ach_bias_grad(du.ptr, dev(out).ptr, B, n, sp, None, 0, None))
+    ws = gpu.ach_bias_grad_workspace(B, n, sp)
+    dws = dev(np.zeros(ws // 4 + 1, np.float32))
+    check(gpu.ach_bias_grad(du.ptr, dev(out).ptr, B, n, sp, dws.ptr, ws, None))
     assert rel_err(du.numpy(), refu) < 1e-5
