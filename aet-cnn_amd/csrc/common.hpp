@@ -45,6 +45,29 @@ inline unsigned grid_for(size_t n, int block, unsigned cap = 256u * 16u)
     return (unsigned)g;
 }
 
+// Unsigned division by a runtime constant d: q = (mulhi(n, mul) + n) >> shift
+// with shift = ceil(log2 d), mul = floor(2^32 (2^shift - d) / d) + 1
+// (Granlund & Montgomery 1994), exact for n < 2^31.
+struct FastDiv {
+    unsigned mul, shift, d;
+};
+
+inline FastDiv make_fastdiv(unsigned d)
+{
+    FastDiv f;
+    unsigned l = 0;
+    while ((1ull << l) < d) ++l;
+    f.mul = (unsigned)((((1ull << 32) * ((1ull << l) - d)) / d) + 1);
+    f.shift = l;
+    f.d = d;
+    return f;
+}
+
+__device__ __forceinline__ int fdiv(int n, const FastDiv &f)
+{
+    return (int)((__umulhi((unsigned)n, f.mul) + (unsigned)n) >> f.shift);
+}
+
 __device__ __forceinline__ float wave_sum(float v)
 {
 #pragma unroll

@@ -64,28 +64,6 @@ __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, int byte_off)
     return __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
 }
 
-// Unsigned division by a runtime constant d: q = (mulhi(n, mul) + n) >> shift
-// with shift = ceil(log2 d), mul = floor(2^32 (2^shift - d) / d) + 1
-// (Granlund & Montgomery 1994), exact for n < 2^31.
-struct FastDiv {
-    unsigned mul, shift, d;
-};
-
-static FastDiv make_fastdiv(unsigned d)
-{
-    FastDiv f;
-    unsigned l = 0;
-    while ((1ull << l) < d) ++l;
-    f.mul = (unsigned)((((1ull << 32) * ((1ull << l) - d)) / d) + 1);
-    f.shift = l;
-    f.d = d;
-    return f;
-}
-
-__device__ __forceinline__ int fdiv(int n, const FastDiv &f)
-{
-    return (int)((__umulhi((unsigned)n, f.mul) + (unsigned)n) >> f.shift);
-}
 
 struct ConvGeom {
     int B, C, H, W;    // input
@@ -686,8 +664,18 @@ static ConvGeom geom(const ach_conv_desc *d)
     g.F = d->n; g.KS = d->size; g.S = d->stride; g.P = d->pad;
     g.OH = (d->h + 2 * d->pad - d->size) / d->stride + 1;
     g.OW = (d->w + 2 * d->pad - d->size) / d->stride + 1;
-    g.dkk = make_fastdiv((unsigned)(d->size * d->size));
-    g.dks = make_fastdiv((unsigned)d->size);
+    // A kernel that covers the whole unpadded input (one output position: the
+    // fully connected layers expressed as convolutions) is a 1x1 convolution
+    // of the flattened input [B][C*k*k][1][1]; x, w, y, dx and dw keep their
+    // memory layout and the k order (c, ki, kj) is the same.
+    if (g.OH == 1 && g.OW == 1 && g.P == 0 && g.KS == g.H && g.KS == g.W && g.KS > 1) {
+        g.C = g.C * g.KS * g.KS;
+        g.H = g.W = 1;
+        g.KS = 1;
+        g.S = 1;
+    }
+    g.dkk = make_fastdiv((unsigned)(g.KS * g.KS));
+    g.dks = make_fastdiv((unsigned)g.KS);
     return g;
 }
 
@@ -914,13 +902,15 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
     const ConvGeom g = geom(d);
     hipStream_t st = as_stream(stream);
     if (g.S == 1 && g.P <= g.KS - 1) {
-        float *wf = (float *)ws;
         const size_t tot = (size_t)g.F * g.C * g.KS * g.KS;
+        float *part = (float *)((char *)ws + align256(tot * sizeof(float)));
+        // 1x1: the flipped k-major filter Wft[f][c] is W itself
+        if (g.KS == 1) return fwd_impl(dgrad_as_fwd(g), dy, w, dx, part, st);
+        float *wf = (float *)ws;
         hipLaunchKernelGGL(k_weights_flip_kmajor, dim3(grid_for(tot, 256)), dim3(256), 0, st, w,
                            wf, g.F, g.C, g.KS * g.KS);
         int rc = check_launch();
         if (rc) return rc;
-        float *part = (float *)((char *)ws + align256(tot * sizeof(float)));
         return fwd_impl(dgrad_as_fwd(g), dy, wf, dx, part, st);
     }
     // Strided convolution: the reference's per-image TN GEMM + col2im

@@ -207,7 +207,7 @@ __global__ void k_gradient(const float *__restrict__ y, size_t n, int act, float
 template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_fwd(const float *__restrict__ in, int total,
                                                      int H, int W, int size_, int stride_,
-                                                     int pad, int OH, int OW,
+                                                     int pad, FastDiv dOH, FastDiv dOW,
                                                      float *__restrict__ out,
                                                      int32_t *__restrict__ idx)
 {
@@ -215,8 +215,8 @@ __global__ void __launch_bounds__(256) k_maxpool_fwd(const float *__restrict__ i
     const int off = -pad / 2;
     const int o = blockIdx.x * blockDim.x + threadIdx.x;
     if (o >= total) return;
-    const int r = o / OW, j = o - r * OW;
-    const int bc = r / OH, i = r - bc * OH;
+    const int r = fdiv(o, dOW), j = o - r * (int)dOW.d;
+    const int bc = fdiv(r, dOH), i = r - bc * (int)dOH.d;
     float mx = -FLT_MAX;
     int mi = -1;
     for (int n = 0; n < size; ++n)
@@ -282,15 +282,15 @@ __device__ __forceinline__ int floor_div(int a, int b) { return a >= 0 ? a / b :
 template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ dout,
                                                      const int32_t *__restrict__ idx, int total,
-                                                     int H, int W, int size_, int stride_,
-                                                     int pad, int OH, int OW, float *din,
-                                                     int accumulate)
+                                                     FastDiv dH, FastDiv dW, int size_,
+                                                     int stride_, int pad, int OH, int OW,
+                                                     float *din, int accumulate)
 {
     const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= total) return;
-    const int row = p / W, w = p - row * W;  // row = bc*H + h
-    const int bc = row / H, h = row - bc * H;
+    const int row = fdiv(p, dW), w = p - row * (int)dW.d;  // row = bc*H + h
+    const int bc = fdiv(row, dH), h = row - bc * (int)dH.d;
     const int off = -pad / 2;
     // output row i covers rows off + i*stride .. + size-1
     const int i0 = max(floor_div(h - off - size, stride) + 1, 0);
@@ -745,15 +745,16 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
     }
     const int total = batch * c * OH * OW;
     const dim3 grid((total + 255) / 256);
+    const FastDiv dOH = make_fastdiv((unsigned)OH), dOW = make_fastdiv((unsigned)OW);
     if (size == 3 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_fwd<3, 2>), grid, dim3(256), 0, as_stream(s), in, total, h,
-                           w, size, stride, pad, OH, OW, out, idx);
+                           w, size, stride, pad, dOH, dOW, out, idx);
     else if (size == 2 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_fwd<2, 2>), grid, dim3(256), 0, as_stream(s), in, total, h,
-                           w, size, stride, pad, OH, OW, out, idx);
+                           w, size, stride, pad, dOH, dOW, out, idx);
     else
         hipLaunchKernelGGL((k_maxpool_fwd<0, 0>), grid, dim3(256), 0, as_stream(s), in, total, h,
-                           w, size, stride, pad, OH, OW, out, idx);
+                           w, size, stride, pad, dOH, dOW, out, idx);
     return check_launch();
 }
 
@@ -772,15 +773,16 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
     }
     const int total = batch * c * h * w;  // < 2^31: pool_ok
     const dim3 grid((total + 255) / 256);
+    const FastDiv dH = make_fastdiv((unsigned)h), dW = make_fastdiv((unsigned)w);
     if (size == 3 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<3, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, h, w, size, stride, pad, OH, OW, din, acc);
+                           total, dH, dW, size, stride, pad, OH, OW, din, acc);
     else if (size == 2 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<2, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, h, w, size, stride, pad, OH, OW, din, acc);
+                           total, dH, dW, size, stride, pad, OH, OW, din, acc);
     else
         hipLaunchKernelGGL((k_maxpool_bwd<0, 0>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, h, w, size, stride, pad, OH, OW, din, acc);
+                           total, dH, dW, size, stride, pad, OH, OW, din, acc);
     return check_launch();
 }
 
