@@ -105,15 +105,17 @@ __global__ void k_col2im(const float *__restrict__ col, int C, int H, int W, int
 }
 
 // ---- bias --------------------------------------------------------------------
-__global__ void k_add_bias(float *out, const float *__restrict__ b, size_t total, int n,
-                           int spatial)
+// out[b][c][p] += bias[c]; element counts below 2^31, channel from two
+// magic-number divisions
+__global__ void k_add_bias(float *out, const float *__restrict__ b, int total, FastDiv dsp,
+                           FastDiv dn)
 {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x)
-        out[i] += b[(i / spatial) % n];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int plane = fdiv(i, dsp);
+        out[i] += b[plane - fdiv(plane, dn) * (int)dn.d];
+    }
 }
 
-// one block per channel; double accumulation; updates[c] += sum
 // Bias gradient (BiasData.calcGrad, BiasData.c:40-57): dbias[c] += sum over
 // images and positions of delta.  Two passes so that every CU works: blocks
 // of (channel, image chunk) write double partial sums, then one thread per
@@ -127,16 +129,26 @@ __global__ void __launch_bounds__(256) k_bias_part(const float *__restrict__ d, 
     const int c = blockIdx.x, ch = blockIdx.y;
     const int b0 = ch * BIAS_IMGS, b1 = min(batch, b0 + BIAS_IMGS);
     double s = 0;
-    for (int b = b0; b < b1; ++b) {
-        const float *p = d + ((size_t)b * n + c) * spatial;
-        if ((spatial & 3) == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
-            const float4 *p4 = reinterpret_cast<const float4 *>(p);
+    const size_t plane = (size_t)n * spatial;  // image stride
+    if ((spatial & 3) == 0 && (reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+        for (int b = b0; b < b1; ++b) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(d + b * plane + (size_t)c * spatial);
             for (int q = threadIdx.x; q < (spatial >> 2); q += 256) {
                 const float4 v = p4[q];
                 s += (double)v.x + (double)v.y + (double)v.z + (double)v.w;
             }
-        } else {
-            for (int q = threadIdx.x; q < spatial; q += 256) s += p[q];
+        }
+    } else {
+        // scalar planes: the chunk's images are read together so that each
+        // thread has BIAS_IMGS loads in flight
+        const float *p0 = d + (size_t)b0 * plane + (size_t)c * spatial;
+        const int nb = b1 - b0;
+        for (int q = threadIdx.x; q < spatial; q += 256) {
+            float v[BIAS_IMGS];
+#pragma unroll
+            for (int k = 0; k < BIAS_IMGS; ++k) v[k] = k < nb ? p0[k * plane + q] : 0.f;
+#pragma unroll
+            for (int k = 0; k < BIAS_IMGS; ++k) s += v[k];
         }
     }
     s = wave_sum(s);
@@ -299,11 +311,34 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
     const int j1 = min(floor_div(w - off, stride), OW - 1);
     float v = accumulate ? din[p] : 0.f;
     const int obase = bc * OH * OW;
-    for (int i = i0; i <= i1; ++i)
-        for (int j = j0; j <= j1; ++j) {
-            const int o = obase + i * OW + j;
-            if (idx[o] == (int32_t)p) v += dout[o];
-        }
+    if constexpr (SIZE > 0 && STRIDE > 0) {
+        // at most NC x NC windows hold a pixel: issue all their index loads,
+        // then the matching gradients, then add in ascending output order
+        constexpr int NC = (SIZE + STRIDE - 1) / (STRIDE > 0 ? STRIDE : 1);
+        int o[NC * NC];
+        bool hit[NC * NC];
+        float g[NC * NC];
+#pragma unroll
+        for (int a = 0; a < NC; ++a)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int i = i0 + a, j = j0 + c;
+                const bool in = i <= i1 && j <= j1;
+                o[a * NC + c] = obase + i * OW + j;
+                hit[a * NC + c] = in && idx[o[a * NC + c]] == (int32_t)p;
+            }
+#pragma unroll
+        for (int q = 0; q < NC * NC; ++q) g[q] = hit[q] ? dout[o[q]] : 0.f;
+#pragma unroll
+        for (int q = 0; q < NC * NC; ++q)
+            if (hit[q]) v += g[q];
+    } else {
+        for (int i = i0; i <= i1; ++i)
+            for (int j = j0; j <= j1; ++j) {
+                const int o = obase + i * OW + j;
+                if (idx[o] == (int32_t)p) v += dout[o];
+            }
+    }
     din[p] = v;
 }
 
@@ -659,8 +694,9 @@ int ach_add_bias(float *out, const float *b, int batch, int n, int spatial, ach_
 {
     if (!out || !b || batch <= 0 || n <= 0 || spatial <= 0) return ACH_EINVAL;
     const size_t tot = (size_t)batch * n * spatial;
-    hipLaunchKernelGGL(k_add_bias, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), out, b,
-                       tot, n, spatial);
+    if (tot >= 0x7fffffffull) return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL(k_add_bias, dim3(grid_for(tot, 256, 1u << 20)), dim3(256), 0, as_stream(s),
+                       out, b, (int)tot, make_fastdiv((unsigned)spatial), make_fastdiv((unsigned)n));
     return check_launch();
 }
 
