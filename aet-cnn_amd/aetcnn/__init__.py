@@ -42,6 +42,11 @@ class ConvDesc(C.Structure):
                 ("size", _i), ("stride", _i), ("pad", _i)]
 
 
+class FilterJob(C.Structure):
+    """ach_filter_job"""
+    _fields_ = [("desc", ConvDesc), ("w", _vp), ("wt", _vp), ("wft", _vp)]
+
+
 # name -> (restype, argtypes)
 _OPS = {
     "ach_version": (C.c_char_p, []),
@@ -88,6 +93,9 @@ _OPS = {
                               _vp, _sz, _vp]),
     "ach_bn_train_fwd_from_x": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                                      _vp, _sz, _vp]),
+    "ach_conv_prepare_filters": (_i, [_i, _vp, _vp]),
+    "ach_conv_fwd_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_conv_bwd_data_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ach_bn_infer": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]),
     "ach_bn_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                         _vp, _sz, _vp]),

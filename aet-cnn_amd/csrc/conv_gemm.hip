@@ -640,6 +640,58 @@ __global__ void k_weights_flip_kmajor(const float *__restrict__ w, float *__rest
     }
 }
 
+// Batched filter preparation: for every job one launch writes the k-major
+// copy Wt[K][M] (32x32 LDS tiles) and, when asked, the flipped k-major copy
+// Wft[(f*KK + t)*C + c] = W[f][c][KK-1-t] (one thread per filter channel).
+constexpr int PREP_MAX_JOBS = 32;
+struct PrepJob {
+    const float *w;
+    float *wt, *wft;
+    int M, C, KK;     // filters, input channels, taps
+    int tiles_t;      // k-major transpose tiles: ceil(K/32) * ceil(M/32)
+    int tiles_f;      // flip blocks: ceil(M*C/256), 0 when no flipped copy
+};
+struct PrepTable {
+    PrepJob job[PREP_MAX_JOBS];
+    int n;
+};
+
+__global__ void __launch_bounds__(256) k_prepare_filters(PrepTable tab)
+{
+    __shared__ float t[32][33];
+    int b = blockIdx.x, j = 0;
+    while (j < tab.n && b >= tab.job[j].tiles_t + tab.job[j].tiles_f) {
+        b -= tab.job[j].tiles_t + tab.job[j].tiles_f;
+        ++j;
+    }
+    if (j >= tab.n) return;
+    const PrepJob &J = tab.job[j];
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    if (b < J.tiles_t) {
+        const int K = J.C * J.KK, M = J.M;
+        const int kt = (K + 31) / 32;
+        const int k0 = (b % kt) * 32, m0 = (b / kt) * 32;
+        for (int r = ty; r < 32; r += 8) {
+            const int m = m0 + r, k = k0 + tx;
+            t[r][tx] = (m < M && k < K) ? J.w[(size_t)m * K + k] : 0.f;
+        }
+        __syncthreads();
+        for (int r = ty; r < 32; r += 8) {
+            const int k = k0 + r, m = m0 + tx;
+            if (k < K && m < M) J.wt[(size_t)k * M + m] = t[tx][r];
+        }
+        return;
+    }
+    // flip: one thread per (filter, channel) copies its KK taps; neighbouring
+    // threads read adjacent tap runs and write adjacent channels of a tap
+    const int fc = (b - J.tiles_t) * 256 + threadIdx.x;
+    if (fc >= J.M * J.C) return;
+    const int f = fc / J.C, c = fc - f * J.C, KK = J.KK;
+    const float *src = J.w + (size_t)fc * KK;
+    float *dst = J.wft + (size_t)f * KK * J.C + c;
+    for (int tap = 0; tap < KK; ++tap) dst[(size_t)tap * J.C] = src[KK - 1 - tap];
+}
+
 // ---------------------------------------------------------------------------
 template <class P>
 static int launch_gemm(const P &p, int M, int N, int splits, hipStream_t st)
@@ -926,6 +978,70 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
         if (rc) return rc;
     }
     return ACH_OK;
+}
+
+// ---- prepared filters ----------------------------------------------------
+static bool dgrad_flips(const ConvGeom &g) { return g.S == 1 && g.P <= g.KS - 1 && g.KS > 1; }
+
+int ach_conv_prepare_filters(int njobs, const ach_filter_job *jobs, ach_stream_t stream)
+{
+    if (njobs < 0 || (njobs > 0 && !jobs)) return ACH_EINVAL;
+    hipStream_t st = as_stream(stream);
+    for (int j0 = 0; j0 < njobs; j0 += PREP_MAX_JOBS) {
+        PrepTable tab;
+        tab.n = 0;
+        long long blocks = 0;
+        for (int j = j0; j < njobs && j < j0 + PREP_MAX_JOBS; ++j) {
+            const ach_filter_job &q = jobs[j];
+            if (!conv_ok(&q.desc) || !q.w || !q.wt) return ACH_EINVAL;
+            const ConvGeom g = geom(&q.desc);
+            PrepJob &J = tab.job[tab.n++];
+            J.w = q.w;
+            J.wt = q.wt;
+            J.wft = q.wft;
+            J.M = g.F;
+            J.C = g.C;
+            J.KK = g.KS * g.KS;
+            const int K = J.C * J.KK;
+            J.tiles_t = ((K + 31) / 32) * ((J.M + 31) / 32);
+            J.tiles_f = 0;
+            if (q.wft && dgrad_flips(g))
+                J.tiles_f = (int)(((long long)J.M * J.C + 255) / 256);
+            blocks += J.tiles_t + J.tiles_f;
+        }
+        if (blocks > 0x7fffffffLL) return ACH_EUNSUPPORTED;
+        if (blocks == 0) continue;
+        hipLaunchKernelGGL(k_prepare_filters, dim3((unsigned)blocks), dim3(256), 0, st, tab);
+        int rc = check_launch();
+        if (rc) return rc;
+    }
+    return ACH_OK;
+}
+
+int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *wt, float *y,
+                          void *ws, size_t ws_bytes, ach_stream_t stream)
+{
+    if (!conv_ok(d) || !x || !wt || !y) return ACH_EINVAL;
+    if (!fits_int(d)) return ACH_EUNSUPPORTED;
+    const ConvGeom g = geom(d);
+    const size_t need = fwd_part_bytes(g);
+    if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
+    return fwd_impl(g, x, wt, y, (float *)ws, as_stream(stream));
+}
+
+int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const float *w,
+                               const float *wft, float *dx, void *ws, size_t ws_bytes,
+                               ach_stream_t stream)
+{
+    if (!conv_ok(d) || !dy || !w || !dx) return ACH_EINVAL;
+    if (!fits_int(d)) return ACH_EUNSUPPORTED;
+    const ConvGeom g = geom(d);
+    if (!(g.S == 1 && g.P <= g.KS - 1)) return ACH_EUNSUPPORTED;  // strided: ach_conv_bwd_data
+    if (g.KS > 1 && !wft) return ACH_EINVAL;
+    const ConvGeom t = dgrad_as_fwd(g);
+    const size_t need = fwd_part_bytes(t);
+    if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
+    return fwd_impl(t, dy, g.KS == 1 ? w : wft, dx, (float *)ws, as_stream(stream));
 }
 
 size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)

@@ -43,6 +43,9 @@ struct an_network {
     size_t nweights_total;
     float *bflat, *bvflat;         /* biases (+scales) / their updates       */
     size_t nbias_total;
+    float *wtflat, *wftflat;       /* k-major / flipped k-major filters    */
+    ach_filter_job *jobs;          /* one per conv layer                    */
+    int njobs;
     float *zero_region;            /* deltas that need zeroing per forward */
     size_t zero_floats;
     /* host copies of initial parameters until finalize */
@@ -138,8 +141,8 @@ static int conv_forward(an_network *net, an_layer *l, an_state st)
     ach_stream_t s = net->stream;
     if (l->batch_normalize) {
         /* conv output goes straight into NormData.x; BN writes output */
-        AN_CHECK(ach_conv_fwd(&d, st.input, l->weights, l->x, st.workspace,
-                              st.workspace_bytes, s));
+        AN_CHECK(ach_conv_fwd_prepared(&d, st.input, l->weights_kmajor, l->x, st.workspace,
+                                       st.workspace_bytes, s));
         const int act = fusable(l->activation) ? l->activation : ACH_LINEAR;
         if (st.train)
             AN_CHECK(ach_bn_train_fwd_from_x(l->x, l->output, l->batch, l->n, spatial,
@@ -153,8 +156,8 @@ static int conv_forward(an_network *net, an_layer *l, an_state st)
             AN_CHECK(ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s));
         return ACH_OK;
     }
-    AN_CHECK(ach_conv_fwd(&d, st.input, l->weights, l->output, st.workspace,
-                          st.workspace_bytes, s));
+    AN_CHECK(ach_conv_fwd_prepared(&d, st.input, l->weights_kmajor, l->output, st.workspace,
+                                   st.workspace_bytes, s));
     AN_CHECK(ach_add_bias(l->output, l->biases, l->batch, l->n, spatial, s));
     return ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s);
 }
@@ -183,8 +186,11 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
     AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, st.workspace,
                                  st.workspace_bytes, s));
     if (st.delta)
-        AN_CHECK(ach_conv_bwd_data(&d, l->delta, l->weights, st.delta, st.workspace,
-                                   st.workspace_bytes, s));
+        AN_CHECK(l->stride == 1
+                     ? ach_conv_bwd_data_prepared(&d, l->delta, l->weights, l->weights_flipped,
+                                                  st.delta, st.workspace, st.workspace_bytes, s)
+                     : ach_conv_bwd_data(&d, l->delta, l->weights, st.delta, st.workspace,
+                                         st.workspace_bytes, s));
     return ACH_OK;
 }
 
@@ -502,7 +508,7 @@ int an_finalize(an_network *net)
         nw += (size_t)((l->nweights + 63) & ~63);
         nb += (size_t)((l->n + 63) & ~63) * (l->batch_normalize ? 2 : 1);
     }
-    const size_t extra = al(sizeof(float) * nw) * 2 + al(sizeof(float) * nb) * 2;
+    const size_t extra = al(sizeof(float) * nw) * 4 + al(sizeof(float) * nb) * 2;
     net->arena_bytes = dry.off + extra;
     AN_CHECK(ach_malloc(&net->arena, net->arena_bytes));
     AN_CHECK(ach_stream_create(&net->stream));
@@ -517,6 +523,10 @@ int an_finalize(an_network *net)
     net->bflat = (float *)tail;
     tail += al(sizeof(float) * nb);
     net->bvflat = (float *)tail;
+    tail += al(sizeof(float) * nb);
+    net->wtflat = (float *)tail;
+    tail += al(sizeof(float) * nw);
+    net->wftflat = (float *)tail;
     net->nweights_total = nw;
     net->nbias_total = nb;
     size_t ow = 0, ob = 0;
@@ -525,6 +535,8 @@ int an_finalize(an_network *net)
         if (l->type != AN_CONVOLUTIONAL) continue;
         l->weights = net->wflat + ow;
         l->weight_updates = net->vflat + ow;
+        l->weights_kmajor = net->wtflat + ow;
+        l->weights_flipped = net->wftflat + ow;
         ow += (size_t)((l->nweights + 63) & ~63);
         l->biases = net->bflat + ob;
         l->bias_updates = net->bvflat + ob;
@@ -536,6 +548,21 @@ int an_finalize(an_network *net)
         } else {
             l->scales = l->scale_updates = NULL;
         }
+    }
+    /* filter-layout jobs: the flipped copy only where an input gradient is
+     * computed (not for the first layer, whose state.delta is NULL) */
+    net->jobs = (ach_filter_job *)calloc((size_t)(net->n > 0 ? net->n : 1),
+                                         sizeof(ach_filter_job));
+    if (!net->jobs) return ACH_EINVAL;
+    net->njobs = 0;
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        ach_filter_job *j = &net->jobs[net->njobs++];
+        j->desc = conv_desc(l);
+        j->w = l->weights;
+        j->wt = l->weights_kmajor;
+        j->wft = i > 0 ? l->weights_flipped : NULL;
     }
     /* zero everything once (momentum buffers, biases, stats, deltas) */
     AN_CHECK(ach_fill((float *)net->arena, net->arena_bytes / sizeof(float), 0.f, net->stream));
@@ -563,6 +590,7 @@ void an_free(an_network *net)
     }
     free(net->layers);
     free(net->init_w);
+    free(net->jobs);
     if (net->stream) ach_stream_sync(net->stream);
     ach_free(net->arena);
     ach_stream_destroy(net->stream);
@@ -615,6 +643,8 @@ int an_forward(an_network *net, int train)
     an_state st = base_state(net);
     st.train = train;
     if (!train) st.truth = NULL; /* NNetwork.predict: state.truth = 0 */
+    /* the filter layouts the conv GEMMs read, from the current weights */
+    AN_CHECK(ach_conv_prepare_filters(net->njobs, net->jobs, net->stream));
     if (train && net->zero_floats)
         AN_CHECK(ach_fill(net->zero_region, net->zero_floats, 0.f, net->stream));
     for (int i = 0; i < net->n; ++i) {
@@ -658,6 +688,8 @@ int an_layer_forward(an_network *net, int i, int train)
     st.train = train;
     st.index = i;
     if (i > 0) st.input = net->layers[i - 1]->output;
+    if (l->type == AN_CONVOLUTIONAL)
+        AN_CHECK(ach_conv_prepare_filters(net->njobs, net->jobs, net->stream));
     if (train && l->zero_delta && !l->shares_prev)
         AN_CHECK(ach_fill(l->delta, (size_t)l->batch * l->outputs, 0.f, net->stream));
     return l->forward(net, l, st);
@@ -667,6 +699,8 @@ int an_layer_backward(an_network *net, int i)
 {
     an_layer *l = an_get_layer(net, i);
     if (!l || !net->finalized) return ACH_EINVAL;
+    if (l->type == AN_CONVOLUTIONAL)
+        AN_CHECK(ach_conv_prepare_filters(net->njobs, net->jobs, net->stream));
     return l->backward(net, l, backward_state(net, i));
 }
 

@@ -67,6 +67,8 @@ struct an_layer {
     float *mean, *variance, *rolling_mean, *rolling_variance;
     float *mean_delta, *variance_delta;
     float *x;               /* pre-BN conv output (NormData.x)              */
+    float *weights_kmajor;  /* filter layouts the conv GEMMs read, refreshed */
+    float *weights_flipped; /* from weights at every forward pass            */
     /* maxpool */
     int32_t *indexes;
     /* dropout */

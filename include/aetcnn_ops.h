@@ -110,6 +110,32 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d);
 int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
                         void *ws, size_t ws_bytes, ach_stream_t stream);
 
+/* ---- prepared filters -------------------------------------------------------
+ * The conv GEMMs read the filter k-major (Wt[C*k*k][n]) and, for the stride-1
+ * input gradient, flipped k-major (Wft[(f*k*k + t)*C + c] = W[f][c][k*k-1-t]).
+ * ach_conv_fwd / ach_conv_bwd_data build these in the workspace on every
+ * call; a caller that keeps them (the network refreshes all of them with one
+ * ach_conv_prepare_filters launch per step) calls the _prepared variants.
+ * wft may be NULL when not needed: stride > 1, or a 1x1 filter (including a
+ * kernel covering the whole unpadded input), whose flipped copy is W itself.
+ * No counterpart in the reference, which has no such layouts.              */
+typedef struct {
+    ach_conv_desc desc;
+    const float *w;   /* [n][c][size][size] */
+    float *wt;        /* n*c*size*size floats */
+    float *wft;       /* n*c*size*size floats or NULL */
+} ach_filter_job;
+int ach_conv_prepare_filters(int njobs, const ach_filter_job *jobs, ach_stream_t stream);
+/* workspace: ach_conv_fwd_workspace(d) / ach_conv_bwd_data_workspace(d)
+ * bytes suffice (the _prepared calls use only the split-K part of it)      */
+int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *wt, float *y,
+                          void *ws, size_t ws_bytes, ach_stream_t stream);
+/* stride-1 only (ACH_EUNSUPPORTED otherwise); w is read for 1x1 filters,
+ * wft otherwise                                                             */
+int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const float *w,
+                               const float *wft, float *dx, void *ws, size_t ws_bytes,
+                               ach_stream_t stream);
+
 /* ---- bias (IOData.addBias IOData.c:43-55; BiasData.calcGrad BiasData.c:40-57) */
 int ach_add_bias(float *out, const float *biases, int batch, int n, int spatial,
                  ach_stream_t stream);

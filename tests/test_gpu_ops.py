@@ -401,3 +401,33 @@ def test_bias_ops(gpu, oracle):
     dws = dev(np.zeros(ws // 4 + 1, np.float32))
     check(gpu.ach_bias_grad(du.ptr, dev(out).ptr, B, n, sp, dws.ptr, ws, None))
     assert rel_err(du.numpy(), refu) < 1e-5
+
+
+@pytest.mark.parametrize("shape", [
+    (2, 128, 16, 16, 256, 3, 1, 1),   # 3x3, 256-row tiles, split K
+    (3, 5, 9, 7, 10, 3, 1, 1),
+    (2, 16, 13, 13, 24, 5, 1, 2),     # generic kernel size
+    (2, 512, 8, 8, 10, 1, 1, 0),      # 1x1: the flipped filter is W itself
+    (3, 8, 6, 6, 40, 6, 1, 0),        # kernel covers the input: a 1x1 of the flattened input
+], ids=lambda s: "x".join(map(str, s)))
+def test_conv_prepared_filters(gpu, shape):
+    """ach_conv_prepare_filters + the _prepared entry points give the same
+    bits as ach_conv_fwd / ach_conv_bwd_data (same kernels, same layouts)."""
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, dy = _conv_inputs(shape, 3)
+    d = conv_desc(*shape)
+    ws = max(gpu.ach_conv_fwd_workspace(C.byref(d)), gpu.ach_conv_bwd_data_workspace(C.byref(d)))
+    dws = dev(np.zeros(ws // 4 + 64, np.float32))
+    dx_, dw_, ddy = dev(x), dev(w), dev(dy)
+    wt, wft = dev(np.zeros(w.size, np.float32)), dev(np.full(w.size, np.nan, np.float32))
+    job = aetcnn.FilterJob(d, dw_.ptr, wt.ptr, wft.ptr)
+    check(gpu.ach_conv_prepare_filters(1, C.byref(job), None))
+    y0, y1 = D(dy.shape), D(dy.shape)
+    check(gpu.ach_conv_fwd(C.byref(d), dx_.ptr, dw_.ptr, y0.ptr, dws.ptr, ws, None))
+    check(gpu.ach_conv_fwd_prepared(C.byref(d), dx_.ptr, wt.ptr, y1.ptr, dws.ptr, ws, None))
+    assert np.array_equal(y0.numpy(), y1.numpy())
+    g0, g1 = D(x.shape), D(x.shape)
+    check(gpu.ach_conv_bwd_data(C.byref(d), ddy.ptr, dw_.ptr, g0.ptr, dws.ptr, ws, None))
+    check(gpu.ach_conv_bwd_data_prepared(C.byref(d), ddy.ptr, dw_.ptr, wft.ptr, g1.ptr,
+                                         dws.ptr, ws, None))
+    assert np.array_equal(g0.numpy(), g1.numpy())
