@@ -743,17 +743,16 @@ static bool fits_int(const ach_conv_desc *d)
 }
 
 // y[b][m][p] = sum_z part[z][m][b*OHW+p], z ascending (fixed order).
-__global__ void k_splitk_to_nchw(const float *__restrict__ part, float *__restrict__ y, int M,
-                                 int N, int ohw, int splits)
+__global__ void __launch_bounds__(256) k_splitk_to_nchw(const float *__restrict__ part,
+                                                        float *__restrict__ y, int M, int N,
+                                                        FastDiv dohw, FastDiv dM, int splits)
 {
-    const size_t mn = (size_t)M * N;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < mn;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const int p = (int)(i % ohw);
-        const size_t bm = i / ohw;
-        const int m = (int)(bm % M);
-        const int b = (int)(bm / M);
-        const size_t n = (size_t)b * ohw + p;
+    // M*N < 2^29 (operands below 2 GiB): 32-bit indices, magic-number division
+    const int mn = M * N, ohw = (int)dohw.d;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += gridDim.x * blockDim.x) {
+        const int bm = fdiv(i, dohw), p = i - bm * ohw;
+        const int b = fdiv(bm, dM), m = bm - b * M;
+        const int n = b * ohw + p;
         float s = 0.f;
         for (int z = 0; z < splits; ++z) s += part[((size_t)z * M + m) * N + n];
         y[i] = s;
@@ -829,8 +828,9 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
     if (rc || pl.splits == 1) return rc;
     const int M = g.F, N = g.B * g.OH * g.OW;
     const size_t mn = (size_t)M * N;
-    hipLaunchKernelGGL(k_splitk_to_nchw, dim3(grid_for(mn, 256)), dim3(256), 0, st, part, y, M, N,
-                       g.OH * g.OW, pl.splits);
+    hipLaunchKernelGGL(k_splitk_to_nchw, dim3(grid_for(mn, 256, 1u << 20)), dim3(256), 0, st, part,
+                       y, M, N, make_fastdiv((unsigned)(g.OH * g.OW)), make_fastdiv((unsigned)M),
+                       pl.splits);
     return check_launch();
 }
 
