@@ -157,3 +157,37 @@ def test_top_k_matches_reference_ranking():
         idx = aetcnn.top_k(t, k)
         assert len(set(idx.tolist())) == k and idx.min() >= 0
         assert np.array_equal(t[idx], np.sort(t)[::-1][:k]), (n, k)
+
+
+def test_argument_validation_without_device():
+    """Zero-size work returns ACH_OK before touching the device; malformed
+    shapes, missing buffers and short workspaces are rejected with codes."""
+    ops = aetcnn.ops()
+    OK, EINVAL, EWS = 0, aetcnn.ACH_EINVAL, -2
+    assert ops.ach_activate(None, 0, aetcnn.LEAKY, None) == OK
+    assert ops.ach_activate(None, 0, aetcnn.LINEAR, None) == OK
+    assert ops.ach_gradient(None, 0, aetcnn.LEAKY, None, None) == OK
+    assert ops.ach_activate(None, 16, aetcnn.LEAKY, None) == EINVAL
+    assert ops.ach_dropout_fwd(None, 0, 0.5, 1, 0, 0, None) == OK
+    assert ops.ach_dropout_fwd(C.c_void_p(64).value, 8, 1.5, 1, 0, 0, None) == EINVAL
+    assert ops.ach_gemm(0, 0, 0, 5, 5, 1.0, None, 5, None, 5, 0.0, C.c_void_p(64).value, 5,
+                        None) == OK
+    bad = aetcnn.ConvDesc(2, 3, 4, 4, 8, 7, 1, 0)  # 7x7 kernel on a 4x4 image
+    fake = C.c_void_p(256).value
+    assert ops.ach_conv_fwd(C.byref(bad), fake, fake, fake, fake, 1 << 20, None) == EINVAL
+    assert ops.ach_conv_fwd(C.byref(aetcnn.ConvDesc(2, 3, 8, 8, 8, 3, 1, 1)), None, fake, fake,
+                            fake, 1 << 20, None) == EINVAL
+    small = aetcnn.ConvDesc(128, 512, 8, 8, 512, 3, 1, 1)  # needs split-K scratch
+    assert ops.ach_conv_fwd(C.byref(small), fake, fake, fake, fake, 16, None) == EWS
+    assert ops.ach_bn_train_fwd_from_x(fake, fake, 0, 4, 16, fake, fake, fake, fake, None, None,
+                                       aetcnn.LINEAR, fake, 1 << 20, None) == EINVAL
+    other = C.c_void_p(512).value
+    assert ops.ach_bn_train_fwd_from_x(fake, fake, 2, 4, 16, fake, fake, fake, fake, None, None,
+                                       aetcnn.LINEAR, fake, 1 << 20, None) == EINVAL  # x == out
+    assert ops.ach_bn_train_fwd_from_x(fake, other, 2, 4, 16, fake, fake, fake, fake, None, None,
+                                       aetcnn.LINEAR, fake, 0, None) == EWS
+    assert ops.ach_maxpool_fwd(fake, 1, 1, 4, 4, 0, 2, 0, fake, None, None) == EINVAL
+    assert ops.ach_bias_grad(fake, fake, 2, 4, 16, None, 0, None) == EWS
+    assert ops.ach_conv_prepare_filters(0, None, None) == OK
+    assert ops.ach_conv_bwd_data_prepared(C.byref(aetcnn.ConvDesc(2, 3, 9, 9, 8, 3, 2, 1)),
+                                          fake, fake, fake, fake, fake, 1 << 20, None) == -4
