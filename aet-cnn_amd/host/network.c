@@ -44,6 +44,14 @@ struct an_network {
     float *bflat, *bvflat;         /* biases (+scales) / their updates       */
     size_t nbias_total;
     float *wtflat, *wftflat;       /* k-major / flipped k-major filters    */
+    /* weight gradients run on a second stream, overlapping the input-gradient
+     * chain: its own workspace, one "delta ready" event per layer and one
+     * event that joins it back before the update                           */
+    ach_stream_t wstream;
+    float *wgrad_ws;
+    size_t wgrad_ws_bytes;
+    void **ev_ready;
+    void *ev_joined;
     ach_filter_job *jobs;          /* one per conv layer                    */
     int njobs;
     float *zero_region;            /* deltas that need zeroing per forward */
@@ -183,8 +191,12 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
         AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial,
                                st.workspace, st.workspace_bytes, s));
     }
-    AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, st.workspace,
-                                 st.workspace_bytes, s));
+    /* dW on the weight-gradient stream once delta is final; the input
+     * gradient continues on the main stream */
+    AN_CHECK(ach_event_record(net->ev_ready[l->index], s));
+    AN_CHECK(ach_stream_wait_event(net->wstream, net->ev_ready[l->index]));
+    AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, net->wgrad_ws,
+                                 net->wgrad_ws_bytes, net->wstream));
     if (st.delta)
         AN_CHECK(l->stride == 1
                      ? ach_conv_bwd_data_prepared(&d, l->delta, l->weights, l->weights_flipped,
@@ -479,6 +491,16 @@ static void layout(an_network *net, bump *b)
     }
     net->workspace_bytes = ws;
     net->workspace = (float *)take(b, ws ? ws : 256);
+    size_t wws = 0;
+    for (int i = 0; i < net->n; ++i) {
+        const an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL) continue;
+        ach_conv_desc d = conv_desc(l);
+        const size_t w = ach_conv_bwd_filter_workspace(&d);
+        if (w > wws) wws = w;
+    }
+    net->wgrad_ws_bytes = wws;
+    net->wgrad_ws = (float *)take(b, wws ? wws : 256);
 }
 
 int an_finalize(an_network *net)
@@ -512,6 +534,13 @@ int an_finalize(an_network *net)
     net->arena_bytes = dry.off + extra;
     AN_CHECK(ach_malloc(&net->arena, net->arena_bytes));
     AN_CHECK(ach_stream_create(&net->stream));
+    AN_CHECK(ach_stream_create(&net->wstream));
+    net->ev_ready = (void **)calloc((size_t)(net->n > 0 ? net->n : 1), sizeof(void *));
+    if (!net->ev_ready) return ACH_EINVAL;
+    for (int i = 0; i < net->n; ++i)
+        if (net->layers[i]->type == AN_CONVOLUTIONAL)
+            AN_CHECK(ach_event_create(&net->ev_ready[i]));
+    AN_CHECK(ach_event_create(&net->ev_joined));
     bump real = {(char *)net->arena, 0, 0};
     layout(net, &real);
     /* flat parameter buffers at the arena tail */
@@ -591,8 +620,16 @@ void an_free(an_network *net)
     free(net->layers);
     free(net->init_w);
     free(net->jobs);
+    if (net->wstream) ach_stream_sync(net->wstream);
     if (net->stream) ach_stream_sync(net->stream);
+    if (net->ev_ready) {
+        for (int i = 0; i < net->n; ++i)
+            if (net->ev_ready[i]) ach_event_destroy(net->ev_ready[i]);
+        free(net->ev_ready);
+    }
+    if (net->ev_joined) ach_event_destroy(net->ev_joined);
     ach_free(net->arena);
+    if (net->wstream) ach_stream_destroy(net->wstream);
     ach_stream_destroy(net->stream);
     free(net);
 }
@@ -668,6 +705,13 @@ static an_state backward_state(an_network *net, int i)
 }
 
 /* NNetwork.backward (NNetwork.c:627-654).                                 */
+/* the main stream waits for every weight gradient enqueued so far */
+static int join_wgrad(an_network *net)
+{
+    AN_CHECK(ach_event_record(net->ev_joined, net->wstream));
+    return ach_stream_wait_event(net->stream, net->ev_joined);
+}
+
 int an_backward(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
@@ -675,7 +719,7 @@ int an_backward(an_network *net)
         an_layer *l = net->layers[i];
         AN_CHECK(l->backward(net, l, backward_state(net, i)));
     }
-    return ACH_OK;
+    return join_wgrad(net);
 }
 
 /* One layer of the loops above, with the same NetworkState: the
@@ -701,7 +745,8 @@ int an_layer_backward(an_network *net, int i)
     if (!l || !net->finalized) return ACH_EINVAL;
     if (l->type == AN_CONVOLUTIONAL)
         AN_CHECK(ach_conv_prepare_filters(net->njobs, net->jobs, net->stream));
-    return l->backward(net, l, backward_state(net, i));
+    AN_CHECK(l->backward(net, l, backward_state(net, i)));
+    return join_wgrad(net);
 }
 
 /* NNetwork.updateCPU (NNetwork.c:667-680) with the constant rate policy:
