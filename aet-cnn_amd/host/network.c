@@ -188,13 +188,14 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
                             st.workspace_bytes, s));
     } else {
         AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));
-        AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial,
-                               st.workspace, st.workspace_bytes, s));
     }
-    /* dW on the weight-gradient stream once delta is final; the input
-     * gradient continues on the main stream */
+    /* dbias and dW on the weight-gradient stream once delta is final; the
+     * input gradient continues on the main stream */
     AN_CHECK(ach_event_record(net->ev_ready[l->index], s));
     AN_CHECK(ach_stream_wait_event(net->wstream, net->ev_ready[l->index]));
+    if (!l->batch_normalize)
+        AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial,
+                               net->wgrad_ws, net->wgrad_ws_bytes, net->wstream));
     AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, net->wgrad_ws,
                                  net->wgrad_ws_bytes, net->wstream));
     if (st.delta)
@@ -496,7 +497,9 @@ static void layout(an_network *net, bump *b)
         const an_layer *l = net->layers[i];
         if (l->type != AN_CONVOLUTIONAL) continue;
         ach_conv_desc d = conv_desc(l);
-        const size_t w = ach_conv_bwd_filter_workspace(&d);
+        size_t w = ach_conv_bwd_filter_workspace(&d);
+        if (w > wws) wws = w;
+        w = l->batch_normalize ? 0 : ach_bias_grad_workspace(l->batch, l->n, l->out_h * l->out_w);
         if (w > wws) wws = w;
     }
     net->wgrad_ws_bytes = wws;
