@@ -27,6 +27,8 @@
 // L2.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace ach {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -112,6 +114,55 @@ struct AWeightsT {
 #pragma unroll
         for (int i = 0; i < RA; ++i)
             if (kr + RPI * i < BK) S[kr + RPI * i][mc] = ra[i];
+    }
+};
+
+// The same k-major weights read as float4 when M % 4 == 0: thread -> float4
+// f = tid + 256*i of the BK x BM tile (row f / (BM/4), columns 4*(f % (BM/4))
+// .. +3), one dwordx4 buffer load and one 16-byte LDS store each, instead of
+// four dword loads and stores.
+__device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, int byte_off)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
+    return make_float4(__int_as_float((int)v[0]), __int_as_float((int)v[1]),
+                       __int_as_float((int)v[2]), __int_as_float((int)v[3]));
+}
+
+template <int BM, int BK>
+struct AWeightsT4 {
+    static constexpr int C4 = BM / 4;                      // float4 per tile row
+    static constexpr int NV = (BK * C4 + GNT - 1) / GNT;   // float4 per thread
+    static constexpr int RA = 4 * NV, PAD = LDP;
+    static_assert(BM % 4 == 0 && ((BM + LDP) % 4) == 0, "16-byte LDS rows");
+    __amdgpu_buffer_rsrc_t rs;
+    int M, m0;
+    __device__ __forceinline__ void init(const float *wt, int M_, int K_, int m0_, int)
+    {
+        M = M_;
+        m0 = m0_;
+        rs = make_rsrc(wt, (unsigned)((size_t)M_ * K_ * 4));
+    }
+    __device__ __forceinline__ void load(int k0, int ke, float *ra) const
+    {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + GNT * i;
+            const int row = f / C4, m = m0 + 4 * (f % C4), k = k0 + row;
+            const bool ok = f < BK * C4 && k < ke && m < M;
+            const float4 v = bload4(rs, boff(ok, k * M + m));
+            ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
+        }
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
+    {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + GNT * i;
+            if (f < BK * C4)
+                *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
+                    make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
+        }
     }
 };
 
@@ -391,10 +442,11 @@ struct PlainOperand {
 // Forward: y[b][m][p] = sum_k Wt[k][m] * im2col(x)[k][b*OHW+p].  With
 // splits > 1 each z-slice of K writes part[z][m][n] and a fixed-order
 // reduction produces y (used when the tile grid alone cannot fill the GPU).
-template <int BM_, class BL>
+template <int BM_, class BL, bool VECA = false>
 struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
-    using AL = AWeightsT<BM, BK>;  // w points at the k-major copy Wt[K][M]
+    // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
+    using AL = typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type;
     using BLd = BL;
     const float *x, *w;
     float *y, *part;
@@ -478,8 +530,8 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
     static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
     constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
-    __shared__ float As[2][BK][LA];
-    __shared__ float Bs[2][BK][LB];
+    __shared__ __attribute__((aligned(16))) float As[2][BK][LA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -802,6 +854,10 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
                   float *y, float *part, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
+    if (g.KS == 3 && (M & 3) == 0) {
+        FwdProblem<BM, BIm2col3, true> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        return launch_gemm(p, M, N, pl.splits, st);
+    }
     if (g.KS == 3) {
         FwdProblem<BM, BIm2col3> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
         return launch_gemm(p, M, N, pl.splits, st);
