@@ -92,6 +92,9 @@ CONV_SHAPES = [
     (2, 3, 35, 35, 8, 11, 4, 0),
     (4, 32, 6, 6, 40, 6, 1, 0),
     (5, 7, 1, 1, 9, 1, 1, 0),
+    (3, 6, 12, 12, 20, 3, 1, 1),   # vector im2col loader, partial N tile, ragged K
+    (2, 8, 10, 10, 16, 3, 1, 0),   # vector loader without padding (dgrad: pad 2)
+    (2, 4, 4, 4, 8, 3, 1, 1),      # narrowest input the vector loader takes
 ]
 
 
