@@ -97,6 +97,7 @@ _OPS = {
     "ach_conv_fwd_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ach_conv_bwd_data_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ach_bn_infer": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]),
+    "ach_conv_bn_fold": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ach_bn_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                         _vp, _sz, _vp]),
     "ach_activate": (_i, [_vp, _sz, _i, _vp]),
@@ -138,6 +139,7 @@ _NET = {
     "an_train": (_i, [_vp, _vp, _vp, C.POINTER(_f)]),
     "an_forward": (_i, [_vp, _i]),
     "an_predict": (_i, [_vp, _vp, _vp]),
+    "an_fuse_conv_batchnorm": (_i, [_vp]),
     "an_feeder_create_cifar": (_vp, [_vp, _vp, _i, _i, _u64, _i, _f]),
     "an_feeder_create_synthetic": (_vp, [_vp, _i, _u64]),
     "an_feeder_next": (_i, [_vp]),
@@ -361,6 +363,11 @@ class Network:
         out = np.empty((self.batch, self.lib.an_classes(self.h)), np.float32)
         check(self.lib.an_predict(self.h, x.ctypes.data, out.ctypes.data), "an_predict")
         return out
+
+    def fuse_conv_batchnorm(self):
+        """NNetwork.fuseConvBatchnorm: fold the inference BN of every BN conv
+        layer into its filters and biases (the layers become plain convs)"""
+        check(self.lib.an_fuse_conv_batchnorm(self.h), "an_fuse_conv_batchnorm")
 
     def loss(self) -> float:
         v = _f()

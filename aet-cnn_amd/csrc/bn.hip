@@ -476,6 +476,27 @@ static int bn_fwd(const float *src, float *xcopy, float *xnorm, float *out, int 
     return check_launch();
 }
 
+/* Inference BN folded into the conv filters (ConvolutionalLayer.c:983-1003):
+ * one block per filter; r = sqrt(var + 1e-5), the scale factor and the bias
+ * shift in double, each result rounded once to float.  Every operation is a
+ * single IEEE double op (no fused multiply-add), as in the C expression. */
+__global__ void __launch_bounds__(256) k_bn_fold(int fsize, float *__restrict__ w,
+                                                 float *__restrict__ b,
+                                                 const float *__restrict__ scales,
+                                                 const float *__restrict__ rmean,
+                                                 const float *__restrict__ rvar)
+{
+    const int f = blockIdx.x;
+    const double r = __dsqrt_rn(__dadd_rn((double)rvar[f], 1e-5));
+    const double pre = __ddiv_rn((double)scales[f], r);
+    float *wf = w + (size_t)f * fsize;
+    for (int i = threadIdx.x; i < fsize; i += blockDim.x)
+        wf[i] = (float)__dmul_rn((double)wf[i], pre);
+    if (threadIdx.x == 0)
+        b[f] = (float)__dsub_rn((double)b[f],
+                                __ddiv_rn(__dmul_rn((double)scales[f], (double)rmean[f]), r));
+}
+
 }  // namespace ach
 
 using namespace ach;
@@ -525,6 +546,18 @@ int ach_bn_infer(const float *x, float *out, int batch, int c, int spatial,
         hipLaunchKernelGGL(k_bn_infer<false>, p.apply_grid, dim3(BN_NT), 0, st, x, out, batch, c,
                            p.hwv, p.apply_per, rolling_mean, rolling_variance, scales, biases,
                            activation);
+    return check_launch();
+}
+
+int ach_conv_bn_fold(int filters, int fsize, float *weights, float *biases,
+                     const float *scales, const float *rolling_mean,
+                     const float *rolling_variance, ach_stream_t stream)
+{
+    if (filters <= 0 || fsize <= 0 || filters > 65535 || !weights || !biases || !scales ||
+        !rolling_mean || !rolling_variance)
+        return ACH_EINVAL;
+    hipLaunchKernelGGL(k_bn_fold, dim3(filters), dim3(256), 0, as_stream(stream), fsize,
+                       weights, biases, scales, rolling_mean, rolling_variance);
     return check_launch();
 }
 

@@ -432,8 +432,11 @@ static size_t layer_ws(const an_layer *l, int batch)
                c = ach_conv_bwd_filter_workspace(&d);
         ws = a > b ? a : b;
         ws = ws > c ? ws : c;
-        size_t n = l->batch_normalize ? ach_bn_workspace(batch, l->n, l->out_h * l->out_w)
-                                      : ach_bias_grad_workspace(batch, l->n, l->out_h * l->out_w);
+        /* the bias-gradient size too for BN layers: an_fuse_conv_batchnorm
+         * turns them into plain conv layers that may still be trained */
+        size_t n = ach_bias_grad_workspace(batch, l->n, l->out_h * l->out_w);
+        ws = ws > n ? ws : n;
+        n = l->batch_normalize ? ach_bn_workspace(batch, l->n, l->out_h * l->out_w) : 0;
         ws = ws > n ? ws : n;
     } else if (l->type == AN_SOFTMAX) {
         ws = ach_softmax_workspace(batch, l->groups);
@@ -499,7 +502,7 @@ static void layout(an_network *net, bump *b)
         ach_conv_desc d = conv_desc(l);
         size_t w = ach_conv_bwd_filter_workspace(&d);
         if (w > wws) wws = w;
-        w = l->batch_normalize ? 0 : ach_bias_grad_workspace(l->batch, l->n, l->out_h * l->out_w);
+        w = ach_bias_grad_workspace(l->batch, l->n, l->out_h * l->out_w);
         if (w > wws) wws = w;
     }
     net->wgrad_ws_bytes = wws;
@@ -779,6 +782,25 @@ int an_predict(an_network *net, const float *host_input, float *host_output)
     const an_layer *last = net->layers[net->n - 1];
     return ach_memcpy_d2h(host_output, last->output,
                           sizeof(float) * (size_t)last->batch * last->outputs, net->stream);
+}
+
+/* NNetwork.fuseConvBatchnorm (NNetwork.c:272-288), conv layers: each BN conv
+ * layer's inference BN is folded into its filters and biases
+ * (ach_conv_bn_fold, ConvolutionalLayer.c:983-1003) and the layer becomes a
+ * plain conv layer with bias (batch_normalize = 0).  The reference calls it
+ * after loading weights for validation (Classifier.c:369-373); a saved file
+ * afterwards holds no BN arrays for these layers, as in the reference.      */
+int an_fuse_conv_batchnorm(an_network *net)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    for (int i = 0; i < net->n; ++i) {
+        an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL || !l->batch_normalize) continue;
+        AN_CHECK(ach_conv_bn_fold(l->n, l->nweights / l->n, l->weights, l->biases, l->scales,
+                                  l->rolling_mean, l->rolling_variance, net->stream));
+        l->batch_normalize = 0;
+    }
+    return ach_stream_sync(net->stream);
 }
 
 /* DnnUtils.topK (DnnUtils.c:463-477): indices of the k largest of a[0..n),

@@ -165,6 +165,11 @@ int an_forward(an_network *net, int train);
  * (batch-norm on the rolling statistics, dropout off, no truth); copies the
  * last layer's output, batch x outputs floats, to host_output.              */
 int an_predict(an_network *net, const float *host_input, float *host_output);
+/* NNetwork.fuseConvBatchnorm (NNetwork.c:272-288): fold every batch-norm conv
+ * layer's inference BN into its filters and biases (ach_conv_bn_fold) and
+ * make it a plain conv layer with bias; synchronous.  Used before inference
+ * (Classifier.c:369-373).                                                   */
+int an_fuse_conv_batchnorm(an_network *net);
 /* DnnUtils.topK (DnnUtils.c:463-477): the k largest of a[0..n), largest
  * first (ties ordered as the reference's strict-'>' insertion leaves them);
  * host-only                                                                 */

@@ -177,6 +177,14 @@ int ach_bn_train_fwd_from_x(const float *x, float *out, int batch, int c, int sp
 int ach_bn_infer(const float *x, float *out, int batch, int c, int spatial,
                  const float *scales, const float *biases, const float *rolling_mean,
                  const float *rolling_variance, int activation, ach_stream_t stream);
+/* Conv-BN folding for inference (ConvolutionalLayer.fuseConvBatchnorm,
+ * ConvolutionalLayer.c:983-1003): per filter f, r = sqrt((double)
+ * rolling_variance[f] + 1e-5); biases[f] -= scales[f]*rolling_mean[f]/r and
+ * weights[f][0..fsize) *= scales[f]/r, in double, rounded once to float.
+ * weights is [filters][fsize] (fsize = C*k*k), updated in place.           */
+int ach_conv_bn_fold(int filters, int fsize, float *weights, float *biases,
+                     const float *scales, const float *rolling_mean,
+                     const float *rolling_variance, ach_stream_t stream);
 /* Backward (backwardNormCPU NLayer.c:246-278): scale_updates += sum(d*x_norm);
  * d *= scales; mean_delta, variance_delta; d <- normalize_delta.  No beta
  * gradient (the CPU path computes none).  If activation is ACH_LEAKY/RELU the

@@ -355,6 +355,25 @@ void or_bn_normalize_roll(float *out, int batch, int channels, int spatial,
     }
 }
 
+/* ConvolutionalLayer.fuseConvBatchnorm (ConvolutionalLayer.c:983-1003): fold
+ * the inference BN of one conv layer into its filters and biases.  Per filter
+ * f, with r = sqrt((double)rolling_variance[f] + 1e-5):
+ *   biases[f]  <- biases[f] - scales[f] * rolling_mean[f] / r    (double)
+ *   weights[f] <- weights[f] * (scales[f] / r)                   (double)
+ * each rounded once to float.  Note the eps differs from normalizeByRoll's
+ * 1/(sqrt(var) + 1e-6), as in the reference.                               */
+void or_conv_bn_fold(int filters, int fsize, float *weights, float *biases,
+                     const float *scales, const float *rolling_mean,
+                     const float *rolling_variance)
+{
+    for (int f = 0; f < filters; ++f) {
+        double r = sqrt((double)rolling_variance[f] + .00001);
+        biases[f] = biases[f] - (double)scales[f] * rolling_mean[f] / r;
+        double pre = scales[f] / r;
+        for (int i = 0; i < fsize; ++i) weights[(size_t)f * fsize + i] *= pre;
+    }
+}
+
 /* Batch-norm backward: backwardNormCPU (NLayer.c:246-278) =
  *   ScaleData.backwardScale (ScaleData.c:76-107), NData.scale (NData.c:238-248),
  *   DeltaData.calcMean (DeltaData.c:23-38), calcVariance (:41-58),
@@ -1048,6 +1067,20 @@ void or_net_predict(or_net *net, const float *input, float *output)
     for (int i = 0; i < net->n; ++i) layer_forward(net, &net->layers[i], fwd_state(net, i, 0));
     const or_layer *last = &net->layers[net->n - 1];
     memcpy(output, last->output, sizeof(float) * (size_t)last->batch * last->outputs);
+}
+
+/* NNetwork.fuseConvBatchnorm (NNetwork.c:272-288), conv layers: fold each
+ * BN conv layer (or_conv_bn_fold) and turn it into a plain conv with bias
+ * (batch_normalize = 0; the BN arrays are no longer read).                 */
+void or_net_fuse_conv_batchnorm(or_net *net)
+{
+    for (int i = 0; i < net->n; ++i) {
+        or_layer *l = &net->layers[i];
+        if (l->type != L_CONV || !l->batch_normalize) continue;
+        or_conv_bn_fold(l->n, l->nweights / l->n, l->weights, l->biases, l->scales,
+                        l->rolling_mean, l->rolling_variance);
+        l->batch_normalize = 0;
+    }
 }
 
 float or_net_train(or_net *net, const float *input, const float *truth)

@@ -96,6 +96,13 @@ void or_bn_normalize_roll(float *out, int batch, int c, int spatial,
                           const float *rolling_mean, const float *rolling_variance,
                           const float *scales, const float *biases);
 
+/* ConvolutionalLayer.fuseConvBatchnorm (ConvolutionalLayer.c:983-1003):
+ * weights [filters][fsize] and biases [filters] absorb the inference BN
+ * (eps 1e-5 under the square root, double arithmetic, one float rounding) */
+void or_conv_bn_fold(int filters, int fsize, float *weights, float *biases,
+                     const float *scales, const float *rolling_mean,
+                     const float *rolling_variance);
+
 /* ---- activations (Activation.h:41-113, Activation.c:160-239) ------------ */
 void or_activate(float *x, int n, int act);
 void or_gradient(const float *y, int n, int act, float *delta);
@@ -163,6 +170,9 @@ void or_net_update(or_net *net);
 /* NNetwork.predict (NNetwork.c:411-422): inference forward (BN with rolling
  * statistics, dropout off, no truth); output = last layer's output          */
 void or_net_predict(or_net *net, const float *input, float *output);
+/* NNetwork.fuseConvBatchnorm (NNetwork.c:272-288): fold every BN conv layer
+ * (or_conv_bn_fold) and clear its batch_normalize flag                     */
+void or_net_fuse_conv_batchnorm(or_net *net);
 /* per-layer steps with the network's own state (NetworkState of
  * NNetwork.forward/backward): load one batch, then run layer i             */
 void or_net_load(or_net *net, const float *input, const float *truth);

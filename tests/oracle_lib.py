@@ -38,6 +38,7 @@ _SIGS = {
     "or_bn_normalize": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "or_bn_backward": (None, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "or_bn_normalize_roll": (None, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
+    "or_conv_bn_fold": (None, [_i, _i, _vp, _vp, _vp, _vp, _vp]),
     "or_activate": (None, [_vp, _i, _i]),
     "or_gradient": (None, [_vp, _i, _i, _vp]),
     "or_maxpool_out": (_i, [_i, _i, _i, _i]),
@@ -67,6 +68,7 @@ _SIGS = {
     "or_net_forward_backward": (_f, [_vp, _vp, _vp]),
     "or_net_update": (None, [_vp]),
     "or_net_predict": (None, [_vp, _vp, _vp]),
+    "or_net_fuse_conv_batchnorm": (None, [_vp]),
     "or_net_load": (None, [_vp, _vp, _vp]),
     "or_net_layer_forward": (None, [_vp, _i, _i]),
     "or_net_layer_backward": (None, [_vp, _i]),
@@ -164,6 +166,16 @@ def bn_normalize_roll(out, rolling_mean, rolling_var, scales, biases):
     lib().or_bn_normalize_roll(P(out), B, Cc, sp, P(f32(rolling_mean)), P(f32(rolling_var)),
                                P(f32(scales)), P(f32(biases)))
     return out
+
+
+def conv_bn_fold(weights, biases, scales, rolling_mean, rolling_var):
+    """ConvolutionalLayer.fuseConvBatchnorm; returns folded (weights, biases)"""
+    w = f32(weights).copy()
+    b = f32(biases).copy()
+    F = b.shape[0]
+    lib().or_conv_bn_fold(F, w.size // F, P(w), P(b), P(f32(scales)), P(f32(rolling_mean)),
+                          P(f32(rolling_var)))
+    return w, b
 
 
 def bn_backward(delta, x, xn, mean, var, scales, scale_updates=None):
@@ -302,6 +314,9 @@ class OracleNet:
         out = np.empty((self.batch, classes), np.float32)
         self.L.or_net_predict(self.h, P(f32(x)), P(out))
         return out
+
+    def fuse_conv_batchnorm(self):
+        self.L.or_net_fuse_conv_batchnorm(self.h)
 
     def load(self, x, truth):
         self.L.or_net_load(self.h, P(f32(x)), P(f32(truth)) if truth is not None else None)

@@ -276,3 +276,45 @@ def test_predict_matches_oracle(gpu, oracle, name, batch):
     assert net.iteration() == 0
     net.close()
     onet.close()
+
+
+@pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8)])
+def test_fused_predict_matches_oracle(gpu, oracle, name, batch):
+    """NNetwork.fuseConvBatchnorm then predict: the oracle's trained parameters
+    are loaded into the GPU network, both sides fold; the folded filters and
+    biases agree to 1 ulp, the fused predictions within 1e-4 with identical
+    labels where the top two are apart, and a saved file afterwards carries
+    no batch-norm arrays (the layers are plain convs, as in the reference)."""
+    oracle.lib().or_set_gemm_parallel(1)
+    net, onet = make_pair(oracle, name, batch)
+    for step in range(3):
+        x, truth, _ = configs.synthetic_batch(name, 500 + step, batch)
+        onet.train(x, truth)
+    for i in conv_layers(onet):
+        for code in (2, 4, 6, 8, 9):
+            v = onet.buffer(i, code)
+            if v is not None and v.size:
+                net.set_buffer(i, code, v)
+    onet.fuse_conv_batchnorm()
+    net.fuse_conv_batchnorm()
+    for i in conv_layers(onet):
+        for code in (2, 4):
+            a, b = net.buffer(i, code), onet.buffer(i, code)
+            ulp = np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+            assert ulp.max() <= 1, (i, code)
+    x, _, _ = configs.synthetic_batch(name, 600, batch)
+    p_ref = onet.predict(x)
+    p_gpu = net.predict(x)
+    assert rel_err(p_gpu, p_ref) < TOL
+    top2 = np.sort(p_ref, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 1e-5
+    assert np.array_equal(p_gpu.argmax(1)[clear], p_ref.argmax(1)[clear])
+    n_bias = sum(net.buffer(i, 4).size for i in conv_layers(onet))
+    n_w = sum(net.buffer(i, 2).size for i in conv_layers(onet))
+    path = os.path.join(ROOT, "gpurun_out", "fused_%s.weights" % name)
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    net.save_weights(path)
+    assert os.path.getsize(path) == 20 + 4 * (n_bias + n_w)
+    os.remove(path)
+    net.close()
+    onet.close()

@@ -236,6 +236,34 @@ def test_bn_infer(gpu, oracle, B, Cc, H, W, act):
     assert np.array_equal(d_rm.numpy(), rm) and np.array_equal(d_rv.numpy(), rv)
 
 
+@pytest.mark.parametrize("F,fsize", [(6, 27), (128, 1152), (512, 4608), (1000, 4096)])
+def test_conv_bn_fold(gpu, oracle, F, fsize):
+    """ach_conv_bn_fold vs the oracle's fuseConvBatchnorm: identical floats
+    (both round one double result per value; at most 1 ulp apart where the
+    oracle's -ffast-math build rewrites the double division)."""
+    rng = np.random.default_rng(F + fsize)
+    w = rng.normal(0, .1, (F, fsize)).astype(np.float32)
+    b = rng.normal(0, .2, F).astype(np.float32)
+    g = rng.uniform(.5, 2, F).astype(np.float32)
+    m = rng.uniform(-1, 1, F).astype(np.float32)
+    v = np.exp(rng.uniform(np.log(1e-6), np.log(10.), F)).astype(np.float32)
+    wr, br = oracle.conv_bn_fold(w, b, g, m, v)
+    d_w, d_b, d_g, d_m, d_v = dev(w), dev(b), dev(g), dev(m), dev(v)
+    check(gpu.ach_conv_bn_fold(F, fsize, d_w.ptr, d_b.ptr, d_g.ptr, d_m.ptr, d_v.ptr, None))
+    gw, gb = d_w.numpy(), d_b.numpy()
+    ulp_w = np.abs(gw.view(np.int32).astype(np.int64) - wr.view(np.int32).astype(np.int64))
+    ulp_b = np.abs(gb.view(np.int32).astype(np.int64) - br.view(np.int32).astype(np.int64))
+    assert ulp_w.max() <= 1 and ulp_b.max() <= 1
+    assert np.mean(ulp_w == 0) > 0.999
+    assert np.array_equal(d_g.numpy(), g) and np.array_equal(d_v.numpy(), v)
+
+
+def test_conv_bn_fold_errors(gpu):
+    d = dev(np.zeros(8, np.float32))
+    assert gpu.ach_conv_bn_fold(0, 4, d.ptr, d.ptr, d.ptr, d.ptr, d.ptr, None) == aetcnn.ACH_EINVAL
+    assert gpu.ach_conv_bn_fold(2, 4, None, d.ptr, d.ptr, d.ptr, d.ptr, None) == aetcnn.ACH_EINVAL
+
+
 @pytest.mark.parametrize("B,Cc,H,W", [(8, 16, 32, 32), (4, 24, 13, 13), (128, 32, 8, 8)])
 @pytest.mark.parametrize("act", [aetcnn.LINEAR, aetcnn.LEAKY, aetcnn.RELU])
 def test_bn_bwd(gpu, oracle, B, Cc, H, W, act):

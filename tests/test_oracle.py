@@ -439,3 +439,64 @@ def test_oracle_predict_composes_inference_ops():
     for key, v in before.items():
         assert np.array_equal(net.buffer(*key), v), key
     net.close()
+
+
+def test_conv_bn_fold_equals_conv_then_inference_affine():
+    """or_conv_bn_fold (ConvolutionalLayer.c:983-1003) pinned through the
+    convolution: a float64 brute-force conv with the folded filters plus the
+    folded bias equals the conv with the original filters followed by the
+    per-filter affine g*(y - m)/sqrt(v + 1e-5) + b.  Small variances (1e-6 ..)
+    make the eps placement visible (sqrt(v + 1e-5), not sqrt(v) + 1e-6), a
+    zero-mean filter would hide a dropped mean term, so the means are
+    non-zero; scaling filter f by another filter's factor fails too."""
+    rng = np.random.default_rng(12)
+    F, Cc, k = 6, 3, 3
+    x = rng.uniform(-1, 1, (2, Cc, 7, 7)).astype(np.float32)
+    w = rng.normal(0, .3, (F, Cc, k, k)).astype(np.float32)
+    b = rng.normal(0, .2, F).astype(np.float32)
+    g = rng.uniform(.5, 2, F).astype(np.float32)
+    m = rng.uniform(-1, 1, F).astype(np.float32)
+    v = np.array([1e-6, 3e-6, 1e-4, .01, 1., 4.], np.float32)
+    wf, bf = O.conv_bn_fold(w, b, g, m, v)
+    y = conv_ref(x, w, 1, 1)
+    r = np.sqrt(v.astype(np.float64) + 1e-5)[None, :, None, None]
+    want = (g[None, :, None, None] * (y - m[None, :, None, None]) / r
+            + b[None, :, None, None])
+    got = conv_ref(x, wf.reshape(w.shape), 1, 1) + bf.astype(np.float64)[None, :, None, None]
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+    # each folded value is one float rounding of the double result
+    pre = g.astype(np.float64) / np.sqrt(v.astype(np.float64) + 1e-5)
+    wd = w.reshape(F, -1).astype(np.float64) * pre[:, None]
+    assert np.max(np.abs(wf.reshape(F, -1) - wd) / np.abs(wd)) <= 2 ** -24
+    # an all-identity BN (g=1, m=0, v=1-1e-5) leaves the layer unchanged
+    wi, bi = O.conv_bn_fold(w, b, np.ones(F, np.float32), np.zeros(F, np.float32),
+                            np.full(F, 1 - 1e-5, np.float32))
+    assert np.max(np.abs(wi - w) / np.abs(w)) <= 2 ** -23 and np.array_equal(bi, b)
+
+
+def test_oracle_fused_network_predicts_like_unfused():
+    """or_net_fuse_conv_batchnorm (NNetwork.c:272-288) after training: the BN
+    conv layers become plain convs (biases absorb the shift) and the fused
+    predictions equal the unfused inference up to the reference's eps
+    difference between the fold (sqrt(v + 1e-5)) and normalizeByRoll
+    (sqrt(v) + 1e-6); the predicted labels agree wherever the top two
+    probabilities are apart."""
+    from aetcnn import configs
+    L = O.lib()
+    L.or_rand_seed(5)
+    B, h, w, c = configs.dims("tiny", 8)
+    net = O.OracleNet(B, h, w, c)
+    configs.build(net, "tiny")
+    net.finalize()
+    for s in range(4):
+        x, truth, _ = configs.synthetic_batch("tiny", 40 + s, B)
+        net.train(x, truth)
+    x, _, _ = configs.synthetic_batch("tiny", 77, B)
+    p0 = net.predict(x)
+    net.fuse_conv_batchnorm()
+    p1 = net.predict(x)
+    assert rel_err(p1, p0) < 1e-3
+    top2 = np.sort(p0, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 1e-3
+    assert np.array_equal(p1.argmax(1)[clear], p0.argmax(1)[clear])
+    net.close()
