@@ -18,9 +18,11 @@
 // owns a (BM/WM) x (128/WN) sub-tile of v_mfma_f32_32x32x2f32 accumulators.
 // Operands are fetched with buffer loads whose out-of-range offsets return
 // zero in hardware, so padding, ragged K and partial tiles cost no branches.
-// Loads for k-tile t+1 are issued into registers before the MFMAs of tile t
-// and then written to the other half of a double-buffered LDS stage (one
-// barrier per k-tile).  For 3x3 filters the k-tile is 18 = two input
+// The global loads of k-tile t+1 are issued among the MFMAs of the first two
+// k-steps of tile t and written to the other half of a double-buffered LDS
+// stage among the MFMAs of its last k-step (one barrier per k-tile); the
+// scheduler is told to interleave them with the MFMAs so they issue in the
+// matrix pipe's shadow.  For 3x3 filters the k-tile is 18 = two input
 // channels, which makes the im2col (ki, kj) of every loaded row a
 // compile-time constant.  Workgroups are remapped so that the M-tiles
 // sharing an N-tile (the same input patch) run on the same XCD and share its
@@ -153,15 +155,53 @@ struct AWeightsT4 {
             ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
         }
     }
+    // LDS rows the stores touch: the last pass may run past BK (zeros that
+    // no MFMA reads), so the stage is allocated with ROWS >= BK rows and the
+    // stores need no branch
+    static constexpr int ROWS = (NV * GNT + C4 - 1) / C4;
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
     {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int f = threadIdx.x + GNT * i;
-            if (f < BK * C4)
-                *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
-                    make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
+            *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
+                make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
+        }
+    }
+};
+
+// AWeightsT4 for problems whose every k-tile is full (K a multiple of BK):
+// the per-thread byte offsets of the NV float4 (or the out-of-range offset
+// for columns past M and rows past BK) are loop-invariant, and a k-tile only
+// adds the uniform k0*M*4.  Past K (the prefetch after the last tile) the
+// loads read beyond the buffer or the next split's rows; those values are
+// never used.
+template <int BM, int BK>
+struct AWeightsT4F : AWeightsT4<BM, BK> {
+    using Base = AWeightsT4<BM, BK>;
+    using Base::NV;
+    using Base::C4;
+    unsigned voff[NV];
+    int M4;
+    __device__ __forceinline__ void init(const float *wt, int M_, int K_, int m0_, int)
+    {
+        Base::init(wt, M_, K_, m0_, 0);
+        M4 = M_ * 4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + GNT * i;
+            const int row = f / C4, m = m0_ + 4 * (f % C4);
+            voff[i] = (f < BK * C4 && m < M_) ? (unsigned)(row * M_ + m) * 4u : kOOB;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int, float *ra) const
+    {
+        const unsigned d = (unsigned)(k0 * M4);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const float4 v = bload4(this->rs, (int)(voff[i] + d));
+            ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
         }
     }
 };
@@ -226,6 +266,32 @@ struct BIm2col3 {
         for (int j = 0; j < HC; ++j)
 #pragma unroll
             for (int i = 0; i < 9; ++i) S[(kr * HC + j) * 9 + i][nc] = rb[j * 9 + i];
+    }
+};
+
+// BIm2col3 for inputs with an even channel count (every k-tile full): the
+// nine byte offsets of the thread's first channel (out-of-range where the
+// tap falls in the padding) are loop-invariant; a k-tile adds the uniform
+// (k0/9)*H*W*4.  Out-of-range offsets stay >= 2^31 after the addition.
+struct BIm2col3F : BIm2col3 {
+    static constexpr bool FULL_K = true;
+    unsigned voff[9];
+    unsigned hw4;
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
+                                         int tid)
+    {
+        BIm2col3::init(x, g, N, n0, tid);
+        hw4 = (unsigned)HW * 4u;
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            voff[i] = ((valid >> i) & 1u) ? (unsigned)(base + (i / 3) * W + (i % 3)) * 4u : kOOB;
+    }
+    __device__ __forceinline__ void load(int k0, int, float *rb) const
+    {
+        static_assert(HC == 1, "one channel per thread group");
+        const unsigned d = (unsigned)(k0 / 9) * hw4;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) rb[i] = bload(rs, (int)(voff[i] + d));
     }
 };
 
@@ -446,7 +512,11 @@ template <int BM_, class BL, bool VECA = false>
 struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
     // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
-    using AL = typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type;
+    using AL = typename std::conditional<
+        VECA,
+        typename std::conditional<std::is_same<BL, BIm2col3F>::value, AWeightsT4F<BM, BK>,
+                                  AWeightsT4<BM, BK>>::type,
+        AWeightsT<BM, BK>>::type;
     using BLd = BL;
     const float *x, *w;
     float *y, *part;
@@ -521,6 +591,16 @@ struct GemmProblem {
 };
 
 // ===========================================================================
+// LDS rows of the A stage: BK, or more for a loader whose branch-free stores
+// run past BK (AWeightsT4::ROWS)
+template <class L, class = void> struct has_rows : std::false_type {};
+template <class L> struct has_rows<L, std::void_t<decltype(L::ROWS)>> : std::true_type {};
+template <class L, int BK> constexpr int a_rows()
+{
+    if constexpr (has_rows<L>::value) return L::ROWS > BK ? L::ROWS : BK;
+    else return BK;
+}
+
 template <class P>
 __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 {
@@ -530,7 +610,8 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
     static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
     constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
-    __shared__ __attribute__((aligned(16))) float As[2][BK][LA];
+    constexpr int AROWS = a_rows<typename P::AL, BK>();
+    __shared__ __attribute__((aligned(16))) float As[2][AROWS][LA];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK][LB];
 
     const int tid = threadIdx.x;
@@ -570,14 +651,12 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     __syncthreads();
 
     const int lrow = lane >> 5, lcol = lane & 31;
+    constexpr int KB_LOAD = BK > 2 ? 2 : 0;  // k-step that issues the B loads
     for (int kt = 0; kt < nkt; ++kt) {
         const int cur = kt & 1;
-        const bool more = kt + 1 < nkt;
-        if (more) {
-            const int k0 = kb + (kt + 1) * BK;
-            al.load(k0, ke, ra);
-            bl.load(k0, ke, rb);
-        }
+        // next k-tile (past ke on the last tile: every load reads as zero and
+        // the stores go to the stage nobody reads again)
+        const int k0n = kb + (kt + 1) * BK;
         // fragments of k-step kk+2 are read from LDS while the MFMAs of
         // k-step kk issue, so the LDS latency hides behind the matrix pipe
         float a[2][TM], b[2][TN];
@@ -598,16 +677,38 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
             }
             // keep the scheduler from sinking those reads below the MFMAs
             __builtin_amdgcn_sched_barrier(0);
+            if (kk == 0) al.load(k0n, ke, ra);
+            if (kk == KB_LOAD) bl.load(k0n, ke, rb);
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][i], b[s][j], acc[i][j],
                                                                      0, 0, 0);
-        }
-        if (more) {
-            al.template store<LA>(As[cur ^ 1], ra);
-            bl.template store<LB>(Bs[cur ^ 1], rb);
+            if (kk == BK - 2) {
+                al.template store<LA>(As[cur ^ 1], ra);
+                bl.template store<LB>(Bs[cur ^ 1], rb);
+            }
+            // interleave: per MFMA one LDS read, a few VALU and one global
+            // load (k-steps 0 and 2) or two LDS writes (last k-step)
+            // (group masks: 0x008 MFMA, 0x100 DS read, 0x002 VALU,
+            //  0x020 VMEM read, 0x200 DS write)
+            if (kk == 0 || kk == KB_LOAD) {
+#pragma unroll
+                for (int t = 0; t < TM * TN; ++t) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                }
+            } else if (kk == BK - 2) {
+#pragma unroll
+                for (int t = 0; t < TM * TN; ++t) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+                }
+            }
         }
         __syncthreads();
     }
@@ -854,6 +955,10 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
                   float *y, float *part, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
+    if (g.KS == 3 && (M & 3) == 0 && (g.C & 1) == 0) {
+        FwdProblem<BM, BIm2col3F, true> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        return launch_gemm(p, M, N, pl.splits, st);
+    }
     if (g.KS == 3 && (M & 3) == 0) {
         FwdProblem<BM, BIm2col3, true> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
         return launch_gemm(p, M, N, pl.splits, st);
