@@ -359,7 +359,7 @@ struct BIm2colAny {
 // tid/BK + (256/BK)*i; both operands are read in BK-long runs along k, and
 // the (c, ki, kj) of a thread's B rows are loop-invariant and precomputed.
 struct WgradDivs {
-    FastDiv ohw, ow;
+    FastDiv ohw, ow, batch;
 };
 
 template <int BM, int BK_>
@@ -458,6 +458,95 @@ struct BWgrad {
     }
 };
 
+// Weight gradient over output planes with OH*OW % 16 == 0, K reordered as
+// k = (chunk*B + b)*16 + q: position p = chunk*16 + q of image b.  A split
+// covers images [b0, b1) of ONE position chunk, so each thread's position
+// (q = tid % 16), and with it every output row / input tap it reads, is fixed
+// for the whole split: the byte offsets are computed once and a k-tile (one
+// image) only adds the uniform image stride.  Offsets of invalid elements
+// are >= 2^31 and stay out of range after the addition (operands < 2 GiB).
+template <int BM, int BK_>
+struct AWgradC {
+    static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = LDP;
+    static_assert(BK == 16, "one 16-position chunk per k-tile");
+    __amdgpu_buffer_rsrc_t rs;
+    unsigned voff[RA];
+    unsigned img;      // bytes per image of dy
+    FastDiv db;
+    __device__ __forceinline__ void init(const float *dy, const ConvGeom &g, const WgradDivs &dv,
+                                         int M, int m0, int tid, int kb)
+    {
+        const int ohw = g.OH * g.OW;
+        rs = make_rsrc(dy, (unsigned)((size_t)g.B * M * ohw * 4));
+        img = (unsigned)(M * ohw) * 4u;
+        db = dv.batch;
+        const int p = fdiv(kb >> 4, db) * 16 + tid % BK;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) {
+            const int m = m0 + tid / BK + RPI * i;
+            voff[i] = m < M ? (unsigned)(m * ohw + p) * 4u : kOOB;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int, float *ra) const
+    {
+        const int t = k0 >> 4;
+        const unsigned d = (unsigned)(t - fdiv(t, db) * (int)db.d) * img;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) ra[i] = bload(rs, (int)(voff[i] + d));
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
+    {
+        const int r = threadIdx.x / BK, kc = threadIdx.x % BK;
+#pragma unroll
+        for (int i = 0; i < RA; ++i) S[kc][r + RPI * i] = ra[i];
+    }
+};
+
+template <int BN, int BK_, int KS_T>
+struct BWgradC {
+    static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = LDP;
+    static_assert(BK == 16, "one 16-position chunk per k-tile");
+    __amdgpu_buffer_rsrc_t rs;
+    unsigned voff[RB];
+    unsigned img;      // bytes per image of x
+    FastDiv db;
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, const WgradDivs &dv,
+                                         int N, int n0, int tid, int kb)
+    {
+        rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
+        img = (unsigned)(g.C * g.H * g.W) * 4u;
+        db = dv.batch;
+        const int p = fdiv(kb >> 4, db) * 16 + tid % BK;
+        const int oh = fdiv(p, dv.ow), ow = p - oh * g.OW;
+        const int ihb = oh * g.S - g.P, iwb = ow * g.S - g.P;
+        const int ks = KS_T ? KS_T : g.KS, kk2 = ks * ks;
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int n = n0 + tid / BK + RPI * i;
+            const int c = n / kk2, t = n - c * kk2;
+            const int ki = t / ks, kj = t - ki * ks;
+            const int ih = ihb + ki, iw = iwb + kj;
+            const bool v = n < N && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+            voff[i] = v ? (unsigned)((c * g.H + ih) * g.W + iw) * 4u : kOOB;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int, float *rb) const
+    {
+        const int t = k0 >> 4;
+        const unsigned d = (unsigned)(t - fdiv(t, db) * (int)db.d) * img;
+#pragma unroll
+        for (int i = 0; i < RB; ++i) rb[i] = bload(rs, (int)(voff[i] + d));
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S_)[LD], const float *rb) const
+    {
+        const int r = threadIdx.x / BK, kc = threadIdx.x % BK;
+#pragma unroll
+        for (int i = 0; i < RB; ++i) S_[kc][r + RPI * i] = rb[i];
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Plain row-major GEMM operands (Gemm.c:116-144), BK = 16.
 template <bool T, int BR>
@@ -527,8 +616,8 @@ struct FwdProblem {
         kb = z * kchunk;
         ke = min(K, kb + kchunk);
     }
-    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(w, M, K, m0, tid); }
-    __device__ __forceinline__ void init_b(BL &b, int n0, int tid) const { b.init(x, g, N, n0, tid); }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(w, M, K, m0, tid); }
+    __device__ __forceinline__ void init_b(BL &b, int n0, int tid, int) const { b.init(x, g, N, n0, tid); }
     __device__ __forceinline__ void store(int m, int n, float v, int z) const
     {
         if (m >= M || n >= N) return;
@@ -557,8 +646,39 @@ struct WgradProblem {
         kb = z * kchunk;
         ke = min(K, kb + kchunk);
     }
-    __device__ __forceinline__ void init_a(AL &a, int m0, int tid) const { a.init(dy, g, dv, M, m0, tid); }
-    __device__ __forceinline__ void init_b(BLd &b, int n0, int tid) const { b.init(x, g, dv, N, n0, tid); }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(dy, g, dv, M, m0, tid); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int tid, int) const { b.init(x, g, dv, N, n0, tid); }
+    __device__ __forceinline__ void store(int m, int n, float v, int z) const
+    {
+        if (m >= M || n >= N) return;
+        if (splits == 1)
+            dw[(size_t)m * N + n] += v;
+        else
+            part[((size_t)z * M + m) * N + n] = v;
+    }
+};
+
+// Weight gradient in the chunked K order (AWgradC / BWgradC): split z takes
+// chunk z / spc and images [(z % spc)*nbs, min(B, (z % spc + 1)*nbs)).
+template <int BM_, int BN_, int KS_T>
+struct WgradProblemC {
+    static constexpr int BM = BM_, BN = BN_, BK = WGRAD_BK;
+    using AL = AWgradC<BM, BK>;
+    using BLd = BWgradC<BN, BK, KS_T>;
+    const float *x, *dy;
+    float *dw, *part;
+    ConvGeom g;
+    WgradDivs dv;
+    int M, N, spc, nbs, splits;
+    __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
+    {
+        const int chunk = z / spc, j = z - chunk * spc;
+        const int b0 = j * nbs, b1 = min(g.B, b0 + nbs);
+        kb = (chunk * g.B + b0) * 16;
+        ke = (chunk * g.B + b1) * 16;
+    }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int kb) const { a.init(dy, g, dv, M, m0, tid, kb); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int tid, int kb) const { b.init(x, g, dv, N, n0, tid, kb); }
     __device__ __forceinline__ void store(int m, int n, float v, int z) const
     {
         if (m >= M || n >= N) return;
@@ -580,8 +700,8 @@ struct GemmProblem {
     size_t abytes, bbytes;
     float alpha, beta;
     __device__ __forceinline__ void krange(int, int &kb, int &ke) const { kb = 0; ke = K; }
-    __device__ __forceinline__ void init_a(AL &a, int m0, int) const { a.init(A, M, K, lda, abytes, m0); }
-    __device__ __forceinline__ void init_b(BLd &b, int n0, int) const { b.init(Bm, N, K, ldb, bbytes, n0); }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int, int) const { a.init(A, M, K, lda, abytes, m0); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int, int) const { b.init(Bm, N, K, ldb, bbytes, n0); }
     __device__ __forceinline__ void store(int m, int n, float v, int) const
     {
         if (m >= M || n >= N) return;
@@ -629,8 +749,8 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     p.krange(z, kb, ke);
     typename P::AL al;
     typename P::BLd bl;
-    p.init_a(al, m0, tid);
-    p.init_b(bl, n0, tid);
+    p.init_a(al, m0, tid, kb);
+    p.init_b(bl, n0, tid, kb);
 
     v16f acc[TM][TN];
 #pragma unroll
@@ -999,8 +1119,40 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Split count for wgrad: aim for >= ~1024 workgroups over 256 CUs, K chunks a
 // multiple of the k-tile.
+#ifndef ACH_WGRAD_CHUNKED
+#define ACH_WGRAD_CHUNKED 1
+#endif
+// the chunked K order applies when the output plane is a whole number of
+// 16-position chunks
+static bool wgrad_chunked(const ConvGeom &g)
+{
+    return ACH_WGRAD_CHUNKED && (g.OH * g.OW) % 16 == 0;
+}
+
+// chunked split: spc splits per position chunk, nbs images each, aiming at
+// ACH_WGRAD_TARGET workgroups (tiles x splits) with >= 4 images per split
+static void wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits, int &spc,
+                                int &nbs)
+{
+    const int M = g.F, N = g.C * g.KS * g.KS, nchunks = g.OH * g.OW / 16;
+    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    long long want = (ACH_WGRAD_TARGET + tiles * nchunks - 1) / (tiles * nchunks);
+    const int max_spc = g.B >= 4 ? g.B / 4 : 1;
+    if (want > max_spc) want = max_spc;
+    if (want < 1) want = 1;
+    nbs = (g.B + (int)want - 1) / (int)want;
+    spc = (g.B + nbs - 1) / nbs;
+    splits = nchunks * spc;
+}
+
 static void wgrad_split(const ConvGeom &g, int bm, int bn, int &splits, int &kchunk)
 {
+    if (wgrad_chunked(g)) {
+        int spc, nbs;
+        wgrad_split_chunked(g, bm, bn, splits, spc, nbs);
+        kchunk = 0;
+        return;
+    }
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
     const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int bk = WGRAD_BK;
@@ -1036,6 +1188,22 @@ static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, floa
     WgradDivs dv;
     dv.ohw = make_fastdiv((unsigned)(g.OH * g.OW));
     dv.ow = make_fastdiv((unsigned)g.OW);
+    dv.batch = make_fastdiv((unsigned)g.B);
+    if (wgrad_chunked(g)) {
+        int spc, nbs;
+        wgrad_split_chunked(g, BM, BN, splits, spc, nbs);
+        if (splits > 65535) return ACH_EUNSUPPORTED;
+        if (g.KS == 3) {
+            WgradProblemC<BM, BN, 3> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits};
+            return launch_gemm(p, M, N, splits, st);
+        }
+        if (g.KS == 1) {
+            WgradProblemC<BM, BN, 1> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits};
+            return launch_gemm(p, M, N, splits, st);
+        }
+        WgradProblemC<BM, BN, 0> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits};
+        return launch_gemm(p, M, N, splits, st);
+    }
     if (g.KS == 3) {
         WgradProblem<BM, BN, 3> p{x, dy, dw, part, g, dv, M, N, K, kchunk, splits};
         return launch_gemm(p, M, N, splits, st);
