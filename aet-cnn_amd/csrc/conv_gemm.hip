@@ -1122,6 +1122,9 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 #ifndef ACH_WGRAD_CHUNKED
 #define ACH_WGRAD_CHUNKED 1
 #endif
+#ifndef ACH_WGRAD_TARGET_CHUNKED
+#define ACH_WGRAD_TARGET_CHUNKED 1024  // measured: 1024 beats 512, 1536 and 2048
+#endif
 // the chunked K order applies when the output plane is a whole number of
 // 16-position chunks
 static bool wgrad_chunked(const ConvGeom &g)
@@ -1130,13 +1133,13 @@ static bool wgrad_chunked(const ConvGeom &g)
 }
 
 // chunked split: spc splits per position chunk, nbs images each, aiming at
-// ACH_WGRAD_TARGET workgroups (tiles x splits) with >= 4 images per split
+// ACH_WGRAD_TARGET_CHUNKED workgroups (tiles x splits), >= 4 images per split
 static void wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits, int &spc,
                                 int &nbs)
 {
     const int M = g.F, N = g.C * g.KS * g.KS, nchunks = g.OH * g.OW / 16;
     const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    long long want = (ACH_WGRAD_TARGET + tiles * nchunks - 1) / (tiles * nchunks);
+    long long want = (ACH_WGRAD_TARGET_CHUNKED + tiles * nchunks - 1) / (tiles * nchunks);
     const int max_spc = g.B >= 4 ? g.B / 4 : 1;
     if (want > max_spc) want = max_spc;
     if (want < 1) want = 1;
