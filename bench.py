@@ -33,9 +33,9 @@ ROOFLINE_SHAPE = (256, 256, 16, 3, 1)  # dominant kernel probe: conv fwd GEMM
 # HBM bytes per probe call (filter transpose + split-K GEMM + split-K
 # reduction), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs scaled by a
 # 256 MiB copy dispatch (profiles/conv_fwd_gemm_darknet_b128.md):
-# GEMM 53.1 MB read + 67.1 MB written, reduction 67.2 + 33.6 MB,
+# GEMM 53.7 MB read + 67.1 MB written, reduction 67.1 + 33.6 MB,
 # transpose 2.4 + 2.4 MB.
-ROOFLINE_TRAFFIC_BYTES = 225.6e6
+ROOFLINE_TRAFFIC_BYTES = 226.2e6
 
 
 def log(msg):
@@ -228,7 +228,7 @@ def roofline_phase(aetcnn, batch, reps):
     for a in (x, w, y, ws):
         a.free()
     ops.ach_stream_destroy(stream)
-    return dict(kernel="k_mfma_gemm<FwdProblem<256, BIm2col3, true>> (conv fwd / dgrad implicit GEMM)",
+    return dict(kernel="k_mfma_gemm<FwdProblem<256, BIm2col3F, true>> (conv fwd / dgrad implicit GEMM)",
                 shape=f"{ci}->{co}@{hw}x{hw} k{k} b{batch}", flop=flop, ms=ms, reps=reps)
 
 
