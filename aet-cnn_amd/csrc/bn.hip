@@ -30,9 +30,11 @@ namespace ach {
 constexpr int BN_NT = 256;  // threads per block
 constexpr int BN_U = 4;     // elements (float or float4) per thread in apply
 
+// reduction blocks: about 4096 (channel, image chunk) blocks in all
+// (measured 1-2% faster than 1024 or 2048 on config 2)
 static int bn_chunks(int batch, int c)
 {
-    int nch = (2048 + c - 1) / c;
+    int nch = (4096 + c - 1) / c;
     if (nch > batch) nch = batch;
     if (nch < 1) nch = 1;
     return nch;
