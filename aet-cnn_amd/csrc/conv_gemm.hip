@@ -295,6 +295,102 @@ struct BIm2col3F : BIm2col3 {
     }
 };
 
+// B for the forward pass with a KS x KS kernel, one input channel per k-tile:
+// BK = KS*KS + 1 rows, the last a zero row (KS*KS is odd and a k-step of the
+// MFMA takes two rows), so the GEMM runs over a padded K = C*BK.  Thread ->
+// column n0 + tid%128 and half kr = tid/128 of the BK rows; the byte offsets
+// of its taps (out-of-range for padding taps and the zero row) are
+// loop-invariant and a k-tile adds the uniform channel stride.  Used for
+// 5x5 (BK = 26); larger kernels would not leave room for two workgroups'
+// LDS stages per CU.
+template <int KS>
+struct BIm2colK {
+    static constexpr int T = KS * KS, BK = T + 1, HALF = BK / 2, RB = HALF, PAD = LDP;
+    static_assert(T % 2 == 1, "odd kernel: one zero row completes the k-step");
+    __amdgpu_buffer_rsrc_t rs;
+    unsigned voff[HALF];
+    unsigned hw4;
+    int kr;
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
+                                         int tid)
+    {
+        rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
+        const int n = n0 + tid % GBN;
+        kr = tid / GBN;
+        const int HW = g.H * g.W;
+        hw4 = (unsigned)HW * 4u;
+        const int ohw = g.OH * g.OW;
+        const bool nok = n < N;
+        const int nn = nok ? n : 0;
+        const int b = nn / ohw, p = nn - b * ohw;
+        const int oh = p / g.OW, ow = p - oh * g.OW;
+        const int ihb = oh * g.S - g.P, iwb = ow * g.S - g.P;
+        const int base = b * g.C * HW + ihb * g.W + iwb;
+#pragma unroll
+        for (int j = 0; j < HALF; ++j) {
+            const int t = kr * HALF + j;
+            const int ki = t / KS, kj = t - (t / KS) * KS;
+            const bool v = nok && t < T && (unsigned)(ihb + ki) < (unsigned)g.H &&
+                           (unsigned)(iwb + kj) < (unsigned)g.W;
+            voff[j] = v ? (unsigned)(base + ki * g.W + kj) * 4u : kOOB;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int, float *rb) const
+    {
+        const unsigned d = (unsigned)(k0 / BK) * hw4;
+#pragma unroll
+        for (int j = 0; j < HALF; ++j) rb[j] = bload(rs, (int)(voff[j] + d));
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
+    {
+        const int nc = threadIdx.x % GBN;
+#pragma unroll
+        for (int j = 0; j < HALF; ++j) S[kr * HALF + j][nc] = rb[j];
+    }
+};
+
+// The k-major weights for BIm2colK: padded k-tile c covers weight rows
+// c*T .. c*T + T-1 and a zero row; float4 loads with loop-invariant offsets.
+template <int BM, int KS>
+struct AWeightsT4K : AWeightsT4<BM, KS * KS + 1> {
+    static constexpr int T = KS * KS, BK = T + 1;
+    using Base = AWeightsT4<BM, BK>;
+    using Base::NV;
+    using Base::C4;
+    unsigned voff[NV];
+    int TM4;
+    __device__ __forceinline__ void init(const float *wt, int M_, int K_, int m0_, int)
+    {
+        Base::init(wt, M_, K_, m0_, 0);
+        TM4 = T * M_ * 4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + GNT * i;
+            const int row = f / C4, m = m0_ + 4 * (f % C4);
+            voff[i] = (f < BK * C4 && row < T && m < M_) ? (unsigned)(row * M_ + m) * 4u : kOOB;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int, float *ra) const
+    {
+        const unsigned d = (unsigned)(k0 / BK) * (unsigned)TM4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const float4 v = bload4(this->rs, (int)(voff[i] + d));
+            ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
+        }
+    }
+};
+
+template <class BL> struct PaddedTaps {
+    static constexpr bool value = false;
+    static constexpr int ks = 5;
+};
+template <int KS> struct PaddedTaps<BIm2colK<KS>> {
+    static constexpr bool value = true;
+    static constexpr int ks = KS;
+};
+
 // B for the forward pass with any kernel size, BK = 16: thread -> column
 // n0 + tid%128, rows tid/128 + 2*i.
 template <int KS_T>
@@ -602,10 +698,12 @@ struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
     // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
     using AL = typename std::conditional<
-        VECA,
-        typename std::conditional<std::is_same<BL, BIm2col3F>::value, AWeightsT4F<BM, BK>,
-                                  AWeightsT4<BM, BK>>::type,
-        AWeightsT<BM, BK>>::type;
+        PaddedTaps<BL>::value, AWeightsT4K<BM, PaddedTaps<BL>::ks>,
+        typename std::conditional<
+            VECA,
+            typename std::conditional<std::is_same<BL, BIm2col3F>::value, AWeightsT4F<BM, BK>,
+                                      AWeightsT4<BM, BK>>::type,
+            AWeightsT<BM, BK>>::type>::type;
     using BLd = BL;
     const float *x, *w;
     float *y, *part;
@@ -1040,20 +1138,32 @@ struct FwdPlan {
     int bm, bk, splits, kchunk;
 };
 
+// 5x5 filters with a filter count divisible by 4 take the padded-tap
+// loaders (BIm2colK<5> / AWeightsT4K)
+static bool fwd_padded_taps(const ConvGeom &g) { return g.KS == 5 && (g.F & 3) == 0; }
+
 static FwdPlan fwd_plan(const ConvGeom &g)
 {
     FwdPlan pl;
-    const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
+    const int M = g.F, N = g.B * g.OH * g.OW;
+    int K = g.C * g.KS * g.KS;
     pl.bm = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
     // 3x3 layers with a multiple of 256 filters: 256 x 128 tiles (each wave
     // 128 x 64), measured 2-5% faster on the 256- and 512-filter layers
     if (M % 256 == 0 && g.KS == 3) pl.bm = 256;
     pl.bk = g.KS == 3 ? BIm2col3::BK : 16;
+    if (fwd_padded_taps(g)) {  // 5x5: one channel + a zero row per k-tile
+        pl.bk = BIm2colK<5>::BK;
+        K = g.C * pl.bk;
+    }
     const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + 127) / 128);
     const int ktiles = (K + pl.bk - 1) / pl.bk;
     int s = 1;
-    if (tiles < 512) {
-        s = (512 + tiles - 1) / tiles;
+    // the padded-tap kernel fits two workgroups per CU: aim at two rounds
+    // (measured 0.5% faster on AlexNet than one)
+    const int target = fwd_padded_taps(g) ? 1024 : 512;
+    if (tiles < target) {
+        s = (target + tiles - 1) / tiles;
         if (s > 32) s = 32;
         if (s > ktiles / 8) s = ktiles / 8;  // keep >= 8 k-tiles per slice
         if (s < 1) s = 1;
@@ -1090,6 +1200,13 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     if (g.KS == 1) {
         FwdProblem<BM, BIm2colAny<1>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
         return launch_gemm(p, M, N, pl.splits, st);
+    }
+    if constexpr (BM <= 128) {
+        if (fwd_padded_taps(g)) {
+            FwdProblem<BM, BIm2colK<5>, true> p{x, w, y, part, g, M, N,
+                                                g.C * BIm2colK<5>::BK, pl.kchunk, pl.splits};
+            return launch_gemm(p, M, N, pl.splits, st);
+        }
     }
     FwdProblem<BM, BIm2colAny<0>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
     return launch_gemm(p, M, N, pl.splits, st);

@@ -95,6 +95,12 @@ CONV_SHAPES = [
     (3, 6, 12, 12, 20, 3, 1, 1),   # vector im2col loader, partial N tile, ragged K
     (2, 8, 10, 10, 16, 3, 1, 0),   # vector loader without padding (dgrad: pad 2)
     (2, 4, 4, 4, 8, 3, 1, 1),      # narrowest input the vector loader takes
+    # weight gradient in the chunked K order (OH*OW % 16 == 0):
+    (9, 16, 8, 8, 32, 3, 1, 1),    # odd batch split into uneven image ranges
+    (4, 8, 16, 16, 16, 3, 2, 1),   # stride 2
+    (4, 6, 8, 8, 12, 5, 1, 2),     # 5x5
+    (6, 24, 4, 4, 20, 1, 1, 0),    # 1x1 on a 16-position plane
+    (8, 16, 5, 5, 24, 3, 1, 1),    # 25 positions: the (image, position) order
 ]
 
 
