@@ -554,8 +554,9 @@ struct BWgrad {
     }
 };
 
-// Weight gradient over output planes with OH*OW % 16 == 0, K reordered as
-// k = (chunk*B + b)*16 + q: position p = chunk*16 + q of image b.  A split
+// Weight gradient with K reordered as k = (chunk*B + b)*16 + q: position
+// p = chunk*16 + q of image b, the plane padded to whole 16-position chunks
+// (positions p >= OH*OW read as zero).  A split
 // covers images [b0, b1) of ONE position chunk, so each thread's position
 // (q = tid % 16), and with it every output row / input tap it reads, is fixed
 // for the whole split: the byte offsets are computed once and a k-tile (one
@@ -580,7 +581,7 @@ struct AWgradC {
 #pragma unroll
         for (int i = 0; i < RA; ++i) {
             const int m = m0 + tid / BK + RPI * i;
-            voff[i] = m < M ? (unsigned)(m * ohw + p) * 4u : kOOB;
+            voff[i] = m < M && p < ohw ? (unsigned)(m * ohw + p) * 4u : kOOB;
         }
     }
     __device__ __forceinline__ void load(int k0, int, float *ra) const
@@ -623,7 +624,8 @@ struct BWgradC {
             const int c = n / kk2, t = n - c * kk2;
             const int ki = t / ks, kj = t - ki * ks;
             const int ih = ihb + ki, iw = iwb + kj;
-            const bool v = n < N && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+            const bool v = n < N && p < g.OH * g.OW && (unsigned)ih < (unsigned)g.H &&
+                           (unsigned)iw < (unsigned)g.W;
             voff[i] = v ? (unsigned)((c * g.H + ih) * g.W + iw) * 4u : kOOB;
         }
     }
@@ -1242,11 +1244,16 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 #ifndef ACH_WGRAD_TARGET_CHUNKED
 #define ACH_WGRAD_TARGET_CHUNKED 1024  // measured: 1024 beats 512, 1536 and 2048
 #endif
-// the chunked K order applies when the output plane is a whole number of
-// 16-position chunks
+#ifndef ACH_WGRAD_PAD_WASTE
+#define ACH_WGRAD_PAD_WASTE 0.0625  // largest padded fraction of a plane taken
+#endif
+// the chunked K order applies when padding the output plane to whole
+// 16-position chunks wastes at most ACH_WGRAD_PAD_WASTE of the work
+static int wgrad_nchunks(const ConvGeom &g) { return (g.OH * g.OW + 15) / 16; }
 static bool wgrad_chunked(const ConvGeom &g)
 {
-    return ACH_WGRAD_CHUNKED && (g.OH * g.OW) % 16 == 0;
+    const int ohw = g.OH * g.OW;
+    return ACH_WGRAD_CHUNKED && wgrad_nchunks(g) * 16 - ohw <= ACH_WGRAD_PAD_WASTE * ohw;
 }
 
 // chunked split: spc splits per position chunk, nbs images each, aiming at
@@ -1254,7 +1261,7 @@ static bool wgrad_chunked(const ConvGeom &g)
 static void wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits, int &spc,
                                 int &nbs)
 {
-    const int M = g.F, N = g.C * g.KS * g.KS, nchunks = g.OH * g.OW / 16;
+    const int M = g.F, N = g.C * g.KS * g.KS, nchunks = wgrad_nchunks(g);
     const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     long long want = (ACH_WGRAD_TARGET_CHUNKED + tiles * nchunks - 1) / (tiles * nchunks);
     const int max_spc = g.B >= 4 ? g.B / 4 : 1;
