@@ -826,7 +826,7 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 {
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK;
     // wave grid: 2x2 for 64+ x 128 tiles, 1x4 for 32-row, 4x1 for 32-column
-    constexpr int WM = BN <= 32 ? 4 : (BM >= 64 ? 2 : 1), WN = 4 / WM;
+    constexpr int WM = BN <= 32 ? 4 : (BM % 64 == 0 ? 2 : 1), WN = 4 / WM;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
     static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
     constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
@@ -1157,6 +1157,7 @@ static FwdPlan fwd_plan(const ConvGeom &g)
     if (fwd_padded_taps(g)) {  // 5x5: one channel + a zero row per k-tile
         pl.bk = BIm2colK<5>::BK;
         K = g.C * pl.bk;
+        if (M > 64 && M <= 96) pl.bm = 96;  // three 32-row MFMA tiles per wave
     }
     const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + 127) / 128);
     const int ktiles = (K + pl.bk - 1) / pl.bk;
@@ -1214,6 +1215,18 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     return launch_gemm(p, M, N, pl.splits, st);
 }
 
+// 96-row tiles (one wave column of three 32-row MFMA tiles) for the
+// padded-tap 5x5 path only: the other loaders assume BM | 256 or BM % 64 == 0
+template <int BM>
+static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, const float *w,
+                         float *y, float *part, hipStream_t st)
+{
+    const int M = g.F, N = g.B * g.OH * g.OW;
+    FwdProblem<BM, BIm2colK<5>, true> p{x, w, y, part, g, M, N, g.C * BIm2colK<5>::BK,
+                                        pl.kchunk, pl.splits};
+    return launch_gemm(p, M, N, pl.splits, st);
+}
+
 // w: k-major filter Wt[K][M]; part: fwd_part_bytes(g) of scratch (or NULL
 // when no split is planned)
 static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, float *part,
@@ -1222,6 +1235,7 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
     const FwdPlan pl = fwd_plan(g);
     int rc;
     if (pl.bm == 32) rc = fwd_bm<32>(g, pl, x, w, y, part, st);
+    else if (pl.bm == 96) rc = fwd_bm_padded<96>(g, pl, x, w, y, part, st);
     else if (pl.bm == 64) rc = fwd_bm<64>(g, pl, x, w, y, part, st);
     else if (pl.bm == 256) rc = fwd_bm<256>(g, pl, x, w, y, part, st);
     else rc = fwd_bm<128>(g, pl, x, w, y, part, st);

@@ -99,6 +99,7 @@ CONV_SHAPES = [
     (9, 16, 8, 8, 32, 3, 1, 1),    # odd batch split into uneven image ranges
     (4, 8, 16, 16, 16, 3, 2, 1),   # stride 2
     (4, 6, 8, 8, 12, 5, 1, 2),     # 5x5
+    (2, 96, 9, 9, 80, 5, 1, 2),    # 5x5 with 80 / 96 filters: 96-row tiles
     (6, 24, 4, 4, 20, 1, 1, 0),    # 1x1 on a 16-position plane
     (8, 16, 5, 5, 24, 3, 1, 1),    # 25 positions: the (image, position) order
 ]
