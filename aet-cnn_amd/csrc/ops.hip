@@ -157,6 +157,24 @@ __global__ void __launch_bounds__(256) k_bias_part(const float *__restrict__ d, 
     if (threadIdx.x == 0) part[(size_t)ch * n + c] = sh[0] + sh[1] + sh[2] + sh[3];
 }
 
+// Small planes (a fully connected layer's 1x1 output): one thread per
+// channel sums its batch x spatial values in (image, position) order, the
+// threads of a wave reading consecutive channels.
+constexpr int BIAS_SMALL_SPATIAL = 16;
+
+__global__ void __launch_bounds__(256) k_bias_small(const float *__restrict__ d, int batch, int n,
+                                                    int spatial, float *updates)
+{
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n) return;
+    double s = 0;
+    for (int b = 0; b < batch; ++b) {
+        const float *p = d + ((size_t)b * n + c) * spatial;
+        for (int q = 0; q < spatial; ++q) s += (double)p[q];
+    }
+    updates[c] += (float)s;
+}
+
 __global__ void k_bias_final(const double *__restrict__ part, int nch, int n, float *updates)
 {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -312,26 +330,33 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
     float v = accumulate ? din[p] : 0.f;
     const int obase = bc * OH * OW;
     if constexpr (SIZE > 0 && STRIDE > 0) {
-        // at most NC x NC windows hold a pixel: issue all their index loads,
-        // then the matching gradients, then add in ascending output order
+        // at most NC x NC windows hold a pixel, added in ascending output
+        // order.  Every candidate's index and gradient are loaded unconditionally
+        // (row / column clamped into the output plane, so each address is
+        // valid) and the sum takes a hit by selection, not by branch: the
+        // eight loads are in flight together.
         constexpr int NC = (SIZE + STRIDE - 1) / (STRIDE > 0 ? STRIDE : 1);
         int o[NC * NC];
-        bool hit[NC * NC];
+        bool in[NC * NC];
+        int32_t ix[NC * NC];
         float g[NC * NC];
 #pragma unroll
         for (int a = 0; a < NC; ++a)
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const int i = i0 + a, j = j0 + c;
-                const bool in = i <= i1 && j <= j1;
-                o[a * NC + c] = obase + i * OW + j;
-                hit[a * NC + c] = in && idx[o[a * NC + c]] == (int32_t)p;
+                in[a * NC + c] = i <= i1 && j <= j1;
+                o[a * NC + c] = obase + min(i, OH - 1) * OW + min(j, OW - 1);
             }
 #pragma unroll
-        for (int q = 0; q < NC * NC; ++q) g[q] = hit[q] ? dout[o[q]] : 0.f;
+        for (int q = 0; q < NC * NC; ++q) ix[q] = idx[o[q]];
 #pragma unroll
-        for (int q = 0; q < NC * NC; ++q)
-            if (hit[q]) v += g[q];
+        for (int q = 0; q < NC * NC; ++q) g[q] = dout[o[q]];
+#pragma unroll
+        for (int q = 0; q < NC * NC; ++q) {
+            const float t = v + g[q];
+            v = (in[q] && ix[q] == (int32_t)p) ? t : v;
+        }
     } else {
         for (int i = i0; i <= i1; ++i)
             for (int j = j0; j <= j1; ++j) {
@@ -712,6 +737,11 @@ int ach_bias_grad(float *updates, const float *delta, int batch, int n, int spat
 {
     if (!updates || !delta || batch <= 0 || n <= 0 || spatial <= 0 || n > 65535) return ACH_EINVAL;
     if (!ws || ws_bytes < ach_bias_grad_workspace(batch, n, spatial)) return ACH_EWORKSPACE;
+    if (spatial <= BIAS_SMALL_SPATIAL) {
+        hipLaunchKernelGGL(k_bias_small, dim3((n + 255) / 256), dim3(256), 0, as_stream(s), delta,
+                           batch, n, spatial, updates);
+        return check_launch();
+    }
     const int nch = (batch + BIAS_IMGS - 1) / BIAS_IMGS;
     double *part = (double *)ws;
     hipLaunchKernelGGL(k_bias_part, dim3(n, nch), dim3(256), 0, as_stream(s), delta, batch, n,

@@ -421,9 +421,12 @@ def test_conv_update(gpu, oracle):
         assert rel_err(a.numpy(), r) < 1e-6
 
 
-def test_bias_ops(gpu, oracle):
-    rng = np.random.default_rng(12)
-    B, n, sp = 16, 10, 64
+@pytest.mark.parametrize("B,n,sp", [(16, 10, 64), (8, 300, 1), (5, 40, 12), (9, 6, 169)])
+def test_bias_ops(gpu, oracle, B, n, sp):
+    """add_bias bit-exact; bias gradient (large planes: two-pass partials;
+    planes of <= 16 positions, e.g. FC outputs: one thread per channel)
+    within 1e-5 of the oracle's sums."""
+    rng = np.random.default_rng(12 + B + n + sp)
     out = rng.standard_normal((B, n, sp)).astype(np.float32)
     bias = rng.standard_normal(n).astype(np.float32)
     ref = out.copy()
