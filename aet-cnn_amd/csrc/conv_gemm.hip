@@ -748,11 +748,17 @@ struct WgradProblem {
     }
     __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(dy, g, dv, M, m0, tid); }
     __device__ __forceinline__ void init_b(BLd &b, int n0, int tid, int) const { b.init(x, g, dv, N, n0, tid); }
-    __device__ __forceinline__ void store(int m, int n, float v, int z) const
+    // read-modify-write epilogue: prior() of a whole fragment, then store()
+    static constexpr bool RMW = true;
+    __device__ __forceinline__ float prior(int m, int n, int) const
+    {
+        return (m < M && n < N && splits == 1) ? dw[(size_t)m * N + n] : 0.f;
+    }
+    __device__ __forceinline__ void store(int m, int n, float v, float old, int z) const
     {
         if (m >= M || n >= N) return;
         if (splits == 1)
-            dw[(size_t)m * N + n] += v;
+            dw[(size_t)m * N + n] = old + v;
         else
             part[((size_t)z * M + m) * N + n] = v;
     }
@@ -779,11 +785,17 @@ struct WgradProblemC {
     }
     __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int kb) const { a.init(dy, g, dv, M, m0, tid, kb); }
     __device__ __forceinline__ void init_b(BLd &b, int n0, int tid, int kb) const { b.init(x, g, dv, N, n0, tid, kb); }
-    __device__ __forceinline__ void store(int m, int n, float v, int z) const
+    // read-modify-write epilogue: prior() of a whole fragment, then store()
+    static constexpr bool RMW = true;
+    __device__ __forceinline__ float prior(int m, int n, int) const
+    {
+        return (m < M && n < N && splits == 1) ? dw[(size_t)m * N + n] : 0.f;
+    }
+    __device__ __forceinline__ void store(int m, int n, float v, float old, int z) const
     {
         if (m >= M || n >= N) return;
         if (splits == 1)
-            dw[(size_t)m * N + n] += v;
+            dw[(size_t)m * N + n] = old + v;
         else
             part[((size_t)z * M + m) * N + n] = v;
     }
@@ -802,17 +814,24 @@ struct GemmProblem {
     __device__ __forceinline__ void krange(int, int &kb, int &ke) const { kb = 0; ke = K; }
     __device__ __forceinline__ void init_a(AL &a, int m0, int, int) const { a.init(A, M, K, lda, abytes, m0); }
     __device__ __forceinline__ void init_b(BLd &b, int n0, int, int) const { b.init(Bm, N, K, ldb, bbytes, n0); }
-    __device__ __forceinline__ void store(int m, int n, float v, int) const
+    static constexpr bool RMW = true;
+    __device__ __forceinline__ float prior(int m, int n, int) const
+    {
+        return (m < M && n < N && beta != 0.f) ? C[(size_t)m * ldc + n] : 0.f;
+    }
+    __device__ __forceinline__ void store(int m, int n, float v, float old, int) const
     {
         if (m >= M || n >= N) return;
-        float *cp = C + (size_t)m * ldc + n;
-        *cp = (beta == 0.f) ? alpha * v : alpha * v + beta * *cp;
+        C[(size_t)m * ldc + n] = (beta == 0.f) ? alpha * v : alpha * v + beta * old;
     }
 };
 
 // ===========================================================================
 // LDS rows of the A stage: BK, or more for a loader whose branch-free stores
 // run past BK (AWeightsT4::ROWS)
+template <class P, class = void> struct is_rmw : std::false_type {};
+template <class P> struct is_rmw<P, std::void_t<decltype(P::RMW)>> : std::true_type {};
+
 template <class L, class = void> struct has_rows : std::false_type {};
 template <class L> struct has_rows<L, std::void_t<decltype(L::ROWS)>> : std::true_type {};
 template <class L, int BK> constexpr int a_rows()
@@ -940,10 +959,19 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int n = n0 + wn * (BN / WN) + j * 32 + lcol;
+            const int mb = m0 + wm * (BM / WM) + i * 32 + 4 * lrow;
+            if constexpr (is_rmw<P>::value) {
+                // all 16 prior values in flight before the first store
+                float old[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * lrow + (r & 3);
-                p.store(m, n, acc[i][j][r], z);
+                for (int r = 0; r < 16; ++r) old[r] = p.prior(mb + 8 * (r >> 2) + (r & 3), n, z);
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    p.store(mb + 8 * (r >> 2) + (r & 3), n, acc[i][j][r], old[r], z);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    p.store(mb + 8 * (r >> 2) + (r & 3), n, acc[i][j][r], z);
             }
         }
 }

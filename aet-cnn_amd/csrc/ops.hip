@@ -158,21 +158,23 @@ __global__ void __launch_bounds__(256) k_bias_part(const float *__restrict__ d, 
 }
 
 // Small planes (a fully connected layer's 1x1 output): one thread per
-// channel sums its batch x spatial values in (image, position) order, the
-// threads of a wave reading consecutive channels.
+// (channel, image chunk) sums the chunk's images x positions in order, the
+// threads of a wave reading consecutive channels; k_bias_final then adds
+// the chunks.
 constexpr int BIAS_SMALL_SPATIAL = 16;
 
 __global__ void __launch_bounds__(256) k_bias_small(const float *__restrict__ d, int batch, int n,
-                                                    int spatial, float *updates)
+                                                    int spatial, double *__restrict__ part)
 {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x, ch = blockIdx.y;
     if (c >= n) return;
+    const int b0 = ch * BIAS_IMGS, b1 = min(batch, b0 + BIAS_IMGS);
     double s = 0;
-    for (int b = 0; b < batch; ++b) {
+    for (int b = b0; b < b1; ++b) {
         const float *p = d + ((size_t)b * n + c) * spatial;
         for (int q = 0; q < spatial; ++q) s += (double)p[q];
     }
-    updates[c] += (float)s;
+    part[(size_t)ch * n + c] = s;
 }
 
 __global__ void k_bias_final(const double *__restrict__ part, int nch, int n, float *updates)
@@ -737,15 +739,14 @@ int ach_bias_grad(float *updates, const float *delta, int batch, int n, int spat
 {
     if (!updates || !delta || batch <= 0 || n <= 0 || spatial <= 0 || n > 65535) return ACH_EINVAL;
     if (!ws || ws_bytes < ach_bias_grad_workspace(batch, n, spatial)) return ACH_EWORKSPACE;
-    if (spatial <= BIAS_SMALL_SPATIAL) {
-        hipLaunchKernelGGL(k_bias_small, dim3((n + 255) / 256), dim3(256), 0, as_stream(s), delta,
-                           batch, n, spatial, updates);
-        return check_launch();
-    }
     const int nch = (batch + BIAS_IMGS - 1) / BIAS_IMGS;
     double *part = (double *)ws;
-    hipLaunchKernelGGL(k_bias_part, dim3(n, nch), dim3(256), 0, as_stream(s), delta, batch, n,
-                       spatial, part);
+    if (spatial <= BIAS_SMALL_SPATIAL)
+        hipLaunchKernelGGL(k_bias_small, dim3((n + 255) / 256, nch), dim3(256), 0, as_stream(s),
+                           delta, batch, n, spatial, part);
+    else
+        hipLaunchKernelGGL(k_bias_part, dim3(n, nch), dim3(256), 0, as_stream(s), delta, batch, n,
+                           spatial, part);
     int rc = check_launch();
     if (rc) return rc;
     hipLaunchKernelGGL(k_bias_final, dim3((n + 63) / 64), dim3(64), 0, as_stream(s), part, nch, n,
