@@ -826,6 +826,72 @@ struct GemmProblem {
     }
 };
 
+// Fully connected layers (a 1x1 convolution of a 1x1 input: x is [B][C],
+// y is [B][F], w is [F][C]) as plain GEMMs with coalesced operand loads.
+// Forward / input gradient: M = F, N = B, K = C; A = the k-major filter
+// Wt[K][M] (m contiguous), B[k][n] = x[n][k] read along k (PlainOperand,
+// k fastest); the K split and the output layout are those of FwdProblem.
+template <int BM_, bool VECA>
+struct FcProblem {
+    static constexpr int BM = BM_, BN = 128, BK = 16;
+    using AL = typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type;
+    using BLd = PlainOperand<false, 128>;
+    const float *x, *w;
+    float *y, *part;
+    int M, N, K, kchunk, splits;
+    size_t xbytes;
+    __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
+    {
+        kb = z * kchunk;
+        ke = min(K, kb + kchunk);
+    }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(w, M, K, m0, tid); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int, int) const { b.init(x, N, K, K, xbytes, n0); }
+    __device__ __forceinline__ void store(int m, int n, float v, int z) const
+    {
+        if (m >= M || n >= N) return;
+        if (splits > 1)
+            part[((size_t)z * M + m) * N + n] = v;
+        else
+            y[(size_t)n * M + m] = v;
+    }
+};
+
+// Weight gradient of a fully connected layer: M = F, N = C, K = B;
+// A[m][k] = dy[k][m] (k-major, m contiguous), B[k][n] = x[k][n] (n
+// contiguous, PlainOperand transposed); dw[m][n] += the sum (K split over
+// images with a fixed-order reduction when planned).
+template <int BM_, bool VECA>
+struct FcWgradProblem {
+    static constexpr int BM = BM_, BN = 128, BK = 16;
+    using AL = typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type;
+    using BLd = PlainOperand<true, 128>;
+    const float *x, *dy;
+    float *dw, *part;
+    int M, N, K, kchunk, splits;
+    size_t xbytes;
+    __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
+    {
+        kb = z * kchunk;
+        ke = min(K, kb + kchunk);
+    }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(dy, M, K, m0, tid); }
+    __device__ __forceinline__ void init_b(BLd &b, int n0, int, int) const { b.init(x, N, K, N, xbytes, n0); }
+    static constexpr bool RMW = true;
+    __device__ __forceinline__ float prior(int m, int n, int) const
+    {
+        return (m < M && n < N && splits == 1) ? dw[(size_t)m * N + n] : 0.f;
+    }
+    __device__ __forceinline__ void store(int m, int n, float v, float old, int z) const
+    {
+        if (m >= M || n >= N) return;
+        if (splits == 1)
+            dw[(size_t)m * N + n] = old + v;
+        else
+            part[((size_t)z * M + m) * N + n] = v;
+    }
+};
+
 // ===========================================================================
 // LDS rows of the A stage: BK, or more for a loader whose branch-free stores
 // run past BK (AWeightsT4::ROWS)
@@ -1168,6 +1234,10 @@ struct FwdPlan {
     int bm, bk, splits, kchunk;
 };
 
+// a 1x1 convolution of a 1x1 input (the fully connected layers once geom()
+// has flattened them): FcProblem / FcWgradProblem
+static bool fc_geom(const ConvGeom &g) { return g.KS == 1 && g.H == 1 && g.W == 1 && g.P == 0; }
+
 // 5x5 filters with a filter count divisible by 4 take the padded-tap
 // loaders (BIm2colK<5> / AWeightsT4K)
 static bool fwd_padded_taps(const ConvGeom &g) { return g.KS == 5 && (g.F & 3) == 0; }
@@ -1227,6 +1297,17 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     if (g.KS == 3) {
         FwdProblem<BM, BIm2col3> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
         return launch_gemm(p, M, N, pl.splits, st);
+    }
+    if constexpr (BM <= 128) {
+        if (fc_geom(g)) {
+            const size_t xb = (size_t)N * K * sizeof(float);
+            if ((M & 3) == 0) {
+                FcProblem<BM, true> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
+                return launch_gemm(p, M, N, pl.splits, st);
+            }
+            FcProblem<BM, false> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
+            return launch_gemm(p, M, N, pl.splits, st);
+        }
     }
     if (g.KS == 1) {
         FwdProblem<BM, BIm2colAny<1>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
@@ -1345,6 +1426,7 @@ static int wgrad_bm(const ConvGeom &g)
 }
 static int wgrad_bn(const ConvGeom &g)
 {
+    if (fc_geom(g)) return 128;
     if (g.C * g.KS * g.KS <= 32 && g.F > 64) return 32;
     return g.F > 64 ? ACH_WGRAD_BN : 128;
 }
@@ -1383,6 +1465,28 @@ static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, floa
     }
     WgradProblem<BM, BN, 0> p{x, dy, dw, part, g, dv, M, N, K, kchunk, splits};
     return launch_gemm(p, M, N, splits, st);
+}
+
+template <int BM>
+static int fc_wgrad_bm(const ConvGeom &g, const float *x, const float *dy, float *dw,
+                       float *part, int splits, int kchunk, hipStream_t st)
+{
+    const int M = g.F, N = g.C, K = g.B;
+    const size_t xb = (size_t)K * N * sizeof(float);
+    if ((M & 3) == 0) {
+        FcWgradProblem<BM, true> p{x, dy, dw, part, M, N, K, kchunk, splits, xb};
+        return launch_gemm(p, M, N, splits, st);
+    }
+    FcWgradProblem<BM, false> p{x, dy, dw, part, M, N, K, kchunk, splits, xb};
+    return launch_gemm(p, M, N, splits, st);
+}
+
+static int fc_wgrad_launch(const ConvGeom &g, const float *x, const float *dy, float *dw,
+                           float *part, int bm, int splits, int kchunk, hipStream_t st)
+{
+    if (bm == 32) return fc_wgrad_bm<32>(g, x, dy, dw, part, splits, kchunk, st);
+    if (bm == 64) return fc_wgrad_bm<64>(g, x, dy, dw, part, splits, kchunk, st);
+    return fc_wgrad_bm<128>(g, x, dy, dw, part, splits, kchunk, st);
 }
 
 }  // namespace ach
@@ -1567,7 +1671,8 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
     hipStream_t st = as_stream(stream);
     float *part = (float *)ws;
     int rc;
-    if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st);
+    if (fc_geom(g)) rc = fc_wgrad_launch(g, x, dy, dw, part, bm, splits, kchunk, st);
+    else if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st);
 #if ACH_WGRAD_BN == 64
     else if (bn == 64) rc = wgrad_launch<128, 64>(g, x, dy, dw, part, splits, kchunk, st);
 #endif

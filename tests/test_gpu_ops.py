@@ -102,6 +102,9 @@ CONV_SHAPES = [
     (2, 96, 9, 9, 80, 5, 1, 2),    # 5x5 with 80 / 96 filters: 96-row tiles
     (6, 24, 4, 4, 20, 1, 1, 0),    # 1x1 on a 16-position plane
     (8, 16, 5, 5, 24, 3, 1, 1),    # 25 positions: the (image, position) order
+    # fully connected layers (1x1 of a 1x1 input, after flattening):
+    (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
+    (8, 64, 1, 1, 48, 1, 1, 0),    # 64 -> 48, 64-row tiles
 ]
 
 
