@@ -120,6 +120,7 @@ _NET = {
     "an_rand_seed": (None, [C.c_uint]),
     "an_network_create": (_vp, [_i, _i, _i, _i]),
     "an_add_convolutional": (_i, [_vp, _i, _i, _i, _i, _i, _i]),
+    "an_add_connected": (_i, [_vp, _i, _i, _i]),
     "an_add_maxpool": (_i, [_vp, _i, _i, _i]),
     "an_add_avgpool": (_i, [_vp]),
     "an_add_dropout": (_i, [_vp, _f]),
@@ -299,6 +300,12 @@ class Network:
         r = self.lib.an_add_convolutional(self.h, filters, size, stride, pad, activation, int(bn))
         if r < 0:
             raise ValueError(f"an_add_convolutional: {r}")
+        return r
+
+    def connected(self, outputs, activation, bn):
+        r = self.lib.an_add_connected(self.h, outputs, activation, int(bn))
+        if r < 0:
+            raise ValueError(f"an_add_connected: {r}")
         return r
 
     def maxpool(self, size, stride, padding):

@@ -14,6 +14,7 @@ LOGISTIC, RELU, LINEAR, LEAKY = 0, 1, 3, 7
 
 # name -> dict(batch, h, w, c, classes, lr, momentum, decay, layers)
 # layer tuples: ("conv", filters, size, stride, pad, activation, bn)
+#               ("connected", outputs, activation, bn)
 #               ("maxpool", size, stride, padding)   ("avgpool",)
 #               ("dropout", p)   ("softmax",)
 CONFIGS = {
@@ -31,6 +32,12 @@ CONFIGS = {
                     [("conv", 512, 3, 1, 1, LEAKY, 1)] * 3 +
                     [("dropout", 0.5), ("conv", 10, 1, 1, 0, LINEAR, 0), ("avgpool",),
                      ("softmax",)]),
+    # fully connected layers on a non-square input (test net, not a benchmark
+    # config): conv -> maxpool -> connected+BN -> dropout -> connected -> softmax
+    "fcnet": dict(batch=16, h=6, w=10, c=3, classes=10, lr=0.05, momentum=0.9, decay=5e-4,
+                  layers=[("conv", 8, 3, 1, 1, LEAKY, 1), ("maxpool", 2, 2, 1),
+                          ("connected", 24, LEAKY, 1), ("dropout", 0.5),
+                          ("connected", 10, LINEAR, 0), ("softmax",)]),
     # config 4: AlexNet-style; FC layers expressed as convolutions
     "alexnet": dict(batch=128, h=227, w=227, c=3, classes=1000, lr=0.01, momentum=0.9,
                     decay=5e-4,
@@ -50,6 +57,8 @@ def build(builder, name: str, batch: int | None = None):
         kind = layer[0]
         if kind == "conv":
             builder.conv(*layer[1:])
+        elif kind == "connected":
+            builder.connected(*layer[1:])
         elif kind == "maxpool":
             builder.maxpool(*layer[1:])
         elif kind == "avgpool":

@@ -10,6 +10,9 @@
  *                    filters=1 size=1 stride=1 pad=0 padding=0
  *                    (pad=1 -> padding=size/2) activation=logistic
  *                    batch_normalize=0
+ *   [connected]      not built by the reference (no CONNECTED case in
+ *                    createLayer, NetworkFactory.c:615-654); darknet's keys:
+ *                    output=1 activation=logistic batch_normalize=0
  *   [maxpool]        createMaxPool NetworkFactory.c:543-548
  *                    stride=1 size=stride padding=size-1
  *   [avgpool]        createAvgPool NetworkFactory.c:572-584
@@ -175,6 +178,14 @@ an_network *an_parse_cfg(const char *path)
             }
             rc = an_add_convolutional(net, geti(g, "filters", 1), size, stride, padding, act,
                                       geti(g, "batch_normalize", 0));
+        } else if (!strcmp(g->name, "connected") || !strcmp(g->name, "conn")) {
+            const char *an = find(g, "activation");
+            const int act = activation_id(an ? an : "logistic");
+            if (act < 0) {
+                fprintf(stderr, "an_parse_cfg: activation %s is not supported\n", an);
+                goto fail;
+            }
+            rc = an_add_connected(net, geti(g, "output", 1), act, geti(g, "batch_normalize", 0));
         } else if (!strcmp(g->name, "maxpool") || !strcmp(g->name, "max")) {
             if (unsupported(g, "maxpool_depth", 0) || unsupported(g, "antialiasing", 0))
                 goto fail;

@@ -217,8 +217,10 @@ static int conv_update(an_network *net, an_layer *l, int batch, float lr, float 
                            momentum, decay, net->stream);
 }
 
-int an_add_convolutional(an_network *net, int filters, int size, int stride, int pad,
-                         int activation, int batch_normalize)
+/* flatten != 0: the layer reads the previous output [batch][c][h][w] as
+ * [batch][c*h*w][1][1] (the same memory), for an_add_connected */
+static int add_conv(an_network *net, int filters, int size, int stride, int pad, int activation,
+                    int batch_normalize, int flatten)
 {
     if (!net || filters <= 0 || size <= 0 || stride <= 0 || pad < 0) return ACH_EINVAL;
     if (activation != ACH_LEAKY && activation != ACH_RELU && activation != ACH_LINEAR &&
@@ -226,6 +228,11 @@ int an_add_convolutional(an_network *net, int filters, int size, int stride, int
         return ACH_EUNSUPPORTED;
     an_layer *l = push_layer(net);
     if (!l) return ACH_EINVAL;
+    if (flatten) {
+        l->c = l->c * l->h * l->w;
+        l->h = l->w = 1;
+        l->connected = 1;
+    }
     l->type = AN_CONVOLUTIONAL;
     l->n = filters;
     l->size = size;
@@ -255,6 +262,22 @@ int an_add_convolutional(an_network *net, int filters, int size, int stride, int
     for (int i = 0; i < l->nweights; ++i) w[i] = scale * rand_uniform(-1, 1);
     net->init_w[net->n] = w;
     return net->n++;
+}
+
+int an_add_convolutional(an_network *net, int filters, int size, int stride, int pad,
+                         int activation, int batch_normalize)
+{
+    return add_conv(net, filters, size, stride, pad, activation, batch_normalize, 0);
+}
+
+/* A fully connected layer: the previous output flattened to c*h*w features
+ * per image, y = act(W x + b) (or BN) with W [outputs][inputs]; it runs as a
+ * 1x1 convolution of the flattened input, so the GEMM kernels take their
+ * fully connected path.  Init sqrt(2/inputs)*randUniform(-1,1), which is
+ * the convolution's rule with k = 1. */
+int an_add_connected(an_network *net, int outputs, int activation, int batch_normalize)
+{
+    return add_conv(net, outputs, 1, 1, 0, activation, batch_normalize, 1);
 }
 
 /* ======================================================================== */
@@ -943,6 +966,17 @@ double an_step_conv_gflop(const an_network *net)
 static int conv_param_arrays(an_layer *l, float **ptr, size_t *cnt)
 {
     int k = 0;
+    if (l->connected) {
+        /* darknet's connected-layer order: biases, weights, then BN arrays */
+        ptr[k] = l->biases; cnt[k++] = (size_t)l->n;
+        ptr[k] = l->weights; cnt[k++] = (size_t)l->nweights;
+        if (l->batch_normalize) {
+            ptr[k] = l->scales; cnt[k++] = (size_t)l->n;
+            ptr[k] = l->rolling_mean; cnt[k++] = (size_t)l->n;
+            ptr[k] = l->rolling_variance; cnt[k++] = (size_t)l->n;
+        }
+        return k;
+    }
     ptr[k] = l->biases; cnt[k++] = (size_t)l->n;
     if (l->batch_normalize) {
         ptr[k] = l->scales; cnt[k++] = (size_t)l->n;

@@ -62,6 +62,7 @@ struct an_layer {
     int h, w, c, out_h, out_w, out_c;
     /* convolutional (ConvolutionalLayer.h:20-114) */
     int n, size, stride, pad, activation, batch_normalize, nweights;
+    int connected;          /* an_add_connected: input read flattened       */
     float *weights, *weight_updates, *biases, *bias_updates;
     float *scales, *scale_updates;
     float *mean, *variance, *rolling_mean, *rolling_variance;
@@ -97,6 +98,13 @@ an_network *an_network_create(int batch, int h, int w, int c);
 /* return the new layer's index or a negative error                          */
 int an_add_convolutional(an_network *net, int filters, int size, int stride, int pad,
                          int activation, int batch_normalize);
+/* Fully connected layer: the previous output flattened to inputs = c*h*w
+ * features per image, weights [outputs][inputs], y = act(W x + b) or BN.
+ * No counterpart in the reference's createLayer (NetworkFactory.c:615-654
+ * has no CONNECTED case; the enum exists at NLayer.h:62); it follows
+ * darknet's [connected] layer and runs as a 1x1 convolution of the
+ * flattened input.  Init sqrt(2/inputs) * randUniform(-1,1).               */
+int an_add_connected(an_network *net, int outputs, int activation, int batch_normalize);
 int an_add_maxpool(an_network *net, int size, int stride, int padding);
 int an_add_avgpool(an_network *net);
 int an_add_dropout(an_network *net, float probability);
@@ -109,15 +117,17 @@ void an_free(an_network *net);
 /* Builds a network from a darknet-style .cfg file (ConfigFile.c:12-208,
  * NetworkFactory.c:615-1013): [net] batch/subdivisions/width/height/channels/
  * learning_rate/momentum/decay; [convolutional] filters/size/stride/pad/
- * padding/activation/batch_normalize; [maxpool] size/stride/padding;
- * [avgpool]; [dropout] probability; [softmax] groups/temperature.  Returns
+ * padding/activation/batch_normalize; [connected] output/activation/
+ * batch_normalize (darknet's keys, an_add_connected); [maxpool] size/stride/
+ * padding; [avgpool]; [dropout] probability; [softmax] groups/temperature.  Returns
  * NULL on error (message on stderr).  The network is finalized.            */
 an_network *an_parse_cfg(const char *path);
 
 /* ---- darknet .weights files (NNetwork.c:64-151, ConvolutionalLayer.c:422-486)
  * header int32 {0, 2, 5} + uint64 seen, then per convolutional layer:
  * biases, [scales, rolling_mean, rolling_variance if batch_normalize],
- * weights (float32).  Load accepts older headers without seen and stops
+ * weights (float32); per connected layer darknet's order: biases, weights,
+ * [scales, rolling_mean, rolling_variance].  Load accepts older headers without seen and stops
  * quietly at end of file, as the reference does; it sets seen and the
  * iteration.  The network must be finalized.                              */
 int an_save_weights(an_network *net, const char *path);

@@ -727,10 +727,14 @@ static or_layer *push_layer(or_net *net)
 
 static float *fzalloc(size_t n) { return (float *)calloc(n ? n : 1, sizeof(float)); }
 
-int or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
-                    int activation, int batch_normalize)
+static int add_conv(or_net *net, int filters, int size, int stride, int pad, int activation,
+                    int batch_normalize, int flatten)
 {
     or_layer *l = push_layer(net);
+    if (flatten) { /* [batch][c][h][w] read as [batch][c*h*w][1][1] */
+        l->c = l->c * l->h * l->w;
+        l->h = l->w = 1;
+    }
     l->type = L_CONV;
     l->n = filters;
     l->size = size;
@@ -768,6 +772,22 @@ int or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
         l->x_norm = fzalloc(bo);
     }
     return net->n++;
+}
+
+int or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
+                    int activation, int batch_normalize)
+{
+    return add_conv(net, filters, size, stride, pad, activation, batch_normalize, 0);
+}
+
+/* A fully connected layer (darknet's [connected]; the reference builds none,
+ * NetworkFactory.c:615-654): the previous output flattened to c*h*w
+ * features, then the 1x1 convolution path of this file -- out_i = W x_i
+ * (Gemm.c:53-66), bias or batch-norm, activation -- with init
+ * sqrt(2/inputs)*randUniform(-1,1) (WeightData.c:153-166 with k = 1).      */
+int or_net_add_connected(or_net *net, int outputs, int activation, int batch_normalize)
+{
+    return add_conv(net, outputs, 1, 1, 0, activation, batch_normalize, 1);
 }
 
 int or_net_add_maxpool(or_net *net, int size, int stride, int padding)

@@ -153,6 +153,8 @@ or_net *or_net_create(int batch, int h, int w, int c);
 /* layer constructors return the layer index, or -1 on error                 */
 int  or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
                      int activation, int batch_normalize);
+/* fully connected: previous output flattened to c*h*w, then a 1x1 conv   */
+int  or_net_add_connected(or_net *net, int outputs, int activation, int batch_normalize);
 int  or_net_add_maxpool(or_net *net, int size, int stride, int padding);
 int  or_net_add_avgpool(or_net *net);
 int  or_net_add_dropout(or_net *net, float probability);

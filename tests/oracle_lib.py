@@ -56,6 +56,7 @@ _SIGS = {
     "or_rand_uniform": (_f, [_f, _f]),
     "or_net_create": (_vp, [_i, _i, _i, _i]),
     "or_net_add_conv": (_i, [_vp, _i, _i, _i, _i, _i, _i]),
+    "or_net_add_connected": (_i, [_vp, _i, _i, _i]),
     "or_net_add_maxpool": (_i, [_vp, _i, _i, _i]),
     "or_net_add_avgpool": (_i, [_vp]),
     "or_net_add_dropout": (_i, [_vp, _f]),
@@ -273,6 +274,11 @@ class OracleNet:
 
     def conv(self, filters, size, stride, pad, act, bn):
         r = self.L.or_net_add_conv(self.h, filters, size, stride, pad, act, int(bn))
+        assert r >= 0
+        return r
+
+    def connected(self, outputs, act, bn):
+        r = self.L.or_net_add_connected(self.h, outputs, act, int(bn))
         assert r >= 0
         return r
 

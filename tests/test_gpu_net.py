@@ -54,7 +54,11 @@ def owner(onet, i):
 def dw_truth(onet, name, i, batch, delta_in, x_img):
     """float64 weight gradient of BN conv layer i from the oracle's state."""
     _, F, OH, OW, Cin, H, W, _ = onet.info(i)
-    _, f, k, s, p, act, bn = configs.CONFIGS[name]["layers"][i]
+    layer = configs.CONFIGS[name]["layers"][i]
+    if layer[0] == "connected":  # a 1x1 convolution of the flattened input
+        (_, f, act, bn), k, s, p = layer, 1, 1, 0
+    else:
+        _, f, k, s, p, act, bn = layer
     shp = (batch, F, OH, OW)
     d64, _ = bn_backward_ref(delta_in.reshape(shp), onet.buffer(i, 0).reshape(shp),
                              onet.buffer(i, 12).reshape(shp), onet.buffer(i, 10),
@@ -64,7 +68,8 @@ def dw_truth(onet, name, i, batch, delta_in, x_img):
     return wgrad_ref(inp, d64, k, s, p).ravel()
 
 
-@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("alexnet", 2)])
+@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("alexnet", 2),
+                                        ("fcnet", 16)])
 def test_teacher_forced_layers(gpu, oracle, name, batch):
     """Every layer of one training step, fed the oracle's exact inputs and
     state (layer input, incoming delta, BN statistics, argmax indices):
@@ -143,7 +148,7 @@ def test_teacher_forced_layers(gpu, oracle, name, batch):
     print(name, {k: f"{v:.1e}" for k, v in errs.items()})
 
 
-@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8)])
+@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("fcnet", 16)])
 def test_free_running_step(gpu, oracle, name, batch):
     """One untaught step: loss within 1e-3 and predicted labels agree."""
     oracle.lib().or_set_gemm_parallel(1)
@@ -318,3 +323,49 @@ def test_fused_predict_matches_oracle(gpu, oracle, name, batch):
     os.remove(path)
     net.close()
     onet.close()
+
+
+def test_connected_layer_cfg_and_weights_file(gpu, oracle, tmp_path):
+    """[connected] sections build the same network as an_add_connected (same
+    initial weights), and a saved .weights file holds a connected layer in
+    darknet's order -- biases, weights, then scales / rolling mean / rolling
+    variance -- unlike a convolutional layer (biases, BN arrays, weights)."""
+    net, _ = make_pair(oracle, "fcnet", 16)
+    cfg = tmp_path / "fc.cfg"
+    cfg.write_text("[net]\nbatch=16\nheight=6\nwidth=10\nchannels=3\n"
+                   "learning_rate=0.05\nmomentum=0.9\ndecay=0.0005\n"
+                   "[convolutional]\nfilters=8\nsize=3\nstride=1\npad=1\n"
+                   "activation=leaky\nbatch_normalize=1\n"
+                   "[maxpool]\nsize=2\nstride=2\npadding=1\n"
+                   "[connected]\noutput=24\nactivation=leaky\nbatch_normalize=1\n"
+                   "[dropout]\nprobability=0.5\n"
+                   "[connected]\noutput=10\nactivation=linear\n[softmax]\n")
+    aetcnn.net_lib().an_rand_seed(1)
+    net2 = aetcnn.Network.from_cfg(str(cfg))
+    for i in (0, 2, 4):
+        assert np.array_equal(net.buffer(i, 2), net2.buffer(i, 2)), i
+    rng = np.random.default_rng(3)
+    vals = {}
+    for i in (0, 2, 4):
+        for code in (2, 4, 6, 8, 9):
+            b = net.buffer(i, code)
+            if b is not None and b.size:
+                v = rng.standard_normal(b.size).astype(np.float32)
+                net.set_buffer(i, code, v)
+                vals[(i, code)] = v
+    path = tmp_path / "fc.weights"
+    net.save_weights(str(path))
+    raw = np.fromfile(str(path), dtype=np.float32, offset=20)
+    # conv layer 0 (BN): biases, scales, rolling mean, rolling var, weights
+    order = [(0, 4), (0, 6), (0, 8), (0, 9), (0, 2),
+             # connected layer 2 (BN): biases, weights, scales, rolling mean, var
+             (2, 4), (2, 2), (2, 6), (2, 8), (2, 9),
+             # connected layer 4: biases, weights
+             (4, 4), (4, 2)]
+    want = np.concatenate([vals[k] for k in order])
+    assert np.array_equal(raw, want)
+    net2.load_weights(str(path))
+    for k, v in vals.items():
+        assert np.array_equal(net2.buffer(*k), v), k
+    net.close()
+    net2.close()

@@ -500,3 +500,47 @@ def test_oracle_fused_network_predicts_like_unfused():
     clear = (top2[:, 1] - top2[:, 0]) > 1e-3
     assert np.array_equal(p1.argmax(1)[clear], p0.argmax(1)[clear])
     net.close()
+
+
+def test_oracle_connected_layer():
+    """or_net_add_connected: on a square input it is the convolution whose
+    kernel covers the input (same initial weights, identical outputs, since
+    im2col of the whole input is the flattened input in (c, h, w) order); on
+    a non-square input its output equals a float64 product of the flattened
+    input with the [outputs][inputs] weights."""
+    L = O.lib()
+    rng = np.random.default_rng(8)
+    B = 4
+    x = rng.uniform(-1, 1, (B, 3, 5, 5)).astype(np.float32)
+    outs = []
+    for connected in (True, False):
+        L.or_rand_seed(11)
+        net = O.OracleNet(B, 5, 5, 3)
+        if connected:
+            net.connected(7, 3, 0)
+        else:
+            net.conv(7, 5, 1, 0, 3, 0)
+        net.softmax()
+        net.finalize()
+        net.load(x, None)
+        net.layer_forward(0, 0)
+        outs.append((net.buffer(0, 0).copy(), net.buffer(0, 2).copy()))
+        net.close()
+    assert np.array_equal(outs[0][1], outs[1][1])  # weights
+    assert np.array_equal(outs[0][0], outs[1][0])  # outputs
+    x2 = rng.uniform(-1, 1, (B, 2, 3, 4)).astype(np.float32)
+    L.or_rand_seed(12)
+    net = O.OracleNet(B, 3, 4, 2)
+    net.connected(5, 3, 0)
+    net.softmax()
+    net.finalize()
+    w = net.buffer(0, 2).reshape(5, 24).astype(np.float64)
+    bias = rng.standard_normal(5).astype(np.float32)
+    net.set_buffer(0, 4, bias)
+    net.load(x2, None)
+    net.layer_forward(0, 0)
+    want = x2.reshape(B, 24).astype(np.float64) @ w.T + bias
+    assert np.max(np.abs(net.buffer(0, 0).reshape(B, 5) - want)) < 1e-6
+    # init: sqrt(2/inputs) * U(-1, 1)
+    assert np.max(np.abs(w)) <= np.sqrt(2 / 24) + 1e-7
+    net.close()
