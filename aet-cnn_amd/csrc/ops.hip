@@ -487,9 +487,17 @@ __device__ __forceinline__ float drop1(float v, float r, float p, float scale)
     return (r < p) ? 0.f : v * scale;
 }
 
-__global__ void k_dropout(float *x, size_t n, float p, float scale, uint64_t seed,
-                          uint32_t iter, uint32_t layer)
+// counter += v (a device-side step index advanced inside a replayed graph)
+__global__ void k_counter_add(uint32_t *counter, uint32_t v)
 {
+    if (threadIdx.x == 0) counter[0] += v;
+}
+
+__global__ void k_dropout(float *x, size_t n, float p, float scale, uint64_t seed,
+                          uint32_t iter0, const uint32_t *__restrict__ iter_ptr, uint32_t layer)
+{
+    // the step index comes from device memory when a replayed graph supplies it
+    const uint32_t iter = iter_ptr ? *iter_ptr : iter0;
     const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     size_t done = 0;
@@ -899,21 +907,80 @@ float ach_dropout_uniform(uint64_t seed, uint32_t iter, uint32_t layer, uint32_t
     return dropout_uniform(seed, iter, layer, i);
 }
 
-int ach_dropout_fwd(float *x, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
-                    ach_stream_t s)
+static int dropout_launch(float *x, size_t n, float p, uint64_t seed, uint32_t iter,
+                          const uint32_t *iter_ptr, uint32_t layer, ach_stream_t s)
 {
     if (n == 0) return ACH_OK;
     if (!x || !(p >= 0.f && p < 1.f) || n > 0xffffffffull) return ACH_EINVAL;
     const float scale = (float)(1. / (1.0 - p));
     hipLaunchKernelGGL(k_dropout, dim3(grid_stream(n)), dim3(256), 0, as_stream(s), x, n, p,
-                       scale, seed, iter, layer);
+                       scale, seed, iter, iter_ptr, layer);
     return check_launch();
+}
+
+int ach_dropout_fwd(float *x, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
+                    ach_stream_t s)
+{
+    return dropout_launch(x, n, p, seed, iter, nullptr, layer, s);
 }
 
 int ach_dropout_bwd(float *d, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
                     ach_stream_t s)
 {
-    return ach_dropout_fwd(d, n, p, seed, iter, layer, s);
+    return dropout_launch(d, n, p, seed, iter, nullptr, layer, s);
+}
+
+int ach_dropout_fwd_dev(float *x, size_t n, float p, uint64_t seed, const uint32_t *iter,
+                        uint32_t layer, ach_stream_t s)
+{
+    if (!iter) return ACH_EINVAL;
+    return dropout_launch(x, n, p, seed, 0, iter, layer, s);
+}
+
+int ach_dropout_bwd_dev(float *d, size_t n, float p, uint64_t seed, const uint32_t *iter,
+                        uint32_t layer, ach_stream_t s)
+{
+    if (!iter) return ACH_EINVAL;
+    return dropout_launch(d, n, p, seed, 0, iter, layer, s);
+}
+
+int ach_counter_add(uint32_t *counter, uint32_t v, ach_stream_t s)
+{
+    if (!counter) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_counter_add, dim3(1), dim3(64), 0, as_stream(s), counter, v);
+    return check_launch();
+}
+
+// ---- HIP graphs: record a stream's work once, replay it -----------------
+int ach_graph_capture_begin(ach_stream_t s)
+{
+    return check(hipStreamBeginCapture(as_stream(s), hipStreamCaptureModeThreadLocal));
+}
+
+int ach_graph_capture_end(ach_stream_t s, void **exec)
+{
+    if (!exec) return ACH_EINVAL;
+    *exec = nullptr;
+    hipGraph_t g = nullptr;
+    int rc = check(hipStreamEndCapture(as_stream(s), &g));
+    if (rc) return rc;
+    hipGraphExec_t e = nullptr;
+    rc = check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
+    (void)hipGraphDestroy(g);
+    if (rc) return rc;
+    *exec = (void *)e;
+    return ACH_OK;
+}
+
+int ach_graph_launch(void *exec, ach_stream_t s)
+{
+    if (!exec) return ACH_EINVAL;
+    return check(hipGraphLaunch((hipGraphExec_t)exec, as_stream(s)));
+}
+
+int ach_graph_destroy(void *exec)
+{
+    return exec ? check(hipGraphExecDestroy((hipGraphExec_t)exec)) : ACH_OK;
 }
 
 int ach_sgd_update(size_t n, float *w, float *v, float dc, float lc, float mom, ach_stream_t s)

@@ -56,6 +56,12 @@ struct an_network {
     int njobs;
     float *zero_region;            /* deltas that need zeroing per forward */
     size_t zero_floats;
+    /* graph replay of the training step (an_set_graph): the recorded step,
+     * and the device copy of cur_iteration its dropout kernels read and its
+     * last kernel advances                                                  */
+    int graph_on, recording;
+    void *graph_exec;
+    uint32_t *d_iter;
     /* host copies of initial parameters until finalize */
     float **init_w;
 };
@@ -350,20 +356,28 @@ int an_add_avgpool(an_network *net)
 /* ======================================================================== */
 /* Dropout: DropoutLayer.c:55-86; shares the previous layer's output and
  * delta (NetworkFactory.c:644-650).                                        */
+/* In a recorded step the step index comes from the device copy
+ * (net->d_iter), so every replay of it draws its own masks.               */
 static int dropout_forward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.train) return ACH_OK;
-    return ach_dropout_fwd((float *)st.input, (size_t)l->batch * l->inputs, l->probability,
-                           net->dropout_seed, (uint32_t)net->cur_iteration, (uint32_t)l->index,
-                           net->stream);
+    const size_t n = (size_t)l->batch * l->inputs;
+    if (net->recording)
+        return ach_dropout_fwd_dev((float *)st.input, n, l->probability, net->dropout_seed,
+                                   net->d_iter, (uint32_t)l->index, net->stream);
+    return ach_dropout_fwd((float *)st.input, n, l->probability, net->dropout_seed,
+                           (uint32_t)net->cur_iteration, (uint32_t)l->index, net->stream);
 }
 
 static int dropout_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
-    return ach_dropout_bwd(st.delta, (size_t)l->batch * l->inputs, l->probability,
-                           net->dropout_seed, (uint32_t)net->cur_iteration, (uint32_t)l->index,
-                           net->stream);
+    const size_t n = (size_t)l->batch * l->inputs;
+    if (net->recording)
+        return ach_dropout_bwd_dev(st.delta, n, l->probability, net->dropout_seed, net->d_iter,
+                                   (uint32_t)l->index, net->stream);
+    return ach_dropout_bwd(st.delta, n, l->probability, net->dropout_seed,
+                           (uint32_t)net->cur_iteration, (uint32_t)l->index, net->stream);
 }
 
 int an_add_dropout(an_network *net, float probability)
@@ -419,14 +433,37 @@ int an_add_softmax(an_network *net, int groups, float temperature)
     return net->n++;
 }
 
+/* a recorded step holds the hyper-parameters, the dropout seed and the
+ * layer functions as they were: any change drops it (re-recorded lazily) */
+static void drop_graph(an_network *net)
+{
+    if (net->graph_exec) {
+        ach_graph_destroy(net->graph_exec);
+        net->graph_exec = NULL;
+    }
+}
+
 void an_set_hyper(an_network *net, float learning_rate, float momentum, float decay)
 {
     net->learning_rate = learning_rate;
     net->momentum = momentum;
     net->decay = decay;
+    drop_graph(net);
 }
 
-void an_set_dropout_seed(an_network *net, uint64_t seed) { net->dropout_seed = seed; }
+void an_set_dropout_seed(an_network *net, uint64_t seed)
+{
+    net->dropout_seed = seed;
+    drop_graph(net);
+}
+
+int an_set_graph(an_network *net, int on)
+{
+    if (!net) return ACH_EINVAL;
+    if (!on) drop_graph(net);
+    net->graph_on = on ? 1 : 0;
+    return ACH_OK;
+}
 
 /* ======================================================================== */
 /* Arena layout and workspace sizing (NetworkFactory.c:999-1005 sizes one
@@ -530,6 +567,7 @@ static void layout(an_network *net, bump *b)
     }
     net->wgrad_ws_bytes = wws;
     net->wgrad_ws = (float *)take(b, wws ? wws : 256);
+    net->d_iter = (uint32_t *)take(b, sizeof(uint32_t));
 }
 
 int an_finalize(an_network *net)
@@ -651,6 +689,7 @@ void an_free(an_network *net)
     free(net->jobs);
     if (net->wstream) ach_stream_sync(net->wstream);
     if (net->stream) ach_stream_sync(net->stream);
+    drop_graph(net);
     if (net->ev_ready) {
         for (int i = 0; i < net->n; ++i)
             if (net->ev_ready[i]) ach_event_destroy(net->ev_ready[i]);
@@ -816,6 +855,7 @@ int an_predict(an_network *net, const float *host_input, float *host_output)
 int an_fuse_conv_batchnorm(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
+    drop_graph(net);
     for (int i = 0; i < net->n; ++i) {
         an_layer *l = net->layers[i];
         if (l->type != AN_CONVOLUTIONAL || !l->batch_normalize) continue;
@@ -844,14 +884,46 @@ void an_top_k(const float *a, int n, int k, int *index)
     }
 }
 
+/* the kernels of one training step: forward, both backward streams, update
+ * and, in graph mode, the device step index advanced                       */
+static int enqueue_step(an_network *net)
+{
+    AN_CHECK(an_forward(net, 1));
+    AN_CHECK(an_backward(net));
+    AN_CHECK(an_update(net));
+    return net->recording ? ach_counter_add(net->d_iter, 1u, net->stream) : ACH_OK;
+}
+
+/* Graph mode records enqueue_step once (after copying cur_iteration to the
+ * device) and replays it; every replay is the same kernel sequence with the
+ * same arguments, reading the current input, weights and step index.      */
+static int train_step_graph(an_network *net)
+{
+    if (!net->graph_exec) {
+        const uint32_t it = (uint32_t)net->cur_iteration;
+        AN_CHECK(ach_memcpy_h2d(net->d_iter, &it, sizeof(it), net->stream));
+        AN_CHECK(ach_graph_capture_begin(net->stream));
+        net->recording = 1;
+        const int rc = enqueue_step(net);
+        net->recording = 0;
+        void *exec = NULL;
+        const int rc2 = ach_graph_capture_end(net->stream, &exec);
+        if (rc || rc2) {
+            ach_graph_destroy(exec);
+            return rc ? rc : rc2;
+        }
+        net->graph_exec = exec;
+    }
+    return ach_graph_launch(net->graph_exec, net->stream);
+}
+
 int an_train_step(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
     net->seen += (uint64_t)net->batch;
-    AN_CHECK(an_forward(net, 1));
-    AN_CHECK(an_backward(net));
+    AN_CHECK(net->graph_on ? train_step_graph(net) : enqueue_step(net));
     net->cur_iteration += 1;
-    return an_update(net);
+    return ACH_OK;
 }
 
 int an_get_loss(an_network *net, float *loss)
@@ -1051,6 +1123,7 @@ int an_load_weights(an_network *net, const char *path)
         net->seen = seen;
     }
     net->cur_iteration = (int)(net->seen / (uint64_t)net->batch);
+    drop_graph(net); /* the recorded step's device step index is stale */
     int rc = ACH_OK;
     float *host = NULL;
     size_t host_cap = 0;

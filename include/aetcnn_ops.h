@@ -246,6 +246,26 @@ int ach_dropout_fwd(float *x, size_t n, float probability, uint64_t seed,
                     uint32_t iter, uint32_t layer, ach_stream_t stream);
 int ach_dropout_bwd(float *delta, size_t n, float probability, uint64_t seed,
                     uint32_t iter, uint32_t layer, ach_stream_t stream);
+/* The same with the step index read from device memory (*iter) when the
+ * kernel runs, for work recorded once into a HIP graph and replayed every
+ * step.  No counterpart in the reference (its dropout is a host loop). */
+int ach_dropout_fwd_dev(float *x, size_t n, float probability, uint64_t seed,
+                        const uint32_t *iter, uint32_t layer, ach_stream_t stream);
+int ach_dropout_bwd_dev(float *delta, size_t n, float probability, uint64_t seed,
+                        const uint32_t *iter, uint32_t layer, ach_stream_t stream);
+/* *counter += v on the stream (advances such a device-side step index).  */
+int ach_counter_add(uint32_t *counter, uint32_t v, ach_stream_t stream);
+
+/* ---- HIP graphs (no counterpart in the reference; the reference launches
+ * every op eagerly).  capture_begin records the stream's work (and that of
+ * streams forked from it by events) instead of running it, in the calling
+ * thread's capture mode; capture_end instantiates the recording into
+ * *exec; launch replays it on a stream; destroy frees it.  Recorded work
+ * must not allocate, copy to or from the host, or synchronise.            */
+int ach_graph_capture_begin(ach_stream_t stream);
+int ach_graph_capture_end(ach_stream_t stream, void **exec);
+int ach_graph_launch(void *exec, ach_stream_t stream);
+int ach_graph_destroy(void *exec);
 
 /* ---- SGD momentum / weight-decay update ----------------------------------
  * ConvolutionalLayer.update (ConvolutionalLayer.c:959-980):

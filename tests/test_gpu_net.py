@@ -369,3 +369,52 @@ def test_connected_layer_cfg_and_weights_file(gpu, oracle, tmp_path):
         assert np.array_equal(net2.buffer(*k), v), k
     net.close()
     net2.close()
+
+
+def _twin_nets(name, batch, seed=3, dropout_seed=0xd00d):
+    B, h, w, c = configs.dims(name, batch)
+    nets = []
+    for _ in range(2):
+        aetcnn.net_lib().an_rand_seed(seed)
+        n = aetcnn.Network(B, h, w, c)
+        configs.build(n, name)
+        n.dropout_seed(dropout_seed)
+        n.finalize()
+        nets.append(n)
+    return nets
+
+
+@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("fcnet", 16)])
+def test_graph_replay_matches_eager(gpu, name, batch):
+    """an_set_graph: replayed steps give bit-identical losses and parameters to
+    eager steps, with eager copies and reads between the replays, a new batch
+    every step, dropout masks advancing with the iteration, and a re-record
+    after a hyper-parameter change."""
+    eager, graph = _twin_nets(name, batch)
+    graph.set_graph(True)
+    n = eager.n_layers()
+    for step in range(6):
+        if step == 3:
+            for net in (eager, graph):
+                net.hyper(0.0005, 0.8, 0.001)
+        x, truth, _ = configs.synthetic_batch(name, 40 + step, batch)
+        losses = []
+        for net in (eager, graph):
+            net.set_input(x, truth)
+            net.train_step()
+            losses.append(net.loss())
+            # eager work between replays: a device read of a live buffer
+            net.buffer(0, 0)
+        assert losses[0] == losses[1], (name, step, losses)
+        assert eager.iteration() == graph.iteration() == step + 1
+        assert eager.seen() == graph.seen()
+    for i in range(n):
+        for which in (0, 2, 3, 4, 5, 6, 8, 9):
+            a, b = eager.buffer(i, which), graph.buffer(i, which)
+            if a is None:
+                continue
+            assert np.array_equal(a, b), (name, i, which)
+    # switching back to eager steps continues from the same state
+    graph.set_graph(False)
+    x, truth, _ = configs.synthetic_batch(name, 99, batch)
+    assert eager.train(x, truth) == graph.train(x, truth)
