@@ -29,6 +29,10 @@ LOGISTIC, RELU, LINEAR, LEAKY = 0, 1, 3, 7
 
 AN_CONVOLUTIONAL, AN_MAXPOOL, AN_AVGPOOL, AN_DROPOUT, AN_SOFTMAX = 0, 1, 2, 3, 4
 
+# an_policy (the reference's LearningRatePolicy order)
+(POLICY_CONSTANT, POLICY_STEP, POLICY_EXP, POLICY_POLY, POLICY_STEPS, POLICY_SIG,
+ POLICY_RANDOM) = range(7)
+
 _vp = C.c_void_p
 _sz = C.c_size_t
 _i = C.c_int
@@ -134,6 +138,10 @@ _NET = {
     "an_add_softmax": (_i, [_vp, _i, _f]),
     "an_set_hyper": (None, [_vp, _f, _f, _f]),
     "an_set_dropout_seed": (None, [_vp, _u64]),
+    "an_set_policy": (_i, [_vp, _i, _i, _f, _f, _f, _i, _i, _i, _vp, _vp]),
+    "an_rate": (_f, [_vp, _u64]),
+    "an_current_rate": (_f, [_vp]),
+    "an_set_subdivisions": (_i, [_vp, _i]),
     "an_finalize": (_i, [_vp]),
     "an_free": (None, [_vp]),
     "an_parse_cfg": (_vp, [C.c_char_p]),
@@ -339,6 +347,26 @@ class Network:
 
     def dropout_seed(self, seed):
         self.lib.an_set_dropout_seed(self.h, seed)
+
+    def policy(self, policy, burn_in=0, power=4.0, gamma=1.0, scale=1.0, step=1,
+               max_batches=0, steps=(), scales=()):
+        """NNetwork.getCurrentRate's policy (ids: POLICY_*)."""
+        st = np.ascontiguousarray(steps, np.int32)
+        sc = np.ascontiguousarray(scales, np.float32)
+        if st.size != sc.size:
+            raise ValueError("steps and scales need the same length")
+        check(self.lib.an_set_policy(self.h, policy, burn_in, power, gamma, scale, step,
+                                     max_batches, st.size, st.ctypes.data if st.size else None,
+                                     sc.ctypes.data if sc.size else None), "an_set_policy")
+
+    def rate(self, batch_num=None) -> float:
+        """getCurrentRate at batch_num (default: the next update's)."""
+        if batch_num is None:
+            return self.lib.an_current_rate(self.h)
+        return self.lib.an_rate(self.h, batch_num)
+
+    def subdivisions(self, s):
+        check(self.lib.an_set_subdivisions(self.h, s), "an_set_subdivisions")
 
     def finalize(self):
         check(self.lib.an_finalize(self.h), "an_finalize")

@@ -6,6 +6,11 @@
  *   [net]            parseNetOption NetworkFactory.c:671-700
  *                    batch=1 learning_rate=.001 momentum=.9 decay=.0001
  *                    subdivisions=1 (batch /= subdivisions)
+ *                    policy=constant burn_in=0 power=4 max_batches=0
+ *                    (NetworkFactory.c:676,763-823): step: step=1 scale=1;
+ *                    steps: steps=, scales= (comma lists, required);
+ *                    exp: gamma=1; sigmoid: gamma=1 step=1; unknown
+ *                    policy names fall back to constant (ConfigFile.c:159-168)
  *   [convolutional]  createConvolutional NetworkFactory.c:77-103
  *                    filters=1 size=1 stride=1 pad=0 padding=0
  *                    (pad=1 -> padding=size/2) activation=logistic
@@ -132,6 +137,82 @@ static int unsupported(const cfg_group *g, const char *key, int def)
     return 0;
 }
 
+/* a comma list of up to `cap` numbers ('#' ends it); returns the count or -1 */
+static int parse_list(const char *v, int cap, int *iv, float *fv)
+{
+    int n = 0;
+    const char *p = v;
+    while (*p && *p != '#') {
+        if (n == cap) return -1;
+        char *end;
+        const double x = strtod(p, &end);
+        if (end == p) return -1;
+        if (iv) iv[n] = (int)x;
+        if (fv) fv[n] = (float)x;
+        ++n;
+        p = end;
+        while (isspace((unsigned char)*p)) ++p;
+        if (*p == ',') ++p;
+        else if (*p && *p != '#') return -1;
+    }
+    return n;
+}
+
+#define CFG_MAX_STEPS 64
+
+/* parseNetOption's policy keys (NetworkFactory.c:763-823) */
+static int parse_policy(an_network *net, const cfg_group *g)
+{
+    static const struct { const char *name; int id; } names[] = {
+        {"random", AN_POLICY_RANDOM}, {"poly", AN_POLICY_POLY},
+        {"constant", AN_POLICY_CONSTANT}, {"step", AN_POLICY_STEP},
+        {"exp", AN_POLICY_EXP}, {"sigmoid", AN_POLICY_SIG}, {"steps", AN_POLICY_STEPS}};
+    const char *ps = find(g, "policy");
+    int policy = AN_POLICY_CONSTANT;
+    if (ps) {
+        int found = 0;
+        for (size_t i = 0; i < sizeof(names) / sizeof(names[0]); ++i)
+            if (!strcmp(ps, names[i].name)) {
+                policy = names[i].id;
+                found = 1;
+            }
+        if (!found) fprintf(stderr, "Couldn't find policy %s, going with constant\n", ps);
+    }
+    const int burn_in = geti(g, "burn_in", 0);
+    const float power = getf(g, "power", 4.f);
+    const int max_batches = geti(g, "max_batches", 0);
+    float gamma = 1.f, scale = 1.f;
+    int step = 1, nsteps = 0;
+    int steps[CFG_MAX_STEPS];
+    float scales[CFG_MAX_STEPS];
+    if (policy == AN_POLICY_STEP) {
+        step = geti(g, "step", 1);
+        scale = getf(g, "scale", 1.f);
+    } else if (policy == AN_POLICY_STEPS) {
+        const char *l = find(g, "steps"), *p = find(g, "scales");
+        if (!l || !p) {
+            fprintf(stderr, "an_parse_cfg: STEPS policy must have steps and scales\n");
+            return -1;
+        }
+        nsteps = parse_list(l, CFG_MAX_STEPS, steps, NULL);
+        if (nsteps <= 0 || parse_list(p, CFG_MAX_STEPS, NULL, scales) != nsteps) {
+            fprintf(stderr, "an_parse_cfg: steps and scales need the same count of numbers\n");
+            return -1;
+        }
+    } else if (policy == AN_POLICY_EXP) {
+        gamma = getf(g, "gamma", 1.f);
+    } else if (policy == AN_POLICY_SIG) {
+        gamma = getf(g, "gamma", 1.f);
+        step = geti(g, "step", 1);
+    }
+    if (an_set_policy(net, policy, burn_in, power, gamma, scale, step, max_batches, nsteps,
+                      steps, scales)) {
+        fprintf(stderr, "an_parse_cfg: invalid learning-rate policy settings\n");
+        return -1;
+    }
+    return 0;
+}
+
 an_network *an_parse_cfg(const char *path)
 {
     cfg_group *gs = NULL;
@@ -157,6 +238,7 @@ an_network *an_parse_cfg(const char *path)
         }
         an_set_hyper(net, getf(g, "learning_rate", .001f), getf(g, "momentum", .9f),
                      getf(g, "decay", .0001f));
+        if (an_set_subdivisions(net, subdivs) || parse_policy(net, g)) goto fail;
     }
     for (int i = 1; i < ng; ++i) {
         const cfg_group *g = &gs[i];

@@ -30,6 +30,16 @@ struct an_network {
     uint64_t dropout_seed;
     int cur_iteration;
     uint64_t seen;
+    /* minibatches per update (NNetwork.h:35); batch is the minibatch       */
+    int subdivisions;
+    /* index seen/batch of the current minibatch, taken before seen += batch:
+     * the step index of its dropout masks                                  */
+    uint32_t dropout_step;
+    /* learning-rate policy (NNetwork.h:29-31,39,45-51)                     */
+    int policy, burn_in, step, max_batches, num_steps;
+    float power, gamma, scale;
+    int *steps;
+    float *scales;
     int finalized;
     ach_stream_t stream;
     /* device memory */
@@ -61,6 +71,7 @@ struct an_network {
      * last kernel advances                                                  */
     int graph_on, recording;
     void *graph_exec;
+    float graph_rate;              /* the learning rate recorded in it      */
     uint32_t *d_iter;
     /* host copies of initial parameters until finalize */
     float **init_w;
@@ -94,6 +105,13 @@ an_network *an_network_create(int batch, int h, int w, int c)
     net->momentum = .9f;
     net->decay = .0001f;
     net->dropout_seed = 0x5eed;
+    net->subdivisions = 1;
+    /* policy defaults (NetworkFactory.c:763-773,817) */
+    net->policy = AN_POLICY_CONSTANT;
+    net->power = 4;
+    net->gamma = 1;
+    net->scale = 1;
+    net->step = 1;
     return net;
 }
 
@@ -366,7 +384,7 @@ static int dropout_forward(an_network *net, an_layer *l, an_state st)
         return ach_dropout_fwd_dev((float *)st.input, n, l->probability, net->dropout_seed,
                                    net->d_iter, (uint32_t)l->index, net->stream);
     return ach_dropout_fwd((float *)st.input, n, l->probability, net->dropout_seed,
-                           (uint32_t)net->cur_iteration, (uint32_t)l->index, net->stream);
+                           net->dropout_step, (uint32_t)l->index, net->stream);
 }
 
 static int dropout_backward(an_network *net, an_layer *l, an_state st)
@@ -377,7 +395,7 @@ static int dropout_backward(an_network *net, an_layer *l, an_state st)
         return ach_dropout_bwd_dev(st.delta, n, l->probability, net->dropout_seed, net->d_iter,
                                    (uint32_t)l->index, net->stream);
     return ach_dropout_bwd(st.delta, n, l->probability, net->dropout_seed,
-                           (uint32_t)net->cur_iteration, (uint32_t)l->index, net->stream);
+                           net->dropout_step, (uint32_t)l->index, net->stream);
 }
 
 int an_add_dropout(an_network *net, float probability)
@@ -455,6 +473,81 @@ void an_set_dropout_seed(an_network *net, uint64_t seed)
 {
     net->dropout_seed = seed;
     drop_graph(net);
+}
+
+int an_set_policy(an_network *net, int policy, int burn_in, float power, float gamma,
+                  float scale, int step, int max_batches, int num_steps, const int *steps,
+                  const float *scales)
+{
+    if (!net || policy < AN_POLICY_CONSTANT || policy > AN_POLICY_RANDOM || num_steps < 0 ||
+        (num_steps && (!steps || !scales)) || (policy == AN_POLICY_STEPS && !num_steps) ||
+        ((policy == AN_POLICY_STEP || policy == AN_POLICY_SIG) && step <= 0) || burn_in < 0)
+        return ACH_EINVAL;
+    int *st = NULL;
+    float *sc = NULL;
+    if (num_steps) {
+        st = (int *)malloc(sizeof(int) * num_steps);
+        sc = (float *)malloc(sizeof(float) * num_steps);
+        if (!st || !sc) {
+            free(st);
+            free(sc);
+            return ACH_EINVAL; /* host allocation failed */
+        }
+        memcpy(st, steps, sizeof(int) * num_steps);
+        memcpy(sc, scales, sizeof(float) * num_steps);
+    }
+    free(net->steps);
+    free(net->scales);
+    net->steps = st;
+    net->scales = sc;
+    net->num_steps = num_steps;
+    net->policy = policy;
+    net->burn_in = burn_in;
+    net->power = power;
+    net->gamma = gamma;
+    net->scale = scale;
+    net->step = step;
+    net->max_batches = max_batches;
+    drop_graph(net);
+    return ACH_OK;
+}
+
+int an_set_subdivisions(an_network *net, int subdivisions)
+{
+    if (!net || subdivisions < 1) return ACH_EINVAL;
+    net->subdivisions = subdivisions;
+    drop_graph(net);
+    return ACH_OK;
+}
+
+/* NNetwork.getCurrentRate (NNetwork.c:215-246) with the reference's types:
+ * batch_num is size_t (getCurrentBatch, NNetwork.c:154-157), so in the
+ * sigmoid policy batch_num - step wraps around below step (the rate is
+ * then 0 for gamma > 0), and burn_in and steps[i] compare as size_t.  The
+ * random policy draws randUniform(0,1) from rand() (DnnUtils.c:196-209).  */
+float an_rate(an_network *net, uint64_t batch_num64)
+{
+    const size_t batch_num = (size_t)batch_num64;
+    const float lr = net->learning_rate;
+    if (batch_num < (size_t)net->burn_in)
+        return lr * pow((float)batch_num / net->burn_in, net->power);
+    switch (net->policy) {
+    case AN_POLICY_STEP: return lr * pow(net->scale, batch_num / (size_t)net->step);
+    case AN_POLICY_STEPS: {
+        float rate = lr;
+        for (int i = 0; i < net->num_steps; ++i) {
+            if ((size_t)net->steps[i] > batch_num) return rate;
+            rate *= net->scales[i];
+        }
+        return rate;
+    }
+    case AN_POLICY_EXP: return lr * pow(net->gamma, (int)batch_num);
+    case AN_POLICY_POLY: return lr * pow(1 - (float)batch_num / net->max_batches, net->power);
+    case AN_POLICY_RANDOM: return lr * pow(rand_uniform(0, 1), net->power);
+    case AN_POLICY_SIG:
+        return lr * (1. / (1. + exp(net->gamma * (float)(batch_num - (size_t)net->step))));
+    default: return lr;
+    }
 }
 
 int an_set_graph(an_network *net, int on)
@@ -690,6 +783,8 @@ void an_free(an_network *net)
     if (net->wstream) ach_stream_sync(net->wstream);
     if (net->stream) ach_stream_sync(net->stream);
     drop_graph(net);
+    free(net->steps);
+    free(net->scales);
     if (net->ev_ready) {
         for (int i = 0; i < net->n; ++i)
             if (net->ev_ready[i]) ach_event_destroy(net->ev_ready[i]);
@@ -817,19 +912,29 @@ int an_layer_backward(an_network *net, int i)
     return join_wgrad(net);
 }
 
-/* NNetwork.updateCPU (NNetwork.c:667-680) with the constant rate policy:
- * every conv layer's update, as two launches over the flat buffers.        */
-int an_update(an_network *net)
+/* NNetwork.updateCPU (NNetwork.c:667-680): every conv layer's update with
+ * update batch = batch * subdivisions, as two launches over the flat
+ * buffers.                                                                 */
+static int update_at_rate(an_network *net, float rate)
 {
-    if (!net || !net->finalized) return ACH_EINVAL;
-    const int batch = net->batch; /* batch * subdivisions, subdivisions = 1 */
-    const float rate = net->learning_rate;
+    const int batch = net->batch * net->subdivisions;
     const float a1 = -net->decay * batch;
     const float a2 = rate / batch;
     AN_CHECK(ach_sgd_update(net->nweights_total, net->wflat, net->vflat, a1, a2, net->momentum,
                             net->stream));
     return ach_sgd_update(net->nbias_total, net->bflat, net->bvflat, 0.f, a2, net->momentum,
                           net->stream);
+}
+
+float an_current_rate(an_network *net)
+{
+    return an_rate(net, net->seen / ((uint64_t)net->batch * (uint64_t)net->subdivisions));
+}
+
+int an_update(an_network *net)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    return update_at_rate(net, an_current_rate(net));
 }
 
 /* NNetwork.predict (NNetwork.c:411-422): forward with train = 0 (BN on the
@@ -886,25 +991,25 @@ void an_top_k(const float *a, int n, int k, int *index)
 
 /* the kernels of one training step: forward, both backward streams, update
  * and, in graph mode, the device step index advanced                       */
-static int enqueue_step(an_network *net)
+static int enqueue_step(an_network *net, int update, float rate)
 {
     AN_CHECK(an_forward(net, 1));
     AN_CHECK(an_backward(net));
-    AN_CHECK(an_update(net));
+    if (update) AN_CHECK(update_at_rate(net, rate));
     return net->recording ? ach_counter_add(net->d_iter, 1u, net->stream) : ACH_OK;
 }
 
 /* Graph mode records enqueue_step once (after copying cur_iteration to the
  * device) and replays it; every replay is the same kernel sequence with the
  * same arguments, reading the current input, weights and step index.      */
-static int train_step_graph(an_network *net)
+static int train_step_graph(an_network *net, float rate)
 {
+    if (net->graph_exec && rate != net->graph_rate) drop_graph(net);
     if (!net->graph_exec) {
-        const uint32_t it = (uint32_t)net->cur_iteration;
-        AN_CHECK(ach_memcpy_h2d(net->d_iter, &it, sizeof(it), net->stream));
+        AN_CHECK(ach_memcpy_h2d(net->d_iter, &net->dropout_step, sizeof(uint32_t), net->stream));
         AN_CHECK(ach_graph_capture_begin(net->stream));
         net->recording = 1;
-        const int rc = enqueue_step(net);
+        const int rc = enqueue_step(net, 1, rate);
         net->recording = 0;
         void *exec = NULL;
         const int rc2 = ach_graph_capture_end(net->stream, &exec);
@@ -913,16 +1018,25 @@ static int train_step_graph(an_network *net)
             return rc ? rc : rc2;
         }
         net->graph_exec = exec;
+        net->graph_rate = rate;
     }
     return ach_graph_launch(net->graph_exec, net->stream);
 }
 
+/* One minibatch of NNetwork.train(ImageData) (NNetwork.c:762-805, with
+ * NNetwork.train(input, truth) at :740-758): seen += batch, forward,
+ * backward; after every subdivisions-th minibatch cur_iteration += 1 and
+ * the update at the policy's rate.                                        */
 int an_train_step(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
+    if (net->graph_on && net->subdivisions != 1) return ACH_EINVAL;
+    net->dropout_step = (uint32_t)(net->seen / (uint64_t)net->batch);
     net->seen += (uint64_t)net->batch;
-    AN_CHECK(net->graph_on ? train_step_graph(net) : enqueue_step(net));
-    net->cur_iteration += 1;
+    const int update = (net->seen / (uint64_t)net->batch) % (uint64_t)net->subdivisions == 0;
+    const float rate = update ? an_current_rate(net) : 0.f;
+    AN_CHECK(net->graph_on ? train_step_graph(net, rate) : enqueue_step(net, update, rate));
+    if (update) net->cur_iteration += 1;
     return ACH_OK;
 }
 
@@ -1032,7 +1146,9 @@ double an_step_conv_gflop(const an_network *net)
  *   for each convolutional layer in order:
  *     biases[n], (batch_normalize: scales[n], rolling_mean[n],
  *     rolling_variance[n]), weights[nweights]  (float32 each)
- * seen = iteration * batch * subdivisions (subdivisions = 1 here).        */
+ * Save writes seen = cur_iteration * batch * subdivisions and, as the
+ * reference does (NNetwork.c:125), makes that the network's seen; load
+ * sets cur_iteration = seen / (batch * subdivisions) (NNetwork.c:88).     */
 
 /* one conv layer's parameter arrays in file order */
 static int conv_param_arrays(an_layer *l, float **ptr, size_t *cnt)
@@ -1068,7 +1184,9 @@ int an_save_weights(an_network *net, const char *path)
         return ACH_EINVAL;
     }
     const int32_t hdr[3] = {0, 2, 5};
-    const uint64_t seen = (uint64_t)net->cur_iteration * (uint64_t)net->batch;
+    const uint64_t seen =
+        (uint64_t)net->cur_iteration * (uint64_t)net->batch * (uint64_t)net->subdivisions;
+    net->seen = seen;
     int rc = ACH_OK;
     if (fwrite(hdr, sizeof(int32_t), 3, fp) != 3 || fwrite(&seen, sizeof(seen), 1, fp) != 1)
         rc = ACH_EINVAL;
@@ -1122,7 +1240,7 @@ int an_load_weights(an_network *net, const char *path)
         }
         net->seen = seen;
     }
-    net->cur_iteration = (int)(net->seen / (uint64_t)net->batch);
+    net->cur_iteration = (int)(net->seen / ((uint64_t)net->batch * net->subdivisions));
     drop_graph(net); /* the recorded step's device step index is stale */
     int rc = ACH_OK;
     float *host = NULL;

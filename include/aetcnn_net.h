@@ -111,12 +111,42 @@ int an_add_dropout(an_network *net, float probability);
 int an_add_softmax(an_network *net, int groups, float temperature);
 void an_set_hyper(an_network *net, float learning_rate, float momentum, float decay);
 void an_set_dropout_seed(an_network *net, uint64_t seed);
+
+/* Learning-rate policy: NNetwork.getCurrentRate (NNetwork.c:215-246) with
+ * the [net] keys of parseNetOption (NetworkFactory.c:763-823); ids in the
+ * order of the LearningRatePolicy enum (NNetwork.h:29-31).  Defaults:
+ * constant, burn_in 0, power 4, gamma 1, scale 1, step 1.  steps/scales
+ * (num_steps each, STEPS policy) are copied.  Rates are computed on the
+ * host as the reference computes them, including its size_t arithmetic
+ * (the sigmoid policy gives 0 below `step` for gamma > 0).                */
+typedef enum {
+    AN_POLICY_CONSTANT = 0,
+    AN_POLICY_STEP = 1,
+    AN_POLICY_EXP = 2,
+    AN_POLICY_POLY = 3,
+    AN_POLICY_STEPS = 4,
+    AN_POLICY_SIG = 5,
+    AN_POLICY_RANDOM = 6
+} an_policy;
+int an_set_policy(an_network *net, int policy, int burn_in, float power, float gamma,
+                  float scale, int step, int max_batches, int num_steps, const int *steps,
+                  const float *scales);
+/* getCurrentRate at batch_num (host only; the random policy draws rand()) */
+float an_rate(an_network *net, uint64_t batch_num);
+/* the rate the next update uses: an_rate at seen / (batch * subdivisions)  */
+float an_current_rate(an_network *net);
+/* subdivisions (NNetwork.h:35): minibatches per update.  The network's
+ * batch is the minibatch (the cfg's batch / subdivisions); an_train_step
+ * runs one minibatch and updates after every subdivisions-th, with update
+ * batch = batch * subdivisions (NNetwork.c:667-680, 762-805).           */
+int an_set_subdivisions(an_network *net, int subdivisions);
 /* allocate device memory, upload initial parameters, size the workspace   */
 int an_finalize(an_network *net);
 void an_free(an_network *net);
 /* Builds a network from a darknet-style .cfg file (ConfigFile.c:12-208,
  * NetworkFactory.c:615-1013): [net] batch/subdivisions/width/height/channels/
- * learning_rate/momentum/decay; [convolutional] filters/size/stride/pad/
+ * learning_rate/momentum/decay and the policy keys policy/burn_in/power/
+ * step/scale/steps/scales/gamma/max_batches; [convolutional] filters/size/stride/pad/
  * padding/activation/batch_normalize; [connected] output/activation/
  * batch_normalize (darknet's keys, an_add_connected); [maxpool] size/stride/
  * padding; [avgpool]; [dropout] probability; [softmax] groups/temperature.  Returns
@@ -162,9 +192,12 @@ ach_stream_t an_stream(an_network *net);
 int an_set_input(an_network *net, const float *host_input, const float *host_truth);
 /* the same from device buffers (device-to-device copy on the net stream) */
 int an_set_input_device(an_network *net, const float *dev_input, const float *dev_truth);
-/* NNetwork.train(input, truth) + update, on the resident input: enqueues the
- * whole step on the network's stream and returns without synchronising;
- * the loss stays on the device until an_get_loss.                          */
+/* One minibatch of NNetwork.train (NNetwork.c:740-805) on the resident
+ * input: seen += batch, forward, backward, and after every
+ * subdivisions-th minibatch cur_iteration += 1 and the update.  Enqueues
+ * on the network's stream and returns without synchronising; the loss
+ * stays on the device until an_get_loss.  Dropout masks use the index
+ * seen/batch of the minibatch (before the increment) as their step.       */
 int an_train_step(an_network *net);
 /* Graph replay of an_train_step; no counterpart in the reference (its
  * training loop calls the layers one by one, NNetwork.c:740-805).  For
@@ -173,10 +206,13 @@ int an_train_step(an_network *net);
  * into a HIP graph and every step replays it: the same kernels and
  * arguments, reading the current input, truth and weights, and a device
  * copy of the iteration for the dropout masks, so results are the same as
- * eager steps.  an_set_hyper, an_set_dropout_seed, an_load_weights,
- * an_fuse_conv_batchnorm and on == 0 drop the recording.                   */
+ * eager steps.  an_set_hyper, an_set_dropout_seed, an_set_policy,
+ * an_set_subdivisions, an_load_weights, an_fuse_conv_batchnorm and
+ * on == 0 drop the recording; a step whose learning rate differs from the
+ * recorded one re-records it.  Needs subdivisions == 1 (ACH_EINVAL).      */
 int an_set_graph(an_network *net, int on);
-/* synchronises and returns sum(cost)/batch of the last step (NNetwork.c:804) */
+/* synchronises and returns sum(cost)/batch of the last minibatch (the
+ * reference returns the mean of these over the subdivisions, NNetwork.c:804) */
 int an_get_loss(an_network *net, float *loss);
 /* host-buffer convenience: set_input + train_step + get_loss               */
 int an_train(an_network *net, const float *host_input, const float *host_truth, float *loss);

@@ -681,6 +681,16 @@ struct or_net {
     float learning_rate, momentum, decay;
     uint64_t dropout_seed;
     uint32_t cur_iteration;
+    /* NNetwork.seen / subdivisions (NNetwork.h:32-35); the dropout masks of
+     * a minibatch use its index seen/batch taken before seen += batch      */
+    uint64_t seen;
+    uint32_t dropout_step;
+    int subdivisions;
+    /* learning-rate policy (NNetwork.h:29-31,39,45-51) */
+    int policy, burn_in, step, max_batches, num_steps;
+    float power, gamma, scale;
+    int *steps;
+    float *scales;
     float *workspace;
     size_t workspace_size;
     float *input; /* host copy of the current input (layer 0 reads it) */
@@ -699,6 +709,13 @@ or_net *or_net_create(int batch, int h, int w, int c)
     net->momentum = .9f;
     net->decay = .0001f;
     net->dropout_seed = 0x5eed;
+    net->subdivisions = 1;
+    /* parseNetOption defaults (NetworkFactory.c:763-773,817) */
+    net->policy = OR_POLICY_CONSTANT;
+    net->power = 4;
+    net->gamma = 1;
+    net->scale = 1;
+    net->step = 1;
     return net;
 }
 
@@ -865,6 +882,75 @@ void or_net_set_hyper(or_net *net, float learning_rate, float momentum, float de
 
 void or_net_set_dropout_seed(or_net *net, uint64_t seed) { net->dropout_seed = seed; }
 
+void or_net_set_subdivisions(or_net *net, int subdivisions)
+{
+    net->subdivisions = subdivisions > 0 ? subdivisions : 1;
+}
+
+void or_net_set_policy(or_net *net, int policy, int burn_in, float power, float gamma,
+                       float scale, int step, int max_batches, int num_steps, const int *steps,
+                       const float *scales)
+{
+    net->policy = policy;
+    net->burn_in = burn_in;
+    net->power = power;
+    net->gamma = gamma;
+    net->scale = scale;
+    net->step = step;
+    net->max_batches = max_batches;
+    free(net->steps);
+    free(net->scales);
+    net->steps = NULL;
+    net->scales = NULL;
+    net->num_steps = num_steps > 0 ? num_steps : 0;
+    if (net->num_steps) {
+        net->steps = (int *)malloc(sizeof(int) * net->num_steps);
+        net->scales = (float *)malloc(sizeof(float) * net->num_steps);
+        memcpy(net->steps, steps, sizeof(int) * net->num_steps);
+        memcpy(net->scales, scales, sizeof(float) * net->num_steps);
+    }
+}
+
+/* NNetwork.getCurrentRate (NNetwork.c:215-246) with the reference's types:
+ * batch_num is size_t (getCurrentBatch, NNetwork.c:154-157), so in the
+ * sigmoid policy batch_num - step wraps around below step (the rate is
+ * then 0 for gamma > 0); burn_in and steps[i] compare as size_t.  The
+ * random policy draws randUniform(0,1) from rand().                     */
+float or_lr_rate(int policy, float learning_rate, uint64_t batch_num64, int burn_in, float power,
+                 float gamma, float scale, int step, int max_batches, int num_steps,
+                 const int *steps, const float *scales)
+{
+    const size_t batch_num = (size_t)batch_num64;
+    if (batch_num < (size_t)burn_in)
+        return learning_rate * pow((float)batch_num / burn_in, power);
+    switch (policy) {
+    case OR_POLICY_CONSTANT: return learning_rate;
+    case OR_POLICY_STEP: return learning_rate * pow(scale, batch_num / (size_t)step);
+    case OR_POLICY_STEPS: {
+        float rate = learning_rate;
+        for (int i = 0; i < num_steps; ++i) {
+            if ((size_t)steps[i] > batch_num) return rate;
+            rate *= scales[i];
+        }
+        return rate;
+    }
+    case OR_POLICY_EXP: return learning_rate * pow(gamma, (int)batch_num);
+    case OR_POLICY_POLY: return learning_rate * pow(1 - (float)batch_num / max_batches, power);
+    case OR_POLICY_RANDOM: return learning_rate * pow(or_rand_uniform(0, 1), power);
+    case OR_POLICY_SIG:
+        return learning_rate * (1. / (1. + exp(gamma * (float)(batch_num - (size_t)step))));
+    default: return learning_rate;
+    }
+}
+
+float or_net_rate(or_net *net)
+{
+    const uint64_t batch_num = net->seen / ((uint64_t)net->batch * net->subdivisions);
+    return or_lr_rate(net->policy, net->learning_rate, batch_num, net->burn_in, net->power,
+                      net->gamma, net->scale, net->step, net->max_batches, net->num_steps,
+                      net->steps, net->scales);
+}
+
 int or_net_finalize(or_net *net)
 {
     size_t ws = 0;
@@ -900,6 +986,8 @@ void or_net_free(or_net *net)
     free(net->workspace);
     free(net->input);
     free(net->truth);
+    free(net->steps);
+    free(net->scales);
     free(net);
 }
 
@@ -965,7 +1053,7 @@ static void layer_forward(or_net *net, or_layer *l, or_state st)
     case L_DROPOUT:
         if (st.train)
             or_dropout_forward(st.input, l->batch * l->inputs, l->probability,
-                               net->dropout_seed, net->cur_iteration, (uint32_t)st.index);
+                               net->dropout_seed, net->dropout_step, (uint32_t)st.index);
         break;
     case L_SOFTMAX:
         l->cost = or_softmax_xent_forward(st.input, l->batch, l->inputs, l->groups,
@@ -990,7 +1078,7 @@ static void layer_backward(or_net *net, or_layer *l, or_state st)
     case L_DROPOUT:
         if (st.delta)
             or_dropout_backward(st.delta, l->batch * l->inputs, l->probability,
-                                net->dropout_seed, net->cur_iteration, (uint32_t)st.index);
+                                net->dropout_seed, net->dropout_step, (uint32_t)st.index);
         break;
     case L_SOFTMAX:
         if (st.delta) or_softmax_backward(l->delta, l->batch * l->inputs, st.delta);
@@ -1057,24 +1145,31 @@ float or_net_cost(or_net *net)
     return cost / net->batch;
 }
 
+/* NNetwork.train(input, truth) (NNetwork.c:740-758): seen += batch, then
+ * forward and backward; returns the cost / batch.                        */
 float or_net_forward_backward(or_net *net, const float *input, const float *truth)
 {
+    net->dropout_step = (uint32_t)(net->seen / (uint64_t)net->batch);
+    net->seen += (uint64_t)net->batch;
     or_net_load(net, input, truth);
     for (int i = 0; i < net->n; ++i) or_net_layer_forward(net, i, 1);
     for (int i = net->n - 1; i >= 0; --i) or_net_layer_backward(net, i);
     return or_net_cost(net);
 }
 
+/* cur_iteration += 1, then updateCPU (NNetwork.c:667-680, 788-789): every
+ * conv layer with update batch = batch * subdivisions and the policy's rate */
 void or_net_update(or_net *net)
 {
-    /* updateCPU, NNetwork.c:667-680 (constant policy, burn_in 0) */
     net->cur_iteration += 1;
+    const int update_batch = net->batch * net->subdivisions;
+    const float rate = or_net_rate(net);
     for (int i = 0; i < net->n; ++i) {
         or_layer *l = &net->layers[i];
         if (l->type != L_CONV) continue;
         or_conv_update(l->nweights, l->weights, l->weight_updates, l->n, l->biases,
-                       l->bias_updates, l->scales, l->scale_updates, net->batch,
-                       net->learning_rate, net->momentum, net->decay);
+                       l->bias_updates, l->scales, l->scale_updates, update_batch, rate,
+                       net->momentum, net->decay);
     }
 }
 
@@ -1103,12 +1198,18 @@ void or_net_fuse_conv_batchnorm(or_net *net)
     }
 }
 
+/* One minibatch of NNetwork.train(ImageData) (NNetwork.c:762-805): the
+ * update runs after every subdivisions-th minibatch, when the gradient sums
+ * hold the whole batch * subdivisions images.                             */
 float or_net_train(or_net *net, const float *input, const float *truth)
 {
     float loss = or_net_forward_backward(net, input, truth);
-    or_net_update(net);
+    if ((net->seen / (uint64_t)net->batch) % (uint64_t)net->subdivisions == 0) or_net_update(net);
     return loss;
 }
+
+uint64_t or_net_seen(const or_net *net) { return net->seen; }
+int or_net_iteration(const or_net *net) { return (int)net->cur_iteration; }
 
 int or_net_n_layers(const or_net *net) { return net->n; }
 

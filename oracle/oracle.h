@@ -147,6 +147,15 @@ void or_conv_update(int n_weights, float *weights, float *weight_updates,
 void or_rand_seed(unsigned seed);
 float or_rand_uniform(float min, float max);
 
+/* ---- learning-rate policy (NNetwork.c:215-246; ids in the order of the
+ *      LearningRatePolicy enum, NNetwork.h:29-31) --------------------------- */
+enum { OR_POLICY_CONSTANT = 0, OR_POLICY_STEP = 1, OR_POLICY_EXP = 2, OR_POLICY_POLY = 3,
+       OR_POLICY_STEPS = 4, OR_POLICY_SIG = 5, OR_POLICY_RANDOM = 6 };
+/* getCurrentRate at batch_num = seen / (batch * subdivisions)              */
+float or_lr_rate(int policy, float learning_rate, uint64_t batch_num, int burn_in, float power,
+                 float gamma, float scale, int step, int max_batches, int num_steps,
+                 const int *steps, const float *scales);
+
 /* ---- whole network (NNetwork.c:382-396, 627-680, 740-805) ------------------ */
 typedef struct or_net or_net;
 or_net *or_net_create(int batch, int h, int w, int c);
@@ -161,12 +170,25 @@ int  or_net_add_dropout(or_net *net, float probability);
 int  or_net_add_softmax(or_net *net, int groups, float temperature);
 void or_net_set_hyper(or_net *net, float learning_rate, float momentum, float decay);
 void or_net_set_dropout_seed(or_net *net, uint64_t seed);
+/* parseNetOption's policy keys (NetworkFactory.c:768-823); steps/scales
+ * are copied                                                              */
+void or_net_set_policy(or_net *net, int policy, int burn_in, float power, float gamma,
+                       float scale, int step, int max_batches, int num_steps, const int *steps,
+                       const float *scales);
+/* minibatches per update (NNetwork.h:35); batch given to or_net_create is
+ * the minibatch                                                           */
+void or_net_set_subdivisions(or_net *net, int subdivisions);
+/* the rate the next update uses: or_lr_rate at seen/(batch*subdivisions)   */
+float or_net_rate(or_net *net);
+uint64_t or_net_seen(const or_net *net);
+int  or_net_iteration(const or_net *net);
 int  or_net_finalize(or_net *net);   /* allocates workspace */
 void or_net_free(or_net *net);
-/* one train step on host buffers: input [batch][c][h][w], truth [batch][classes]
- * returns the loss reported by NNetwork.train (sum(cost)/batch)            */
+/* one minibatch on host buffers: input [batch][c][h][w], truth
+ * [batch][classes]; forward + backward, then the update after every
+ * subdivisions-th minibatch.  Returns that minibatch's sum(cost)/batch.     */
 float or_net_train(or_net *net, const float *input, const float *truth);
-/* forward + backward only (no update)                                       */
+/* NNetwork.train(input, truth): seen += batch, forward + backward only      */
 float or_net_forward_backward(or_net *net, const float *input, const float *truth);
 void or_net_update(or_net *net);
 /* NNetwork.predict (NNetwork.c:411-422): inference forward (BN with rolling

@@ -63,6 +63,12 @@ _SIGS = {
     "or_net_add_softmax": (_i, [_vp, _i, _f]),
     "or_net_set_hyper": (None, [_vp, _f, _f, _f]),
     "or_net_set_dropout_seed": (None, [_vp, _u64]),
+    "or_lr_rate": (_f, [_i, _f, _u64, _i, _f, _f, _f, _i, _i, _i, _vp, _vp]),
+    "or_net_set_policy": (None, [_vp, _i, _i, _f, _f, _f, _i, _i, _i, _vp, _vp]),
+    "or_net_set_subdivisions": (None, [_vp, _i]),
+    "or_net_rate": (_f, [_vp]),
+    "or_net_seen": (_u64, [_vp]),
+    "or_net_iteration": (_i, [_vp]),
     "or_net_finalize": (_i, [_vp]),
     "or_net_free": (None, [_vp]),
     "or_net_train": (_f, [_vp, _vp, _vp]),
@@ -302,6 +308,27 @@ class OracleNet:
     def dropout_seed(self, seed):
         self.L.or_net_set_dropout_seed(self.h, seed)
 
+    def policy(self, policy, burn_in=0, power=4.0, gamma=1.0, scale=1.0, step=1,
+               max_batches=0, steps=(), scales=()):
+        st = np.ascontiguousarray(steps, np.int32)
+        sc = np.ascontiguousarray(scales, np.float32)
+        assert st.size == sc.size
+        self.L.or_net_set_policy(self.h, policy, burn_in, power, gamma, scale, step,
+                                 max_batches, st.size, P(st) if st.size else None,
+                                 P(sc) if sc.size else None)
+
+    def subdivisions(self, s):
+        self.L.or_net_set_subdivisions(self.h, s)
+
+    def rate(self):
+        return self.L.or_net_rate(self.h)
+
+    def seen(self):
+        return self.L.or_net_seen(self.h)
+
+    def iteration(self):
+        return self.L.or_net_iteration(self.h)
+
     def finalize(self):
         assert self.L.or_net_finalize(self.h) == 0
 
@@ -370,3 +397,16 @@ class OracleNet:
             self.close()
         except Exception:
             pass
+
+
+# LearningRatePolicy ids (NNetwork.h:29-31)
+CONSTANT, STEP, EXP, POLY, STEPS, SIG, RANDOM = range(7)
+
+
+def lr_rate(policy, lr, batch_num, burn_in=0, power=4.0, gamma=1.0, scale=1.0, step=1,
+            max_batches=0, steps=(), scales=()):
+    st = np.ascontiguousarray(steps, np.int32)
+    sc = np.ascontiguousarray(scales, np.float32)
+    return lib().or_lr_rate(policy, lr, batch_num, burn_in, power, gamma, scale, step,
+                            max_batches, st.size, P(st) if st.size else None,
+                            P(sc) if sc.size else None)

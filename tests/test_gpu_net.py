@@ -418,3 +418,82 @@ def test_graph_replay_matches_eager(gpu, name, batch):
     graph.set_graph(False)
     x, truth, _ = configs.synthetic_batch(name, 99, batch)
     assert eager.train(x, truth) == graph.train(x, truth)
+
+
+def test_policy_and_subdivisions_match_oracle(gpu, oracle):
+    """Config 3 at minibatch 8 with subdivisions = 2 (BN, dropout), a burn-in
+    ramp and the poly policy.  At the start of each iteration the GPU network
+    takes the oracle's training state (as in the teacher-forced steps above);
+    each minibatch's loss agrees within 1e-3, the update runs only after
+    every second minibatch, and the updated parameters agree within 1e-4."""
+    oracle.lib().or_set_gemm_parallel(1)
+    net, onet = make_pair(oracle, "darknet", 8)
+    kw = dict(burn_in=2, power=1.0, max_batches=20)
+    net.policy(aetcnn.POLICY_POLY, **kw)
+    onet.policy(oracle.POLY, **kw)
+    net.subdivisions(2)
+    onet.subdivisions(2)
+    for step in range(6):
+        if step % 2 == 0:
+            for i in conv_layers(onet):
+                for code in STATE_CODES:
+                    v = onet.buffer(i, code)
+                    if v is not None and v.size:
+                        net.set_buffer(i, code, v)
+            w0 = net.buffer(0, 2).copy()
+        x, truth, _ = configs.synthetic_batch("darknet", 300 + step, 8)
+        l_gpu = net.train(x, truth)
+        l_ref = onet.train(x, truth)
+        assert abs(l_gpu - l_ref) <= 1e-3, (step, l_gpu, l_ref)
+        assert net.iteration() == onet.iteration() == (step + 1) // 2
+        assert net.seen() == onet.seen() == 8 * (step + 1)
+        assert net.rate() == onet.rate(), step
+        if step % 2 == 0:
+            assert np.array_equal(net.buffer(0, 2), w0), "updated after one minibatch"
+            continue
+        for i in conv_layers(onet):
+            for code in (2, 4, 6):
+                v = onet.buffer(i, code)
+                if v is not None and v.size:
+                    assert rel_err(net.buffer(i, code), v) < TOL, (step, i, code)
+
+
+def test_graph_replay_with_changing_rate(gpu):
+    """A policy whose rate changes every update re-records the graph each
+    step; the replays still equal eager steps bit for bit.  Graph mode
+    refuses subdivisions > 1."""
+    eager, graph = _twin_nets("darknet", 8)
+    for net in (eager, graph):
+        net.policy(aetcnn.POLICY_EXP, gamma=0.9)
+    graph.set_graph(True)
+    for step in range(3):
+        x, truth, _ = configs.synthetic_batch("darknet", 70 + step, 8)
+        assert eager.train(x, truth) == graph.train(x, truth), step
+    for i in range(eager.n_layers()):
+        for which in (2, 4, 6, 8, 9):
+            a, b = eager.buffer(i, which), graph.buffer(i, which)
+            if a is not None:
+                assert np.array_equal(a, b), (i, which)
+    graph.subdivisions(2)
+    assert aetcnn.net_lib().an_train_step(graph.h) == aetcnn.ACH_EINVAL
+
+
+def test_cfg_policy_keys(gpu, oracle, tmp_path):
+    """[net] policy keys and subdivisions parsed as parseNetOption does."""
+    cfg = tmp_path / "p.cfg"
+    cfg.write_text("[net]\nbatch=16\nsubdivisions=2\nheight=8\nwidth=8\nchannels=3\n"
+                   "learning_rate=0.2\npolicy=steps\nsteps=3, 6 ,9\nscales=.5,.1,2\n"
+                   "burn_in=2\npower=1\n\n"
+                   "[convolutional]\nfilters=4\nsize=3\npad=1\nactivation=leaky\n\n"
+                   "[avgpool]\n\n[softmax]\n")
+    net = aetcnn.Network.from_cfg(str(cfg))
+    assert net.batch == 8
+    for n in range(12):
+        want = oracle.lr_rate(oracle.STEPS, 0.2, n, burn_in=2, power=1.0, steps=[3, 6, 9],
+                              scales=[0.5, 0.1, 2.0])
+        assert net.rate(n) == want, n
+    bad = tmp_path / "bad.cfg"
+    bad.write_text("[net]\nbatch=4\nheight=8\nwidth=8\nchannels=3\npolicy=steps\nsteps=3\n\n"
+                   "[convolutional]\nfilters=4\nsize=1\n\n[avgpool]\n\n[softmax]\n")
+    with pytest.raises(ValueError):
+        aetcnn.Network.from_cfg(str(bad))
