@@ -100,6 +100,7 @@ _OPS = {
     "ach_conv_prepare_filters": (_i, [_i, _vp, _vp]),
     "ach_conv_fwd_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ach_conv_bwd_data_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_conv_fwd_bias_act_prepared": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _sz, _vp]),
     "ach_bn_infer": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]),
     "ach_conv_bn_fold": (_i, [_i, _i, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ach_bn_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,

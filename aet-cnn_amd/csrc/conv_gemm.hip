@@ -692,10 +692,35 @@ struct PlainOperand {
 // ===========================================================================
 // Problems: operand loaders + k range + epilogue.
 // ===========================================================================
+// Output epilogue of the forward GEMMs: the layer's bias and activation
+// applied to each finished sum, as the separate passes would apply them
+// (IOData.addBias then activate, IOData.c:43-72), in one branch-free form
+// so the kernel keeps a single epilogue.  Kernels instantiated with the
+// epilogue (EPI) hold every accumulator in VGPRs at the end, so 256-row
+// tiles, whose 128 accumulators would halve the occupancy, take it only in
+// the split-K reduction.
+//   v += bias[m]            (no bias: v + -0.0f, which is v for every v)
+//   v = v > 0 ? v : (float)(slope * (double)v)
+// slope 0.1 is act_forward's leaky; slope 0 gives relu's v * (v > 0)
+// (+-0 with the sign of v, NaN kept); slope 1 is linear.  The default
+// (no bias, slope 1) leaves v unchanged.  The logistic activation, with
+// its double exp, stays a separate pass.
+struct Epi {
+    const float *bias = nullptr;
+    double slope = 1.0;
+    bool active() const { return bias != nullptr || slope != 1.0; }
+    __device__ __forceinline__ float apply(float v, int m) const
+    {
+        const float b = bias ? bias[m] : -0.0f;
+        v = v + b;
+        return v > 0.f ? v : (float)(slope * (double)v);
+    }
+};
+
 // Forward: y[b][m][p] = sum_k Wt[k][m] * im2col(x)[k][b*OHW+p].  With
 // splits > 1 each z-slice of K writes part[z][m][n] and a fixed-order
 // reduction produces y (used when the tile grid alone cannot fill the GPU).
-template <int BM_, class BL, bool VECA = false>
+template <int BM_, class BL, bool VECA = false, bool EPI = false>
 struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
     // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
@@ -711,6 +736,7 @@ struct FwdProblem {
     float *y, *part;
     ConvGeom g;
     int M, N, K, kchunk, splits;
+    Epi e;  // EPI: applied here (only without a K split)
     __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
     {
         kb = z * kchunk;
@@ -727,6 +753,7 @@ struct FwdProblem {
         }
         const int ohw = g.OH * g.OW;
         const int b = n / ohw, p = n - b * ohw;
+        if constexpr (EPI) v = e.apply(v, m);
         y[((size_t)b * M + m) * ohw + p] = v;
     }
 };
@@ -831,7 +858,7 @@ struct GemmProblem {
 // Forward / input gradient: M = F, N = B, K = C; A = the k-major filter
 // Wt[K][M] (m contiguous), B[k][n] = x[n][k] read along k (PlainOperand,
 // k fastest); the K split and the output layout are those of FwdProblem.
-template <int BM_, bool VECA>
+template <int BM_, bool VECA, bool EPI = false>
 struct FcProblem {
     static constexpr int BM = BM_, BN = 128, BK = 16;
     using AL = typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type;
@@ -840,6 +867,7 @@ struct FcProblem {
     float *y, *part;
     int M, N, K, kchunk, splits;
     size_t xbytes;
+    Epi e;
     __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
     {
         kb = z * kchunk;
@@ -853,7 +881,7 @@ struct FcProblem {
         if (splits > 1)
             part[((size_t)z * M + m) * N + n] = v;
         else
-            y[(size_t)n * M + m] = v;
+            y[(size_t)n * M + m] = EPI ? e.apply(v, m) : v;
     }
 };
 
@@ -1209,10 +1237,13 @@ static bool fits_int(const ach_conv_desc *d)
     return in <= lim && out <= lim && (double)g.F * g.C * g.KS * g.KS <= lim;
 }
 
-// y[b][m][p] = sum_z part[z][m][b*OHW+p], z ascending (fixed order).
+// y[b][m][p] = sum_z part[z][m][b*OHW+p], z ascending (fixed order), then
+// the epilogue.
+template <bool EPI>
 __global__ void __launch_bounds__(256) k_splitk_to_nchw(const float *__restrict__ part,
                                                         float *__restrict__ y, int M, int N,
-                                                        FastDiv dohw, FastDiv dM, int splits)
+                                                        FastDiv dohw, FastDiv dM, int splits,
+                                                        Epi e)
 {
     // M*N < 2^29 (operands below 2 GiB): 32-bit indices, magic-number division
     const int mn = M * N, ohw = (int)dohw.d;
@@ -1222,7 +1253,7 @@ __global__ void __launch_bounds__(256) k_splitk_to_nchw(const float *__restrict_
         const int n = b * ohw + p;
         float s = 0.f;
         for (int z = 0; z < splits; ++z) s += part[((size_t)z * M + m) * N + n];
-        y[i] = s;
+        y[i] = EPI ? e.apply(s, m) : s;
     }
 }
 
@@ -1281,79 +1312,108 @@ static size_t fwd_part_bytes(const ConvGeom &g)
     return (size_t)pl.splits * g.F * g.B * g.OH * g.OW * sizeof(float);
 }
 
-template <int BM>
+// EPI: the bias / activation epilogue in the GEMM (used without a K split
+// and for tiles of at most 128 rows only)
+template <int BM, bool EPI>
 static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const float *w,
-                  float *y, float *part, hipStream_t st)
+                  float *y, float *part, const Epi &e, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
     if (g.KS == 3 && (M & 3) == 0 && (g.C & 1) == 0) {
-        FwdProblem<BM, BIm2col3F, true> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        FwdProblem<BM, BIm2col3F, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        p.e = e;
         return launch_gemm(p, M, N, pl.splits, st);
     }
     if (g.KS == 3 && (M & 3) == 0) {
-        FwdProblem<BM, BIm2col3, true> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        FwdProblem<BM, BIm2col3, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        p.e = e;
         return launch_gemm(p, M, N, pl.splits, st);
     }
     if (g.KS == 3) {
-        FwdProblem<BM, BIm2col3> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        FwdProblem<BM, BIm2col3, false, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        p.e = e;
         return launch_gemm(p, M, N, pl.splits, st);
     }
     if constexpr (BM <= 128) {
         if (fc_geom(g)) {
             const size_t xb = (size_t)N * K * sizeof(float);
             if ((M & 3) == 0) {
-                FcProblem<BM, true> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
+                FcProblem<BM, true, EPI> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
+                p.e = e;
                 return launch_gemm(p, M, N, pl.splits, st);
             }
-            FcProblem<BM, false> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
+            FcProblem<BM, false, EPI> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
+            p.e = e;
             return launch_gemm(p, M, N, pl.splits, st);
         }
     }
     if (g.KS == 1) {
-        FwdProblem<BM, BIm2colAny<1>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        FwdProblem<BM, BIm2colAny<1>, false, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk,
+                                                     pl.splits};
+        p.e = e;
         return launch_gemm(p, M, N, pl.splits, st);
     }
     if constexpr (BM <= 128) {
         if (fwd_padded_taps(g)) {
-            FwdProblem<BM, BIm2colK<5>, true> p{x, w, y, part, g, M, N,
-                                                g.C * BIm2colK<5>::BK, pl.kchunk, pl.splits};
+            FwdProblem<BM, BIm2colK<5>, true, EPI> p{x, w, y, part, g, M, N,
+                                                     g.C * BIm2colK<5>::BK, pl.kchunk,
+                                                     pl.splits};
+            p.e = e;
             return launch_gemm(p, M, N, pl.splits, st);
         }
     }
-    FwdProblem<BM, BIm2colAny<0>> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+    FwdProblem<BM, BIm2colAny<0>, false, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+    p.e = e;
     return launch_gemm(p, M, N, pl.splits, st);
 }
 
 // 96-row tiles (one wave column of three 32-row MFMA tiles) for the
 // padded-tap 5x5 path only: the other loaders assume BM | 256 or BM % 64 == 0
-template <int BM>
+template <int BM, bool EPI>
 static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, const float *w,
-                         float *y, float *part, hipStream_t st)
+                         float *y, float *part, const Epi &e, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW;
-    FwdProblem<BM, BIm2colK<5>, true> p{x, w, y, part, g, M, N, g.C * BIm2colK<5>::BK,
-                                        pl.kchunk, pl.splits};
+    FwdProblem<BM, BIm2colK<5>, true, EPI> p{x, w, y, part, g, M, N, g.C * BIm2colK<5>::BK,
+                                             pl.kchunk, pl.splits};
+    p.e = e;
     return launch_gemm(p, M, N, pl.splits, st);
 }
 
 // w: k-major filter Wt[K][M]; part: fwd_part_bytes(g) of scratch (or NULL
-// when no split is planned)
+// when no split is planned).  An active epilogue e runs in the GEMM when K
+// is not split (tiles of at most 128 rows; returns ACH_EUNSUPPORTED for a
+// 256-row plan, which the caller handles) or in the split-K reduction.
 static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, float *part,
-                    hipStream_t st)
+                    hipStream_t st, const Epi &e = Epi())
 {
     const FwdPlan pl = fwd_plan(g);
+    const bool gemm_epi = e.active() && pl.splits == 1;
+    if (gemm_epi && pl.bm == 256) return ACH_EUNSUPPORTED;
     int rc;
-    if (pl.bm == 32) rc = fwd_bm<32>(g, pl, x, w, y, part, st);
-    else if (pl.bm == 96) rc = fwd_bm_padded<96>(g, pl, x, w, y, part, st);
-    else if (pl.bm == 64) rc = fwd_bm<64>(g, pl, x, w, y, part, st);
-    else if (pl.bm == 256) rc = fwd_bm<256>(g, pl, x, w, y, part, st);
-    else rc = fwd_bm<128>(g, pl, x, w, y, part, st);
+    if (gemm_epi) {
+        if (pl.bm == 32) rc = fwd_bm<32, true>(g, pl, x, w, y, part, e, st);
+        else if (pl.bm == 96) rc = fwd_bm_padded<96, true>(g, pl, x, w, y, part, e, st);
+        else if (pl.bm == 64) rc = fwd_bm<64, true>(g, pl, x, w, y, part, e, st);
+        else rc = fwd_bm<128, true>(g, pl, x, w, y, part, e, st);
+        return rc;
+    }
+    if (pl.bm == 32) rc = fwd_bm<32, false>(g, pl, x, w, y, part, e, st);
+    else if (pl.bm == 96) rc = fwd_bm_padded<96, false>(g, pl, x, w, y, part, e, st);
+    else if (pl.bm == 64) rc = fwd_bm<64, false>(g, pl, x, w, y, part, e, st);
+    else if (pl.bm == 256) rc = fwd_bm<256, false>(g, pl, x, w, y, part, e, st);
+    else rc = fwd_bm<128, false>(g, pl, x, w, y, part, e, st);
     if (rc || pl.splits == 1) return rc;
     const int M = g.F, N = g.B * g.OH * g.OW;
     const size_t mn = (size_t)M * N;
-    hipLaunchKernelGGL(k_splitk_to_nchw, dim3(grid_for(mn, 256, 1u << 20)), dim3(256), 0, st, part,
-                       y, M, N, make_fastdiv((unsigned)(g.OH * g.OW)), make_fastdiv((unsigned)M),
-                       pl.splits);
+    if (e.active())
+        hipLaunchKernelGGL(k_splitk_to_nchw<true>, dim3(grid_for(mn, 256, 1u << 20)), dim3(256),
+                           0, st, part, y, M, N, make_fastdiv((unsigned)(g.OH * g.OW)),
+                           make_fastdiv((unsigned)M), pl.splits, e);
+    else
+        hipLaunchKernelGGL(k_splitk_to_nchw<false>, dim3(grid_for(mn, 256, 1u << 20)), dim3(256),
+                           0, st, part, y, M, N, make_fastdiv((unsigned)(g.OH * g.OW)),
+                           make_fastdiv((unsigned)M), pl.splits, e);
     return check_launch();
 }
 
@@ -1629,6 +1689,34 @@ int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *w
     const size_t need = fwd_part_bytes(g);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
     return fwd_impl(g, x, wt, y, (float *)ws, as_stream(stream));
+}
+
+int ach_conv_fwd_bias_act_prepared(const ach_conv_desc *d, const float *x, const float *wt,
+                                   const float *bias, int activation, float *y, void *ws,
+                                   size_t ws_bytes, ach_stream_t stream)
+{
+    if (!conv_ok(d) || !x || !wt || !y) return ACH_EINVAL;
+    if (activation != ACH_LOGISTIC && activation != ACH_RELU && activation != ACH_LINEAR &&
+        activation != ACH_LEAKY)
+        return ACH_EUNSUPPORTED;
+    if (!fits_int(d)) return ACH_EUNSUPPORTED;
+    const ConvGeom g = geom(d);
+    const size_t need = fwd_part_bytes(g);
+    if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
+    Epi e;
+    e.bias = bias;
+    e.slope = activation == ACH_LEAKY ? 0.1 : (activation == ACH_RELU ? 0.0 : 1.0);
+    hipStream_t st = as_stream(stream);
+    int rc = fwd_impl(g, x, wt, y, (float *)ws, st, e);
+    bool act_pass = activation == ACH_LOGISTIC;  // after the bias epilogue
+    if (rc == ACH_EUNSUPPORTED) {
+        // 256-row tiles without a K split: the plain GEMM, then the passes
+        rc = fwd_impl(g, x, wt, y, (float *)ws, st);
+        if (!rc && bias) rc = ach_add_bias(y, bias, g.B, g.F, g.OH * g.OW, stream);
+        act_pass = activation != ACH_LINEAR;
+    }
+    if (rc || !act_pass) return rc;
+    return ach_activate(y, (size_t)g.B * g.F * g.OH * g.OW, activation, stream);
 }
 
 int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const float *w,

@@ -188,6 +188,11 @@ static int conv_forward(an_network *net, an_layer *l, an_state st)
             AN_CHECK(ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s));
         return ACH_OK;
     }
+    /* conv + addBias + activate in one pass (the GEMM epilogue) */
+    if (fusable(l->activation) || l->activation == ACH_LOGISTIC)
+        return ach_conv_fwd_bias_act_prepared(&d, st.input, l->weights_kmajor, l->biases,
+                                              l->activation, l->output, st.workspace,
+                                              st.workspace_bytes, s);
     AN_CHECK(ach_conv_fwd_prepared(&d, st.input, l->weights_kmajor, l->output, st.workspace,
                                    st.workspace_bytes, s));
     AN_CHECK(ach_add_bias(l->output, l->biases, l->batch, l->n, spatial, s));

@@ -130,6 +130,19 @@ int ach_conv_prepare_filters(int njobs, const ach_filter_job *jobs, ach_stream_t
  * bytes suffice (the _prepared calls use only the split-K part of it)      */
 int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *wt, float *y,
                           void *ws, size_t ws_bytes, ach_stream_t stream);
+/* The forward of a convolutional layer without batch-norm in one pass:
+ * y = act(conv(x) + bias), the output-side steps of ConvolutionalLayer.
+ * forward (ConvolutionalLayer.c:684-716, then IOData.addBias IOData.c:43-55
+ * and activate IOData.c:60-72) applied to each sum in the GEMM epilogue
+ * (or the split-K reduction) with the same fp32 arithmetic: the results
+ * are those of ach_conv_fwd_prepared + ach_add_bias + ach_activate, bit for
+ * bit.  bias may be NULL (no bias); activation is ACH_LOGISTIC, ACH_RELU,
+ * ACH_LINEAR or ACH_LEAKY (else ACH_EUNSUPPORTED); the logistic activation
+ * (a double exp per element) and, for 256-row tiles without a K split,
+ * bias and activation run as separate passes inside the call.             */
+int ach_conv_fwd_bias_act_prepared(const ach_conv_desc *d, const float *x, const float *wt,
+                                   const float *bias, int activation, float *y, void *ws,
+                                   size_t ws_bytes, ach_stream_t stream);
 /* stride-1 only (ACH_EUNSUPPORTED otherwise); w is read for 1x1 filters,
  * wft otherwise                                                             */
 int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const float *w,

@@ -448,6 +448,47 @@ def test_bias_ops(gpu, oracle, B, n, sp):
 
 
 @pytest.mark.parametrize("shape", [
+    (2, 128, 16, 16, 256, 3, 1, 1),   # 256-row tiles, split K (reduction epilogue)
+    (2, 128, 32, 32, 128, 3, 1, 1),   # no split (GEMM epilogue)
+    (3, 5, 9, 7, 10, 3, 1, 1),        # scalar loaders, ragged tiles
+    (2, 96, 9, 9, 80, 5, 1, 2),       # padded-tap 5x5, 96-row tiles
+    (2, 16, 13, 13, 24, 5, 1, 2),
+    (2, 3, 35, 35, 8, 11, 4, 0),      # generic loader, stride 4
+    (2, 512, 8, 8, 10, 1, 1, 0),      # 1x1
+    (8, 64, 1, 1, 48, 1, 1, 0),       # fully connected GEMM
+    (4, 300, 1, 1, 64, 1, 1, 0),      # fully connected, split K
+], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("act", [aetcnn.LEAKY, aetcnn.RELU, aetcnn.LINEAR, aetcnn.LOGISTIC])
+def test_conv_fwd_bias_act_fused(gpu, shape, act):
+    """ach_conv_fwd_bias_act_prepared equals ach_conv_fwd_prepared +
+    ach_add_bias + ach_activate bit for bit (with and without a bias)."""
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, dy = _conv_inputs(shape, 11)
+    rng = np.random.default_rng(12)
+    bias = rng.standard_normal(F).astype(np.float32)
+    d = conv_desc(*shape)
+    ws = gpu.ach_conv_fwd_workspace(C.byref(d))
+    dws = dev(np.zeros(ws // 4 + 64, np.float32))
+    dx_, dw_, db = dev(x), dev(w), dev(bias)
+    wt = dev(np.zeros(w.size, np.float32))
+    job = aetcnn.FilterJob(d, dw_.ptr, wt.ptr, None)
+    check(gpu.ach_conv_prepare_filters(1, C.byref(job), None))
+    oh, ow = gpu.ach_conv_out_h(C.byref(d)), gpu.ach_conv_out_w(C.byref(d))
+    for bptr in (db.ptr, None):
+        y0, y1 = D(dy.shape), D(dy.shape)
+        check(gpu.ach_conv_fwd_prepared(C.byref(d), dx_.ptr, wt.ptr, y0.ptr, dws.ptr, ws, None))
+        if bptr is not None:
+            check(gpu.ach_add_bias(y0.ptr, bptr, B, F, oh * ow, None))
+        check(gpu.ach_activate(y0.ptr, int(np.prod(dy.shape)), act, None))
+        check(gpu.ach_conv_fwd_bias_act_prepared(C.byref(d), dx_.ptr, wt.ptr, bptr, act, y1.ptr,
+                                                 dws.ptr, ws, None))
+        a, b = y0.numpy(), y1.numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (shape, act, bptr is None)
+    assert gpu.ach_conv_fwd_bias_act_prepared(C.byref(d), dx_.ptr, wt.ptr, db.ptr, 2, y1.ptr,
+                                              dws.ptr, ws, None) == aetcnn.ACH_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("shape", [
     (2, 128, 16, 16, 256, 3, 1, 1),   # 3x3, 256-row tiles, split K
     (3, 5, 9, 7, 10, 3, 1, 1),
     (2, 16, 13, 13, 24, 5, 1, 2),     # generic kernel size
