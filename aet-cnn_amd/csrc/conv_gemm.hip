@@ -171,6 +171,61 @@ struct AWeightsT4 {
     }
 };
 
+// A = a filter in its own layout W[M][K] (k contiguous: the fully
+// connected layers, whose k-major copy would cost a pass over the largest
+// weights every step).  Thread -> float4 f = tid + 256*i of the BM x BK tile
+// (row m0 + f / (BK/4), k 4*(f % (BK/4)) .. +3): one dwordx4 load when K % 4
+// == 0 (16-byte aligned rows), four dword loads otherwise; the four values
+// go to four LDS rows of the k-major stage.
+template <int BM, int BK>
+struct AWeightsN {
+    static constexpr int K4 = BK / 4;                      // float4 per tile row
+    static constexpr int NV = (BM * K4 + GNT - 1) / GNT;   // float4 per thread
+    static constexpr int RA = 4 * NV, PAD = LDP;
+    static_assert(BK % 4 == 0, "k-tile of whole float4");
+    __amdgpu_buffer_rsrc_t rs;
+    int M, K, m0;
+    bool v4;
+    __device__ __forceinline__ void init(const float *w, int M_, int K_, int m0_, int)
+    {
+        M = M_;
+        K = K_;
+        m0 = m0_;
+        v4 = (K_ & 3) == 0;
+        rs = make_rsrc(w, (unsigned)((size_t)M_ * K_ * 4));
+    }
+    __device__ __forceinline__ void load(int k0, int ke, float *ra) const
+    {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + GNT * i;
+            const int m = m0 + f / K4, k = k0 + 4 * (f % K4);
+            const bool ok = f < BM * K4 && m < M;
+            if (v4) {
+                const float4 v = bload4(rs, boff(ok && k < ke, m * K + k));
+                ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    ra[4 * i + j] = bload(rs, boff(ok && k + j < ke, m * K + k + j));
+            }
+        }
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
+    {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = threadIdx.x + GNT * i;
+            if (f < BM * K4) {
+                const int mc = f / K4, kc = 4 * (f % K4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) S[kc + j][mc] = ra[4 * i + j];
+            }
+        }
+    }
+};
+
 // AWeightsT4 for problems whose every k-tile is full (K a multiple of BK):
 // the per-thread byte offsets of the NV float4 (or the out-of-range offset
 // for columns past M and rows past BK) are loop-invariant, and a k-tile only
@@ -858,10 +913,13 @@ struct GemmProblem {
 // Forward / input gradient: M = F, N = B, K = C; A = the k-major filter
 // Wt[K][M] (m contiguous), B[k][n] = x[n][k] read along k (PlainOperand,
 // k fastest); the K split and the output layout are those of FwdProblem.
-template <int BM_, bool VECA, bool EPI = false>
+template <int BM_, bool VECA, bool EPI = false, bool NAT = false>
 struct FcProblem {
     static constexpr int BM = BM_, BN = 128, BK = 16;
-    using AL = typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type;
+    // NAT: w is the filter itself, W[M][K]; else its k-major copy Wt[K][M]
+    using AL = typename std::conditional<
+        NAT, AWeightsN<BM, BK>,
+        typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type>::type;
     using BLd = PlainOperand<false, 128>;
     const float *x, *w;
     float *y, *part;
@@ -1337,7 +1395,7 @@ static size_t fwd_part_bytes(const ConvGeom &g)
 // and for tiles of at most 128 rows only)
 template <int BM, bool EPI>
 static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const float *w,
-                  float *y, float *part, const Epi &e, hipStream_t st)
+                  float *y, float *part, const Epi &e, bool w_nat, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
     if (g.KS == 3 && (M & 3) == 0 && (g.C & 1) == 0) {
@@ -1358,6 +1416,12 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     if constexpr (BM <= 128) {
         if (fc_geom(g)) {
             const size_t xb = (size_t)N * K * sizeof(float);
+            if (w_nat) {
+                FcProblem<BM, false, EPI, true> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits,
+                                                  xb};
+                p.e = e;
+                return launch_gemm(p, M, N, pl.splits, st);
+            }
             if ((M & 3) == 0) {
                 FcProblem<BM, true, EPI> p{x, w, y, part, M, N, K, pl.kchunk, pl.splits, xb};
                 p.e = e;
@@ -1405,25 +1469,26 @@ static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, c
 // when no split is planned).  An active epilogue e runs in the GEMM when K
 // is not split (tiles of at most 128 rows; returns ACH_EUNSUPPORTED for a
 // 256-row plan, which the caller handles) or in the split-K reduction.
+// w_nat: a fully connected geometry's w is the filter itself (W[F][K]).
 static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, float *part,
-                    hipStream_t st, const Epi &e = Epi())
+                    hipStream_t st, const Epi &e = Epi(), bool w_nat = false)
 {
     const FwdPlan pl = fwd_plan(g);
     const bool gemm_epi = e.active() && pl.splits == 1;
     if (gemm_epi && pl.bm == 256) return ACH_EUNSUPPORTED;
     int rc;
     if (gemm_epi) {
-        if (pl.bm == 32) rc = fwd_bm<32, true>(g, pl, x, w, y, part, e, st);
+        if (pl.bm == 32) rc = fwd_bm<32, true>(g, pl, x, w, y, part, e, w_nat, st);
         else if (pl.bm == 96) rc = fwd_bm_padded<96, true>(g, pl, x, w, y, part, e, st);
-        else if (pl.bm == 64) rc = fwd_bm<64, true>(g, pl, x, w, y, part, e, st);
-        else rc = fwd_bm<128, true>(g, pl, x, w, y, part, e, st);
+        else if (pl.bm == 64) rc = fwd_bm<64, true>(g, pl, x, w, y, part, e, w_nat, st);
+        else rc = fwd_bm<128, true>(g, pl, x, w, y, part, e, w_nat, st);
         return rc;
     }
-    if (pl.bm == 32) rc = fwd_bm<32, false>(g, pl, x, w, y, part, e, st);
+    if (pl.bm == 32) rc = fwd_bm<32, false>(g, pl, x, w, y, part, e, w_nat, st);
     else if (pl.bm == 96) rc = fwd_bm_padded<96, false>(g, pl, x, w, y, part, e, st);
-    else if (pl.bm == 64) rc = fwd_bm<64, false>(g, pl, x, w, y, part, e, st);
-    else if (pl.bm == 256) rc = fwd_bm<256, false>(g, pl, x, w, y, part, e, st);
-    else rc = fwd_bm<128, false>(g, pl, x, w, y, part, e, st);
+    else if (pl.bm == 64) rc = fwd_bm<64, false>(g, pl, x, w, y, part, e, w_nat, st);
+    else if (pl.bm == 256) rc = fwd_bm<256, false>(g, pl, x, w, y, part, e, w_nat, st);
+    else rc = fwd_bm<128, false>(g, pl, x, w, y, part, e, w_nat, st);
     if (rc || pl.splits == 1) return rc;
     const int M = g.F, N = g.B * g.OH * g.OW;
     const size_t mn = (size_t)M * N;
@@ -1608,6 +1673,8 @@ int ach_conv_fwd(const ach_conv_desc *d, const float *x, const float *w, float *
     const int M = g.F, K = g.C * g.KS * g.KS;
     float *wt = (float *)ws;
     float *part = (float *)((char *)ws + align256((size_t)M * K * sizeof(float)));
+    // a fully connected geometry reads the filter in its own layout
+    if (fc_geom(g)) return fwd_impl(g, x, w, y, part, st, Epi(), true);
     hipLaunchKernelGGL(k_weights_kmajor, dim3((K + 31) / 32, (M + 31) / 32), dim3(256), 0, st, w,
                        wt, M, K);
     int rc = check_launch();
@@ -1695,7 +1762,8 @@ int ach_conv_prepare_filters(int njobs, const ach_filter_job *jobs, ach_stream_t
             J.C = g.C;
             J.KK = g.KS * g.KS;
             const int K = J.C * J.KK;
-            J.tiles_t = ((K + 31) / 32) * ((J.M + 31) / 32);
+            // fully connected geometry: the forward reads W itself, no copy
+            J.tiles_t = fc_geom(g) ? 0 : ((K + 31) / 32) * ((J.M + 31) / 32);
             J.tiles_f = 0;
             if (q.wft && dgrad_flips(g))
                 J.tiles_f = (int)(((long long)J.M * J.C + 255) / 256);
@@ -1718,7 +1786,12 @@ int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *w
     const ConvGeom g = geom(d);
     const size_t need = fwd_part_bytes(g);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
-    return fwd_impl(g, x, wt, y, (float *)ws, as_stream(stream));
+    return fwd_impl(g, x, wt, y, (float *)ws, as_stream(stream), Epi(), fc_geom(g));
+}
+
+int ach_conv_is_fully_connected(const ach_conv_desc *d)
+{
+    return conv_ok(d) && fc_geom(geom(d)) ? 1 : 0;
 }
 
 int ach_conv_fwd_bias_act_prepared(const ach_conv_desc *d, const float *x, const float *wt,
@@ -1737,11 +1810,11 @@ int ach_conv_fwd_bias_act_prepared(const ach_conv_desc *d, const float *x, const
     e.bias = bias;
     e.slope = activation == ACH_LEAKY ? 0.1 : (activation == ACH_RELU ? 0.0 : 1.0);
     hipStream_t st = as_stream(stream);
-    int rc = fwd_impl(g, x, wt, y, (float *)ws, st, e);
+    int rc = fwd_impl(g, x, wt, y, (float *)ws, st, e, fc_geom(g));
     bool act_pass = activation == ACH_LOGISTIC;  // after the bias epilogue
     if (rc == ACH_EUNSUPPORTED) {
         // 256-row tiles without a K split: the plain GEMM, then the passes
-        rc = fwd_impl(g, x, wt, y, (float *)ws, st);
+        rc = fwd_impl(g, x, wt, y, (float *)ws, st, Epi(), fc_geom(g));
         if (!rc && bias) rc = ach_add_bias(y, bias, g.B, g.F, g.OH * g.OW, stream);
         act_pass = activation != ACH_LINEAR;
     }

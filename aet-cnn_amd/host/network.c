@@ -729,7 +729,9 @@ int an_finalize(an_network *net)
         if (l->type != AN_CONVOLUTIONAL) continue;
         l->weights = net->wflat + ow;
         l->weight_updates = net->vflat + ow;
-        l->weights_kmajor = net->wtflat + ow;
+        /* fully connected geometry: the forward GEMM reads W itself */
+        const ach_conv_desc dl = conv_desc(l);
+        l->weights_kmajor = ach_conv_is_fully_connected(&dl) ? l->weights : net->wtflat + ow;
         l->weights_flipped = net->wftflat + ow;
         ow += (size_t)((l->nweights + 63) & ~63);
         l->biases = net->bflat + ob;

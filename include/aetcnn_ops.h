@@ -118,6 +118,10 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
  * ach_conv_prepare_filters launch per step) calls the _prepared variants.
  * wft may be NULL when not needed: stride > 1, or a 1x1 filter (including a
  * kernel covering the whole unpadded input), whose flipped copy is W itself.
+ * A fully connected geometry (ach_conv_is_fully_connected: a kernel covering
+ * the whole unpadded input, or a 1x1 filter on a 1x1 input) needs no copy at
+ * all: ach_conv_prepare_filters leaves its wt untouched and the _prepared
+ * forward reads its wt argument as the filter itself, so pass w there.
  * No counterpart in the reference, which has no such layouts.              */
 typedef struct {
     ach_conv_desc desc;
@@ -126,6 +130,8 @@ typedef struct {
     float *wft;       /* n*c*size*size floats or NULL */
 } ach_filter_job;
 int ach_conv_prepare_filters(int njobs, const ach_filter_job *jobs, ach_stream_t stream);
+/* 1 for a fully connected geometry (see above), else 0                    */
+int ach_conv_is_fully_connected(const ach_conv_desc *d);
 /* workspace: ach_conv_fwd_workspace(d) / ach_conv_bwd_data_workspace(d)
  * bytes suffice (the _prepared calls use only the split-K part of it)      */
 int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *wt, float *y,

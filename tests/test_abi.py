@@ -59,6 +59,13 @@ def test_conv_shape_and_workspace_queries():
     assert ops.ach_conv_bwd_filter_workspace(C.byref(big)) > 0
     assert ops.ach_maxpool_out(32, 2, 2, 1) == 16  # darknet default padding = size-1
     assert ops.ach_maxpool_out(55, 3, 2, 0) == 27
+    # fully connected geometry: a kernel covering the unpadded input, or 1x1 on 1x1
+    fc = lambda *a: ops.ach_conv_is_fully_connected(C.byref(aetcnn.ConvDesc(*a)))
+    assert fc(128, 256, 6, 6, 4096, 6, 1, 0) == 1
+    assert fc(128, 4096, 1, 1, 4096, 1, 1, 0) == 1
+    assert fc(128, 256, 6, 6, 4096, 6, 1, 1) == 0   # padded
+    assert fc(128, 512, 8, 8, 10, 1, 1, 0) == 0     # 1x1 on an 8x8 plane
+    assert fc(128, 256, 7, 6, 4096, 6, 1, 0) == 0   # kernel covers 6 of 7 rows
 
 
 def test_dropout_generator_matches_oracle(oracle):

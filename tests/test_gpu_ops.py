@@ -473,6 +473,8 @@ def test_conv_fwd_bias_act_fused(gpu, shape, act):
     wt = dev(np.zeros(w.size, np.float32))
     job = aetcnn.FilterJob(d, dw_.ptr, wt.ptr, None)
     check(gpu.ach_conv_prepare_filters(1, C.byref(job), None))
+    if gpu.ach_conv_is_fully_connected(C.byref(d)):
+        wt = dw_  # the forward reads W itself
     oh, ow = gpu.ach_conv_out_h(C.byref(d)), gpu.ach_conv_out_w(C.byref(d))
     for bptr in (db.ptr, None):
         y0, y1 = D(dy.shape), D(dy.shape)
@@ -507,9 +509,13 @@ def test_conv_prepared_filters(gpu, shape):
     wt, wft = dev(np.zeros(w.size, np.float32)), dev(np.full(w.size, np.nan, np.float32))
     job = aetcnn.FilterJob(d, dw_.ptr, wt.ptr, wft.ptr)
     check(gpu.ach_conv_prepare_filters(1, C.byref(job), None))
+    fc = gpu.ach_conv_is_fully_connected(C.byref(d))
+    if fc:  # no k-major copy: the forward reads W itself
+        assert not wt.numpy().any()
     y0, y1 = D(dy.shape), D(dy.shape)
     check(gpu.ach_conv_fwd(C.byref(d), dx_.ptr, dw_.ptr, y0.ptr, dws.ptr, ws, None))
-    check(gpu.ach_conv_fwd_prepared(C.byref(d), dx_.ptr, wt.ptr, y1.ptr, dws.ptr, ws, None))
+    check(gpu.ach_conv_fwd_prepared(C.byref(d), dx_.ptr, dw_.ptr if fc else wt.ptr, y1.ptr,
+                                    dws.ptr, ws, None))
     assert np.array_equal(y0.numpy(), y1.numpy())
     g0, g1 = D(x.shape), D(x.shape)
     check(gpu.ach_conv_bwd_data(C.byref(d), ddy.ptr, dw_.ptr, g0.ptr, dws.ptr, ws, None))
