@@ -369,6 +369,66 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
     din[p] = v;
 }
 
+// The same gather for output planes that fit in LDS: one workgroup per
+// (image, channel) plane first stages the plane's argmax indices and output
+// gradients in LDS (each read from HBM once, coalesced), then every input
+// pixel of the plane takes its candidates from LDS in ascending output
+// order -- the sums of k_maxpool_bwd, bit for bit, without its eight
+// dependent global loads per pixel (which stall when the kernel shares the
+// CUs with a GEMM).  Dynamic LDS: 8 bytes per output position.
+constexpr int POOL_PLANE_MAX = 4096;  // output positions of a plane staged in LDS
+template <int SIZE, int STRIDE>
+__global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restrict__ dout,
+                                                           const int32_t *__restrict__ idx,
+                                                           FastDiv dW, int H, int size_,
+                                                           int stride_, int pad, int OH, int OW,
+                                                           float *din, int accumulate)
+{
+    extern __shared__ int32_t pool_lds[];
+    const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
+    const int ohw = OH * OW, W = (int)dW.d, hw = H * W;
+    int32_t *six = pool_lds;
+    float *sg = reinterpret_cast<float *>(pool_lds + ohw);
+    const int bc = blockIdx.x;
+    const size_t obase = (size_t)bc * ohw;
+    for (int q = threadIdx.x; q < ohw; q += blockDim.x) {
+        six[q] = idx[obase + q];
+        sg[q] = dout[obase + q];
+    }
+    __syncthreads();
+    const int off = -pad / 2;
+    const int pbase = bc * hw;  // < 2^31: the caller's pool_ok
+    for (int r = threadIdx.x; r < hw; r += blockDim.x) {
+        const int h = fdiv(r, dW), w = r - h * W;
+        const int p = pbase + r;
+        const int i0 = max(floor_div(h - off - size, stride) + 1, 0);
+        const int i1 = min(floor_div(h - off, stride), OH - 1);
+        const int j0 = max(floor_div(w - off - size, stride) + 1, 0);
+        const int j1 = min(floor_div(w - off, stride), OW - 1);
+        float v = accumulate ? din[p] : 0.f;
+        if constexpr (SIZE > 0 && STRIDE > 0) {
+            constexpr int NC = (SIZE + STRIDE - 1) / STRIDE;
+#pragma unroll
+            for (int a = 0; a < NC; ++a)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const int i = i0 + a, j = j0 + c;
+                    if (i <= i1 && j <= j1) {
+                        const int o = i * OW + j;
+                        if (six[o] == p) v += sg[o];
+                    }
+                }
+        } else {
+            for (int i = i0; i <= i1; ++i)
+                for (int j = j0; j <= j1; ++j) {
+                    const int o = i * OW + j;
+                    if (six[o] == p) v += sg[o];
+                }
+        }
+        din[p] = v;
+    }
+}
+
 // Backward of k_maxpool2_fwd: every input pixel lies in exactly one window.
 __device__ __forceinline__ float pick(float v, int p, int ix, float d)
 {
@@ -849,6 +909,20 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
     const int total = batch * c * h * w;  // < 2^31: pool_ok
     const dim3 grid((total + 255) / 256);
     const FastDiv dH = make_fastdiv((unsigned)h), dW = make_fastdiv((unsigned)w);
+    if (OH * OW <= POOL_PLANE_MAX) {  // one workgroup per plane, outputs staged in LDS
+        const dim3 pg((unsigned)(batch * c));
+        const size_t lds = (size_t)OH * OW * 8;
+        if (size == 3 && stride == 2)
+            hipLaunchKernelGGL((k_maxpool_bwd_plane<3, 2>), pg, dim3(256), lds, as_stream(s), dout,
+                               idx, dW, h, size, stride, pad, OH, OW, din, acc);
+        else if (size == 2 && stride == 2)
+            hipLaunchKernelGGL((k_maxpool_bwd_plane<2, 2>), pg, dim3(256), lds, as_stream(s), dout,
+                               idx, dW, h, size, stride, pad, OH, OW, din, acc);
+        else
+            hipLaunchKernelGGL((k_maxpool_bwd_plane<0, 0>), pg, dim3(256), lds, as_stream(s), dout,
+                               idx, dW, h, size, stride, pad, OH, OW, din, acc);
+        return check_launch();
+    }
     if (size == 3 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<3, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
                            total, dH, dW, size, stride, pad, OH, OW, din, acc);

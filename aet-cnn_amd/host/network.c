@@ -218,15 +218,26 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
     } else {
         AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));
     }
-    /* dbias and dW on the weight-gradient stream once delta is final; the
-     * input gradient continues on the main stream */
-    AN_CHECK(ach_event_record(net->ev_ready[l->index], s));
-    AN_CHECK(ach_stream_wait_event(net->wstream, net->ev_ready[l->index]));
+    /* dbias and dW on the weight-gradient stream once delta is final, while
+     * the input gradient continues on the main stream.  A layer without an
+     * input gradient (the first) computes them on the main stream, which has
+     * nothing else left to do, so they overlap the weight gradients still
+     * queued on the other stream instead of waiting behind them.          */
+    ach_stream_t gs = s;
+    float *gws = st.workspace;
+    size_t gws_bytes = st.workspace_bytes;
+    if (st.delta) {
+        AN_CHECK(ach_event_record(net->ev_ready[l->index], s));
+        AN_CHECK(ach_stream_wait_event(net->wstream, net->ev_ready[l->index]));
+        gs = net->wstream;
+        gws = net->wgrad_ws;
+        gws_bytes = net->wgrad_ws_bytes;
+    }
     if (!l->batch_normalize)
-        AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial,
-                               net->wgrad_ws, net->wgrad_ws_bytes, net->wstream));
-    AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, net->wgrad_ws,
-                                 net->wgrad_ws_bytes, net->wstream));
+        AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial, gws,
+                               gws_bytes, gs));
+    AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, gws, gws_bytes,
+                                 gs));
     if (st.delta)
         AN_CHECK(l->stride == 1
                      ? ach_conv_bwd_data_prepared(&d, l->delta, l->weights, l->weights_flipped,

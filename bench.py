@@ -228,7 +228,7 @@ def roofline_phase(aetcnn, batch, reps):
     for a in (x, w, y, ws):
         a.free()
     ops.ach_stream_destroy(stream)
-    return dict(kernel="k_mfma_gemm<FwdProblem<256, BIm2col3F, true>> (conv fwd / dgrad implicit GEMM)",
+    return dict(kernel="k_mfma_gemm<FwdProblem<256, BIm2col3F, true, false>> (conv fwd / dgrad implicit GEMM)",
                 shape=f"{ci}->{co}@{hw}x{hw} k{k} b{batch}", flop=flop, ms=ms, reps=reps)
 
 

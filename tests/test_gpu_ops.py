@@ -330,6 +330,8 @@ def test_activation_bit_exact(gpu, oracle, act):
     (2, 3, 16, 16, 2, 2, 0),
     (2, 3, 8, 12, 2, 2, 1),       # 2x2/2 fast path, non-square
     (1, 2, 6, 6, 2, 2, 1),        # W % 4 != 0: generic kernel
+    (1, 2, 140, 140, 3, 2, 0),    # output plane above the LDS-staged limit
+    (2, 3, 150, 40, 2, 1, 1),     # generic window, plane above the limit
 ])
 def test_maxpool_bit_exact(gpu, oracle, B, Cc, H, W, size, stride, pad):
     rng = np.random.default_rng(H * W + size)
