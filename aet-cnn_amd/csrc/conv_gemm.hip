@@ -1363,6 +1363,8 @@ static FwdPlan fwd_plan(const ConvGeom &g)
         pl.bk = BIm2colK<5>::BK;
         K = g.C * pl.bk;
         if (M > 64 && M <= 96) pl.bm = 96;  // three 32-row MFMA tiles per wave
+    } else if (M > 64 && M <= 96 && (M & 3) == 0 && g.KS != 3 && g.KS != 1) {
+        pl.bm = 96;  // generic loader, 65-96 filters (AlexNet conv1: 96 of 128 rows)
     }
     const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + 127) / 128);
     const int ktiles = (K + pl.bk - 1) / pl.bk;
@@ -1452,13 +1454,21 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     return launch_gemm(p, M, N, pl.splits, st);
 }
 
-// 96-row tiles (one wave column of three 32-row MFMA tiles) for the
-// padded-tap 5x5 path only: the other loaders assume BM | 256 or BM % 64 == 0
+// 96-row tiles (one wave column of three 32-row MFMA tiles) for 65-96
+// filters with float4 k-major weights: the padded-tap 5x5 path and the
+// generic im2col loader (AlexNet's 11x11 first layer); the other loaders
+// assume BM | 256 or BM % 64 == 0
 template <int BM, bool EPI>
 static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, const float *w,
                          float *y, float *part, const Epi &e, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW;
+    if (!fwd_padded_taps(g)) {
+        FwdProblem<BM, BIm2colAny<0>, true, EPI> p{x, w, y, part, g, M, N, g.C * g.KS * g.KS,
+                                                   pl.kchunk, pl.splits};
+        p.e = e;
+        return launch_gemm(p, M, N, pl.splits, st);
+    }
     FwdProblem<BM, BIm2colK<5>, true, EPI> p{x, w, y, part, g, M, N, g.C * BIm2colK<5>::BK,
                                              pl.kchunk, pl.splits};
     p.e = e;

@@ -101,6 +101,9 @@ CONV_SHAPES = [
     (4, 6, 8, 8, 12, 5, 1, 2),     # 5x5
     (2, 96, 9, 9, 80, 5, 1, 2),    # 5x5 with 80 / 96 filters: 96-row tiles
     (6, 24, 4, 4, 20, 1, 1, 0),    # 1x1 on a 16-position plane
+    # 96-row tiles with the generic loader (65-96 filters / input channels):
+    (2, 3, 35, 35, 96, 11, 4, 0),  # AlexNet conv1 shape class
+    (2, 80, 9, 9, 72, 7, 1, 3),    # 7x7: forward M=72, input gradient M=80
     (8, 16, 5, 5, 24, 3, 1, 1),    # 25 positions: the (image, position) order
     # fully connected layers (1x1 of a 1x1 input, after flattening):
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
@@ -456,6 +459,7 @@ def test_bias_ops(gpu, oracle, B, n, sp):
     (2, 96, 9, 9, 80, 5, 1, 2),       # padded-tap 5x5, 96-row tiles
     (2, 16, 13, 13, 24, 5, 1, 2),
     (2, 3, 35, 35, 8, 11, 4, 0),      # generic loader, stride 4
+    (2, 3, 35, 35, 96, 11, 4, 0),     # generic loader, 96-row tiles
     (2, 512, 8, 8, 10, 1, 1, 0),      # 1x1
     (8, 64, 1, 1, 48, 1, 1, 0),       # fully connected GEMM
     (4, 300, 1, 1, 64, 1, 1, 0),      # fully connected, split K
