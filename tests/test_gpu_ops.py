@@ -104,6 +104,8 @@ CONV_SHAPES = [
     # 96-row tiles with the generic loader (65-96 filters / input channels):
     (2, 3, 35, 35, 96, 11, 4, 0),  # AlexNet conv1 shape class
     (2, 80, 9, 9, 72, 7, 1, 3),    # 7x7: forward M=72, input gradient M=80
+    (2, 16, 8, 8, 80, 3, 1, 1),    # weight gradient 96 x 128 tiles, chunked K, 3x3
+    (3, 4, 11, 11, 96, 4, 1, 0),   # weight gradient 96 x 128 tiles, chunked K, 4x4
     (8, 16, 5, 5, 24, 3, 1, 1),    # 25 positions: the (image, position) order
     # fully connected layers (1x1 of a 1x1 input, after flattening):
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
