@@ -198,3 +198,14 @@ def test_argument_validation_without_device():
     assert ops.ach_conv_prepare_filters(0, None, None) == OK
     assert ops.ach_conv_bwd_data_prepared(C.byref(aetcnn.ConvDesc(2, 3, 9, 9, 8, 3, 2, 1)),
                                           fake, fake, fake, fake, fake, 1 << 20, None) == -4
+    # operands at or above 2 GiB (32-bit buffer offsets): refused, never launched
+    huge = aetcnn.ConvDesc(1024, 256, 64, 64, 8, 3, 1, 1)  # x = 4 GiB
+    for f in (ops.ach_conv_fwd, ops.ach_conv_bwd_data):
+        assert f(C.byref(huge), fake, fake, fake, fake, 1 << 40, None) == -4
+    assert ops.ach_conv_bwd_filter(C.byref(huge), fake, fake, fake, fake, 1 << 40, None) == -4
+    assert ops.ach_conv_fwd_bias_act_prepared(C.byref(huge), fake, fake, None, aetcnn.LEAKY,
+                                              fake, fake, 1 << 40, None) == -4
+    # the fused forward refuses activations it does not implement
+    assert ops.ach_conv_fwd_bias_act_prepared(C.byref(aetcnn.ConvDesc(2, 3, 8, 8, 8, 3, 1, 1)),
+                                              fake, fake, None, 2, fake, fake, 1 << 20,
+                                              None) == -4
