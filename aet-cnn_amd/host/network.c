@@ -61,6 +61,11 @@ struct an_network {
     float *wgrad_ws;
     size_t wgrad_ws_bytes;
     void **ev_ready;
+    void **ev_dgrad;               /* per layer: its input gradient enqueued */
+    /* set by an_train_step around a step that updates: each conv layer's
+     * SGD update is enqueued right after its gradients (early_rate)       */
+    int early_update;
+    float early_rate;
     void *ev_joined;
     ach_filter_job *jobs;          /* one per conv layer                    */
     int njobs;
@@ -244,7 +249,22 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
                                                   st.delta, st.workspace, st.workspace_bytes, s)
                      : ach_conv_bwd_data(&d, l->delta, l->weights, st.delta, st.workspace,
                                          st.workspace_bytes, s));
-    return ACH_OK;
+    if (!net->early_update) return ACH_OK;
+    /* The layer's SGD update (ConvolutionalLayer.update, the per-layer step
+     * of NNetwork.updateCPU) as soon as nothing else reads its parameters:
+     * after its gradients (stream gs) and, on the other stream, after its
+     * input gradient, which reads W (or, for stride 1 and k > 1, the
+     * flipped copy made at the forward).  The same arithmetic as an_update;
+     * it overlaps the backward of the layers below instead of ending the
+     * step (AlexNet's FC weights are 94% of its parameters).               */
+    if (gs != s) {
+        AN_CHECK(ach_event_record(net->ev_dgrad[l->index], s));
+        AN_CHECK(ach_stream_wait_event(gs, net->ev_dgrad[l->index]));
+    }
+    return ach_conv_update((size_t)l->nweights, l->weights, l->weight_updates, (size_t)l->n,
+                           l->biases, l->bias_updates, l->scales, l->scale_updates,
+                           net->batch * net->subdivisions, net->early_rate, net->momentum,
+                           net->decay, gs);
 }
 
 /* per-layer update for callers that drive layers one by one; an_update
@@ -712,10 +732,13 @@ int an_finalize(an_network *net)
     AN_CHECK(ach_stream_create(&net->stream));
     AN_CHECK(ach_stream_create(&net->wstream));
     net->ev_ready = (void **)calloc((size_t)(net->n > 0 ? net->n : 1), sizeof(void *));
-    if (!net->ev_ready) return ACH_EINVAL;
-    for (int i = 0; i < net->n; ++i)
-        if (net->layers[i]->type == AN_CONVOLUTIONAL)
-            AN_CHECK(ach_event_create(&net->ev_ready[i]));
+    net->ev_dgrad = (void **)calloc((size_t)(net->n > 0 ? net->n : 1), sizeof(void *));
+    if (!net->ev_ready || !net->ev_dgrad) return ACH_EINVAL;
+    for (int i = 0; i < net->n; ++i) {
+        if (net->layers[i]->type != AN_CONVOLUTIONAL) continue;
+        AN_CHECK(ach_event_create(&net->ev_ready[i]));
+        AN_CHECK(ach_event_create(&net->ev_dgrad[i]));
+    }
     AN_CHECK(ach_event_create(&net->ev_joined));
     bump real = {(char *)net->arena, 0, 0};
     layout(net, &real);
@@ -807,6 +830,11 @@ void an_free(an_network *net)
         for (int i = 0; i < net->n; ++i)
             if (net->ev_ready[i]) ach_event_destroy(net->ev_ready[i]);
         free(net->ev_ready);
+    }
+    if (net->ev_dgrad) {
+        for (int i = 0; i < net->n; ++i)
+            if (net->ev_dgrad[i]) ach_event_destroy(net->ev_dgrad[i]);
+        free(net->ev_dgrad);
     }
     if (net->ev_joined) ach_event_destroy(net->ev_joined);
     ach_free(net->arena);
@@ -1012,8 +1040,13 @@ void an_top_k(const float *a, int n, int k, int *index)
 static int enqueue_step(an_network *net, int update, float rate)
 {
     AN_CHECK(an_forward(net, 1));
-    AN_CHECK(an_backward(net));
-    if (update) AN_CHECK(update_at_rate(net, rate));
+    /* with an update, each layer's is enqueued by its backward (the join at
+     * the end of an_backward waits for them) */
+    net->early_update = update;
+    net->early_rate = rate;
+    const int rc = an_backward(net);
+    net->early_update = 0;
+    AN_CHECK(rc);
     return net->recording ? ach_counter_add(net->d_iter, 1u, net->stream) : ACH_OK;
 }
 

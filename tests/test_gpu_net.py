@@ -497,3 +497,28 @@ def test_cfg_policy_keys(gpu, oracle, tmp_path):
                    "[convolutional]\nfilters=4\nsize=1\n\n[avgpool]\n\n[softmax]\n")
     with pytest.raises(ValueError):
         aetcnn.Network.from_cfg(str(bad))
+
+
+@pytest.mark.parametrize("name,batch,steps", [("tiny", 32, 3), ("darknet", 8, 1),
+                                              ("alexnet", 2, 1), ("fcnet", 16, 1)])
+def test_train_step_updates_like_separate_update(gpu, name, batch, steps):
+    """an_train_step updates each layer right after its gradients (on the
+    weight-gradient stream); the parameters equal, bit for bit, those of
+    an_forward + an_backward + an_update (one flat update at the end).  (One
+    step where the net has dropout: the separate calls do not advance the
+    iteration the masks use.)"""
+    a, b = _twin_nets(name, batch)
+    for step in range(steps):
+        x, truth, _ = configs.synthetic_batch(name, 80 + step, batch)
+        a.set_input(x, truth)
+        a.train_step()
+        b.set_input(x, truth)
+        b.forward(1)
+        b.backward()
+        b.update()
+        assert a.loss() == b.loss(), step
+    for i in range(a.n_layers()):
+        for which in (2, 3, 4, 5, 6, 7, 8, 9):
+            u, v = a.buffer(i, which), b.buffer(i, which)
+            if u is not None:
+                assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), (name, i, which)
