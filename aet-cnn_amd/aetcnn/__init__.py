@@ -111,6 +111,7 @@ _OPS = {
     "ach_maxpool_out": (_i, [_i, _i, _i, _i]),
     "ach_maxpool_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ach_maxpool_bwd": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp]),
+    "ach_maxpool_bwd_act": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
     "ach_avgpool_fwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "ach_avgpool_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "ach_softmax_workspace": (_sz, [_i, _i]),

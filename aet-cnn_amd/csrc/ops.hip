@@ -304,6 +304,19 @@ __global__ void __launch_bounds__(256) k_maxpool2_fwd(const float *__restrict__ 
 
 __device__ __forceinline__ int floor_div(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 
+// The input gradient of a max-pool can leave the pool with the previous
+// layer's activation gradient already applied (Activation.gradientArray,
+// Activation.c:233-239, which that layer's backward would apply next):
+// din = sum * act_gradient(y[p]), the same fp32 multiply.  y == NULL: none.
+struct GradIn {
+    const float *y;
+    int act;
+    __device__ __forceinline__ float apply(float v, size_t p) const
+    {
+        return y ? v * act_gradient(y[p], act) : v;
+    }
+};
+
 // Gather: each input pixel visits, in ascending output order, the outputs
 // whose window holds it and adds the ones whose argmax is this pixel.  With
 // accumulate == 0 the sum starts from +0 instead of delta_in (the value the
@@ -316,7 +329,7 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
                                                      const int32_t *__restrict__ idx, int total,
                                                      FastDiv dH, FastDiv dW, int size_,
                                                      int stride_, int pad, int OH, int OW,
-                                                     float *din, int accumulate)
+                                                     float *din, int accumulate, GradIn gi)
 {
     const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
@@ -366,7 +379,7 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
                 if (idx[o] == (int32_t)p) v += dout[o];
             }
     }
-    din[p] = v;
+    din[p] = gi.apply(v, (size_t)p);
 }
 
 // The same gather for output planes that fit in LDS: one workgroup per
@@ -382,7 +395,7 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
                                                            const int32_t *__restrict__ idx,
                                                            FastDiv dW, int H, int size_,
                                                            int stride_, int pad, int OH, int OW,
-                                                           float *din, int accumulate)
+                                                           float *din, int accumulate, GradIn gi)
 {
     extern __shared__ int32_t pool_lds[];
     const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
@@ -425,7 +438,7 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
                     if (six[o] == p) v += sg[o];
                 }
         }
-        din[p] = v;
+        din[p] = gi.apply(v, (size_t)p);
     }
 }
 
@@ -438,7 +451,7 @@ __device__ __forceinline__ float pick(float v, int p, int ix, float d)
 __global__ void __launch_bounds__(256) k_maxpool2_bwd(const float *__restrict__ dout,
                                                       const int32_t *__restrict__ idx, int H,
                                                       int W, unsigned pairs, float *din,
-                                                      int accumulate)
+                                                      int accumulate, GradIn gi)
 {
     const int OW2 = W >> 2, OH = H >> 1;
     for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < pairs;
@@ -459,6 +472,14 @@ __global__ void __launch_bounds__(256) k_maxpool2_bwd(const float *__restrict__ 
         b.x = pick(b.x, i0 + W, ix.x, d.x);     b.y = pick(b.y, i0 + W + 1, ix.x, d.x);
         a.z = pick(a.z, i0 + 2, ix.y, d.y);     a.w = pick(a.w, i0 + 3, ix.y, d.y);
         b.z = pick(b.z, i0 + W + 2, ix.y, d.y); b.w = pick(b.w, i0 + W + 3, ix.y, d.y);
+        if (gi.y) {
+            const float4 ya = *reinterpret_cast<const float4 *>(gi.y + i0);
+            const float4 yb = *reinterpret_cast<const float4 *>(gi.y + i0 + W);
+            a.x *= act_gradient(ya.x, gi.act); a.y *= act_gradient(ya.y, gi.act);
+            a.z *= act_gradient(ya.z, gi.act); a.w *= act_gradient(ya.w, gi.act);
+            b.x *= act_gradient(yb.x, gi.act); b.y *= act_gradient(yb.y, gi.act);
+            b.z *= act_gradient(yb.z, gi.act); b.w *= act_gradient(yb.w, gi.act);
+        }
         *reinterpret_cast<float4 *>(din + i0) = a;
         *reinterpret_cast<float4 *>(din + i0 + W) = b;
     }
@@ -893,17 +914,19 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
     return check_launch();
 }
 
-int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
-                    int size, int stride, int pad, float *din, int accumulate, ach_stream_t s)
+static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
+                       int size, int stride, int pad, float *din, int accumulate, GradIn gi,
+                       ach_stream_t s)
 {
     if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
     const int acc = accumulate ? 1 : 0;
     if (pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
-        (reinterpret_cast<uintptr_t>(idx) & 7) == 0) {
+        (reinterpret_cast<uintptr_t>(idx) & 7) == 0 &&
+        (reinterpret_cast<uintptr_t>(gi.y) & 15) == 0) {
         const unsigned pairs = (unsigned)((size_t)batch * c * OH * OW / 2);
         hipLaunchKernelGGL(k_maxpool2_bwd, dim3(grid_for(pairs, 256, 256u * 64u)), dim3(256), 0,
-                           as_stream(s), dout, idx, h, w, pairs, din, acc);
+                           as_stream(s), dout, idx, h, w, pairs, din, acc, gi);
         return check_launch();
     }
     const int total = batch * c * h * w;  // < 2^31: pool_ok
@@ -914,25 +937,43 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
         const size_t lds = (size_t)OH * OW * 8;
         if (size == 3 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<3, 2>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, h, size, stride, pad, OH, OW, din, acc);
+                               idx, dW, h, size, stride, pad, OH, OW, din, acc, gi);
         else if (size == 2 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<2, 2>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, h, size, stride, pad, OH, OW, din, acc);
+                               idx, dW, h, size, stride, pad, OH, OW, din, acc, gi);
         else
             hipLaunchKernelGGL((k_maxpool_bwd_plane<0, 0>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, h, size, stride, pad, OH, OW, din, acc);
+                               idx, dW, h, size, stride, pad, OH, OW, din, acc, gi);
         return check_launch();
     }
     if (size == 3 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<3, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, dH, dW, size, stride, pad, OH, OW, din, acc);
+                           total, dH, dW, size, stride, pad, OH, OW, din, acc, gi);
     else if (size == 2 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<2, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, dH, dW, size, stride, pad, OH, OW, din, acc);
+                           total, dH, dW, size, stride, pad, OH, OW, din, acc, gi);
     else
         hipLaunchKernelGGL((k_maxpool_bwd<0, 0>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, dH, dW, size, stride, pad, OH, OW, din, acc);
+                           total, dH, dW, size, stride, pad, OH, OW, din, acc, gi);
     return check_launch();
+}
+
+int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
+                    int size, int stride, int pad, float *din, int accumulate, ach_stream_t s)
+{
+    return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
+                       GradIn{nullptr, 0}, s);
+}
+
+int ach_maxpool_bwd_act(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
+                        int size, int stride, int pad, float *din, int accumulate,
+                        const float *y_in, int act_in, ach_stream_t s)
+{
+    if (!y_in || (act_in != ACH_LOGISTIC && act_in != ACH_RELU && act_in != ACH_LINEAR &&
+                  act_in != ACH_LEAKY))
+        return ACH_EINVAL;
+    return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
+                       GradIn{y_in, act_in}, s);
 }
 
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out, ach_stream_t s)

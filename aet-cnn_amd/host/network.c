@@ -66,6 +66,10 @@ struct an_network {
      * SGD update is enqueued right after its gradients (early_rate)       */
     int early_update;
     float early_rate;
+    /* set by an_backward (the whole loop, not the per-layer entry point):
+     * a max-pool applies the previous conv layer's activation gradient to
+     * the delta it writes, and that layer skips its own pass             */
+    int in_chain;
     void *ev_joined;
     ach_filter_job *jobs;          /* one per conv layer                    */
     int njobs;
@@ -220,6 +224,8 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
                             l->variance, l->scales, l->biases, l->scale_updates,
                             l->mean_delta, l->variance_delta, act, st.workspace,
                             st.workspace_bytes, s));
+    } else if (l->grad_applied) {
+        l->grad_applied = 0; /* the max-pool above applied f'(y) already */
     } else {
         AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));
     }
@@ -353,7 +359,19 @@ static int maxpool_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
     /* the only contribution to the previous delta, which the reference
-     * zeroes in forward: write the sums instead of adding to zeros */
+     * zeroes in forward: write the sums instead of adding to zeros.  In the
+     * whole backward loop, when that delta is a plain conv layer's own (no
+     * BN, which fuses its gradient itself), the layer's activation gradient
+     * is applied here and the conv layer's backward skips it.              */
+    an_layer *p = l->index > 0 ? net->layers[l->index - 1] : NULL;
+    if (net->in_chain && p && p->type == AN_CONVOLUTIONAL && !p->batch_normalize &&
+        p->delta == st.delta && p->activation != ACH_LINEAR) {
+        AN_CHECK(ach_maxpool_bwd_act(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size,
+                                     l->stride, l->pad, st.delta, 0, p->output, p->activation,
+                                     net->stream));
+        p->grad_applied = 1;
+        return ACH_OK;
+    }
     return ach_maxpool_bwd(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size, l->stride,
                            l->pad, st.delta, 0, net->stream);
 }
@@ -924,10 +942,15 @@ static int join_wgrad(an_network *net)
 int an_backward(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
-    for (int i = net->n - 1; i >= 0; --i) {
+    net->in_chain = 1;
+    int rc = ACH_OK;
+    for (int i = net->n - 1; i >= 0 && rc == ACH_OK; --i) {
         an_layer *l = net->layers[i];
-        AN_CHECK(l->backward(net, l, backward_state(net, i)));
+        rc = l->backward(net, l, backward_state(net, i));
     }
+    net->in_chain = 0;
+    for (int i = 0; i < net->n; ++i) net->layers[i]->grad_applied = 0;
+    AN_CHECK(rc);
     return join_wgrad(net);
 }
 

@@ -239,6 +239,16 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w,
 int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
                     int batch, int c, int h, int w, int size, int stride, int padding,
                     float *delta_in, int accumulate, ach_stream_t stream);
+/* ach_maxpool_bwd, then delta_in *= f'(y_in) with the previous layer's
+ * output y_in and activation act_in (Activation.gradientArray,
+ * Activation.c:233-239, the first step of that layer's backward,
+ * ConvolutionalLayer.c:863-948) in the same pass: the same values, bit for
+ * bit, as ach_maxpool_bwd + ach_gradient.  Used when the pool's input
+ * gradient is that layer's whole delta.                                   */
+int ach_maxpool_bwd_act(const float *delta_out, const int32_t *indexes,
+                        int batch, int c, int h, int w, int size, int stride, int padding,
+                        float *delta_in, int accumulate, const float *y_in, int act_in,
+                        ach_stream_t stream);
 
 /* ---- global average pool (AvgPoolLayer.c:29-46, 73-88) ----------------- */
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out,

@@ -365,6 +365,36 @@ def test_maxpool_bit_exact(gpu, oracle, B, Cc, H, W, size, stride, pad):
     assert np.array_equal(got0.view(np.uint32), ref0.view(np.uint32))
 
 
+@pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [
+    (2, 5, 55, 55, 3, 2, 0),      # LDS-staged plane kernel
+    (4, 3, 32, 32, 2, 2, 1),      # 2x2/2 fast path (float4 y loads)
+    (1, 2, 140, 140, 3, 2, 0),    # gather kernel (plane above the LDS limit)
+    (3, 2, 7, 9, 2, 1, 1),        # generic window
+])
+@pytest.mark.parametrize("act", [aetcnn.RELU, aetcnn.LEAKY, aetcnn.LOGISTIC])
+def test_maxpool_bwd_act_fused(gpu, oracle, B, Cc, H, W, size, stride, pad, act):
+    """ach_maxpool_bwd_act == ach_maxpool_bwd then ach_gradient, bit for bit."""
+    rng = np.random.default_rng(H + 7 * act)
+    x = rng.integers(-3, 4, (B, Cc, H, W)).astype(np.float32)
+    out, idx = oracle.maxpool_forward(x, size, stride, pad)
+    y = rng.standard_normal(x.shape).astype(np.float32)
+    if act == aetcnn.LOGISTIC:
+        y = 1 / (1 + np.exp(-y)).astype(np.float32)
+    y.reshape(-1)[::5] = 0.0
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    dg, di, dy_ = dev(g), dev(idx.astype(np.int32)), dev(y)
+    ref = dev(np.zeros(x.shape, np.float32))
+    check(gpu.ach_maxpool_bwd(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, ref.ptr, 0, None))
+    check(gpu.ach_gradient(dy_.ptr, x.size, act, ref.ptr, None))
+    got = dev(np.full(x.shape, np.nan, np.float32))
+    check(gpu.ach_maxpool_bwd_act(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, got.ptr, 0,
+                                  dy_.ptr, act, None))
+    a, b = ref.numpy(), got.numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert gpu.ach_maxpool_bwd_act(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, got.ptr, 0,
+                                   None, act, None) == aetcnn.ACH_EINVAL
+
+
 def test_avgpool_bit_exact(gpu, oracle):
     rng = np.random.default_rng(5)
     x = rng.standard_normal((128, 10, 8, 8)).astype(np.float32)
