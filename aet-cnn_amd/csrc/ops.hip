@@ -550,6 +550,60 @@ __global__ void __launch_bounds__(256) k_softmax_xent(const float *__restrict__ 
     }
 }
 
+// The same for rows of at least 256 classes: one 256-thread workgroup per
+// row (four times the parallelism of a wave per row for the double exp),
+// the four waves' max / sum / error combined through LDS in wave order.
+__device__ __forceinline__ float block4_combine(float v, float *sh, bool is_max)
+{
+    v = is_max ? wave_max(v) : wave_sum(v);
+    __syncthreads();  // sh is reused by consecutive combines
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return is_max ? fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]))
+                  : ((sh[0] + sh[1]) + sh[2]) + sh[3];
+}
+
+__global__ void __launch_bounds__(256) k_softmax_xent_row(const float *__restrict__ in, int n,
+                                                          float T,
+                                                          const float *__restrict__ truth,
+                                                          float *__restrict__ out,
+                                                          float *__restrict__ delta,
+                                                          float *__restrict__ err,
+                                                          float *__restrict__ row_err)
+{
+    __shared__ float sh[4];
+    const int row = blockIdx.x;
+    const float *x = in + (size_t)row * n;
+    float *o = out + (size_t)row * n;
+    float mx = -FLT_MAX;
+    for (int i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, x[i]);
+    mx = block4_combine(mx, sh, true);
+    const float lt = mx / T;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float e = (float)exp((double)(x[i] / T - lt));
+        o[i] = e;
+        s += e;
+    }
+    s = block4_combine(s, sh, false);
+    float es = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float p = o[i] / s;
+        o[i] = p;
+        if (truth) {
+            const float t = truth[(size_t)row * n + i];
+            const float e = (t != 0.f) ? -logf(p) : 0.f;
+            err[(size_t)row * n + i] = e;
+            delta[(size_t)row * n + i] = t - p;
+            es += e;
+        }
+    }
+    if (truth) {
+        es = block4_combine(es, sh, false);
+        if (threadIdx.x == 0) row_err[row] = es;
+    }
+}
+
 __global__ void __launch_bounds__(256) k_sum_rows(const float *__restrict__ row_err, int rows,
                                                   float *cost)
 {
@@ -1009,8 +1063,12 @@ int ach_softmax_xent(const float *in, int batch, int inputs, int groups, float T
     const int rows = batch * groups, n = inputs / groups;
     if (truth && (!ws || ws_bytes < ach_softmax_workspace(batch, groups))) return ACH_EWORKSPACE;
     hipStream_t st = as_stream(s);
-    hipLaunchKernelGGL(k_softmax_xent, dim3((rows + 3) / 4), dim3(256), 0, st, in, rows, n, T,
-                       truth, out, delta, err, (float *)ws);
+    if (n >= 256)
+        hipLaunchKernelGGL(k_softmax_xent_row, dim3(rows), dim3(256), 0, st, in, n, T, truth, out,
+                           delta, err, (float *)ws);
+    else
+        hipLaunchKernelGGL(k_softmax_xent, dim3((rows + 3) / 4), dim3(256), 0, st, in, rows, n,
+                           T, truth, out, delta, err, (float *)ws);
     int rc = check_launch();
     if (rc || !truth) return rc;
     hipLaunchKernelGGL(k_sum_rows, dim3(1), dim3(256), 0, st, (const float *)ws, rows, cost);

@@ -410,7 +410,8 @@ def test_avgpool_bit_exact(gpu, oracle):
     assert np.array_equal(ddin.numpy(), refb)
 
 
-@pytest.mark.parametrize("B,n,groups", [(128, 10, 1), (512, 1000, 1), (7, 12, 3)])
+@pytest.mark.parametrize("B,n,groups", [(128, 10, 1), (512, 1000, 1), (7, 12, 3),
+                                        (5, 300, 1), (3, 1536, 3)])  # workgroup per row
 def test_softmax_xent(gpu, oracle, B, n, groups):
     rng = np.random.default_rng(n)
     x = (rng.standard_normal((B, n)) * 3).astype(np.float32)
