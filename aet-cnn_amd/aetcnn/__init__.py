@@ -112,6 +112,10 @@ _OPS = {
     "ach_maxpool_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ach_maxpool_bwd": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp]),
     "ach_maxpool_bwd_act": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
+    "ach_maxpool_fwd_dropout": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _f, _u64, _u32,
+                                     _vp, _u32, _vp]),
+    "ach_maxpool_bwd_dropout": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _u64,
+                                     _u32, _vp, _u32, _vp]),
     "ach_avgpool_fwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "ach_avgpool_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "ach_softmax_workspace": (_sz, [_i, _i]),

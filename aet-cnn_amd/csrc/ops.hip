@@ -279,9 +279,35 @@ __device__ __forceinline__ void max4(float a, float b, float c, float d, int ia,
     if (d > mx) { mx = d; mi = ia + W + 1; }
 }
 
+// A dropout layer that follows a 2x2 max-pool and shares its output
+// (DropoutLayer.c:55-86, NetworkFactory.c:644-650) can run inside the pool
+// kernels: the forward writes r < p ? 0 : v * scale for pooled element e,
+// the backward applies the same mask to the output gradient it reads
+// (r = dropout_uniform(seed, iter, layer, e), iter from device memory when
+// iter_ptr is set) -- the values k_dropout would leave, bit for bit.
+struct DropIn {
+    float p, scale;
+    uint64_t seed;
+    uint32_t iter0;
+    const uint32_t *iter_ptr;
+    uint32_t layer;
+    int on;
+    __device__ __forceinline__ float2 apply(float2 v, unsigned t) const
+    {
+        if (!on) return v;
+        const uint32_t it = iter_ptr ? *iter_ptr : iter0;
+        const uint32_t e = 2u * t;
+        const float r0 = dropout_uniform(seed, it, layer, e);
+        const float r1 = dropout_uniform(seed, it, layer, e + 1);
+        v.x = (r0 < p) ? 0.f : v.x * scale;
+        v.y = (r1 < p) ? 0.f : v.y * scale;
+        return v;
+    }
+};
+
 __global__ void __launch_bounds__(256) k_maxpool2_fwd(const float *__restrict__ in, int H, int W,
                                                       unsigned pairs, float *__restrict__ out,
-                                                      int32_t *__restrict__ idx)
+                                                      int32_t *__restrict__ idx, DropIn dr)
 {
     const int OW2 = W >> 2, OH = H >> 1;
     for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < pairs;
@@ -297,7 +323,7 @@ __global__ void __launch_bounds__(256) k_maxpool2_fwd(const float *__restrict__ 
         int2 ix;
         max4(a.x, a.y, b.x, b.y, i0, W, o.x, ix.x);
         max4(a.z, a.w, b.z, b.w, i0 + 2, W, o.y, ix.y);
-        reinterpret_cast<float2 *>(out)[t] = o;
+        reinterpret_cast<float2 *>(out)[t] = dr.apply(o, t);
         if (idx) reinterpret_cast<int2 *>(idx)[t] = ix;
     }
 }
@@ -451,7 +477,7 @@ __device__ __forceinline__ float pick(float v, int p, int ix, float d)
 __global__ void __launch_bounds__(256) k_maxpool2_bwd(const float *__restrict__ dout,
                                                       const int32_t *__restrict__ idx, int H,
                                                       int W, unsigned pairs, float *din,
-                                                      int accumulate, GradIn gi)
+                                                      int accumulate, GradIn gi, DropIn dr)
 {
     const int OW2 = W >> 2, OH = H >> 1;
     for (unsigned t = blockIdx.x * blockDim.x + threadIdx.x; t < pairs;
@@ -461,7 +487,7 @@ __global__ void __launch_bounds__(256) k_maxpool2_bwd(const float *__restrict__ 
         const int i = (int)(r % OH);
         const int bc = (int)(r / OH);
         const int i0 = (bc * H + 2 * i) * W + 4 * jp;
-        const float2 d = reinterpret_cast<const float2 *>(dout)[t];
+        const float2 d = dr.apply(reinterpret_cast<const float2 *>(dout)[t], t);
         const int2 ix = reinterpret_cast<const int2 *>(idx)[t];
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
         if (accumulate) {
@@ -941,8 +967,13 @@ static bool pool2_fast(const void *a, const void *b, int h, int w, int size, int
            ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
 }
 
-int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, int stride,
-                    int pad, float *out, int32_t *idx, ach_stream_t s)
+static int dropout_launch(float *x, size_t n, float p, uint64_t seed, uint32_t iter,
+                          const uint32_t *iter_ptr, uint32_t layer, ach_stream_t s);
+
+// dr.on: the following dropout runs in the 2x2 kernel, or after the pool
+// on the other paths
+static int maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, int stride,
+                       int pad, float *out, int32_t *idx, DropIn dr, ach_stream_t s)
 {
     if (!in || !out || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
@@ -950,8 +981,16 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
         (reinterpret_cast<uintptr_t>(idx) & 7) == 0) {
         const unsigned pairs = (unsigned)((size_t)batch * c * OH * OW / 2);
         hipLaunchKernelGGL(k_maxpool2_fwd, dim3(grid_for(pairs, 256, 256u * 64u)), dim3(256), 0,
-                           as_stream(s), in, h, w, pairs, out, idx);
+                           as_stream(s), in, h, w, pairs, out, idx, dr);
         return check_launch();
+    }
+    if (dr.on) {
+        DropIn none = dr;
+        none.on = 0;
+        const int rc = maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, none, s);
+        if (rc) return rc;
+        return dropout_launch(out, (size_t)batch * c * OH * OW, dr.p, dr.seed, dr.iter0,
+                              dr.iter_ptr, dr.layer, s);
     }
     const int total = batch * c * OH * OW;
     const dim3 grid((total + 255) / 256);
@@ -968,19 +1007,43 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
     return check_launch();
 }
 
+int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, int stride,
+                    int pad, float *out, int32_t *idx, ach_stream_t s)
+{
+    DropIn none{};
+    return maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, none, s);
+}
+
+int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w, int size,
+                            int stride, int pad, float *out, int32_t *idx, float probability,
+                            uint64_t seed, uint32_t iter, const uint32_t *iter_ptr,
+                            uint32_t layer, ach_stream_t s)
+{
+    if (!(probability >= 0.f && probability < 1.f)) return ACH_EINVAL;
+    const DropIn dr{probability, (float)(1. / (1.0 - probability)), seed, iter, iter_ptr, layer, 1};
+    return maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, dr, s);
+}
+
 static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
                        int size, int stride, int pad, float *din, int accumulate, GradIn gi,
-                       ach_stream_t s)
+                       DropIn dr, ach_stream_t s)
 {
     if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
     const int acc = accumulate ? 1 : 0;
-    if (pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
-        (reinterpret_cast<uintptr_t>(idx) & 7) == 0 &&
-        (reinterpret_cast<uintptr_t>(gi.y) & 15) == 0) {
+    const bool fast2 = pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
+                       (reinterpret_cast<uintptr_t>(idx) & 7) == 0 &&
+                       (reinterpret_cast<uintptr_t>(gi.y) & 15) == 0;
+    if (dr.on && !fast2) {  // the dropout backward in place on dout first
+        const int rc = dropout_launch(const_cast<float *>(dout), (size_t)batch * c * OH * OW,
+                                      dr.p, dr.seed, dr.iter0, dr.iter_ptr, dr.layer, s);
+        if (rc) return rc;
+        dr.on = 0;
+    }
+    if (fast2) {
         const unsigned pairs = (unsigned)((size_t)batch * c * OH * OW / 2);
         hipLaunchKernelGGL(k_maxpool2_bwd, dim3(grid_for(pairs, 256, 256u * 64u)), dim3(256), 0,
-                           as_stream(s), dout, idx, h, w, pairs, din, acc, gi);
+                           as_stream(s), dout, idx, h, w, pairs, din, acc, gi, dr);
         return check_launch();
     }
     const int total = batch * c * h * w;  // < 2^31: pool_ok
@@ -1016,7 +1079,18 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
                     int size, int stride, int pad, float *din, int accumulate, ach_stream_t s)
 {
     return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
-                       GradIn{nullptr, 0}, s);
+                       GradIn{nullptr, 0}, DropIn{}, s);
+}
+
+int ach_maxpool_bwd_dropout(float *dout, const int32_t *idx, int batch, int c, int h, int w,
+                            int size, int stride, int pad, float *din, int accumulate,
+                            float probability, uint64_t seed, uint32_t iter,
+                            const uint32_t *iter_ptr, uint32_t layer, ach_stream_t s)
+{
+    if (!(probability >= 0.f && probability < 1.f)) return ACH_EINVAL;
+    const DropIn dr{probability, (float)(1. / (1.0 - probability)), seed, iter, iter_ptr, layer, 1};
+    return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
+                       GradIn{nullptr, 0}, dr, s);
 }
 
 int ach_maxpool_bwd_act(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
@@ -1027,7 +1101,7 @@ int ach_maxpool_bwd_act(const float *dout, const int32_t *idx, int batch, int c,
                   act_in != ACH_LEAKY))
         return ACH_EINVAL;
     return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
-                       GradIn{y_in, act_in}, s);
+                       GradIn{y_in, act_in}, DropIn{}, s);
 }
 
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out, ach_stream_t s)

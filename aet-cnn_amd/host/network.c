@@ -70,6 +70,7 @@ struct an_network {
      * a max-pool applies the previous conv layer's activation gradient to
      * the delta it writes, and that layer skips its own pass             */
     int in_chain;
+    int in_chain_fwd;              /* the same for an_forward's loop      */
     void *ev_joined;
     ach_filter_job *jobs;          /* one per conv layer                    */
     int njobs;
@@ -349,8 +350,44 @@ int an_add_connected(an_network *net, int outputs, int activation, int batch_nor
 /* ======================================================================== */
 /* Max-pool: MaxPoolLayer.c:237-272 / :318-331, defaults from createMaxPool
  * (NetworkFactory.c:543-570: padding = size-1 unless given).              */
+/* the dropout layer right after a max-pool, sharing its output and delta */
+static an_layer *dropout_after(an_network *net, const an_layer *l)
+{
+    if (l->index + 1 >= net->n) return NULL;
+    an_layer *d = net->layers[l->index + 1];
+    return d->type == AN_DROPOUT && d->shares_prev ? d : NULL;
+}
+
+/* the conv layer whose delta a max-pool's input gradient is, when the pool
+ * applies that layer's activation gradient (whole backward loop only)    */
+static an_layer *pool_act_target(an_network *net, const an_layer *l, const float *delta)
+{
+    an_layer *p = l->index > 0 ? net->layers[l->index - 1] : NULL;
+    if (net->in_chain && p && p->type == AN_CONVOLUTIONAL && !p->batch_normalize &&
+        p->delta == delta && p->activation != ACH_LINEAR)
+        return p;
+    return NULL;
+}
+
+/* In the whole loops a dropout layer after a max-pool runs inside the pool's
+ * kernels (its forward skips, its backward leaves the mask to the pool)   */
+static int pool_fuses_dropout_bwd(an_network *net, const an_layer *l)
+{
+    if (!net->in_chain || !dropout_after(net, l) || l->index == 0) return 0;
+    return pool_act_target(net, l, net->layers[l->index - 1]->delta) == NULL;
+}
+
 static int maxpool_forward(an_network *net, an_layer *l, an_state st)
 {
+    an_layer *d = st.train && net->in_chain_fwd ? dropout_after(net, l) : NULL;
+    if (d) {
+        d->drop_fused = 1;
+        return ach_maxpool_fwd_dropout(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride,
+                                       l->pad, l->output, l->indexes, d->probability,
+                                       net->dropout_seed, net->dropout_step,
+                                       net->recording ? net->d_iter : NULL, (uint32_t)d->index,
+                                       net->stream);
+    }
     return ach_maxpool_fwd(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride, l->pad,
                            l->output, l->indexes, net->stream);
 }
@@ -358,14 +395,21 @@ static int maxpool_forward(an_network *net, an_layer *l, an_state st)
 static int maxpool_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
+    if (pool_fuses_dropout_bwd(net, l)) {
+        const an_layer *d = dropout_after(net, l);
+        return ach_maxpool_bwd_dropout(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size,
+                                       l->stride, l->pad, st.delta, 0, d->probability,
+                                       net->dropout_seed, net->dropout_step,
+                                       net->recording ? net->d_iter : NULL, (uint32_t)d->index,
+                                       net->stream);
+    }
     /* the only contribution to the previous delta, which the reference
      * zeroes in forward: write the sums instead of adding to zeros.  In the
      * whole backward loop, when that delta is a plain conv layer's own (no
      * BN, which fuses its gradient itself), the layer's activation gradient
      * is applied here and the conv layer's backward skips it.              */
-    an_layer *p = l->index > 0 ? net->layers[l->index - 1] : NULL;
-    if (net->in_chain && p && p->type == AN_CONVOLUTIONAL && !p->batch_normalize &&
-        p->delta == st.delta && p->activation != ACH_LINEAR) {
+    an_layer *p = pool_act_target(net, l, st.delta);
+    if (p) {
         AN_CHECK(ach_maxpool_bwd_act(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size,
                                      l->stride, l->pad, st.delta, 0, p->output, p->activation,
                                      net->stream));
@@ -432,6 +476,10 @@ int an_add_avgpool(an_network *net)
  * (net->d_iter), so every replay of it draws its own masks.               */
 static int dropout_forward(an_network *net, an_layer *l, an_state st)
 {
+    if (l->drop_fused) { /* applied by the max-pool before it */
+        l->drop_fused = 0;
+        return ACH_OK;
+    }
     if (!st.train) return ACH_OK;
     const size_t n = (size_t)l->batch * l->inputs;
     if (net->recording)
@@ -444,6 +492,9 @@ static int dropout_forward(an_network *net, an_layer *l, an_state st)
 static int dropout_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
+    const an_layer *p = net->layers[l->index - 1];  /* dropout is never first */
+    if (p->type == AN_MAXPOOL && pool_fuses_dropout_bwd(net, p))
+        return ACH_OK; /* the max-pool's backward applies the mask */
     const size_t n = (size_t)l->batch * l->inputs;
     if (net->recording)
         return ach_dropout_bwd_dev(st.delta, n, l->probability, net->dropout_seed, net->d_iter,
@@ -911,13 +962,17 @@ int an_forward(an_network *net, int train)
     AN_CHECK(ach_conv_prepare_filters(net->njobs, net->jobs, net->stream));
     if (train && net->zero_floats)
         AN_CHECK(ach_fill(net->zero_region, net->zero_floats, 0.f, net->stream));
-    for (int i = 0; i < net->n; ++i) {
+    net->in_chain_fwd = 1;
+    int rc = ACH_OK;
+    for (int i = 0; i < net->n && rc == ACH_OK; ++i) {
         an_layer *l = net->layers[i];
         st.index = i;
-        AN_CHECK(l->forward(net, l, st));
+        rc = l->forward(net, l, st);
         st.input = l->output;
     }
-    return ACH_OK;
+    net->in_chain_fwd = 0;
+    for (int i = 0; i < net->n; ++i) net->layers[i]->drop_fused = 0;
+    return rc;
 }
 
 static an_state backward_state(an_network *net, int i)

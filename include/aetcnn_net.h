@@ -84,6 +84,7 @@ struct an_layer {
     float *output, *delta;
     int zero_delta;         /* delta is accumulated into by the next layer */
     int grad_applied;       /* this step's f'(y) already applied to delta   */
+    int drop_fused;         /* dropout: this forward ran inside the max-pool */
     int (*forward)(an_network *net, an_layer *l, an_state st);
     int (*backward)(an_network *net, an_layer *l, an_state st);
     int (*update)(an_network *net, an_layer *l, int batch, float lr, float momentum,

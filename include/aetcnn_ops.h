@@ -245,6 +245,23 @@ int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
  * ConvolutionalLayer.c:863-948) in the same pass: the same values, bit for
  * bit, as ach_maxpool_bwd + ach_gradient.  Used when the pool's input
  * gradient is that layer's whole delta.                                   */
+/* A dropout layer that follows the max-pool and shares its output
+ * (DropoutLayer.c:55-86, NetworkFactory.c:644-650), applied by the pool:
+ * the forward writes the masked output (ach_maxpool_fwd + ach_dropout_fwd on
+ * out), the backward masks delta_out as it reads it (ach_dropout_bwd on
+ * delta_out + ach_maxpool_bwd; delta_out itself may be left unmasked) --
+ * the same values bit for bit.  iter_ptr, when set, supplies the step index
+ * from device memory (as ach_dropout_fwd_dev).  Fused into the 2x2 / stride
+ * 2 kernels; other windows run the two steps inside the call.            */
+int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w,
+                            int size, int stride, int padding, float *out, int32_t *indexes,
+                            float probability, uint64_t seed, uint32_t iter,
+                            const uint32_t *iter_ptr, uint32_t layer, ach_stream_t stream);
+int ach_maxpool_bwd_dropout(float *delta_out, const int32_t *indexes,
+                            int batch, int c, int h, int w, int size, int stride, int padding,
+                            float *delta_in, int accumulate, float probability, uint64_t seed,
+                            uint32_t iter, const uint32_t *iter_ptr, uint32_t layer,
+                            ach_stream_t stream);
 int ach_maxpool_bwd_act(const float *delta_out, const int32_t *indexes,
                         int batch, int c, int h, int w, int size, int stride, int padding,
                         float *delta_in, int accumulate, const float *y_in, int act_in,
