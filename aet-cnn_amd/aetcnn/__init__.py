@@ -46,6 +46,12 @@ class ConvDesc(C.Structure):
                 ("size", _i), ("stride", _i), ("pad", _i)]
 
 
+class LayerOptions(C.Structure):
+    """an_layer_options"""
+    _fields_ = [("stopbackward", _i), ("onlyforward", _i), ("dontload", _i),
+                ("dontloadscales", _i), ("flipped", _i), ("learning_rate_scale", _f)]
+
+
 class FilterJob(C.Structure):
     """ach_filter_job"""
     _fields_ = [("desc", ConvDesc), ("w", _vp), ("wt", _vp), ("wft", _vp)]
@@ -79,8 +85,8 @@ _OPS = {
     "ach_axpy": (_i, [_sz, _f, _vp, _vp, _vp]),
     "ach_scal": (_i, [_sz, _f, _vp, _vp]),
     "ach_gemm": (_i, [_i, _i, _i, _i, _i, _f, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
-    "ach_im2col": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
-    "ach_col2im": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "ach_im2col": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "ach_col2im": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "ach_conv_out_h": (_i, [C.POINTER(ConvDesc)]),
     "ach_conv_out_w": (_i, [C.POINTER(ConvDesc)]),
     "ach_conv_fwd_workspace": (_sz, [C.POINTER(ConvDesc)]),
@@ -152,6 +158,9 @@ _NET = {
     "an_finalize": (_i, [_vp]),
     "an_free": (None, [_vp]),
     "an_parse_cfg": (_vp, [C.c_char_p]),
+    "an_parse_cfg_unfinalized": (_vp, [C.c_char_p]),
+    "an_set_layer_options": (_i, [_vp, _i, C.POINTER(LayerOptions)]),
+    "an_get_layer_options": (_i, [_vp, _i, C.POINTER(LayerOptions)]),
     "an_save_weights": (_i, [_vp, C.c_char_p]),
     "an_load_weights": (_i, [_vp, C.c_char_p]),
     "an_stream": (_vp, [_vp]),
@@ -308,9 +317,12 @@ class Network:
         self.batch = batch
 
     @classmethod
-    def from_cfg(cls, path: str) -> "Network":
+    def from_cfg(cls, path: str, finalize: bool = True) -> "Network":
+        """an_parse_cfg, or with finalize=False an_parse_cfg_unfinalized (host
+        only: no device memory is touched until finalize())."""
         lib = net_lib()
-        h = lib.an_parse_cfg(path.encode())
+        fn = lib.an_parse_cfg if finalize else lib.an_parse_cfg_unfinalized
+        h = fn(os.fsencode(path))
         if not h:
             raise ValueError(f"an_parse_cfg({path}) failed")
         n = cls.__new__(cls)
@@ -318,6 +330,18 @@ class Network:
         n.h = h
         n.batch = lib.an_batch(h)
         return n
+
+    def layer_options(self, i: int) -> dict:
+        o = LayerOptions()
+        check(self.lib.an_get_layer_options(self.h, i, C.byref(o)), "an_get_layer_options")
+        return {k: getattr(o, k) for k, _ in LayerOptions._fields_}
+
+    def set_layer_options(self, i: int, **kw):
+        """an_set_layer_options (before finalize); unnamed options keep their values"""
+        cur = self.layer_options(i)
+        cur.update(kw)
+        o = LayerOptions(**cur)
+        check(self.lib.an_set_layer_options(self.h, i, C.byref(o)), "an_set_layer_options")
 
     def conv(self, filters, size, stride, pad, activation, bn):
         r = self.lib.an_add_convolutional(self.h, filters, size, stride, pad, activation, int(bn))

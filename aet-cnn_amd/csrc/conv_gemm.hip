@@ -1750,7 +1750,7 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
         int rc = ach_gemm(1, 0, n, k, m, 1.f, w, n, dy + (size_t)i * m * k, k, 0.f, col, k,
                           stream);
         if (rc) return rc;
-        rc = ach_col2im(col, g.C, g.H, g.W, g.KS, g.KS, g.P, g.P, g.S, g.S,
+        rc = ach_col2im(col, g.C, g.H, g.W, g.KS, g.KS, g.P, g.P, g.S, g.S, 1, 1,
                         dx + (size_t)i * g.C * g.H * g.W, stream);
         if (rc) return rc;
     }

@@ -53,7 +53,7 @@ __global__ void k_scal(size_t n, float a, float *x)
 
 // ---- im2col / col2im (one image) ----------------------------------------------
 __global__ void k_im2col(const float *__restrict__ im, int C, int H, int W, int kh, int kw,
-                         int ph, int pw, int sh, int sw, int OH, int OW,
+                         int ph, int pw, int sh, int sw, int dh, int dw, int OH, int OW,
                          float *__restrict__ col)
 {
     const size_t total = (size_t)C * kh * kw * OH * OW;
@@ -67,7 +67,7 @@ __global__ void k_im2col(const float *__restrict__ im, int C, int H, int W, int 
         r /= kw;
         const int ki = (int)(r % kh);
         const int c = (int)(r / kh);
-        const int ih = oh * sh - ph + ki, iw = ow * sw - pw + kj;
+        const int ih = oh * sh - ph + ki * dh, iw = ow * sw - pw + kj * dw;
         col[i] = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
                      ? im[((size_t)c * H + ih) * W + iw]
                      : 0.f;
@@ -75,9 +75,10 @@ __global__ void k_im2col(const float *__restrict__ im, int C, int H, int W, int 
 }
 
 // Gather form of col2im: every image pixel adds its column entries in the
-// reference's (ki, kj) scan order starting from zero -> bit-identical sums.
+// reference's (ki, kj) scan order starting from zero -> bit-identical sums
+// (for one tap (ki, kj) at most one output position reads the pixel).
 __global__ void k_col2im(const float *__restrict__ col, int C, int H, int W, int kh, int kw,
-                         int ph, int pw, int sh, int sw, int OH, int OW,
+                         int ph, int pw, int sh, int sw, int dh, int dw, int OH, int OW,
                          float *__restrict__ im)
 {
     const size_t total = (size_t)C * H * W;
@@ -88,12 +89,12 @@ __global__ void k_col2im(const float *__restrict__ col, int C, int H, int W, int
         const int c = (int)(i / ((size_t)W * H));
         float v = 0.f;
         for (int ki = 0; ki < kh; ++ki) {
-            const int t = h + ph - ki;
+            const int t = h + ph - ki * dh;
             if (t < 0 || t % sh) continue;
             const int oh = t / sh;
             if (oh >= OH) continue;
             for (int kj = 0; kj < kw; ++kj) {
-                const int u = w + pw - kj;
+                const int u = w + pw - kj * dw;
                 if (u < 0 || u % sw) continue;
                 const int ow = u / sw;
                 if (ow >= OW) continue;
@@ -859,30 +860,33 @@ int ach_scal(size_t n, float a, float *x, ach_stream_t s)
 }
 
 int ach_im2col(const float *im, int C, int H, int W, int kh, int kw, int ph, int pw, int sh,
-               int sw, float *col, ach_stream_t s)
+               int sw, int dh, int dw, float *col, ach_stream_t s)
 {
     if (!im || !col || C <= 0 || H <= 0 || W <= 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 ||
-        ph < 0 || pw < 0)
+        ph < 0 || pw < 0 || dh <= 0 || dw <= 0)
         return ACH_EINVAL;
-    const int OH = (H + 2 * ph - kh) / sh + 1, OW = (W + 2 * pw - kw) / sw + 1;
-    if (OH <= 0 || OW <= 0) return ACH_EINVAL;
+    /* output size of the dilated window (Im2Col.c:70-73) */
+    const int ekh = dh * (kh - 1) + 1, ekw = dw * (kw - 1) + 1;
+    if (H + 2 * ph < ekh || W + 2 * pw < ekw) return ACH_EINVAL;
+    const int OH = (H + 2 * ph - ekh) / sh + 1, OW = (W + 2 * pw - ekw) / sw + 1;
     const size_t tot = (size_t)C * kh * kw * OH * OW;
     hipLaunchKernelGGL(k_im2col, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), im, C, H,
-                       W, kh, kw, ph, pw, sh, sw, OH, OW, col);
+                       W, kh, kw, ph, pw, sh, sw, dh, dw, OH, OW, col);
     return check_launch();
 }
 
 int ach_col2im(const float *col, int C, int H, int W, int kh, int kw, int ph, int pw, int sh,
-               int sw, float *im, ach_stream_t s)
+               int sw, int dh, int dw, float *im, ach_stream_t s)
 {
     if (!im || !col || C <= 0 || H <= 0 || W <= 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 ||
-        ph < 0 || pw < 0)
+        ph < 0 || pw < 0 || dh <= 0 || dw <= 0)
         return ACH_EINVAL;
-    const int OH = (H + 2 * ph - kh) / sh + 1, OW = (W + 2 * pw - kw) / sw + 1;
-    if (OH <= 0 || OW <= 0) return ACH_EINVAL;
+    const int ekh = dh * (kh - 1) + 1, ekw = dw * (kw - 1) + 1;
+    if (H + 2 * ph < ekh || W + 2 * pw < ekw) return ACH_EINVAL;
+    const int OH = (H + 2 * ph - ekh) / sh + 1, OW = (W + 2 * pw - ekw) / sw + 1;
     const size_t tot = (size_t)C * H * W;
     hipLaunchKernelGGL(k_col2im, dim3(grid_for(tot, 256)), dim3(256), 0, as_stream(s), col, C, H,
-                       W, kh, kw, ph, pw, sh, sw, OH, OW, im);
+                       W, kh, kw, ph, pw, sh, sw, dh, dw, OH, OW, im);
     return check_launch();
 }
 

@@ -23,8 +23,18 @@
  *   [avgpool]        createAvgPool NetworkFactory.c:572-584
  *   [dropout]        createDropoutLayer NetworkFactory.c:328-329  probability=.2
  *   [softmax]        createSoftMax NetworkFactory.c:586-601 groups=1 temperature=1
- * Keys this build does not implement (xnor, groups>1 convs, dilation,
- * antialiasing, ...) are rejected when set to a non-default value.
+ * Every layer section also takes the options of createLayer /
+ * createNetwork (NetworkFactory.c:656-663, 926-935) that the CPU path acts
+ * on: stopbackward, onlyforward, dontload, dontloadscales, learning_rate
+ * (a float scale of the layer's rate) and, for [convolutional], flipped.
+ * Keys the reference reads whose non-default values change its CPU
+ * training step but this build does not implement (groups, dilation,
+ * xnor, binary, bin_output, antialiasing, cbn, deformable sway / rotate /
+ * stretch, assisted_excitation, share_index, unequal stride_x / stride_y,
+ * maxpool_depth, dropblock, softmax spatial / noloss / tree, [net]
+ * time_steps) are rejected with a message.  Keys the reference reads but
+ * its CPU path never acts on are accepted; keys it does not read are
+ * reported as unused (darknet's behaviour).
  */
 #include "aetcnn_net.h"
 
@@ -88,6 +98,10 @@ static int read_groups(const char *path, cfg_group **out, int *count)
     }
     int cap = 16, n = 0;
     cfg_group *gs = (cfg_group *)calloc(cap, sizeof(cfg_group));
+    if (!gs) {
+        fclose(f);
+        return -1;
+    }
     char line[512];
     int lineno = 0;
     while (fgets(line, sizeof(line), f)) {
@@ -99,8 +113,15 @@ static int read_groups(const char *path, cfg_group **out, int *count)
             if (!e) goto bad;
             *e = 0;
             if (n == cap) {
+                cfg_group *ng = (cfg_group *)realloc(gs, sizeof(cfg_group) * cap * 2);
+                if (!ng) {
+                    fprintf(stderr, "an_parse_cfg: out of host memory\n");
+                    fclose(f);
+                    free(gs);
+                    return -1;
+                }
+                gs = ng;
                 cap *= 2;
-                gs = (cfg_group *)realloc(gs, sizeof(cfg_group) * cap);
             }
             memset(&gs[n], 0, sizeof(cfg_group));
             snprintf(gs[n].name, sizeof(gs[n].name), "%s", trim(s + 1));
@@ -133,6 +154,104 @@ static int unsupported(const cfg_group *g, const char *key, int def)
     if (v && atoi(v) != def) {
         fprintf(stderr, "an_parse_cfg: [%s] %s=%s is not supported\n", g->name, key, v);
         return 1;
+    }
+    return 0;
+}
+
+/* a key whose mere presence asks for something not built */
+static int present_unsupported(const cfg_group *g, const char *key)
+{
+    const char *v = find(g, key);
+    if (v) {
+        fprintf(stderr, "an_parse_cfg: [%s] %s=%s is not supported\n", g->name, key, v);
+        return 1;
+    }
+    return 0;
+}
+
+/* The keys the reference reads in each section (NetworkFactory.c:77-173,
+ * 328-340, 543-601, 656-663, 671-823, 926-935); any other key is reported
+ * as unused, as darknet does.                                              */
+static const char *const NET_KEYS[] = {
+    "max_batches", "batch", "learning_rate", "learning_rate_min", "sgdr_cycle", "sgdr_mult",
+    "momentum", "decay", "subdivisions", "time_steps", "track", "augment_speed",
+    "sequential_subdivisions", "try_fix_nan", "weights_reject_freq", "equidistant_point",
+    "badlabels_rejection_percentage", "num_sigmas_reject_badlabels", "ema_alpha",
+    "use_cuda_graph", "loss_scale", "dynamic_minibatch", "optimized_memory",
+    "workspace_size_limit_MB", "adam", "B1", "B2", "eps", "height", "width", "channels",
+    "inputs", "max_crop", "min_crop", "flip", "blur", "gaussian_noise", "mixup", "cutmix",
+    "mosaic", "letter_box", "mosaic_bound", "contrastive", "contrastive_jit_flip",
+    "contrastive_color", "unsupervised", "label_smooth_eps", "resize_step", "attention",
+    "adversarial_lr", "max_chart_loss", "angle", "aspect", "saturation", "exposure", "hue",
+    "power", "policy", "burn_in", "step", "scale", "steps", "scales", "seq_scales", "gamma",
+    NULL};
+static const char *const LAYER_KEYS[] = { /* createLayer + createNetwork, every layer */
+    "truth", "onlyforward", "stopbackward", "dontsave", "dontload", "numload",
+    "dontloadscales", "learning_rate", "smooth", "clip", "dont_update", "burnin_update",
+    "train_only_bn", NULL};
+static const char *const CONV_KEYS[] = {
+    "filters", "groups", "size", "stride", "stride_x", "stride_y", "dilation", "antialiasing",
+    "pad", "padding", "activation", "assisted_excitation", "share_index", "batch_normalize",
+    "cbn", "binary", "xnor", "bin_output", "sway", "rotate", "stretch", "stretch_sway",
+    "flipped", "dot", "angle", "grad_centr", "reverse", "coordconv", "stream", "wait_stream",
+    NULL};
+static const char *const CONN_KEYS[] = {"output", "activation", "batch_normalize", NULL};
+static const char *const MAXPOOL_KEYS[] = {
+    "stride", "stride_x", "stride_y", "size", "padding", "maxpool_depth", "out_channels",
+    "antialiasing", "maxpool_zero_nonmax", NULL};
+static const char *const DROPOUT_KEYS[] = {
+    "probability", "dropblock", "dropblock_size_rel", "dropblock_size_abs", NULL};
+static const char *const SOFTMAX_KEYS[] = {
+    "groups", "temperature", "spatial", "noloss", "tree", NULL};
+static const char *const NO_KEYS[] = {NULL};
+
+static int in_list(const char *const *l, const char *k)
+{
+    for (; *l; ++l)
+        if (!strcmp(*l, k)) return 1;
+    return 0;
+}
+
+static void report_unused(const cfg_group *g, const char *const *own, int layer)
+{
+    for (int i = 0; i < g->nkv; ++i)
+        if (!in_list(own, g->key[i]) && !(layer && in_list(LAYER_KEYS, g->key[i])))
+            fprintf(stderr, "an_parse_cfg: unused field [%s] %s=%s\n", g->name, g->key[i],
+                    g->val[i]);
+}
+
+/* stride_x / stride_y as createConvolutional / createMaxPool resolve them
+ * (NetworkFactory.c:83-93, 545-546); a non-square stride is not built.
+ * Returns the stride or -1.                                                */
+static int square_stride(const cfg_group *g, int conv)
+{
+    const int stride = geti(g, "stride", 1);
+    int sx = geti(g, "stride_x", conv ? -1 : stride), sy = geti(g, "stride_y", conv ? -1 : stride);
+    if (conv && (sx < 1 || sy < 1)) {
+        if (sx < 1) sx = stride;
+        if (sy < 1) sy = stride;
+    }
+    if (sx != sy) {
+        fprintf(stderr, "an_parse_cfg: [%s] stride_x=%d stride_y=%d: non-square strides are "
+                        "not supported\n", g->name, sx, sy);
+        return -1;
+    }
+    return sx;
+}
+
+/* the createLayer / createNetwork options of layer `idx` */
+static int layer_options(an_network *net, int idx, const cfg_group *g, int conv)
+{
+    an_layer_options o;
+    o.stopbackward = geti(g, "stopbackward", 0);
+    o.onlyforward = geti(g, "onlyforward", 0);
+    o.dontload = geti(g, "dontload", 0);
+    o.dontloadscales = geti(g, "dontloadscales", 0);
+    o.flipped = conv ? geti(g, "flipped", 0) : 0;
+    o.learning_rate_scale = getf(g, "learning_rate", 1.f);
+    if (an_set_layer_options(net, idx, &o) != ACH_OK) {
+        fprintf(stderr, "an_parse_cfg: [%s] invalid layer options\n", g->name);
+        return -1;
     }
     return 0;
 }
@@ -213,7 +332,7 @@ static int parse_policy(an_network *net, const cfg_group *g)
     return 0;
 }
 
-an_network *an_parse_cfg(const char *path)
+an_network *an_parse_cfg_unfinalized(const char *path)
 {
     cfg_group *gs = NULL;
     int ng = 0;
@@ -230,7 +349,13 @@ an_network *an_parse_cfg(const char *path)
         if (subdivs <= 0) goto fail;
         batch /= subdivs;
         if (batch < 1) batch = 1;
+        if (unsupported(g, "time_steps", 1)) goto fail;
         const int h = geti(g, "height", 0), w = geti(g, "width", 0), c = geti(g, "channels", 0);
+        if (find(g, "inputs") && geti(g, "inputs", 0) != h * w * c) {
+            fprintf(stderr, "an_parse_cfg: [net] inputs must equal height*width*channels\n");
+            goto fail;
+        }
+        report_unused(g, NET_KEYS, 0);
         net = an_network_create(batch, h, w, c);
         if (!net) {
             fprintf(stderr, "an_parse_cfg: [net] needs height, width and channels\n");
@@ -243,13 +368,22 @@ an_network *an_parse_cfg(const char *path)
     for (int i = 1; i < ng; ++i) {
         const cfg_group *g = &gs[i];
         int rc;
+        int conv = 0;
         if (!strcmp(g->name, "convolutional") || !strcmp(g->name, "conv")) {
-            if (unsupported(g, "groups", 1) || unsupported(g, "dilation", 1) ||
-                unsupported(g, "xnor", 0) || unsupported(g, "binary", 0) ||
-                unsupported(g, "antialiasing", 0) || unsupported(g, "cbn", 0))
-                goto fail;
             const int size = geti(g, "size", 1);
-            const int stride = geti(g, "stride", 1);
+            conv = 1;
+            report_unused(g, CONV_KEYS, 1);
+            /* dilation is forced to 1 for 1x1 filters (NetworkFactory.c:97-98) */
+            if (unsupported(g, "groups", 1) || (size != 1 && unsupported(g, "dilation", 1)) ||
+                unsupported(g, "xnor", 0) || unsupported(g, "binary", 0) ||
+                unsupported(g, "bin_output", 0) || unsupported(g, "antialiasing", 0) ||
+                unsupported(g, "cbn", 0) || unsupported(g, "sway", 0) ||
+                unsupported(g, "rotate", 0) || unsupported(g, "stretch", 0) ||
+                unsupported(g, "stretch_sway", 0) || unsupported(g, "assisted_excitation", 0) ||
+                present_unsupported(g, "share_index"))
+                goto fail;
+            const int stride = square_stride(g, 1);
+            if (stride < 0) goto fail;
             int padding = geti(g, "padding", 0);
             if (geti(g, "pad", 0)) padding = size / 2;
             const char *an = find(g, "activation");
@@ -261,6 +395,7 @@ an_network *an_parse_cfg(const char *path)
             rc = an_add_convolutional(net, geti(g, "filters", 1), size, stride, padding, act,
                                       geti(g, "batch_normalize", 0));
         } else if (!strcmp(g->name, "connected") || !strcmp(g->name, "conn")) {
+            report_unused(g, CONN_KEYS, 1);
             const char *an = find(g, "activation");
             const int act = activation_id(an ? an : "logistic");
             if (act < 0) {
@@ -269,17 +404,25 @@ an_network *an_parse_cfg(const char *path)
             }
             rc = an_add_connected(net, geti(g, "output", 1), act, geti(g, "batch_normalize", 0));
         } else if (!strcmp(g->name, "maxpool") || !strcmp(g->name, "max")) {
+            report_unused(g, MAXPOOL_KEYS, 1);
             if (unsupported(g, "maxpool_depth", 0) || unsupported(g, "antialiasing", 0))
                 goto fail;
-            const int stride = geti(g, "stride", 1);
+            const int stride = square_stride(g, 0);
+            if (stride < 0) goto fail;
             const int size = geti(g, "size", stride);
             rc = an_add_maxpool(net, size, stride, geti(g, "padding", size - 1));
         } else if (!strcmp(g->name, "avgpool") || !strcmp(g->name, "avg")) {
+            report_unused(g, NO_KEYS, 1);
             rc = an_add_avgpool(net);
         } else if (!strcmp(g->name, "dropout")) {
+            report_unused(g, DROPOUT_KEYS, 1);
             if (unsupported(g, "dropblock", 0)) goto fail;
             rc = an_add_dropout(net, getf(g, "probability", .2f));
         } else if (!strcmp(g->name, "softmax") || !strcmp(g->name, "soft")) {
+            report_unused(g, SOFTMAX_KEYS, 1);
+            if (unsupported(g, "spatial", 0) || unsupported(g, "noloss", 0) ||
+                present_unsupported(g, "tree"))
+                goto fail;
             rc = an_add_softmax(net, geti(g, "groups", 1), getf(g, "temperature", 1.f));
         } else {
             fprintf(stderr, "an_parse_cfg: layer type [%s] is not supported\n", g->name);
@@ -290,10 +433,7 @@ an_network *an_parse_cfg(const char *path)
                     i, rc);
             goto fail;
         }
-    }
-    if (an_finalize(net) != ACH_OK) {
-        fprintf(stderr, "an_parse_cfg: finalize failed\n");
-        goto fail;
+        if (layer_options(net, rc, g, conv)) goto fail;
     }
     free(gs);
     return net;
@@ -301,4 +441,16 @@ fail:
     free(gs);
     an_free(net);
     return NULL;
+}
+
+an_network *an_parse_cfg(const char *path)
+{
+    an_network *net = an_parse_cfg_unfinalized(path);
+    if (!net) return NULL;
+    if (an_finalize(net) != ACH_OK) {
+        fprintf(stderr, "an_parse_cfg: finalize failed\n");
+        an_free(net);
+        return NULL;
+    }
+    return net;
 }

@@ -70,7 +70,6 @@ struct an_network {
      * a max-pool applies the previous conv layer's activation gradient to
      * the delta it writes, and that layer skips its own pass             */
     int in_chain;
-    int in_chain_fwd;              /* the same for an_forward's loop      */
     void *ev_joined;
     ach_filter_job *jobs;          /* one per conv layer                    */
     int njobs;
@@ -85,6 +84,10 @@ struct an_network {
     uint32_t *d_iter;
     /* host copies of initial parameters until finalize */
     float **init_w;
+    /* some layer sets stopbackward / onlyforward / a learning-rate scale, or
+     * is frozen (train = 0): updates then run layer by layer after the
+     * backward loop instead of the flat or early forms                     */
+    int layer_opts;
 };
 
 /* ---- randUniform over glibc rand() (DnnUtils.c:196-209) ------------------- */
@@ -152,6 +155,8 @@ static an_layer *push_layer(an_network *net)
         l->c = p->out_c;
     }
     l->inputs = l->h * l->w * l->c;
+    l->train = 1;
+    l->learning_rate_scale = 1.f;
     net->layers[net->n] = l;
     net->init_w[net->n] = NULL;
     return l;
@@ -350,14 +355,6 @@ int an_add_connected(an_network *net, int outputs, int activation, int batch_nor
 /* ======================================================================== */
 /* Max-pool: MaxPoolLayer.c:237-272 / :318-331, defaults from createMaxPool
  * (NetworkFactory.c:543-570: padding = size-1 unless given).              */
-/* the dropout layer right after a max-pool, sharing its output and delta */
-static an_layer *dropout_after(an_network *net, const an_layer *l)
-{
-    if (l->index + 1 >= net->n) return NULL;
-    an_layer *d = net->layers[l->index + 1];
-    return d->type == AN_DROPOUT && d->shares_prev ? d : NULL;
-}
-
 /* the conv layer whose delta a max-pool's input gradient is, when the pool
  * applies that layer's activation gradient (whole backward loop only)    */
 static an_layer *pool_act_target(an_network *net, const an_layer *l, const float *delta)
@@ -369,25 +366,8 @@ static an_layer *pool_act_target(an_network *net, const an_layer *l, const float
     return NULL;
 }
 
-/* In the whole loops a dropout layer after a max-pool runs inside the pool's
- * kernels (its forward skips, its backward leaves the mask to the pool)   */
-static int pool_fuses_dropout_bwd(an_network *net, const an_layer *l)
-{
-    if (!net->in_chain || !dropout_after(net, l) || l->index == 0) return 0;
-    return pool_act_target(net, l, net->layers[l->index - 1]->delta) == NULL;
-}
-
 static int maxpool_forward(an_network *net, an_layer *l, an_state st)
 {
-    an_layer *d = st.train && net->in_chain_fwd ? dropout_after(net, l) : NULL;
-    if (d) {
-        d->drop_fused = 1;
-        return ach_maxpool_fwd_dropout(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride,
-                                       l->pad, l->output, l->indexes, d->probability,
-                                       net->dropout_seed, net->dropout_step,
-                                       net->recording ? net->d_iter : NULL, (uint32_t)d->index,
-                                       net->stream);
-    }
     return ach_maxpool_fwd(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride, l->pad,
                            l->output, l->indexes, net->stream);
 }
@@ -395,14 +375,6 @@ static int maxpool_forward(an_network *net, an_layer *l, an_state st)
 static int maxpool_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
-    if (pool_fuses_dropout_bwd(net, l)) {
-        const an_layer *d = dropout_after(net, l);
-        return ach_maxpool_bwd_dropout(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size,
-                                       l->stride, l->pad, st.delta, 0, d->probability,
-                                       net->dropout_seed, net->dropout_step,
-                                       net->recording ? net->d_iter : NULL, (uint32_t)d->index,
-                                       net->stream);
-    }
     /* the only contribution to the previous delta, which the reference
      * zeroes in forward: write the sums instead of adding to zeros.  In the
      * whole backward loop, when that delta is a plain conv layer's own (no
@@ -476,10 +448,6 @@ int an_add_avgpool(an_network *net)
  * (net->d_iter), so every replay of it draws its own masks.               */
 static int dropout_forward(an_network *net, an_layer *l, an_state st)
 {
-    if (l->drop_fused) { /* applied by the max-pool before it */
-        l->drop_fused = 0;
-        return ACH_OK;
-    }
     if (!st.train) return ACH_OK;
     const size_t n = (size_t)l->batch * l->inputs;
     if (net->recording)
@@ -492,9 +460,6 @@ static int dropout_forward(an_network *net, an_layer *l, an_state st)
 static int dropout_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
-    const an_layer *p = net->layers[l->index - 1];  /* dropout is never first */
-    if (p->type == AN_MAXPOOL && pool_fuses_dropout_bwd(net, p))
-        return ACH_OK; /* the max-pool's backward applies the mask */
     const size_t n = (size_t)l->batch * l->inputs;
     if (net->recording)
         return ach_dropout_bwd_dev(st.delta, n, l->probability, net->dropout_seed, net->d_iter,
@@ -768,11 +733,63 @@ static void layout(an_network *net, bump *b)
     net->d_iter = (uint32_t *)take(b, sizeof(uint32_t));
 }
 
+int an_set_layer_options(an_network *net, int layer, const an_layer_options *opt)
+{
+    an_layer *l = an_get_layer(net, layer);
+    if (!l || !opt || net->finalized) return ACH_EINVAL;
+    if (opt->flipped && l->type != AN_CONVOLUTIONAL) return ACH_EINVAL;
+    l->stopbackward = opt->stopbackward ? 1 : 0;
+    l->onlyforward = opt->onlyforward ? 1 : 0;
+    l->dontload = opt->dontload ? 1 : 0;
+    l->dontloadscales = opt->dontloadscales ? 1 : 0;
+    l->flipped = opt->flipped ? 1 : 0;
+    l->learning_rate_scale = opt->learning_rate_scale;
+    return ACH_OK;
+}
+
+int an_get_layer_options(const an_network *net, int layer, an_layer_options *opt)
+{
+    if (!net || layer < 0 || layer >= net->n || !opt) return ACH_EINVAL;
+    const an_layer *l = net->layers[layer];
+    opt->stopbackward = l->stopbackward;
+    opt->onlyforward = l->onlyforward;
+    opt->dontload = l->dontload;
+    opt->dontloadscales = l->dontloadscales;
+    opt->flipped = l->flipped;
+    opt->learning_rate_scale = l->learning_rate_scale;
+    return ACH_OK;
+}
+
 int an_finalize(an_network *net)
 {
     if (!net || net->finalized || net->n == 0) return ACH_EINVAL;
     an_layer *last = net->layers[net->n - 1];
     net->classes = last->outputs;
+    /* the layers below the last stopbackward layer run forward only and are
+     * not updated (NetworkFactory.c:881-893, 981-991) */
+    int last_stop = -1;
+    for (int i = 0; i < net->n; ++i)
+        if (net->layers[i]->stopbackward) last_stop = i;
+    for (int k = 0; k < last_stop; ++k) {
+        net->layers[k]->onlyforward = 1;
+        net->layers[k]->train = 0;
+    }
+    /* a layer the backward loop skips writes no input delta: the layer
+     * below then reads the delta the forward zeroed (NNetwork.c:388-391),
+     * so that delta joins the region zeroed every forward pass           */
+    for (int i = last_stop + 1; i < net->n; ++i) {
+        const an_layer *l = net->layers[i];
+        if (!l->onlyforward || l->shares_prev || i == 0) continue;
+        int j = i - 1;
+        while (j > 0 && net->layers[j]->shares_prev) --j;
+        net->layers[j]->zero_delta = 1;
+    }
+    net->layer_opts = 0;
+    for (int i = 0; i < net->n; ++i) {
+        const an_layer *l = net->layers[i];
+        if (l->stopbackward || l->onlyforward || !l->train || l->learning_rate_scale != 1.f)
+            net->layer_opts = 1;
+    }
     /* deltas the next layer accumulates into (+=) must start at zero:
      * avgpool / softmax backward add into their input delta.  Max-pool
      * backward writes its input delta outright (accumulate = 0), which is
@@ -962,7 +979,6 @@ int an_forward(an_network *net, int train)
     AN_CHECK(ach_conv_prepare_filters(net->njobs, net->jobs, net->stream));
     if (train && net->zero_floats)
         AN_CHECK(ach_fill(net->zero_region, net->zero_floats, 0.f, net->stream));
-    net->in_chain_fwd = 1;
     int rc = ACH_OK;
     for (int i = 0; i < net->n && rc == ACH_OK; ++i) {
         an_layer *l = net->layers[i];
@@ -970,8 +986,6 @@ int an_forward(an_network *net, int train)
         rc = l->forward(net, l, st);
         st.input = l->output;
     }
-    net->in_chain_fwd = 0;
-    for (int i = 0; i < net->n; ++i) net->layers[i]->drop_fused = 0;
     return rc;
 }
 
@@ -1001,6 +1015,8 @@ int an_backward(an_network *net)
     int rc = ACH_OK;
     for (int i = net->n - 1; i >= 0 && rc == ACH_OK; --i) {
         an_layer *l = net->layers[i];
+        if (l->stopbackward) break; /* NNetwork.c:648-651 */
+        if (l->onlyforward) continue;
         rc = l->backward(net, l, backward_state(net, i));
     }
     net->in_chain = 0;
@@ -1042,6 +1058,17 @@ int an_layer_backward(an_network *net, int i)
 static int update_at_rate(an_network *net, float rate)
 {
     const int batch = net->batch * net->subdivisions;
+    if (net->layer_opts) {
+        /* layer by layer: frozen layers skip, the rest at rate * their scale
+         * (updateCPU NNetwork.c:667-680; ConvolutionalLayer.c:959-960) */
+        for (int i = 0; i < net->n; ++i) {
+            an_layer *l = net->layers[i];
+            if (l->type != AN_CONVOLUTIONAL || !l->train) continue;
+            AN_CHECK(conv_update(net, l, batch, rate * l->learning_rate_scale, net->momentum,
+                                 net->decay));
+        }
+        return ACH_OK;
+    }
     const float a1 = -net->decay * batch;
     const float a2 = rate / batch;
     AN_CHECK(ach_sgd_update(net->nweights_total, net->wflat, net->vflat, a1, a2, net->momentum,
@@ -1119,12 +1146,14 @@ static int enqueue_step(an_network *net, int update, float rate)
 {
     AN_CHECK(an_forward(net, 1));
     /* with an update, each layer's is enqueued by its backward (the join at
-     * the end of an_backward waits for them) */
-    net->early_update = update;
+     * the end of an_backward waits for them); with layer options some
+     * layers run no backward, so the updates follow the loop instead */
+    net->early_update = update && !net->layer_opts;
     net->early_rate = rate;
     const int rc = an_backward(net);
     net->early_update = 0;
     AN_CHECK(rc);
+    if (update && net->layer_opts) AN_CHECK(update_at_rate(net, rate));
     return net->recording ? ach_counter_add(net->d_iter, 1u, net->stream) : ACH_OK;
 }
 
@@ -1344,10 +1373,29 @@ int an_save_weights(an_network *net, const char *path)
     return rc;
 }
 
+/* ConvolutionalLayer.transposeMatrix (ConvolutionalLayer.c:443-453): a is
+ * rows x cols row-major on entry, cols x rows on return.                  */
+static int transpose_host(float *a, int rows, int cols)
+{
+    float *t = (float *)malloc(sizeof(float) * (size_t)rows * cols);
+    if (!t) return ACH_EINVAL;
+    for (int x = 0; x < rows; ++x)
+        for (int y = 0; y < cols; ++y) t[(size_t)y * rows + x] = a[(size_t)x * cols + y];
+    memcpy(a, t, sizeof(float) * (size_t)rows * cols);
+    free(t);
+    return ACH_OK;
+}
+
 /* Reads as the reference does: a version >= 0.2 header carries a 64-bit
  * seen (older files none); layers are filled in order until the file ends,
  * a short array keeps the values it read (the rest unchanged) with a
- * warning.  Sets seen and the iteration (seen / batch).                     */
+ * warning.  Sets seen and the iteration (seen / batch).  A dontload layer
+ * is skipped without reading (NNetwork.c:93-94), a dontloadscales layer
+ * reads no BN arrays (ConvolutionalLayer.c:467), a flipped layer's weights
+ * are transposed from [C*k*k][n] after the read (ConvolutionalLayer.c:
+ * 483-485), and a header with major or minor above 1000 transposes the
+ * weights of connected layers from [inputs][outputs] (darknet's
+ * load_connected_weights; NNetwork.c:90 computes the flag).               */
 int an_load_weights(an_network *net, const char *path)
 {
     if (!net || !net->finalized || !path) return ACH_EINVAL;
@@ -1369,6 +1417,7 @@ int an_load_weights(an_network *net, const char *path)
         }
         net->seen = seen;
     }
+    const int transpose = hdr[0] > 1000 || hdr[1] > 1000;
     net->cur_iteration = (int)(net->seen / ((uint64_t)net->batch * net->subdivisions));
     drop_graph(net); /* the recorded step's device step index is stale */
     int rc = ACH_OK;
@@ -1376,11 +1425,15 @@ int an_load_weights(an_network *net, const char *path)
     size_t host_cap = 0;
     for (int i = 0; i < net->n && rc == ACH_OK && !feof(fp); ++i) {
         an_layer *l = net->layers[i];
-        if (l->type != AN_CONVOLUTIONAL) continue;
+        if (l->type != AN_CONVOLUTIONAL || l->dontload) continue;
         float *ptr[5];
         size_t cnt[5];
         const int na = conv_param_arrays(l, ptr, cnt);
         for (int a = 0; a < na && rc == ACH_OK; ++a) {
+            const int is_w = ptr[a] == l->weights;
+            const int is_bn = ptr[a] == l->scales || ptr[a] == l->rolling_mean ||
+                              ptr[a] == l->rolling_variance;
+            if (is_bn && l->dontloadscales) continue;
             if (cnt[a] > host_cap) {
                 float *nh = (float *)realloc(host, cnt[a] * sizeof(float));
                 if (!nh) { rc = ACH_EINVAL; break; }
@@ -1391,6 +1444,25 @@ int an_load_weights(an_network *net, const char *path)
             if (got > 0 && got < cnt[a])
                 fprintf(stderr, "an_load_weights: unexpected end of weights file at layer %d\n",
                         i);
+            /* the flipped / transposed weights: whole-array transposes over
+             * what was read and, past a short read, the values kept */
+            const int fl = is_w && (l->connected ? transpose : l->flipped);
+            if (fl) {
+                if (got < cnt[a]) {
+                    float *keep = (float *)malloc(sizeof(float) * cnt[a]);
+                    if (!keep) { rc = ACH_EINVAL; break; }
+                    rc = ach_memcpy_d2h(keep, ptr[a], cnt[a] * sizeof(float), net->stream);
+                    if (rc == ACH_OK)
+                        memcpy(host + got, keep + got, (cnt[a] - got) * sizeof(float));
+                    free(keep);
+                    if (rc != ACH_OK) break;
+                }
+                /* conv: [C*k*k][n] -> [n][C*k*k]; connected: [inputs][outputs] */
+                rc = transpose_host(host, l->nweights / l->n, l->n);
+                if (rc == ACH_OK)
+                    rc = ach_memcpy_h2d(ptr[a], host, cnt[a] * sizeof(float), net->stream);
+                continue;
+            }
             if (got > 0) rc = ach_memcpy_h2d(ptr[a], host, got * sizeof(float), net->stream);
         }
     }

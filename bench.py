@@ -149,6 +149,16 @@ def aetcnn_check(rc, what):
     aetcnn.check(rc, what)
 
 
+def config1_inputs(rng, batch, ci, co, hw, k, p):
+    """Config 1 operands of one sweep layer: x ~ U[-1,1], w ~ N(0, 0.05),
+    dy ~ U[-1,1] (also the inputs of the config-1 parity tests)."""
+    oh = (hw + 2 * p - k) + 1
+    x = rng.uniform(-1, 1, (batch, ci, hw, hw)).astype(np.float32)
+    w = (rng.standard_normal((co, ci, k, k)) * 0.05).astype(np.float32)
+    dy = rng.uniform(-1, 1, (batch, co, oh, oh)).astype(np.float32)
+    return x, w, dy
+
+
 def sweep_phase(aetcnn, batch, reps):
     ops = aetcnn.ops()
     D = aetcnn.DeviceArray
@@ -160,10 +170,9 @@ def sweep_phase(aetcnn, batch, reps):
     for (ci, co, hw, k, p) in SWEEP:
         d = aetcnn.ConvDesc(batch, ci, hw, hw, co, k, 1, p)
         oh = (hw + 2 * p - k) + 1
-        x = D.from_numpy(rng.uniform(-1, 1, (batch, ci, hw, hw)).astype(np.float32))
-        w = D.from_numpy((rng.standard_normal((co, ci, k, k)) * 0.05).astype(np.float32))
+        xh, wh, dyh = config1_inputs(rng, batch, ci, co, hw, k, p)
+        x, w, dy = D.from_numpy(xh), D.from_numpy(wh), D.from_numpy(dyh)
         y = D((batch, co, oh, oh))
-        dy = D.from_numpy(rng.uniform(-1, 1, (batch, co, oh, oh)).astype(np.float32))
         dx = D((batch, ci, hw, hw))
         dw = D((co, ci, k, k))
         dw.zero()
@@ -234,6 +243,29 @@ def roofline_phase(aetcnn, batch, reps):
 
 BW_SHAPE = (512, 128, 32, 32)  # config 2: x ~ N(0,1), S = 256 MiB per tensor
 SGD_PARAMS = 60_000_000        # config 2: SGD over a 60 M-parameter flat buffer
+SGD_HYPER = (0.1, 0.9, 5e-4, 512)  # learning rate, momentum, decay, batch
+SOFTMAX_SHAPE = (512, 1000)
+
+
+def config2_inputs(seed=2):
+    """The host arrays of config 2 (also the inputs of its parity tests):
+    x and the BN / leaky gradient ~ N(0,1) over [512][128][32][32], the
+    2x2 max-pool output gradient, SGD weights / momenta over 60 M
+    parameters, 512 x 1000 logits with one-hot labels."""
+    B, Cc, H, W = BW_SHAPE
+    n = B * Cc * H * W
+    rng = np.random.default_rng(seed)
+    out = dict(x=rng.standard_normal(n, dtype=np.float32),
+               delta=rng.standard_normal(n, dtype=np.float32))
+    out["pool_delta"] = rng.standard_normal(n // 4, dtype=np.float32)
+    out["sgd_w"] = rng.standard_normal(SGD_PARAMS, dtype=np.float32) * np.float32(0.05)
+    out["sgd_v"] = rng.standard_normal(SGD_PARAMS, dtype=np.float32) * np.float32(0.01)
+    SB, SK = SOFTMAX_SHAPE
+    out["logits"] = rng.standard_normal(SB * SK, dtype=np.float32)
+    truth = np.zeros((SB, SK), np.float32)
+    truth[np.arange(SB), rng.integers(0, SK, SB)] = 1
+    out["truth"] = truth
+    return out
 
 
 def bandwidth_phase(aetcnn, reps):
@@ -253,10 +285,9 @@ def bandwidth_phase(aetcnn, reps):
     HW = H * W
     stream = C.c_void_p()
     aetcnn.check(ops.ach_stream_create(C.byref(stream)), "stream")
-    rng = np.random.default_rng(2)
-    x = D.from_numpy(rng.standard_normal(n, dtype=np.float32))
-    delta0 = rng.standard_normal(n, dtype=np.float32)
-    delta = D.from_numpy(delta0)
+    host = config2_inputs()
+    x = D.from_numpy(host["x"])
+    delta = D.from_numpy(host["delta"])
     out = D(n)
     chan = [D.from_numpy(np.full(Cc, v, np.float32)) for v in (1.0, 0.0, 0, 0, 0, 0, 0)]
     scales, biases, mean, var, rmean, rvar, supd = chan
@@ -265,7 +296,7 @@ def bandwidth_phase(aetcnn, reps):
     OH, OW = H // 2, W // 2
     pout = D(B * Cc * OH * OW)
     pidx = D(B * Cc * OH * OW, np.int32)
-    pdelta = D.from_numpy(rng.standard_normal(B * Cc * OH * OW, dtype=np.float32))
+    pdelta = D.from_numpy(host["pool_delta"])
     LEAKY, LINEAR = aetcnn.LEAKY, aetcnn.LINEAR
     rows = []
     # cache flush: a read-only reduction over 1 GiB (a write pass would leave
@@ -306,19 +337,19 @@ def bandwidth_phase(aetcnn, reps):
                                         0, stream)), 1.5 * S)
     for a in (x, delta, out, ws, pout, pidx, pdelta, *chan):
         a.free()
+    del host["x"], host["delta"], host["pool_delta"]
     P = SGD_PARAMS
-    w = D.from_numpy(rng.standard_normal(P, dtype=np.float32) * 0.05)
-    v = D.from_numpy(rng.standard_normal(P, dtype=np.float32) * 0.01)
+    w = D.from_numpy(host.pop("sgd_w"))
+    v = D.from_numpy(host.pop("sgd_v"))
+    lr, mom, decay, batch = SGD_HYPER
     run("sgd_update (60 M params)",
-        lambda: chk(ops.ach_sgd_update(P, w.ptr, v.ptr, -5e-4 * 512, 0.1 / 512, 0.9, stream)),
+        lambda: chk(ops.ach_sgd_update(P, w.ptr, v.ptr, -decay * batch, lr / batch, mom, stream)),
         16.0 * P)
     w.free()
     v.free()
-    SB, SK = 512, 1000
-    logits = D.from_numpy(rng.standard_normal(SB * SK, dtype=np.float32))
-    truth = np.zeros((SB, SK), np.float32)
-    truth[np.arange(SB), rng.integers(0, SK, SB)] = 1
-    dtruth = D.from_numpy(truth)
+    SB, SK = SOFTMAX_SHAPE
+    logits = D.from_numpy(host["logits"])
+    dtruth = D.from_numpy(host["truth"])
     prob, sdelta, err, cost = D(SB * SK), D(SB * SK), D(SB * SK), D(4)
     sws = ops.ach_softmax_workspace(SB, 1)
     swsb = D(sws // 4 + 64)

@@ -82,9 +82,17 @@ struct an_layer {
     float *cost;            /* device scalar: sum(loss)                    */
     /* common */
     float *output, *delta;
+    /* per-layer options (NLayer.h:115-125; NetworkFactory.c:656-663,
+     * 926-935, 981-991): stopbackward ends the backward loop at this layer,
+     * onlyforward skips its backward, train = 0 skips its update (set for
+     * every layer below the last stopbackward layer), learning_rate_scale
+     * multiplies the rate of its update, dontload / dontloadscales /
+     * flipped shape how a .weights file is read into it                   */
+    int stopbackward, onlyforward, train;
+    int dontload, dontloadscales, flipped;
+    float learning_rate_scale;
     int zero_delta;         /* delta is accumulated into by the next layer */
     int grad_applied;       /* this step's f'(y) already applied to delta   */
-    int drop_fused;         /* dropout: this forward ran inside the max-pool */
     int (*forward)(an_network *net, an_layer *l, an_state st);
     int (*backward)(an_network *net, an_layer *l, an_state st);
     int (*update)(an_network *net, an_layer *l, int batch, float lr, float momentum,
@@ -142,6 +150,29 @@ float an_current_rate(an_network *net);
  * runs one minibatch and updates after every subdivisions-th, with update
  * batch = batch * subdivisions (NNetwork.c:667-680, 762-805).           */
 int an_set_subdivisions(an_network *net, int subdivisions);
+/* The per-layer cfg options the reference's CPU path acts on (NLayer.h:
+ * 115-125, read by NetworkFactory.createLayer / createNetwork,
+ * NetworkFactory.c:656-663, 926-935):
+ *   stopbackward        NNetwork.backward (NNetwork.c:648) stops before this
+ *                       layer's backward; an_finalize also freezes every
+ *                       layer below the last such layer (train = 0,
+ *                       onlyforward = 1; NetworkFactory.c:981-991)
+ *   onlyforward         the backward loop skips the layer (NNetwork.c:650)
+ *   learning_rate_scale the layer's update runs at rate * scale
+ *                       (ConvolutionalLayer.c:960)
+ *   dontload            an_load_weights skips the layer without reading its
+ *                       arrays (NNetwork.c:93-94)
+ *   dontloadscales      ... reads no scales / rolling mean / rolling
+ *                       variance for it (ConvolutionalLayer.c:467)
+ *   flipped             the weights read are transposed from [C*k*k][n] to
+ *                       [n][C*k*k] (ConvolutionalLayer.c:483-485, 443-453)
+ * Defaults 0 and scale 1.  Set before an_finalize (ACH_EINVAL after).    */
+typedef struct {
+    int stopbackward, onlyforward, dontload, dontloadscales, flipped;
+    float learning_rate_scale;
+} an_layer_options;
+int an_set_layer_options(an_network *net, int layer, const an_layer_options *opt);
+int an_get_layer_options(const an_network *net, int layer, an_layer_options *opt);
 /* allocate device memory, upload initial parameters, size the workspace   */
 int an_finalize(an_network *net);
 void an_free(an_network *net);
@@ -151,9 +182,24 @@ void an_free(an_network *net);
  * step/scale/steps/scales/gamma/max_batches; [convolutional] filters/size/stride/pad/
  * padding/activation/batch_normalize; [connected] output/activation/
  * batch_normalize (darknet's keys, an_add_connected); [maxpool] size/stride/
- * padding; [avgpool]; [dropout] probability; [softmax] groups/temperature.  Returns
- * NULL on error (message on stderr).  The network is finalized.            */
+ * padding; [avgpool]; [dropout] probability; [softmax] groups/temperature;
+ * in every layer section the options of an_layer_options (stopbackward,
+ * onlyforward, dontload, dontloadscales, learning_rate, and flipped for
+ * [convolutional]); stride_x / stride_y when they give one square stride.
+ * Keys the reference reads that change its CPU training step but this
+ * build does not implement (groups != 1, dilation != 1, xnor, binary,
+ * bin_output, antialiasing, cbn, deformable sway / rotate / stretch,
+ * assisted_excitation, share_index, stride_x != stride_y, maxpool_depth,
+ * dropblock, softmax spatial / noloss / tree, [net] time_steps != 1) make
+ * the parse fail with a message; keys the reference reads but its CPU path
+ * never acts on (e.g. dontsave, clip, train_only_bn, dont_update, adam,
+ * the augmentation keys) are accepted; keys the reference does not know
+ * are reported on stderr as unused.  Returns NULL on error (message on
+ * stderr).  The network is finalized.                                     */
 an_network *an_parse_cfg(const char *path);
+/* The same without an_finalize (host only: no device memory is touched);
+ * the caller may inspect or change the layers, then finalizes.            */
+an_network *an_parse_cfg_unfinalized(const char *path);
 
 /* ---- darknet .weights files (NNetwork.c:64-151, ConvolutionalLayer.c:422-486)
  * header int32 {0, 2, 5} + uint64 seen, then per convolutional layer:
@@ -161,7 +207,12 @@ an_network *an_parse_cfg(const char *path);
  * weights (float32); per connected layer darknet's order: biases, weights,
  * [scales, rolling_mean, rolling_variance].  Load accepts older headers without seen and stops
  * quietly at end of file, as the reference does; it sets seen and the
- * iteration.  The network must be finalized.                              */
+ * iteration.  It honours the layer options dontload, dontloadscales and
+ * flipped as NNetwork.loadWeights / ConvolutionalLayer.loadWeights do, and
+ * a header whose major or minor exceeds 1000 (darknet's transposed files)
+ * transposes connected layers' weights from [inputs][outputs] (darknet's
+ * load_connected_weights; the reference computes this flag but loads no
+ * connected layers, NNetwork.c:90).  The network must be finalized.        */
 int an_save_weights(an_network *net, const char *path);
 int an_load_weights(an_network *net, const char *path);
 

@@ -79,14 +79,18 @@ int ach_gemm(int TA, int TB, int M, int N, int K, float ALPHA,
              const float *A, int lda, const float *B, int ldb,
              float BETA, float *C, int ldc, ach_stream_t stream);
 
-/* ---- im2col / col2im for one image (Im2Col.c:65-103, 155-192) ---------- */
+/* ---- im2col / col2im for one image (Im2Col.c:65-103, 155-192; the
+ * signatures of Im2Col.h:10-15, 24-28, dilation included: window taps at
+ * k*dilation, output size (in + 2*pad - (dilation*(k-1)+1))/stride + 1).
+ * Dilation below 1 returns ACH_EINVAL.  (The conv entry points below take
+ * no dilation: the cfg parser rejects dilated convolutions.)              */
 int ach_im2col(const float *im, int channels, int height, int width,
                int kh, int kw, int ph, int pw, int sh, int sw,
-               float *col, ach_stream_t stream);
+               int dilation_h, int dilation_w, float *col, ach_stream_t stream);
 /* col2im zeroes `im` first, as the reference does (Im2Col.c:162)          */
 int ach_col2im(const float *col, int channels, int height, int width,
                int kh, int kw, int ph, int pw, int sh, int sw,
-               float *im, ach_stream_t stream);
+               int dilation_h, int dilation_w, float *im, ach_stream_t stream);
 
 /* ---- convolution (ConvolutionalLayer.c:684-803, 906-947) ---------------- */
 typedef struct {
@@ -239,12 +243,6 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w,
 int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
                     int batch, int c, int h, int w, int size, int stride, int padding,
                     float *delta_in, int accumulate, ach_stream_t stream);
-/* ach_maxpool_bwd, then delta_in *= f'(y_in) with the previous layer's
- * output y_in and activation act_in (Activation.gradientArray,
- * Activation.c:233-239, the first step of that layer's backward,
- * ConvolutionalLayer.c:863-948) in the same pass: the same values, bit for
- * bit, as ach_maxpool_bwd + ach_gradient.  Used when the pool's input
- * gradient is that layer's whole delta.                                   */
 /* A dropout layer that follows the max-pool and shares its output
  * (DropoutLayer.c:55-86, NetworkFactory.c:644-650), applied by the pool:
  * the forward writes the masked output (ach_maxpool_fwd + ach_dropout_fwd on
@@ -252,7 +250,9 @@ int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
  * delta_out + ach_maxpool_bwd; delta_out itself may be left unmasked) --
  * the same values bit for bit.  iter_ptr, when set, supplies the step index
  * from device memory (as ach_dropout_fwd_dev).  Fused into the 2x2 / stride
- * 2 kernels; other windows run the two steps inside the call.            */
+ * 2 kernels; other windows run the two steps inside the call.  (The network
+ * loops of aetcnn_net.h run pool and dropout as separate layers, as the
+ * reference does, so the shared delta is masked in place.)                */
 int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w,
                             int size, int stride, int padding, float *out, int32_t *indexes,
                             float probability, uint64_t seed, uint32_t iter,
@@ -262,6 +262,12 @@ int ach_maxpool_bwd_dropout(float *delta_out, const int32_t *indexes,
                             float *delta_in, int accumulate, float probability, uint64_t seed,
                             uint32_t iter, const uint32_t *iter_ptr, uint32_t layer,
                             ach_stream_t stream);
+/* ach_maxpool_bwd, then delta_in *= f'(y_in) with the previous layer's
+ * output y_in and activation act_in (Activation.gradientArray,
+ * Activation.c:233-239, the first step of that layer's backward,
+ * ConvolutionalLayer.c:863-948) in the same pass: the same values, bit for
+ * bit, as ach_maxpool_bwd + ach_gradient.  Used when the pool's input
+ * gradient is that layer's whole delta.                                   */
 int ach_maxpool_bwd_act(const float *delta_out, const int32_t *indexes,
                         int batch, int c, int h, int w, int size, int stride, int padding,
                         float *delta_in, int accumulate, const float *y_in, int act_in,

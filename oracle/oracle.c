@@ -672,6 +672,12 @@ typedef struct {
     float *loss;
     float cost;
     float *output, *delta;
+    /* NLayer options (NLayer.h:115-121): NNetwork.backward stops before a
+     * stopbackward layer and skips an onlyforward one (NNetwork.c:648-651);
+     * updateCPU skips train == 0 (NNetwork.c:673-674); the conv update runs
+     * at rate * learning_rate_scale (ConvolutionalLayer.c:960)            */
+    int stopbackward, onlyforward, train;
+    float learning_rate_scale;
 } or_layer;
 
 struct or_net {
@@ -739,6 +745,8 @@ static or_layer *push_layer(or_net *net)
         l->c = p->out_c;
     }
     l->inputs = l->h * l->w * l->c;
+    l->train = 1;
+    l->learning_rate_scale = 1;
     return l;
 }
 
@@ -951,8 +959,26 @@ float or_net_rate(or_net *net)
                       net->steps, net->scales);
 }
 
+void or_net_set_layer_options(or_net *net, int i, int stopbackward, int onlyforward,
+                              float learning_rate_scale)
+{
+    or_layer *l = &net->layers[i];
+    l->stopbackward = stopbackward;
+    l->onlyforward = onlyforward;
+    l->learning_rate_scale = learning_rate_scale;
+}
+
 int or_net_finalize(or_net *net)
 {
+    /* NetworkFactory.c:881-893, 981-991: every layer below the last
+     * stopbackward layer runs forward only and is not updated */
+    int last_stop = -1;
+    for (int i = 0; i < net->n; ++i)
+        if (net->layers[i].stopbackward) last_stop = i;
+    for (int k = 0; k < last_stop; ++k) {
+        net->layers[k].onlyforward = 1;
+        net->layers[k].train = 0;
+    }
     size_t ws = 0;
     for (int i = 0; i < net->n; ++i) {
         or_layer *l = &net->layers[i];
@@ -1153,7 +1179,11 @@ float or_net_forward_backward(or_net *net, const float *input, const float *trut
     net->seen += (uint64_t)net->batch;
     or_net_load(net, input, truth);
     for (int i = 0; i < net->n; ++i) or_net_layer_forward(net, i, 1);
-    for (int i = net->n - 1; i >= 0; --i) or_net_layer_backward(net, i);
+    for (int i = net->n - 1; i >= 0; --i) {
+        if (net->layers[i].stopbackward) break;
+        if (net->layers[i].onlyforward) continue;
+        or_net_layer_backward(net, i);
+    }
     return or_net_cost(net);
 }
 
@@ -1166,10 +1196,10 @@ void or_net_update(or_net *net)
     const float rate = or_net_rate(net);
     for (int i = 0; i < net->n; ++i) {
         or_layer *l = &net->layers[i];
-        if (l->type != L_CONV) continue;
+        if (l->type != L_CONV || !l->train) continue;
         or_conv_update(l->nweights, l->weights, l->weight_updates, l->n, l->biases,
-                       l->bias_updates, l->scales, l->scale_updates, update_batch, rate,
-                       net->momentum, net->decay);
+                       l->bias_updates, l->scales, l->scale_updates, update_batch,
+                       rate * l->learning_rate_scale, net->momentum, net->decay);
     }
 }
 

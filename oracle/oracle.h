@@ -182,6 +182,11 @@ void or_net_set_subdivisions(or_net *net, int subdivisions);
 float or_net_rate(or_net *net);
 uint64_t or_net_seen(const or_net *net);
 int  or_net_iteration(const or_net *net);
+/* NLayer options stopbackward / onlyforward / learning_rate_scale
+ * (NLayer.h:115-121); set before or_net_finalize, which freezes the layers
+ * below the last stopbackward layer (NetworkFactory.c:981-991)           */
+void or_net_set_layer_options(or_net *net, int layer, int stopbackward, int onlyforward,
+                              float learning_rate_scale);
 int  or_net_finalize(or_net *net);   /* allocates workspace */
 void or_net_free(or_net *net);
 /* one minibatch on host buffers: input [batch][c][h][w], truth

@@ -69,6 +69,7 @@ _SIGS = {
     "or_net_rate": (_f, [_vp]),
     "or_net_seen": (_u64, [_vp]),
     "or_net_iteration": (_i, [_vp]),
+    "or_net_set_layer_options": (None, [_vp, _i, _i, _i, _f]),
     "or_net_finalize": (_i, [_vp]),
     "or_net_free": (None, [_vp]),
     "or_net_train": (_f, [_vp, _vp, _vp]),
@@ -328,6 +329,11 @@ class OracleNet:
 
     def iteration(self):
         return self.L.or_net_iteration(self.h)
+
+    def set_layer_options(self, i, stopbackward=0, onlyforward=0, learning_rate_scale=1.0,
+                          **_):
+        self.L.or_net_set_layer_options(self.h, i, stopbackward, onlyforward,
+                                        learning_rate_scale)
 
     def finalize(self):
         assert self.L.or_net_finalize(self.h) == 0

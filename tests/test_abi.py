@@ -196,6 +196,10 @@ def test_argument_validation_without_device():
     assert ops.ach_maxpool_fwd(fake, 1, 1, 4, 4, 0, 2, 0, fake, None, None) == EINVAL
     assert ops.ach_bias_grad(fake, fake, 2, 4, 16, None, 0, None) == EWS
     assert ops.ach_conv_prepare_filters(0, None, None) == OK
+    # im2col / col2im take the reference's dilation arguments (>= 1)
+    for f in (ops.ach_im2col, ops.ach_col2im):
+        assert f(fake, 3, 8, 8, 3, 3, 1, 1, 1, 1, 1, 0, fake, None) == EINVAL
+        assert f(fake, 3, 8, 8, 3, 3, 1, 1, 1, 1, 5, 1, fake, None) == EINVAL  # window > input
     assert ops.ach_conv_bwd_data_prepared(C.byref(aetcnn.ConvDesc(2, 3, 9, 9, 8, 3, 2, 1)),
                                           fake, fake, fake, fake, fake, 1 << 20, None) == -4
     # operands at or above 2 GiB (32-bit buffer offsets): refused, never launched

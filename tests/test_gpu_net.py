@@ -284,7 +284,7 @@ def test_predict_matches_oracle(gpu, oracle, name, batch):
 
 
 @pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8)])
-def test_fused_predict_matches_oracle(gpu, oracle, name, batch):
+def test_fused_predict_matches_oracle(gpu, oracle, name, batch, tmp_path):
     """NNetwork.fuseConvBatchnorm then predict: the oracle's trained parameters
     are loaded into the GPU network, both sides fold; the folded filters and
     biases agree to 1 ulp, the fused predictions within 1e-4 with identical
@@ -316,8 +316,7 @@ def test_fused_predict_matches_oracle(gpu, oracle, name, batch):
     assert np.array_equal(p_gpu.argmax(1)[clear], p_ref.argmax(1)[clear])
     n_bias = sum(net.buffer(i, 4).size for i in conv_layers(onet))
     n_w = sum(net.buffer(i, 2).size for i in conv_layers(onet))
-    path = os.path.join(ROOT, "gpurun_out", "fused_%s.weights" % name)
-    os.makedirs(os.path.dirname(path), exist_ok=True)
+    path = str(tmp_path / ("fused_%s.weights" % name))
     net.save_weights(path)
     assert os.path.getsize(path) == 20 + 4 * (n_bias + n_w)
     os.remove(path)
@@ -522,3 +521,50 @@ def test_train_step_updates_like_separate_update(gpu, name, batch, steps):
             u, v = a.buffer(i, which), b.buffer(i, which)
             if u is not None:
                 assert np.array_equal(u.view(np.uint32), v.view(np.uint32)), (name, i, which)
+
+
+@pytest.mark.parametrize("name,batch,options", [
+    # learning-rate scale on the first conv, the second max-pool skipped in backward
+    ("tiny", 32, {0: dict(learning_rate_scale=0.5), 3: dict(onlyforward=1)}),
+    # stop at the first 256-filter conv (layers 0-4 frozen), the last dropout
+    # skipped in backward (no mask on its delta), a scaled last conv
+    ("darknet", 8, {5: dict(stopbackward=1), 13: dict(onlyforward=1),
+                    14: dict(learning_rate_scale=2.0)}),
+    # a dropout after a 2x2 max-pool skipped in backward: the pool must not
+    # apply its mask either
+    ("darknet", 8, {4: dict(onlyforward=1)}),
+])
+def test_layer_options_match_oracle(gpu, oracle, name, batch, options):
+    """stopbackward / onlyforward / learning_rate (NNetwork.c:648-651,
+    NetworkFactory.c:981-991, ConvolutionalLayer.c:960): three steps against
+    the oracle with the same options -- losses within 1e-3, parameters
+    within 1e-4, and the frozen layers exactly at their initial values."""
+    oracle.lib().or_set_gemm_parallel(1)
+    B, h, w, c = configs.dims(name, batch)
+    aetcnn.net_lib().an_rand_seed(1)
+    net = aetcnn.Network(B, h, w, c)
+    configs.build(net, name)
+    oracle.lib().or_rand_seed(1)
+    onet = oracle.OracleNet(B, h, w, c)
+    configs.build(onet, name)
+    for i, o in options.items():
+        net.set_layer_options(i, **o)
+        onet.set_layer_options(i, **o)
+    net.finalize()
+    onet.finalize()
+    stop = max([i for i, o in options.items() if o.get("stopbackward")], default=-1)
+    init = {i: net.buffer(i, 2).copy() for i in conv_layers(onet) if i < stop}
+    for step in range(3):
+        x, truth, _ = configs.synthetic_batch(name, 700 + step, batch)
+        l_gpu = net.train(x, truth)
+        l_ref = onet.train(x, truth)
+        assert abs(l_gpu - l_ref) <= 1e-3, (step, l_gpu, l_ref)
+        for i in conv_layers(onet):
+            for code in (2, 4, 6):
+                v = onet.buffer(i, code)
+                if v is not None and v.size:
+                    assert rel_err(net.buffer(i, code), v) < TOL, (step, i, code)
+    for i, w0 in init.items():
+        assert np.array_equal(net.buffer(i, 2), w0), i
+    net.close()
+    onet.close()

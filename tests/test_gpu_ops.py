@@ -58,23 +58,26 @@ def test_gemm(gpu, oracle, TA, TB, M, N, K):
         assert rel_err(got, ref) < 1e-5, (alpha, beta)
 
 
-@pytest.mark.parametrize("Cc,H,W,k,p,s", [(3, 7, 9, 3, 1, 1), (4, 12, 12, 5, 2, 2),
-                                          (2, 35, 35, 11, 0, 4), (6, 6, 6, 6, 0, 1),
-                                          (5, 8, 8, 1, 0, 1)])
-def test_im2col_col2im_bit_exact(gpu, oracle, Cc, H, W, k, p, s):
+@pytest.mark.parametrize("Cc,H,W,k,p,s,dl", [(3, 7, 9, 3, 1, 1, 1), (4, 12, 12, 5, 2, 2, 1),
+                                             (2, 35, 35, 11, 0, 4, 1), (6, 6, 6, 6, 0, 1, 1),
+                                             (5, 8, 8, 1, 0, 1, 1),
+                                             (3, 11, 9, 3, 2, 1, 2),   # dilated (Im2Col.c ext)
+                                             (2, 13, 13, 3, 3, 2, 3)])
+def test_im2col_col2im_bit_exact(gpu, oracle, Cc, H, W, k, p, s, dl):
     rng = np.random.default_rng(Cc * H + k)
     im = rng.standard_normal((Cc, H, W)).astype(np.float32)
-    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    ek = dl * (k - 1) + 1
+    OH, OW = (H + 2 * p - ek) // s + 1, (W + 2 * p - ek) // s + 1
     col_ref = np.zeros(Cc * k * k * OH * OW, np.float32)
-    oracle.lib().or_im2col(oracle.P(im), Cc, H, W, k, k, p, p, s, s, 1, 1, oracle.P(col_ref))
+    oracle.lib().or_im2col(oracle.P(im), Cc, H, W, k, k, p, p, s, s, dl, dl, oracle.P(col_ref))
     dim, dcol = dev(im), D(col_ref.shape)
-    check(gpu.ach_im2col(dim.ptr, Cc, H, W, k, k, p, p, s, s, dcol.ptr, None))
+    check(gpu.ach_im2col(dim.ptr, Cc, H, W, k, k, p, p, s, s, dl, dl, dcol.ptr, None))
     assert np.array_equal(dcol.numpy(), col_ref)
     col = rng.standard_normal(col_ref.shape).astype(np.float32)
     im_ref = np.zeros_like(im)
-    oracle.lib().or_col2im(oracle.P(col), Cc, H, W, k, k, p, p, s, s, 1, 1, oracle.P(im_ref))
+    oracle.lib().or_col2im(oracle.P(col), Cc, H, W, k, k, p, p, s, s, dl, dl, oracle.P(im_ref))
     dcol2, dim2 = dev(col), dev(np.full_like(im, 7.0))  # col2im must overwrite
-    check(gpu.ach_col2im(dcol2.ptr, Cc, H, W, k, k, p, p, s, s, dim2.ptr, None))
+    check(gpu.ach_col2im(dcol2.ptr, Cc, H, W, k, k, p, p, s, s, dl, dl, dim2.ptr, None))
     assert np.array_equal(dim2.numpy(), im_ref)
 
 

@@ -45,26 +45,31 @@ def test_gemm_parallel_is_bit_identical():
 
 
 # ---- im2col / col2im -----------------------------------------------------------
-@pytest.mark.parametrize("Cc,H,W,k,p,s", [(2, 5, 6, 3, 1, 1), (3, 9, 9, 5, 2, 2), (1, 11, 11, 11, 0, 4)])
-def test_im2col_index_map_and_col2im_adjoint(Cc, H, W, k, p, s):
+@pytest.mark.parametrize("Cc,H,W,k,p,s,dl", [(2, 5, 6, 3, 1, 1, 1), (3, 9, 9, 5, 2, 2, 1),
+                                             (1, 11, 11, 11, 0, 4, 1), (3, 11, 9, 3, 2, 1, 2),
+                                             (2, 13, 13, 3, 3, 2, 3)])
+def test_im2col_index_map_and_col2im_adjoint(Cc, H, W, k, p, s, dl):
+    """Exact index map (taps at k*dilation, Im2Col.c:65-103) and col2im as
+    its adjoint (Im2Col.c:155-192)."""
     rng = np.random.default_rng(k)
     im = rng.standard_normal((Cc, H, W)).astype(np.float32)
-    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    ek = dl * (k - 1) + 1
+    OH, OW = (H + 2 * p - ek) // s + 1, (W + 2 * p - ek) // s + 1
     col = np.zeros(Cc * k * k * OH * OW, np.float32)
-    O.lib().or_im2col(O.P(im), Cc, H, W, k, k, p, p, s, s, 1, 1, O.P(col))
+    O.lib().or_im2col(O.P(im), Cc, H, W, k, k, p, p, s, s, dl, dl, O.P(col))
     col = col.reshape(Cc, k, k, OH, OW)
     for c in range(Cc):
         for ki in range(k):
             for kj in range(k):
                 for oh in range(OH):
                     for ow in range(OW):
-                        ih, iw = oh * s - p + ki, ow * s - p + kj
+                        ih, iw = oh * s - p + ki * dl, ow * s - p + kj * dl
                         v = im[c, ih, iw] if 0 <= ih < H and 0 <= iw < W else 0.0
                         assert col[c, ki, kj, oh, ow] == v
     # col2im is the adjoint of im2col: <im2col(x), y> == <x, col2im(y)>
     y = rng.standard_normal(col.size).astype(np.float32)
     back = np.full((Cc, H, W), 9.0, np.float32)  # must be zeroed first
-    O.lib().or_col2im(O.P(y), Cc, H, W, k, k, p, p, s, s, 1, 1, O.P(back))
+    O.lib().or_col2im(O.P(y), Cc, H, W, k, k, p, p, s, s, dl, dl, O.P(back))
     lhs = float(np.dot(col.ravel().astype(np.float64), y.astype(np.float64)))
     rhs = float(np.dot(im.ravel().astype(np.float64), back.ravel().astype(np.float64)))
     assert abs(lhs - rhs) <= 1e-5 * max(1.0, abs(lhs))
