@@ -52,6 +52,20 @@ class LayerOptions(C.Structure):
                 ("dontloadscales", _i), ("flipped", _i), ("learning_rate_scale", _f)]
 
 
+class Augment(C.Structure):
+    """an_augment: the [net] augmentation keys (defaults: an_augment_defaults)"""
+    _fields_ = [("min_crop", _i), ("max_crop", _i), ("angle", _f), ("aspect", _f), ("hue", _f),
+                ("saturation", _f), ("exposure", _f), ("flip", _i)]
+
+    @classmethod
+    def defaults(cls, net_w, **kw):
+        a = cls()
+        net_lib().an_augment_defaults(C.byref(a), net_w)
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+
 class FilterJob(C.Structure):
     """ach_filter_job"""
     _fields_ = [("desc", ConvDesc), ("w", _vp), ("wt", _vp), ("wft", _vp)]
@@ -173,8 +187,19 @@ _NET = {
     "an_forward": (_i, [_vp, _i]),
     "an_predict": (_i, [_vp, _vp, _vp]),
     "an_fuse_conv_batchnorm": (_i, [_vp]),
-    "an_feeder_create_cifar": (_vp, [_vp, _vp, _i, _i, _u64, _i, _f]),
-    "an_feeder_create_synthetic": (_vp, [_vp, _i, _u64]),
+    "an_feeder_create_cifar": (_vp, [_vp, _vp, _i, _i, _u64, C.POINTER(Augment), _f]),
+    "an_feeder_create_synthetic": (_vp, [_vp, _i, _u64, C.POINTER(Augment)]),
+    "an_feeder_create_paths": (_vp, [_vp, C.c_char_p, _vp, _i, _i, _u64, C.POINTER(Augment),
+                                     _f]),
+    "an_augment_defaults": (None, [C.POINTER(Augment), _i]),
+    "an_cfg_augment": (_i, [C.c_char_p, C.POINTER(Augment), C.POINTER(_f)]),
+    "an_augment_image": (_i, [_vp, _i, _i, _i, C.POINTER(Augment), _u64, _u64, _i, _vp]),
+    "an_image_rotate_crop": (None, [_vp, _i, _i, _i, _f, _f, _i, _i, _f, _f, _f, _vp]),
+    "an_image_flip": (None, [_vp, _i, _i, _i]),
+    "an_image_distort": (None, [_vp, _i, _i, _f, _f, _f]),
+    "an_image_resize": (None, [_vp, _i, _i, _i, _i, _i, _vp]),
+    "an_image_load": (_i, [C.c_char_p, _i, _i, _i, _vp]),
+    "an_label_from_path": (_i, [C.c_char_p, _vp, _i]),
     "an_feeder_next": (_i, [_vp]),
     "an_feeder_served": (_u64, [_vp]),
     "an_feeder_sample": (_u64, [_u64, _u64, _i, _i]),
@@ -523,22 +548,37 @@ def top_k(a: np.ndarray, k: int) -> np.ndarray:
     return idx
 
 
+def _cstrings(items):
+    return (C.c_char_p * len(items))(*[os.fsencode(p) for p in items])
+
+
 class Feeder:
     """Input pipeline (an_feeder_*): worker threads fill pinned host batches,
     next() makes the next one the network's input (copy overlapped with the
-    previous step)."""
+    previous step).  Source: an image list file with labels from path
+    substrings (paths_list + labels), CIFAR-10 binary batches (cifar_files)
+    or synthetic pixels; augment (an Augment) applies the reference's
+    training-time augmentation to every image."""
 
     def __init__(self, net: "Network", cifar_files=None, threads: int = 8, seed: int = 0,
-                 flip: bool = False, label_smooth_eps: float = 0.0):
+                 augment: Optional[Augment] = None, label_smooth_eps: float = 0.0,
+                 paths_list: Optional[str] = None, labels=None):
         self.lib = net_lib()
         self.net = net
-        if cifar_files:
-            arr = (C.c_char_p * len(cifar_files))(*[os.fsencode(p) for p in cifar_files])
+        self._augment = augment
+        aug = C.byref(augment) if augment is not None else None
+        if paths_list:
+            self._labels = _cstrings(labels)
+            self.h = self.lib.an_feeder_create_paths(net.h, os.fsencode(paths_list),
+                                                     C.cast(self._labels, _vp), len(labels),
+                                                     threads, seed, aug, label_smooth_eps)
+        elif cifar_files:
+            arr = _cstrings(cifar_files)
             self._files = arr
             self.h = self.lib.an_feeder_create_cifar(net.h, arr, len(cifar_files), threads, seed,
-                                                     int(flip), label_smooth_eps)
+                                                     aug, label_smooth_eps)
         else:
-            self.h = self.lib.an_feeder_create_synthetic(net.h, threads, seed)
+            self.h = self.lib.an_feeder_create_synthetic(net.h, threads, seed, aug)
         if not self.h:
             raise HipError("an_feeder_create failed (see stderr)")
 
@@ -558,3 +598,26 @@ class Feeder:
             self.close()
         except Exception:
             pass
+
+
+def augment_image(src: np.ndarray, augment: Augment, seed: int, batch_no: int,
+                  image: int) -> np.ndarray:
+    """an_augment_image on a host image [c][h][w]"""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    c, h, w = src.shape
+    dst = np.empty_like(src)
+    check(net_lib().an_augment_image(src.ctypes.data, w, h, c, C.byref(augment), seed, batch_no,
+                                     image, dst.ctypes.data), "an_augment_image")
+    return dst
+
+
+def image_load(path: str, w: int, h: int, c: int) -> np.ndarray:
+    """an_image_load: a PNG / PPM / PGM file as float planes [c][h][w]"""
+    dst = np.empty((c, h, w), np.float32)
+    check(net_lib().an_image_load(os.fsencode(path), w, h, c, dst.ctypes.data), "an_image_load")
+    return dst
+
+
+def label_from_path(path: str, labels) -> int:
+    arr = _cstrings(labels)
+    return net_lib().an_label_from_path(os.fsencode(path), C.cast(arr, _vp), len(labels))

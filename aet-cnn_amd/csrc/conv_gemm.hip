@@ -46,9 +46,6 @@ constexpr int WGRAD_BK = ACH_WGRAD_BK;  // k-tile of the weight-gradient GEMM
 #ifndef ACH_WGRAD_TARGET
 #define ACH_WGRAD_TARGET 2048  // weight-gradient workgroups aimed for (tiles x splits)
 #endif
-#ifndef ACH_WGRAD_BN
-#define ACH_WGRAD_BN 64        // weight-gradient N tile for layers with > 64 filters
-#endif
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, unsigned bytes)
 {
@@ -66,6 +63,19 @@ __device__ __forceinline__ int boff(bool ok, int elem)
 __device__ __forceinline__ float bload(__amdgpu_buffer_rsrc_t r, int byte_off)
 {
     return __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
+
+// The same with a wave-uniform byte offset in the instruction's scalar
+// offset operand (an SGPR): loaders with loop-invariant per-thread offsets
+// add the k-tile's uniform advance there instead of in one VGPR per load.
+// Callers keep voff + soff inside the buffer for every in-range voff (the
+// prefetch past the last k-tile re-reads the last tile), so the address is
+// valid whether or not the range check includes the scalar offset; an
+// out-of-range voff (>= 2^31) reads zero either way.
+__device__ __forceinline__ float bload_so(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff)
+{
+    return __int_as_float(
+        (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
 
 
@@ -130,6 +140,13 @@ __device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, int byte_off)
                        __int_as_float((int)v[2]), __int_as_float((int)v[3]));
 }
 
+__device__ __forceinline__ float4 bload4_so(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    return make_float4(__int_as_float((int)v[0]), __int_as_float((int)v[1]),
+                       __int_as_float((int)v[2]), __int_as_float((int)v[3]));
+}
+
 template <int BM, int BK>
 struct AWeightsT4 {
     static constexpr int C4 = BM / 4;                      // float4 per tile row
@@ -155,18 +172,22 @@ struct AWeightsT4 {
             ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
         }
     }
-    // LDS rows the stores touch: the last pass may run past BK (zeros that
-    // no MFMA reads), so the stage is allocated with ROWS >= BK rows and the
-    // stores need no branch
-    static constexpr int ROWS = (NV * GNT + C4 - 1) / C4;
+    // The last pass may run past the BK rows of the stage (BK*C4 not a
+    // multiple of 256: 18 x 32 float4 for 3x3 filters and 128-row tiles);
+    // those stores are skipped.  For the 3x3 and 5x5 tiles of 128 and 256
+    // rows the cut falls on a wave boundary, so the branch is uniform per
+    // wave.  (Allocating the
+    // overflow rows instead cost 6 of the 24 A rows of LDS and left 3
+    // 128-row workgroups per CU instead of 4.)
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
     {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int f = threadIdx.x + GNT * i;
-            *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
-                make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
+            if (i + 1 < NV || NV * GNT <= BK * C4 || f < BK * C4)
+                *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
+                    make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
         }
     }
 };
@@ -229,9 +250,8 @@ struct AWeightsN {
 // AWeightsT4 for problems whose every k-tile is full (K a multiple of BK):
 // the per-thread byte offsets of the NV float4 (or the out-of-range offset
 // for columns past M and rows past BK) are loop-invariant, and a k-tile only
-// adds the uniform k0*M*4.  Past K (the prefetch after the last tile) the
-// loads read beyond the buffer or the next split's rows; those values are
-// never used.
+// adds the uniform k0*M*4 (the scalar offset).  The prefetch after the last
+// tile (k0 >= ke) re-reads the last tile; those values are never used.
 template <int BM, int BK>
 struct AWeightsT4F : AWeightsT4<BM, BK> {
     using Base = AWeightsT4<BM, BK>;
@@ -250,12 +270,12 @@ struct AWeightsT4F : AWeightsT4<BM, BK> {
             voff[i] = (f < BK * C4 && m < M_) ? (unsigned)(row * M_ + m) * 4u : kOOB;
         }
     }
-    __device__ __forceinline__ void load(int k0, int, float *ra) const
+    __device__ __forceinline__ void load(int k0, int ke, float *ra) const
     {
-        const unsigned d = (unsigned)(k0 * M4);
+        const unsigned d = (unsigned)((k0 < ke ? k0 : k0 - BK) * M4);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const float4 v = bload4(this->rs, (int)(voff[i] + d));
+            const float4 v = bload4_so(this->rs, voff[i], d);
             ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
         }
     }
@@ -327,7 +347,8 @@ struct BIm2col3 {
 // BIm2col3 for inputs with an even channel count (every k-tile full): the
 // nine byte offsets of the thread's first channel (out-of-range where the
 // tap falls in the padding) are loop-invariant; a k-tile adds the uniform
-// (k0/9)*H*W*4.  Out-of-range offsets stay >= 2^31 after the addition.
+// (k0/9)*H*W*4 as the scalar offset.  The prefetch after the last tile
+// (k0 >= ke) re-reads the last tile.
 struct BIm2col3F : BIm2col3 {
     static constexpr bool FULL_K = true;
     unsigned voff[9];
@@ -341,12 +362,12 @@ struct BIm2col3F : BIm2col3 {
         for (int i = 0; i < 9; ++i)
             voff[i] = ((valid >> i) & 1u) ? (unsigned)(base + (i / 3) * W + (i % 3)) * 4u : kOOB;
     }
-    __device__ __forceinline__ void load(int k0, int, float *rb) const
+    __device__ __forceinline__ void load(int k0, int ke, float *rb) const
     {
         static_assert(HC == 1, "one channel per thread group");
-        const unsigned d = (unsigned)(k0 / 9) * hw4;
+        const unsigned d = (unsigned)((k0 < ke ? k0 : k0 - BK) / 9) * hw4;
 #pragma unroll
-        for (int i = 0; i < 9; ++i) rb[i] = bload(rs, (int)(voff[i] + d));
+        for (int i = 0; i < 9; ++i) rb[i] = bload_so(rs, voff[i], d);
     }
 };
 
@@ -390,11 +411,11 @@ struct BIm2colK {
             voff[j] = v ? (unsigned)(base + ki * g.W + kj) * 4u : kOOB;
         }
     }
-    __device__ __forceinline__ void load(int k0, int, float *rb) const
+    __device__ __forceinline__ void load(int k0, int ke, float *rb) const
     {
-        const unsigned d = (unsigned)(k0 / BK) * hw4;
+        const unsigned d = (unsigned)((k0 < ke ? k0 : k0 - BK) / BK) * hw4;
 #pragma unroll
-        for (int j = 0; j < HALF; ++j) rb[j] = bload(rs, (int)(voff[j] + d));
+        for (int j = 0; j < HALF; ++j) rb[j] = bload_so(rs, voff[j], d);
     }
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
@@ -426,12 +447,12 @@ struct AWeightsT4K : AWeightsT4<BM, KS * KS + 1> {
             voff[i] = (f < BK * C4 && row < T && m < M_) ? (unsigned)(row * M_ + m) * 4u : kOOB;
         }
     }
-    __device__ __forceinline__ void load(int k0, int, float *ra) const
+    __device__ __forceinline__ void load(int k0, int ke, float *ra) const
     {
-        const unsigned d = (unsigned)(k0 / BK) * (unsigned)TM4;
+        const unsigned d = (unsigned)((k0 < ke ? k0 : k0 - BK) / BK) * (unsigned)TM4;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const float4 v = bload4(this->rs, (int)(voff[i] + d));
+            const float4 v = bload4_so(this->rs, voff[i], d);
             ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
         }
     }
@@ -513,9 +534,15 @@ struct WgradDivs {
     FastDiv ohw, ow, batch;
 };
 
+// LDS rows of the weight-gradient stages are padded to a stride of 2 (mod 32
+// floats): a half-wave's transposed stores S[kc][r + RPI*i] (kc = lane % 16,
+// r = lane / 16) then hit 32 distinct banks (2*kc + r), and the fragment
+// reads (32 consecutive floats of one row) stay conflict-free.
+constexpr int WG_PAD = 2;
+
 template <int BM, int BK_>
 struct AWgrad {
-    static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = 1;
+    static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = WG_PAD;
     __amdgpu_buffer_rsrc_t rs;
     int kc, MO;        // MO = M*ohw
     int moff[RA];      // m*ohw or -1
@@ -555,7 +582,7 @@ struct AWgrad {
 
 template <int BN, int BK_, int KS_T>
 struct BWgrad {
-    static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = 1;
+    static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = WG_PAD;
     __amdgpu_buffer_rsrc_t rs;
     int kc, S, P, H, W, CHW;
     FastDiv dohw, dow;
@@ -619,7 +646,7 @@ struct BWgrad {
 // are >= 2^31 and stay out of range after the addition (operands < 2 GiB).
 template <int BM, int BK_>
 struct AWgradC {
-    static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = LDP;
+    static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = WG_PAD;
     static_assert(BK == 16, "one 16-position chunk per k-tile");
     __amdgpu_buffer_rsrc_t rs;
     unsigned voff[RA];
@@ -641,10 +668,11 @@ struct AWgradC {
     }
     __device__ __forceinline__ void load(int k0, int, float *ra) const
     {
+        // image (k0/16) mod B: the prefetch past the split wraps to a valid image
         const int t = k0 >> 4;
         const unsigned d = (unsigned)(t - fdiv(t, db) * (int)db.d) * img;
 #pragma unroll
-        for (int i = 0; i < RA; ++i) ra[i] = bload(rs, (int)(voff[i] + d));
+        for (int i = 0; i < RA; ++i) ra[i] = bload_so(rs, voff[i], d);
     }
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
@@ -657,7 +685,7 @@ struct AWgradC {
 
 template <int BN, int BK_, int KS_T>
 struct BWgradC {
-    static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = LDP;
+    static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = WG_PAD;
     static_assert(BK == 16, "one 16-position chunk per k-tile");
     __amdgpu_buffer_rsrc_t rs;
     unsigned voff[RB];
@@ -689,7 +717,7 @@ struct BWgradC {
         const int t = k0 >> 4;
         const unsigned d = (unsigned)(t - fdiv(t, db) * (int)db.d) * img;
 #pragma unroll
-        for (int i = 0; i < RB; ++i) rb[i] = bload(rs, (int)(voff[i] + d));
+        for (int i = 0; i < RB; ++i) rb[i] = bload_so(rs, voff[i], d);
     }
     template <int LD>
     __device__ __forceinline__ void store(float (*S_)[LD], const float *rb) const
@@ -981,30 +1009,22 @@ struct FcWgradProblem {
 };
 
 // ===========================================================================
-// LDS rows of the A stage: BK, or more for a loader whose branch-free stores
-// run past BK (AWeightsT4::ROWS)
 template <class P, class = void> struct is_rmw : std::false_type {};
 template <class P> struct is_rmw<P, std::void_t<decltype(P::RMW)>> : std::true_type {};
 
-template <class L, class = void> struct has_rows : std::false_type {};
-template <class L> struct has_rows<L, std::void_t<decltype(L::ROWS)>> : std::true_type {};
-template <class L, int BK> constexpr int a_rows()
-{
-    if constexpr (has_rows<L>::value) return L::ROWS > BK ? L::ROWS : BK;
-    else return BK;
-}
 
 template <class P>
 __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
 {
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK;
     // wave grid: 2x2 for 64+ x 128 tiles, 1x4 for 32-row, 4x1 for 32-column
-    constexpr int WM = BN <= 32 ? 4 : (BM % 64 == 0 ? 2 : 1), WN = 4 / WM;
+    // and for 128 x 96 tiles (each wave 32 x 96)
+    constexpr int WM = BN <= 32 ? 4 : (BN % 64 != 0 && BM % 128 == 0 ? 4 : (BM % 64 == 0 ? 2 : 1));
+    constexpr int WN = 4 / WM;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
     static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
     constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
-    constexpr int AROWS = a_rows<typename P::AL, BK>();
-    __shared__ __attribute__((aligned(16))) float As[2][AROWS][LA];
+    __shared__ __attribute__((aligned(16))) float As[2][BK][LA];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK][LB];
 
     const int tid = threadIdx.x;
@@ -1524,13 +1544,10 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Split count for wgrad: aim for >= ~1024 workgroups over 256 CUs, K chunks a
-// multiple of the k-tile.
+// Split count of the weight gradient in the (image, position) K order: aim
+// for ~ACH_WGRAD_TARGET workgroups, K chunks a multiple of the k-tile.
 #ifndef ACH_WGRAD_CHUNKED
 #define ACH_WGRAD_CHUNKED 1
-#endif
-#ifndef ACH_WGRAD_TARGET_CHUNKED
-#define ACH_WGRAD_TARGET_CHUNKED 1024  // measured: 1024 beats 512, 1536 and 2048
 #endif
 #ifndef ACH_WGRAD_PAD_WASTE
 #define ACH_WGRAD_PAD_WASTE 0.0625  // largest padded fraction of a plane taken
@@ -1544,20 +1561,38 @@ static bool wgrad_chunked(const ConvGeom &g)
     return ACH_WGRAD_CHUNKED && wgrad_nchunks(g) * 16 - ohw <= ACH_WGRAD_PAD_WASTE * ohw;
 }
 
-// chunked split: spc splits per position chunk, nbs images each, aiming at
-// ACH_WGRAD_TARGET_CHUNKED workgroups (tiles x splits), >= 4 images per split
-static void wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits, int &spc,
-                                int &nbs)
+// Grid cost model of the weight-gradient GEMM: all its workgroups do equal
+// work, so the kernel takes about ceil(workgroups / 256 CUs) times one
+// workgroup's work; below two workgroups per CU the matrix pipes idle.
+static double wgrad_cost(long long wgs, double work)
+{
+    const double c = (double)((wgs + 255) / 256) * work;
+    return wgs < 512 ? c * 1.25 : c;
+}
+
+// chunked split: spc splits per position chunk, nbs images each (>= 4 per
+// split), the count with the lowest grid cost (ties: fewer workgroups, so
+// fewer partial sums)
+static double wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits, int &spc,
+                                  int &nbs)
 {
     const int M = g.F, N = g.C * g.KS * g.KS, nchunks = wgrad_nchunks(g);
     const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    long long want = (ACH_WGRAD_TARGET_CHUNKED + tiles * nchunks - 1) / (tiles * nchunks);
     const int max_spc = g.B >= 4 ? g.B / 4 : 1;
-    if (want > max_spc) want = max_spc;
-    if (want < 1) want = 1;
-    nbs = (g.B + (int)want - 1) / (int)want;
-    spc = (g.B + nbs - 1) / nbs;
+    double best = -1;
+    for (int want = 1; want <= max_spc && want <= 64; ++want) {
+        const int b = (g.B + want - 1) / want, s = (g.B + b - 1) / b;
+        const long long wgs = tiles * nchunks * s;
+        if (wgs > 65535LL * 1024) break;
+        const double c = wgrad_cost(wgs, (double)bm * bn * b);
+        if (best < 0 || c < best * (1 - 1e-9)) {
+            best = c;
+            nbs = b;
+            spc = s;
+        }
+    }
     splits = nchunks * spc;
+    return best;
 }
 
 static void wgrad_split(const ConvGeom &g, int bm, int bn, int &splits, int &kchunk)
@@ -1596,12 +1631,33 @@ static int wgrad_bm(const ConvGeom &g)
     if (wgrad_96(g)) return 96;
     return g.F <= 32 ? 32 : (g.F <= 64 ? 64 : 128);
 }
+// Layers with more than 96 filters in the chunked order take the N tile of
+// 64, 96 or 128 columns with the lowest grid cost (ties: fewer workgroups);
+// e.g. every config-1 3x3 layer at batch 128 has 1152 (tile, chunk) pairs
+// of 128 x 64, which leave a 12%-full second round on 1024 workgroup slots,
+// against exactly 3 x 256 workgroups of 128 x 96.
 static int wgrad_bn(const ConvGeom &g)
 {
     if (fc_geom(g)) return 128;
     if (g.C * g.KS * g.KS <= 32 && g.F > 64) return 32;
     if (wgrad_96(g)) return 128;
-    return g.F > 64 ? ACH_WGRAD_BN : 128;
+    if (g.F <= 64) return 128;
+    if (!wgrad_chunked(g)) return 64;
+    int best_bn = 64;
+    double best = -1;
+    long long best_wgs = 0;
+    for (int bn : {64, 96, 128}) {
+        int splits, spc, nbs;
+        const double c = wgrad_split_chunked(g, 128, bn, splits, spc, nbs);
+        const long long wgs = (long long)((g.F + 127) / 128) *
+                              ((g.C * g.KS * g.KS + bn - 1) / bn) * splits;
+        if (best < 0 || c < best * (1 - 1e-9) || (c <= best * (1 + 1e-9) && wgs < best_wgs)) {
+            best = c;
+            best_bn = bn;
+            best_wgs = wgs;
+        }
+    }
+    return best_bn;
 }
 
 template <int BM, int BN>
@@ -1882,9 +1938,8 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
     int rc;
     if (fc_geom(g)) rc = fc_wgrad_launch(g, x, dy, dw, part, bm, splits, kchunk, st);
     else if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st);
-#if ACH_WGRAD_BN == 64
     else if (bn == 64) rc = wgrad_launch<128, 64>(g, x, dy, dw, part, splits, kchunk, st);
-#endif
+    else if (bn == 96) rc = wgrad_launch<128, 96>(g, x, dy, dw, part, splits, kchunk, st);
     else if (bm == 96) rc = wgrad_launch<96, 128>(g, x, dy, dw, part, splits, kchunk, st);
     else if (bm == 32) rc = wgrad_launch<32, 128>(g, x, dy, dw, part, splits, kchunk, st);
     else if (bm == 64) rc = wgrad_launch<64, 128>(g, x, dy, dw, part, splits, kchunk, st);

@@ -454,3 +454,32 @@ an_network *an_parse_cfg(const char *path)
     }
     return net;
 }
+
+/* The augmentation keys of [net] (parseNetOption, NetworkFactory.c:727-762:
+ * max_crop = width*2, min_crop = width, flip = 1, angle = 0, aspect = 1,
+ * saturation = 1, exposure = 1, hue = 0; label_smooth_eps = 0) read as the
+ * reference reads them; the input pipeline applies them (an_augment_image). */
+int an_cfg_augment(const char *path, an_augment *a, float *label_smooth_eps)
+{
+    cfg_group *gs = NULL;
+    int ng = 0;
+    if (!path || !a || read_groups(path, &gs, &ng)) return ACH_EINVAL;
+    if (ng == 0 || (strcmp(gs[0].name, "net") && strcmp(gs[0].name, "network"))) {
+        free(gs);
+        return ACH_EINVAL;
+    }
+    const cfg_group *g = &gs[0];
+    const int w = geti(g, "width", 0);
+    an_augment_defaults(a, w);
+    a->max_crop = geti(g, "max_crop", w * 2);
+    a->min_crop = geti(g, "min_crop", w);
+    a->flip = geti(g, "flip", 1);
+    a->angle = getf(g, "angle", 0.f);
+    a->aspect = getf(g, "aspect", 1.f);
+    a->saturation = getf(g, "saturation", 1.f);
+    a->exposure = getf(g, "exposure", 1.f);
+    a->hue = getf(g, "hue", 0.f);
+    if (label_smooth_eps) *label_smooth_eps = getf(g, "label_smooth_eps", 0.f);
+    free(gs);
+    return ACH_OK;
+}

@@ -11,15 +11,17 @@
  *   label smoothing (fillTruthSmooth, :77-103).  Classifier.train
  *   (Classifier.c:216-243) sets it up with 12 threads.
  *
- * Differences, by design: the reference decodes image files named in a list
- * (its NImage codecs) and takes labels from substrings of the path; this
- * build reads the CIFAR-10 binary batches (1 label byte + 3x32x32 planar
- * RGB bytes per record), which hold the same images and labels.  The image
- * index and flip of image i of batch k come from a counter-based hash of
- * (seed, k, i) instead of the shared rand() stream, so the batches do not
- * depend on thread scheduling.  The other augmentations of the reference
- * (random crop / aspect / rotation, hue / saturation / exposure distortion)
- * are not built.                                                            */
+ * Sources: a list of image files with labels from substrings of the path,
+ * as the reference reads its training set (getPaths, fillTruthSmooth; PNG /
+ * PPM / PGM decoded by image.c), the CIFAR-10 binary batches (1 label byte
+ * + 3x32x32 planar RGB bytes per record; the same images and labels), or
+ * synthetic pixels.  Every image then takes the reference's augmentation
+ * (loadImageAugmentPaths: random scale / aspect / rotation crop, flip,
+ * hue / saturation / exposure distortion; an_augment_image in image.c)
+ * when the feeder has an an_augment.  The image index and every random draw
+ * of image i of batch k come from a counter-based hash of (seed, k, i)
+ * instead of the shared rand() stream, so the batches do not depend on
+ * thread scheduling.                                                        */
 #include "aetcnn_net.h"
 
 #include <pthread.h>
@@ -30,7 +32,7 @@
 #define CIFAR_REC 3073
 #define CIFAR_SIDE 32
 
-enum { SRC_SYNTHETIC = 0, SRC_CIFAR = 1 };
+enum { SRC_SYNTHETIC = 0, SRC_CIFAR = 1, SRC_PATHS = 2 };
 enum { SLOT_IDLE = 0, SLOT_FILLING = 1, SLOT_READY = 2 };
 
 struct an_feeder {
@@ -39,9 +41,14 @@ struct an_feeder {
     int kind;
     unsigned char *records; /* CIFAR records, nrecords x 3073 bytes */
     size_t nrecords;
+    char **paths;           /* image files and their labels (SRC_PATHS) */
+    int *path_label;
+    size_t npaths;
     uint64_t seed;
-    int flip;
+    int augment;
+    an_augment aug;
     float smooth;
+    int load_error;         /* a worker could not decode an image */
     float *host_in[2], *host_truth[2]; /* pinned */
     float *dev_in[2], *dev_truth[2];
     void *copied[2];
@@ -81,36 +88,41 @@ static void fill_truth(float *truth, int classes, int label, float eps)
         truth[k] = (k == label) ? 1.f - eps : (classes > 1 ? eps / (classes - 1) : 0.f);
 }
 
-static void fill_image(an_feeder *f, int s, uint64_t bn, int i)
+/* image i of batch bn into slot s: the source image (into `tmp` when it is
+ * augmented afterwards, else straight into the slot), then the augmentation;
+ * returns ACH_OK or the decoder's error */
+static int fill_image(an_feeder *f, int s, uint64_t bn, int i, float *tmp)
 {
     float *img = f->host_in[s] + (size_t)i * f->inputs;
     float *truth = f->host_truth[s] + (size_t)i * f->classes;
+    float *src = f->augment ? tmp : img;
+    int label;
     if (f->kind == SRC_CIFAR) {
         const size_t idx = (size_t)(draw(f->seed, bn, (uint64_t)i, 0) % f->nrecords);
-        const int flip = f->flip ? (int)(draw(f->seed, bn, (uint64_t)i, 1) & 1) : 0;
         const unsigned char *rec = f->records + idx * CIFAR_REC;
-        const int plane = CIFAR_SIDE * CIFAR_SIDE;
-        for (int ch = 0; ch < 3; ++ch)
-            for (int y = 0; y < CIFAR_SIDE; ++y)
-                for (int x = 0; x < CIFAR_SIDE; ++x) {
-                    const int xs = flip ? CIFAR_SIDE - 1 - x : x;
-                    img[ch * plane + y * CIFAR_SIDE + x] =
-                        rec[1 + ch * plane + y * CIFAR_SIDE + xs] / 255.f;
-                }
-        fill_truth(truth, f->classes, rec[0], f->smooth);
+        for (int j = 0; j < 3 * CIFAR_SIDE * CIFAR_SIDE; ++j) src[j] = rec[1 + j] / 255.f;
+        label = rec[0];
+    } else if (f->kind == SRC_PATHS) {
+        const size_t idx = (size_t)(draw(f->seed, bn, (uint64_t)i, 0) % f->npaths);
+        const int rc = an_image_load(f->paths[idx], f->w, f->h, f->c, src);
+        if (rc) return rc;
+        label = f->path_label[idx];
     } else {
         for (int j = 0; j < f->inputs; ++j)
-            img[j] = (float)(draw(f->seed, bn, (uint64_t)i * (uint64_t)f->inputs + j, 2) >> 40) *
+            src[j] = (float)(draw(f->seed, bn, (uint64_t)i * (uint64_t)f->inputs + j, 2) >> 40) *
                      (1.0f / 16777216.0f);
-        fill_truth(truth, f->classes, (int)(draw(f->seed, bn, (uint64_t)i, 3) % f->classes),
-                   f->smooth);
+        label = (int)(draw(f->seed, bn, (uint64_t)i, 3) % f->classes);
     }
+    fill_truth(truth, f->classes, label, f->smooth);
+    if (!f->augment) return ACH_OK;
+    return an_augment_image(src, f->w, f->h, f->c, &f->aug, f->seed, bn, i, img);
 }
 
 static void *worker(void *arg)
 {
     an_feeder *f = (an_feeder *)arg;
     const int chunk = f->batch / (2 * f->nthreads) > 0 ? f->batch / (2 * f->nthreads) : 1;
+    float *tmp = (float *)malloc(sizeof(float) * (size_t)f->inputs);
     pthread_mutex_lock(&f->mu);
     for (;;) {
         int s = -1;
@@ -129,8 +141,13 @@ static void *worker(void *arg)
         f->next_img[s] = hi;
         const uint64_t bn = f->slot_batch[s];
         pthread_mutex_unlock(&f->mu);
-        for (int i = lo; i < hi; ++i) fill_image(f, s, bn, i);
+        int err = tmp ? ACH_OK : ACH_EINVAL;
+        for (int i = lo; i < hi && !err; ++i) err = fill_image(f, s, bn, i, tmp);
         pthread_mutex_lock(&f->mu);
+        if (err) { /* wake an_feeder_next, which reports the failure */
+            f->load_error = 1;
+            pthread_cond_broadcast(&f->cv_ready);
+        }
         f->done_img[s] += hi - lo;
         if (f->done_img[s] == f->batch) {
             f->state[s] = SLOT_READY;
@@ -138,6 +155,7 @@ static void *worker(void *arg)
         }
     }
     pthread_mutex_unlock(&f->mu);
+    free(tmp);
     return NULL;
 }
 
@@ -175,10 +193,13 @@ void an_feeder_free(an_feeder *f)
     pthread_cond_destroy(&f->cv_work);
     pthread_cond_destroy(&f->cv_ready);
     free(f->records);
+    for (size_t k = 0; k < f->npaths; ++k) free(f->paths[k]);
+    free(f->paths);
+    free(f->path_label);
     free(f);
 }
 
-static an_feeder *feeder_new(an_network *net, int threads, uint64_t seed, int flip,
+static an_feeder *feeder_new(an_network *net, int threads, uint64_t seed, const an_augment *aug,
                              float label_smooth_eps)
 {
     int shape[8];
@@ -195,12 +216,17 @@ static an_feeder *feeder_new(an_network *net, int threads, uint64_t seed, int fl
     f->inputs = f->c * f->h * f->w;
     f->classes = an_classes(net);
     f->seed = seed;
-    f->flip = flip;
+    f->augment = aug != NULL;
+    if (aug) f->aug = *aug;
     f->smooth = label_smooth_eps;
     f->nthreads = threads;
     pthread_mutex_init(&f->mu, NULL);
     pthread_cond_init(&f->cv_work, NULL);
     pthread_cond_init(&f->cv_ready, NULL);
+    if (aug && (aug->min_crop <= 0 || aug->max_crop <= 0)) {
+        an_feeder_free(f);
+        return NULL;
+    }
     return f;
 }
 
@@ -235,9 +261,10 @@ fail:
 }
 
 an_feeder *an_feeder_create_cifar(an_network *net, const char *const *files, int nfiles,
-                                  int threads, uint64_t seed, int flip, float label_smooth_eps)
+                                  int threads, uint64_t seed, const an_augment *aug,
+                                  float label_smooth_eps)
 {
-    an_feeder *f = feeder_new(net, threads, seed, flip, label_smooth_eps);
+    an_feeder *f = feeder_new(net, threads, seed, aug, label_smooth_eps);
     if (!f) return NULL;
     f->kind = SRC_CIFAR;
     if (!files || nfiles <= 0 || f->c != 3 || f->h != CIFAR_SIDE || f->w != CIFAR_SIDE ||
@@ -281,11 +308,76 @@ an_feeder *an_feeder_create_cifar(an_network *net, const char *const *files, int
     return feeder_start(f);
 }
 
-an_feeder *an_feeder_create_synthetic(an_network *net, int threads, uint64_t seed)
+an_feeder *an_feeder_create_synthetic(an_network *net, int threads, uint64_t seed,
+                                      const an_augment *aug)
 {
-    an_feeder *f = feeder_new(net, threads, seed, 0, 0.f);
+    an_feeder *f = feeder_new(net, threads, seed, aug, 0.f);
     if (!f) return NULL;
     f->kind = SRC_SYNTHETIC;
+    return feeder_start(f);
+}
+
+/* The reference's training list (Classifier.c:79-108: one image path per
+ * line) with labels from path substrings (fillTruthSmooth: exactly one of
+ * the labels must occur in each path; checked here for the whole list). */
+an_feeder *an_feeder_create_paths(an_network *net, const char *list_file,
+                                  const char *const *labels, int nlabels, int threads,
+                                  uint64_t seed, const an_augment *aug, float label_smooth_eps)
+{
+    an_feeder *f = feeder_new(net, threads, seed, aug, label_smooth_eps);
+    if (!f) return NULL;
+    f->kind = SRC_PATHS;
+    if (!list_file || !labels || nlabels != f->classes) {
+        fprintf(stderr, "an_feeder_create_paths: need a list file and one label per class "
+                        "(%d)\n", f->classes);
+        an_feeder_free(f);
+        return NULL;
+    }
+    FILE *fp = fopen(list_file, "r");
+    if (!fp) {
+        fprintf(stderr, "an_feeder_create_paths: cannot open %s\n", list_file);
+        an_feeder_free(f);
+        return NULL;
+    }
+    char line[4096];
+    size_t cap = 0;
+    int ok = 1;
+    while (ok && fgets(line, sizeof(line), fp)) {
+        size_t n = strlen(line);
+        while (n && (line[n - 1] == '\n' || line[n - 1] == '\r' || line[n - 1] == ' '))
+            line[--n] = 0;
+        if (!n) continue;
+        const int lab = an_label_from_path(line, labels, nlabels);
+        if (lab < 0) {
+            fprintf(stderr, "an_feeder_create_paths: %s: too many or too few labels\n", line);
+            ok = 0;
+            break;
+        }
+        if (f->npaths == cap) {
+            cap = cap ? 2 * cap : 1024;
+            char **np = (char **)realloc(f->paths, cap * sizeof(char *));
+            int *nl = np ? (int *)realloc(f->path_label, cap * sizeof(int)) : NULL;
+            if (np) f->paths = np;
+            if (nl) f->path_label = nl;
+            if (!np || !nl) {
+                ok = 0;
+                break;
+            }
+        }
+        f->paths[f->npaths] = strdup(line);
+        f->path_label[f->npaths] = lab;
+        if (!f->paths[f->npaths]) {
+            ok = 0;
+            break;
+        }
+        ++f->npaths;
+    }
+    fclose(fp);
+    if (!ok || f->npaths == 0) {
+        if (ok) fprintf(stderr, "an_feeder_create_paths: %s lists no images\n", list_file);
+        an_feeder_free(f);
+        return NULL;
+    }
     return feeder_start(f);
 }
 
@@ -298,8 +390,10 @@ int an_feeder_next(an_feeder *f)
     if (!f) return ACH_EINVAL;
     const int s = (int)(f->served & 1);
     pthread_mutex_lock(&f->mu);
-    while (f->state[s] != SLOT_READY) pthread_cond_wait(&f->cv_ready, &f->mu);
+    while (f->state[s] != SLOT_READY && !f->load_error) pthread_cond_wait(&f->cv_ready, &f->mu);
+    const int bad = f->load_error;
     pthread_mutex_unlock(&f->mu);
+    if (bad) return ACH_EINVAL; /* the reference aborts on an unreadable image */
     const size_t in_bytes = sizeof(float) * (size_t)f->batch * f->inputs;
     const size_t tr_bytes = sizeof(float) * (size_t)f->batch * f->classes;
     ach_stream_t ns = an_stream(f->net);

@@ -214,6 +214,20 @@ static int conv_forward(an_network *net, an_layer *l, an_state st)
     return ach_activate(l->output, (size_t)l->batch * l->outputs, l->activation, s);
 }
 
+/* A dropout layer right above l that shares l's output (masked in place by
+ * its forward) but whose backward is skipped (onlyforward): l's delta is
+ * then not masked, and the reference takes l's activation gradient from the
+ * masked output (Activation.gradientArray on outputData, f'(0) where a unit
+ * was dropped).  The BN passes derive the gradient's sign from the
+ * recomputed pre-activation instead, which equals f'(y) only where the
+ * output was not masked or its delta is zero.                             */
+static int output_masked_unreverted(const an_network *net, const an_layer *l)
+{
+    if (l->index + 1 >= net->n) return 0;
+    const an_layer *d = net->layers[l->index + 1];
+    return d->type == AN_DROPOUT && d->shares_prev && d->onlyforward;
+}
+
 static int conv_backward(an_network *net, an_layer *l, an_state st)
 {
     ach_conv_desc d = conv_desc(l);
@@ -222,7 +236,8 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
     const size_t nout = (size_t)l->batch * l->outputs;
     if (l->batch_normalize) {
         int act = ACH_LINEAR;
-        if (l->activation == ACH_LEAKY || l->activation == ACH_RELU)
+        if ((l->activation == ACH_LEAKY || l->activation == ACH_RELU) &&
+            !output_masked_unreverted(net, l))
             act = l->activation; /* gradient fused into the BN passes */
         else
             AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));

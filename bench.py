@@ -85,7 +85,9 @@ def fed_phase(aetcnn, configs, name, steps, warmup, threads):
     net = aetcnn.Network(B, h, w, c)
     configs.build(net, name)
     net.finalize()
-    feeder = aetcnn.Feeder(net, threads=threads, seed=3)
+    # the reference's augmentation with its [net] defaults (random 1-2x zoom
+    # crops, flips, the HSV pass) on every image, as Classifier.train feeds
+    feeder = aetcnn.Feeder(net, threads=threads, seed=3, augment=aetcnn.Augment.defaults(w))
     ops = aetcnn.ops()
     for _ in range(warmup):
         feeder.next()
@@ -102,7 +104,8 @@ def fed_phase(aetcnn, configs, name, steps, warmup, threads):
     net.close()
     return dict(images_per_s=round(B * steps / dt, 1), ms_per_step=round(dt * 1e3 / steps, 4),
                 threads=threads, loss=round(loss, 5),
-                source="synthetic, a fresh batch per step through pinned double buffers")
+                source="synthetic images with the reference's default augmentation, a fresh "
+                       "batch per step through pinned double buffers")
 
 
 def time_launch(ops, stream, fn, reps):

@@ -216,24 +216,83 @@ an_network *an_parse_cfg_unfinalized(const char *path);
 int an_save_weights(an_network *net, const char *path);
 int an_load_weights(an_network *net, const char *path);
 
+/* ---- images and their augmentation (NImage.c, ImageData.c:56-104) --------
+ * an_augment holds the [net] keys of the reference's training-time
+ * augmentation (parseNetOption, NetworkFactory.c:727-762), applied to every
+ * image as ImageData.loadImageAugmentPaths does (ImageData.c:56-73):
+ * NImage.randomAugment (NImage.c:1016-1034: aspect = randScale(aspect),
+ * crop side r = randInt(min_crop, max_crop), scale = r / min(h, w*aspect),
+ * rotation randUniform(-angle, angle) degrees, random offset) resampled by
+ * rotateCrop (bilinear, zero outside; NImage.c:551-572), a horizontal flip
+ * with probability 1/2 when flip != 0, randomDistort (hue shift
+ * randUniformStrong(-hue, hue), saturation and exposure factors
+ * randScale(saturation), randScale(exposure), in HSV; 3-channel images
+ * only, NImage.c:201-352) and a bilinear resize back to the input size
+ * (NImage.c:474-530).  Random numbers: the counter-based hash of
+ * an_feeder_sample(seed, batch_no, image, salt), one salt per draw, through
+ * the reference's formulas with RAND_MAX = 2^31 - 1.                       */
+typedef struct {
+    int min_crop, max_crop;     /* crop side range; defaults w and 2*w       */
+    float angle;                /* degrees; default 0                        */
+    float aspect;               /* default 1                                 */
+    float hue;                  /* default 0                                 */
+    float saturation, exposure; /* defaults 1                                */
+    int flip;                   /* default 1                                 */
+} an_augment;
+void an_augment_defaults(an_augment *a, int net_w);
+/* the augmentation keys and label_smooth_eps of a .cfg's [net] section    */
+int an_cfg_augment(const char *cfg_path, an_augment *a, float *label_smooth_eps);
+/* one image of batch batch_no: src and dst are host [c][h][w] planes       */
+int an_augment_image(const float *src, int w, int h, int c, const an_augment *a, uint64_t seed,
+                     uint64_t batch_no, int image, float *dst);
+/* the steps, host-only: rotateCrop (rad, scale s, output w x h, offset dx,
+ * dy, aspect), flip, distort (HSV; 3 channels), resizeImage               */
+void an_image_rotate_crop(const float *src, int W, int H, int c, float rad, float s, int w, int h,
+                          float dx, float dy, float aspect, float *dst);
+void an_image_flip(float *im, int w, int h, int c);
+void an_image_distort(float *im, int w, int h, float hue, float sat, float val);
+void an_image_resize(const float *src, int W, int H, int c, int w, int h, float *dst);
+/* NImage.reload (NImage.c:638-658): decodes a PNG (8-bit, non-interlaced;
+ * grey, RGB, palette, grey+alpha, RGBA) or binary PPM / PGM file into host
+ * planes dst[c][h][w] = sample / 255; the file must have exactly w x h
+ * pixels and c channels (else ACH_EINVAL with a message).  The reference
+ * decodes through stb_image; JPEG and other formats are not supported.     */
+int an_image_load(const char *path, int w, int h, int c, float *dst);
+/* ImageData.fillTruthSmooth (ImageData.c:80-104): the index of the one
+ * label that occurs in path as a substring, or -1 for none or several     */
+int an_label_from_path(const char *path, const char *const *labels, int nlabels);
+
 /* ---- input pipeline (ImageData.c:20-224, DstbCompute.c:60-216) ------------
  * Worker threads fill two pinned host batches; an_feeder_next copies the next
  * one to the device on the feeder's own stream (overlapping the previous
  * training step), orders the network's stream after it and makes it the
  * network's input and truth.  Image i of batch k is drawn from a counter-
- * based hash of (seed, k, i): an_feeder_sample(seed, k, i, 0) % records is
- * its record, bit 0 of an_feeder_sample(seed, k, i, 1) its horizontal flip
- * (when enabled).  Truth is one-hot with label smoothing (fillTruthSmooth,
- * ImageData.c:77-103).  The CIFAR source reads CIFAR-10 binary batches
- * (1 label byte + 3x32x32 planar RGB bytes per record; pixels / 255) and
- * needs a 3x32x32 network input; the synthetic source draws pixels uniform
- * in [0,1) (an_feeder_sample(seed, k, i*inputs + j, 2) >> 40 / 2^24) and
- * labels an_feeder_sample(seed, k, i, 3) % classes.  Free the feeder before
- * the network.                                                             */
+ * based hash of (seed, k, i): an_feeder_sample(seed, k, i, 0) % (number of
+ * images) is its index.  Truth is one-hot with label smoothing
+ * (fillTruthSmooth, ImageData.c:77-103).  Sources:
+ *   paths     a list file of image paths, one per line (the reference's
+ *             training list, Classifier.c:79-108), decoded by an_image_load,
+ *             labels from path substrings (an_label_from_path, checked for
+ *             the whole list at creation; labels[nlabels], nlabels = the
+ *             network's classes)
+ *   cifar     CIFAR-10 binary batches (1 label byte + 3x32x32 planar RGB
+ *             bytes per record; pixels / 255); needs a 3x32x32 input
+ *   synthetic pixels uniform in [0,1) (an_feeder_sample(seed, k,
+ *             i*inputs + j, 2) >> 40 / 2^24), labels an_feeder_sample(seed,
+ *             k, i, 3) % classes
+ * With aug != NULL every image then takes an_augment_image(seed, k, i);
+ * NULL feeds the images as decoded.  an_feeder_next returns ACH_EINVAL when
+ * an image could not be decoded (the reference aborts).  Free the feeder
+ * before the network.                                                     */
 typedef struct an_feeder an_feeder;
+an_feeder *an_feeder_create_paths(an_network *net, const char *list_file,
+                                  const char *const *labels, int nlabels, int threads,
+                                  uint64_t seed, const an_augment *aug, float label_smooth_eps);
 an_feeder *an_feeder_create_cifar(an_network *net, const char *const *files, int nfiles,
-                                  int threads, uint64_t seed, int flip, float label_smooth_eps);
-an_feeder *an_feeder_create_synthetic(an_network *net, int threads, uint64_t seed);
+                                  int threads, uint64_t seed, const an_augment *aug,
+                                  float label_smooth_eps);
+an_feeder *an_feeder_create_synthetic(an_network *net, int threads, uint64_t seed,
+                                      const an_augment *aug);
 int an_feeder_next(an_feeder *f);
 uint64_t an_feeder_served(const an_feeder *f);
 uint64_t an_feeder_sample(uint64_t seed, uint64_t batch_no, int image, int what);

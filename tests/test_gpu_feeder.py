@@ -1,5 +1,7 @@
-"""Input pipeline (an_feeder_*, ImageData.c:20-224): CIFAR-10 binary decode,
-sampling, flips and label smoothing as documented in aetcnn_net.h; batches
+"""Input pipeline (an_feeder_*, ImageData.c:20-224): image-list and CIFAR-10
+binary sources, sampling, the augmentation and label smoothing as documented
+in aetcnn_net.h (each image equals an_augment_image of the decoded source
+image, whose arithmetic is pinned on the CPU in test_augment.py); batches
 arrive in order on the network stream while the copy overlaps the previous
 step; training on fed batches equals training on the same host batches."""
 import numpy as np
@@ -68,20 +70,19 @@ def test_cifar_batches(gpu, tmp_path):
     recs = np.concatenate(recs)
     net = tiny_net(8)
     seed, eps = 5, 0.1
-    feeder = aetcnn.Feeder(net, cifar_files=files, threads=3, seed=seed, flip=True,
+    aug = aetcnn.Augment.defaults(32, angle=10, aspect=1.2, hue=0.1, saturation=1.5,
+                                  exposure=1.5)
+    feeder = aetcnn.Feeder(net, cifar_files=files, threads=3, seed=seed, augment=aug,
                            label_smooth_eps=eps)
     try:
         for bn in range(5):
             feeder.next()
             x, t = device_input(net)
             idx = draw(seed, bn, np.arange(8), 0) % np.uint64(len(recs))
-            flip = draw(seed, bn, np.arange(8), 1) & np.uint64(1)
             for i in range(8):
                 r = recs[int(idx[i])]
                 img = r[1:].reshape(3, 32, 32).astype(np.float32) / np.float32(255)
-                if flip[i]:
-                    img = img[:, :, ::-1]
-                assert np.array_equal(x[i], img), (bn, i)
+                assert np.array_equal(x[i], aetcnn.augment_image(img, aug, seed, bn, i)), (bn, i)
                 want = np.full(10, eps / 9, np.float32)
                 want[r[0]] = 1 - eps
                 assert np.array_equal(t[i], want), (bn, i)
@@ -122,3 +123,77 @@ def test_fed_training_equals_host_batches(gpu):
         feeder.close()
         a.close()
         b.close()
+
+
+LABELS = [f"_c{k}_" for k in range(10)]
+
+
+def write_png(path, pix):
+    """8-bit RGB PNG (filter 0 rows) of pix [H][W][3]"""
+    import struct
+    import zlib
+    H, W, _ = pix.shape
+    raw = b"".join(b"\0" + pix[y].tobytes() for y in range(H))
+
+    def chunk(t, d):
+        return struct.pack(">I", len(d)) + t + d + struct.pack(">I", zlib.crc32(t + d))
+    path.write_bytes(b"\x89PNG\r\n\x1a\n" +
+                     chunk(b"IHDR", struct.pack(">IIBBBBB", W, H, 8, 2, 0, 0, 0)) +
+                     chunk(b"IDAT", zlib.compress(raw)) + chunk(b"IEND", b""))
+
+
+def test_paths_source(gpu, tmp_path):
+    """An image list with labels from path substrings (the reference's
+    training list and fillTruthSmooth): every fed image is the augmented
+    decoded file, its truth the one-hot of the label in its name."""
+    rng = np.random.default_rng(1)
+    (tmp_path / "train").mkdir()
+    paths, pix = [], []
+    for k in range(13):
+        p = tmp_path / "train" / f"img{k}{LABELS[k % 10]}.png"
+        img = rng.integers(0, 256, (32, 32, 3), dtype=np.uint8)
+        write_png(p, img)
+        paths.append(str(p))
+        pix.append(img)
+    lst = tmp_path / "train.list"
+    lst.write_text("\n".join(paths) + "\n")
+    net = tiny_net(8)
+    seed = 21
+    aug = aetcnn.Augment.defaults(32, angle=5, hue=0.05)
+    feeder = aetcnn.Feeder(net, threads=2, seed=seed, augment=aug, paths_list=str(lst),
+                           labels=LABELS)
+    try:
+        for bn in range(3):
+            feeder.next()
+            x, t = device_input(net)
+            idx = draw(seed, bn, np.arange(8), 0) % np.uint64(len(paths))
+            for i in range(8):
+                k = int(idx[i])
+                img = np.transpose(pix[k], (2, 0, 1)).astype(np.float32) / np.float32(255)
+                assert np.array_equal(x[i], aetcnn.augment_image(img, aug, seed, bn, i)), (bn, i)
+                want = np.zeros(10, np.float32)
+                want[k % 10] = 1
+                assert np.array_equal(t[i], want), (bn, i)
+            net.train_step()
+        assert np.isfinite(net.loss())
+    finally:
+        feeder.close()
+        net.close()
+
+
+def test_paths_source_errors(gpu, tmp_path):
+    """A path with no label (or two) refuses the list at creation; a file that
+    cannot be decoded makes an_feeder_next fail (the reference aborts)."""
+    net = tiny_net(8)
+    try:
+        lst = tmp_path / "bad.list"
+        lst.write_text(str(tmp_path / "x_nolabel.png") + "\n")
+        with pytest.raises(aetcnn.HipError):
+            aetcnn.Feeder(net, threads=1, paths_list=str(lst), labels=LABELS)
+        lst.write_text(str(tmp_path / "missing_c1_.png") + "\n")
+        f = aetcnn.Feeder(net, threads=1, paths_list=str(lst), labels=LABELS)
+        with pytest.raises(aetcnn.HipError):
+            f.next()
+        f.close()
+    finally:
+        net.close()

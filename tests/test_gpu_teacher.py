@@ -51,24 +51,51 @@ def param_layers(onet):
     return [i for i in range(onet.n_layers()) if onet.info(i)[0] == 0]
 
 
-def bias_truth(onet, i, b0, v0, lr, batch):
+def bias_truth(delta, b0, v0, lr, batch):
     """float64 biases after the step of a conv layer without BN: b0 + lr/B *
     (v0 + sum of its final delta over images and positions) -- the update
     (ConvolutionalLayer.c:959-980) of the bias gradient (BiasData.c:40-57)
-    in exact arithmetic, from the oracle's delta of the step."""
+    in exact arithmetic, from one network's delta of the step."""
     F = b0.size
-    d = onet.buffer(i, 1).reshape(batch, F, -1).astype(np.float64)
+    d = delta.reshape(batch, F, -1).astype(np.float64)
     db = d.sum(axis=(0, 2))
     return b0.astype(np.float64) + lr / batch * (v0.astype(np.float64) + db)
+
+
+def pool_route_flips(net, onet):
+    """Max-pool windows whose argmax differs between the networks, after
+    checking that each is a tie to fp32 rounding in the oracle's own input
+    (the two candidates within 1e-5 relative, or 1e-6 of the layer's largest
+    output for values near zero, as ReLU outputs): the layer below agrees only
+    to rounding, and the reference's strict '>' (MaxPoolLayer.c:252-262)
+    then picks either.  Returns the number of such windows."""
+    flips = 0
+    for j in range(1, onet.n_layers()):
+        if onet.info(j)[0] != 1:
+            continue
+        ig, io = net.buffer(j, 14), onet.buffer(j, 14)
+        bad = np.nonzero(ig != io)[0]
+        if not bad.size:
+            continue
+        x = onet.buffer(j - 1, 0)
+        a, b = x[ig[bad]], x[io[bad]]
+        tie = 1e-5 * np.abs(b) + 1e-6 * np.abs(x).max()
+        assert np.all(np.abs(a - b) <= tie), (j, bad[:5], a[:5], b[:5])
+        flips += bad.size
+    return flips
 
 
 def teacher_step(net, onet, name, step, batch):
     """One teacher-forced step; returns (|dloss|, worst parameter error).
     Biases of layers without BN are a plain sum of ~10^5 deltas that cancel
-    to a small total; where GPU and oracle differ by more than the bar there,
-    both are judged against float64 arithmetic (the GPU within the bar, and
-    no further from the oracle than the oracle is from float64), as for the
-    BN weight gradients in test_gpu_net.py."""
+    to a small total.  A max-pool window whose two largest inputs tie to
+    fp32 rounding may route its gradient to either (a handful of ~10^6 per
+    step in config 4), and the layers below carry the moved gradient into
+    those sums, which then differ by ~1e-3.  Where GPU and oracle biases
+    differ by more than the bar, every differing route must be such a tie
+    and each network's biases must be within the bar of the float64 update
+    of its own delta (the reduction is accurate; only the routing of its
+    input differs)."""
     layers = param_layers(onet)
     pre = {}
     for i in layers:
@@ -93,12 +120,16 @@ def teacher_step(net, onet, name, step, batch):
             got = net.buffer(i, code)
             e = rel_err(got, v)
             if e >= PARAM_TOL and code == 4 and onet.buffer(i, 6) is None:
-                exact = bias_truth(onet, i, pre[(i, 4)], pre[(i, 5)], lr, batch)
-                e_gpu, e_ref = rel_err(got, exact), rel_err(v, exact)
-                print(f"{name} step {step} layer {i} biases: gpu-oracle {e:.2g}, "
-                      f"gpu-f64 {e_gpu:.2g}, oracle-f64 {e_ref:.2g}")
-                assert e_gpu < PARAM_TOL and e <= e_ref + PARAM_TOL, (name, step, i, e, e_gpu,
-                                                                      e_ref)
+                flips = pool_route_flips(net, onet)
+                e_gpu = rel_err(got, bias_truth(net.buffer(i, 1), pre[(i, 4)], pre[(i, 5)],
+                                                lr, batch))
+                e_ref = rel_err(v, bias_truth(onet.buffer(i, 1), pre[(i, 4)], pre[(i, 5)],
+                                              lr, batch))
+                print(f"{name} step {step} layer {i} biases: gpu-oracle {e:.2g} after {flips} "
+                      f"tied max-pool routes; gpu-f64(own delta) {e_gpu:.2g}, "
+                      f"oracle-f64(own delta) {e_ref:.2g}")
+                assert flips and e_gpu < PARAM_TOL and e_ref < PARAM_TOL, (
+                    name, step, i, e, flips, e_gpu, e_ref)
                 e = e_gpu
             worst = max(worst, e)
             assert e < PARAM_TOL, (name, step, i, code, e)
