@@ -117,6 +117,8 @@ _OPS = {
                               _vp, _sz, _vp]),
     "ach_bn_train_fwd_from_x": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                                      _vp, _sz, _vp]),
+    "ach_bn_train_fwd_from_x_noalloc": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _i, _vp]),
     "ach_conv_prepare_filters": (_i, [_i, _vp, _vp]),
     "ach_conv_is_fully_connected": (_i, [C.POINTER(ConvDesc)]),
     "ach_conv_fwd_prepared": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _vp]),

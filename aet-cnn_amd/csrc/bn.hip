@@ -25,6 +25,8 @@
 // forward), so the activated tensor does not have to be re-read.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace ach {
 
 constexpr int BN_NT = 256;  // threads per block
@@ -529,6 +531,51 @@ int ach_bn_train_fwd_from_x(const float *x, float *out, int batch, int c, int sp
     if (!x || x == out) return ACH_EINVAL;
     return bn_fwd(x, nullptr, nullptr, out, batch, c, spatial, scales, biases, mean, variance,
                   rolling_mean, rolling_variance, activation, ws, ws_bytes, as_stream(stream));
+}
+
+// ---- allocation-free variant of ach_bn_train_fwd_from_x -----------------------
+// The per-(channel, image chunk) partial sums live in a file-scope device
+// array instead of a caller workspace.  Host code never passes the array's
+// name to a kernel: its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and cached here.
+static __device__ __align__(256) double scratch[ACH_BN_NOALLOC_SCRATCH_BYTES / sizeof(double)];
+
+static double *g_scratch_dev[ACH_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// device address of `scratch` on the current device (nullptr on error)
+static double *scratch_ptr()
+{
+    int dev = -1;
+    if (check(hipGetDevice(&dev)) || dev < 0 || dev >= ACH_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        if (check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))) return nullptr;
+        g_scratch_dev[dev] = static_cast<double *>(p);
+    }
+    return g_scratch_dev[dev];
+}
+
+int ach_bn_train_fwd_from_x_noalloc(const float *x, float *out, int batch, int c, int spatial,
+                                    const float *scales, const float *biases, float *mean,
+                                    float *variance, float *rolling_mean,
+                                    float *rolling_variance, int activation,
+                                    ach_stream_t stream)
+{
+    if (!x || x == out) return ACH_EINVAL;
+    if (batch <= 0 || c <= 0) return ACH_EINVAL;
+    const size_t need = bn_ws_bytes(batch, c);
+    if (need > ACH_BN_NOALLOC_SCRATCH_BYTES) {
+        set_error_message("ach_bn_train_fwd_from_x_noalloc: the partial sums of this shape "
+                          "exceed the fixed device scratch (ACH_BN_NOALLOC_SCRATCH_BYTES)");
+        return ACH_EWORKSPACE;
+    }
+    double *ws = scratch_ptr();
+    if (!ws) return ACH_EHIP;
+    // every partial is written before it is read: nothing to clear
+    return bn_fwd(x, nullptr, nullptr, out, batch, c, spatial, scales, biases, mean, variance,
+                  rolling_mean, rolling_variance, activation, ws, need, as_stream(stream));
 }
 
 int ach_bn_infer(const float *x, float *out, int batch, int c, int spatial,

@@ -11,6 +11,12 @@ namespace ach {
 
 // Records the last HIP error string for ach_last_hip_error().
 void set_hip_error(hipError_t e);
+// Records a message of this library for ach_last_hip_error().
+void set_error_message(const char *msg);
+
+// Devices whose per-device state (the device address of a file-scope
+// scratch array) the library caches.
+constexpr int ACH_MAX_DEVICES = 64;
 
 inline int check_launch()
 {

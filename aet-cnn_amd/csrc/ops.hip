@@ -29,6 +29,8 @@ void set_hip_error(hipError_t e)
              hipGetErrorString(e));
 }
 
+void set_error_message(const char *msg) { snprintf(g_last_err, sizeof(g_last_err), "%s", msg); }
+
 // ---- BLAS-1 ----------------------------------------------------------------
 __global__ void k_fill(float *x, size_t n, float v)
 {

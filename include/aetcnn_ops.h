@@ -193,6 +193,25 @@ int ach_bn_train_fwd_from_x(const float *x, float *out, int batch, int c, int sp
                             float *rolling_mean, float *rolling_variance,
                             int activation, void *ws, size_t ws_bytes,
                             ach_stream_t stream);
+/* Allocation-free variant of ach_bn_train_fwd_from_x.  No counterpart in
+ * the reference: it is for callers that cannot allocate or pass scratch
+ * memory (work recorded into a HIP graph, tight serving loops, harnesses
+ * that forbid hipMalloc).  The per-(channel, image chunk) partial sums go to
+ * a fixed device array of ACH_BN_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each device it runs on until the process ends; the call makes no
+ * allocation of any kind.  Same arguments and results as
+ * ach_bn_train_fwd_from_x without (ws, ws_bytes).  Limit: the partial sums
+ * (ach_bn_workspace(batch, c, spatial) bytes) must fit the array, which
+ * holds every shape with c <= 10922 channels; larger shapes return
+ * ACH_EWORKSPACE with a message in ach_last_hip_error().  Every call on one
+ * device shares that device's array: calls that overlap in time on one
+ * device (e.g. on two streams) race and must be ordered by the caller.    */
+#define ACH_BN_NOALLOC_SCRATCH_BYTES (256u * 1024u)
+int ach_bn_train_fwd_from_x_noalloc(const float *x, float *out, int batch, int c, int spatial,
+                                    const float *scales, const float *biases,
+                                    float *mean, float *variance,
+                                    float *rolling_mean, float *rolling_variance,
+                                    int activation, ach_stream_t stream);
 /* Inference (forwardNormCPU test branch, NLayer.c:155-160 ->
  * NormData.normalizeByRoll, NormData.c:291-326): out = act(((x - rolling_mean)
  * * inv) * scales + biases), inv = 1/(sqrt(rolling_variance) + 1e-6) in
