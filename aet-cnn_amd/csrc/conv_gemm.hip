@@ -24,9 +24,9 @@
 // scheduler is told to interleave them with the MFMAs so they issue in the
 // matrix pipe's shadow.  For 3x3 filters the k-tile is 18 = two input
 // channels, which makes the im2col (ki, kj) of every loaded row a
-// compile-time constant.  Workgroups are remapped so that the M-tiles
-// sharing an N-tile (the same input patch) run on the same XCD and share its
-// L2.
+// compile-time constant.  Workgroups are remapped so that neighbouring
+// tiles of one K slice (M-tiles sharing an input patch, N-tiles sharing a
+// delta slice) run on the same XCD and share its L2.
 #include "common.hpp"
 
 #include <type_traits>
@@ -1031,12 +1031,18 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
 
-    // XCD-aware tile order: the 8 XCDs take workgroups round-robin, so give
-    // XCD x the contiguous tile range [x*T/8, (x+1)*T/8) with M fastest.
-    const int nblk = mt * nt;
-    int lin = blockIdx.x;
-    if ((nblk & 7) == 0) lin = (lin & 7) * (nblk >> 3) + (lin >> 3);
-    const int m0 = (lin % mt) * BM, n0 = (lin / mt) * BN, z = blockIdx.y;
+    // XCD-aware order over the whole grid: the 8 XCDs take workgroups
+    // round-robin in dispatch order (x fastest, then y), so XCD x gets the
+    // contiguous range [x*G/8, (x+1)*G/8) of (K slice, tile) pairs, tile
+    // fastest and M fastest within it.  The tiles of one K slice then run
+    // together on one XCD and read their common operand (the weight-gradient
+    // GEMM's delta slice, a forward slice's filter rows) through one L2
+    // instead of through all eight.
+    const int nblk = mt * nt, total = nblk * (int)gridDim.y;
+    int lin = (int)blockIdx.y * nblk + (int)blockIdx.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    const int z = lin / nblk, tile = lin - z * nblk;
+    const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
 
     int kb, ke;
     p.krange(z, kb, ke);
@@ -1272,7 +1278,7 @@ template <class P>
 static int launch_gemm(const P &p, int M, int N, int splits, hipStream_t st)
 {
     const int mt = (M + P::BM - 1) / P::BM, nt = (N + P::BN - 1) / P::BN;
-    if ((long long)mt * nt > 0x7fffffffLL || splits > 65535) return ACH_EINVAL;
+    if ((long long)mt * nt * splits > 0x7fffffffLL || splits > 65535) return ACH_EINVAL;
     hipLaunchKernelGGL(k_mfma_gemm<P>, dim3(mt * nt, splits), dim3(GNT), 0, st, p, mt, nt);
     return check_launch();
 }

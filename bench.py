@@ -10,10 +10,17 @@ fwd+dgrad+wgrad TFLOP/s of the config-1 layer sweep.  Inputs are synthetic
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 import argparse
+import csv
 import ctypes as C
+import glob
 import json
 import os
+import shutil
+import signal
+import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -29,20 +36,29 @@ SWEEP = [  # config 1: (C_in, C_out, H, k, pad)
     (3, 128, 32, 3, 1), (128, 128, 32, 3, 1), (128, 256, 16, 3, 1), (256, 256, 16, 3, 1),
     (256, 512, 8, 3, 1), (512, 512, 8, 3, 1), (512, 10, 8, 1, 0),
 ]
-ROOFLINE_SHAPE = (256, 256, 16, 3, 1)  # dominant kernel probe: conv fwd GEMM
-# HBM bytes per probe call (filter transpose + split-K GEMM + split-K
-# reduction), from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs scaled by a
-# 256 MiB copy dispatch (profiles/conv_fwd_gemm_darknet_b128.md):
-# GEMM 53.7 MB read + 67.1 MB written, reduction 67.1 + 33.6 MB,
-# transpose 2.4 + 2.4 MB.
-ROOFLINE_TRAFFIC_BYTES = 226.2e6
+# Kernel probes, each one config-1 / config-3 layer pass launched back to
+# back on its own stream: the conv forward implicit GEMM (the kernel with the
+# most time per darknet step; the stride-1 input gradient runs it too) and
+# the weight-gradient GEMM (the second most).
+PROBES = {
+    "fwd": dict(shape=(256, 256, 16, 3, 1), op="fwd",
+                kernel="k_mfma_gemm<FwdProblem<256, BIm2col3F, true, false>> "
+                       "(conv fwd / stride-1 dgrad implicit GEMM)"),
+    "wgrad": dict(shape=(128, 128, 32, 3, 1), op="wgrad",
+                  kernel="k_mfma_gemm<WgradProblemC<128, 96, 3>> (conv weight-gradient GEMM)"),
+}
+CALIB_FLOATS = 1 << 26  # the 256 MiB copy-calibration dispatch
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def train_phase(aetcnn, configs, name, steps, warmup, batch):
+def train_phase(aetcnn, configs, name, steps, warmup, batch, sustain_s=0.0):
+    """Warm-up, then exactly `steps` timed steps between two device
+    synchronisations (the headline); then, untimed for the headline, steps in
+    blocks of 50 until `sustain_s` seconds have passed, reported as the
+    sustained rate (clock and thermal behaviour under load)."""
     lib = aetcnn.net_lib()
     lib.an_rand_seed(1)
     B, h, w, c = configs.dims(name, batch)
@@ -70,9 +86,21 @@ def train_phase(aetcnn, configs, name, steps, warmup, batch):
     ops.ach_event_elapsed_ms(ev0, ev1, C.byref(ms))
     loss = net.loss()
     gflop = net.conv_gflop()
+    sustained = None
+    if sustain_s > 0:
+        n = 0
+        s0 = time.perf_counter()
+        while time.perf_counter() - s0 < sustain_s:
+            for _ in range(50):
+                net.train_step()
+            aetcnn.check(ops.ach_device_sync(), "sync")
+            n += 50
+        ds = time.perf_counter() - s0
+        sustained = dict(seconds=round(ds, 2), steps=n, images_per_s=round(B * n / ds, 1),
+                         ms_per_step=round(ds * 1e3 / n, 4))
     net.close()
     return dict(wall_s=t1 - t0, gpu_ms=ms.value, loss=loss, first_loss=first_loss,
-                gflop_step=gflop, batch=B)
+                gflop_step=gflop, batch=B, sustained=sustained)
 
 
 def fed_phase(aetcnn, configs, name, steps, warmup, threads):
@@ -210,38 +238,147 @@ def sweep_phase(aetcnn, batch, reps):
     return rows, tot_flop / (tot_ms * 1e-3) / 1e12
 
 
-def roofline_phase(aetcnn, batch, reps):
-    """The dominant kernel of the training step -- the implicit-GEMM conv
-    forward (also used for the stride-1 input gradient) -- on one config-3 /
-    config-1 layer, launched `reps` times back to back on its own stream with
-    HIP events around the run.  Each ach_conv_fwd call is the filter
-    transpose (k_weights_kmajor, ~1% of the time), the GEMM (256 x 128
-    tiles, K split in two halves because the 256-tile grid is small) and the
-    fixed-order split-K reduction into NCHW (~6%); the average here is the
-    whole call, so it under-states the GEMM's own rate."""
+def probe_setup(aetcnn, which, batch):
+    """Operands of a kernel probe; returns (call, stream, free, flop, shape)."""
     ops = aetcnn.ops()
     D = aetcnn.DeviceArray
-    ci, co, hw, k, p = ROOFLINE_SHAPE
+    ci, co, hw, k, p = PROBES[which]["shape"]
     stream = C.c_void_p()
     aetcnn.check(ops.ach_stream_create(C.byref(stream)), "stream")
     d = aetcnn.ConvDesc(batch, ci, hw, hw, co, k, 1, p)
     rng = np.random.default_rng(1)
-    x = D.from_numpy(rng.uniform(-1, 1, (batch, ci, hw, hw)).astype(np.float32))
-    w = D.from_numpy((rng.standard_normal((co, ci, k, k)) * 0.05).astype(np.float32))
-    y = D((batch, co, hw, hw))
-    wsz = ops.ach_conv_fwd_workspace(C.byref(d))
+    xh, wh, dyh = config1_inputs(rng, batch, ci, co, hw, k, p)
+    x, w, dy = D.from_numpy(xh), D.from_numpy(wh), D.from_numpy(dyh)
+    y, dw = D(dyh.shape), D(wh.shape)
+    wsz = max(ops.ach_conv_fwd_workspace(C.byref(d)),
+              ops.ach_conv_bwd_filter_workspace(C.byref(d)), 256)
     ws = D(wsz // 4 + 64)
+    if PROBES[which]["op"] == "fwd":
+        def call():
+            aetcnn.check(ops.ach_conv_fwd(C.byref(d), x.ptr, w.ptr, y.ptr, ws.ptr, wsz, stream))
+    else:
+        def call():
+            aetcnn.check(ops.ach_conv_bwd_filter(C.byref(d), x.ptr, dy.ptr, dw.ptr, ws.ptr, wsz,
+                                                 stream))
 
-    def fwd():
-        aetcnn.check(ops.ach_conv_fwd(C.byref(d), x.ptr, w.ptr, y.ptr, ws.ptr, wsz, stream))
+    def free():
+        for a in (x, w, dy, y, dw, ws):
+            a.free()
+        ops.ach_stream_destroy(stream)
+    oh = hw + 2 * p - k + 1
+    flop = 2.0 * batch * co * oh * oh * ci * k * k
+    return call, stream, free, flop, f"{ci}->{co}@{hw}x{hw} k{k} b{batch}"
 
-    ms = time_launch(ops, stream, fwd, reps)
-    flop = 2.0 * batch * co * hw * hw * ci * k * k
-    for a in (x, w, y, ws):
-        a.free()
-    ops.ach_stream_destroy(stream)
-    return dict(kernel="k_mfma_gemm<FwdProblem<256, BIm2col3F, true, false>> (conv fwd / dgrad implicit GEMM)",
-                shape=f"{ci}->{co}@{hw}x{hw} k{k} b{batch}", flop=flop, ms=ms, reps=reps)
+
+def roofline_phase(aetcnn, which, batch, reps):
+    """A probe launched `reps` times back to back with HIP events around the
+    run on the probe's stream.  The forward call is the filter transpose
+    (k_weights_kmajor, ~1%), the GEMM (256 x 128 tiles, K split in two
+    halves because the 256-tile grid is small) and the fixed-order split-K
+    reduction into NCHW (~6%); the weight-gradient call is the GEMM over
+    chunked K and its fixed-order split-K reduction.  The average is the
+    whole call, so it under-states the GEMM's own rate."""
+    ops = aetcnn.ops()
+    call, stream, free, flop, shape = probe_setup(aetcnn, which, batch)
+    ms = time_launch(ops, stream, call, reps)
+    free()
+    return dict(kernel=PROBES[which]["kernel"], shape=shape, flop=flop, ms=ms, reps=reps)
+
+
+def traffic_probe_main(aetcnn, which, calls=3):
+    """Child of traffic_phase, run under rocprofv3 --pmc: the copy-calibration
+    dispatch, then `calls` probe calls."""
+    ops = aetcnn.ops()
+    call, stream, free, _, _ = probe_setup(aetcnn, which, 128)
+    aetcnn.check(ops.ach_device_sync(), "sync")
+    copy_calibration_phase(aetcnn)
+    for _ in range(calls):
+        call()
+    aetcnn.check(ops.ach_device_sync(), "sync")
+    free()
+
+
+def _pmc_dispatches(path):
+    """{dispatch id: (kernel name, summed counter value)} of a counter CSV."""
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = int(r["Dispatch_Id"])
+            name, v = out.get(k, (r["Kernel_Name"], 0.0))
+            out[k] = (name, v + float(r["Counter_Value"]))
+    return out
+
+
+def _short_kernel(name):
+    name = name.replace("void ", "").replace("ach::", "")
+    return name.split(">(")[0] + ">" if "k_mfma_gemm" in name else name.split("(")[0]
+
+
+def traffic_phase(which, calls=3, timeout=120):
+    """HBM bytes per probe call, measured in this run: two rocprofv3 --pmc
+    passes (FETCH_SIZE, then WRITE_SIZE) over a child process that runs the
+    256 MiB copy calibration (ach_scal: reads and writes exactly 256 MiB) and
+    `calls` probe calls; each counter is scaled by what it reads for the
+    calibration.  Returns a dict, or None and the reason."""
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None, "rocprofv3 not on PATH"
+    res, scale, kernels = {}, {}, {}
+    tmp = tempfile.mkdtemp(prefix="bench_pmc_")
+    try:
+        for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = os.path.join(tmp, ctr)
+            cmd = [prof, "--pmc", ctr, "-d", d, "-o", "pmc", "--output-format", "csv", "--",
+                   sys.executable, os.path.abspath(__file__), "--traffic-probe", which]
+            pr = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE,
+                                  start_new_session=True, cwd=tmp)
+            try:
+                _, err = pr.communicate(timeout=timeout)
+            except subprocess.TimeoutExpired:
+                os.killpg(pr.pid, signal.SIGKILL)
+                pr.wait()
+                return None, f"rocprofv3 --pmc {ctr} timed out after {timeout} s"
+            files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+            if not files:
+                tail = err.decode(errors="replace").strip().splitlines()[-1:] if err else []
+                return None, f"rocprofv3 --pmc {ctr} wrote no counters (rc {pr.returncode}: " \
+                             f"{' '.join(tail)})"
+            disp = _pmc_dispatches(files[0])
+            ids = sorted(disp)
+            cal = [i for i in ids if "k_scal" in disp[i][0]]
+            if len(cal) != 1:
+                return None, f"{ctr}: expected one calibration dispatch, found {len(cal)}"
+            expect_kib = CALIB_FLOATS * 4 / 1024.0
+            scale[ctr] = expect_kib / disp[cal[0]][1]
+            after = [i for i in ids if i > cal[0]]
+            ngemm = sum(1 for i in after if "k_mfma_gemm" in disp[i][0])
+            if ngemm != calls:
+                return None, f"{ctr}: expected {calls} GEMM dispatches, found {ngemm}"
+            tot = 0.0
+            for i in after:
+                b = disp[i][1] * scale[ctr] * 1024.0 / calls
+                tot += b
+                kn = _short_kernel(disp[i][0])
+                kernels.setdefault(kn, {}).setdefault(ctr, 0.0)
+                kernels[kn][ctr] += b
+            res[ctr] = tot
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return dict(read_bytes=round(res["FETCH_SIZE"]), write_bytes=round(res["WRITE_SIZE"]),
+                bytes=round(res["FETCH_SIZE"] + res["WRITE_SIZE"]),
+                scale={k: round(v, 4) for k, v in scale.items()},
+                per_kernel={k: {"read": round(v.get("FETCH_SIZE", 0.0)),
+                                "write": round(v.get("WRITE_SIZE", 0.0))}
+                            for k, v in kernels.items()}), None
+
+
+def algorithmic_bytes(which, batch=128):
+    """Operands each probe call must move at least once: conv forward reads
+    x and W and writes y; the weight gradient reads x and dy and writes dW."""
+    ci, co, hw, k, p = PROBES[which]["shape"]
+    oh = hw + 2 * p - k + 1
+    x, w, y = batch * ci * hw * hw, co * ci * k * k, batch * co * oh * oh
+    return 4.0 * (x + w + y)
 
 
 BW_SHAPE = (512, 128, 32, 32)  # config 2: x ~ N(0,1), S = 256 MiB per tensor
@@ -365,7 +502,7 @@ def bandwidth_phase(aetcnn, reps):
     return rows, round(ms * 1e3, 2)
 
 
-def copy_calibration_phase(aetcnn, nfloats=1 << 26):
+def copy_calibration_phase(aetcnn, nfloats=CALIB_FLOATS):
     """One ach_scal over a 256 MiB buffer (reads and writes exactly 256 MiB):
     the reference dispatch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE
     counters to bytes."""
@@ -378,14 +515,50 @@ def copy_calibration_phase(aetcnn, nfloats=1 << 26):
     return nfloats * 4
 
 
-def cpu_phase(configs, name, batch, steps, parallel=True):
+def host_cpu():
+    """The box's host CPU as BASELINE's protocol asks it stated."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(model=model, nproc=len(os.sched_getaffinity(0)), cpu_count=os.cpu_count(),
+                omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
+
+
+def oracle_native_build():
+    """Compiles the oracle with the reference's own flags (-march=native,
+    src/makefile:50) on this host into a temporary directory.  Returns
+    (library path, None), or (None, reason) to fall back to the prebuilt
+    x86-64-v3 library."""
+    if not shutil.which("make") or not shutil.which(os.environ.get("CC", "gcc")):
+        return None, "no compiler on this host"
+    out = tempfile.mkdtemp(prefix="oracle_native_")
+    try:
+        r = subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "native",
+                            f"OUT={out}"], capture_output=True, text=True, timeout=300)
+    except subprocess.TimeoutExpired:
+        return None, "native build timed out"
+    so = os.path.join(out, "liboracle.so")
+    if r.returncode != 0 or not os.path.exists(so):
+        return None, f"native build failed: {(r.stderr or r.stdout).strip()[-200:]}"
+    return so, None
+
+
+def cpu_phase(L, configs, name, batch, steps, parallel, build):
     """The oracle (CPU restatement of the reference CPU path) on a bounded
-    sample: `steps` training steps of the same network.  parallel=True is the
-    "oracle-parallel" mode (row-parallel GEMM over OpenMP threads, results
-    bit-identical to serial); parallel=False is "reference-faithful" (the
-    GEMM single-threaded as in the reference, Gemm.c:133)."""
+    sample, per BASELINE's protocol: 1 warm-up step, then `steps` steps
+    timed one by one on the wall clock, median extrapolated to images/s.
+    parallel=True is "oracle-parallel" (row-parallel GEMM over OpenMP
+    threads, results bit-identical to serial); parallel=False is
+    "reference-faithful" (the GEMM single-threaded as in the reference,
+    Gemm.c:133; the elementwise loops still use every OpenMP thread, as the
+    reference's own pragmas do)."""
     import oracle_lib
-    L = oracle_lib.lib()
     L.or_set_gemm_parallel(1 if parallel else 0)
     L.or_rand_seed(1)
     B, h, w, c = configs.dims(name, batch)
@@ -394,18 +567,22 @@ def cpu_phase(configs, name, batch, steps, parallel=True):
     onet.finalize()
     x, truth, _ = configs.synthetic_batch(name, 1234, B)
     onet.train(x, truth)  # warm-up step
-    t0 = time.perf_counter()
+    times = []
     for _ in range(steps):
+        t0 = time.perf_counter()
         onet.train(x, truth)
-    dt = time.perf_counter() - t0
-    threads = L.or_max_threads() if parallel else 1
+        times.append(time.perf_counter() - t0)
+    threads = int(L.or_max_threads())
     onet.close()
-    how = (f"row-parallel GEMM on {threads} OpenMP threads" if parallel
-           else "single-threaded GEMM (reference-faithful)")
-    return dict(value=round(B * steps / dt, 3), unit="images/s", cores=int(threads),
-                kind="port",
-                sample=f"oracle {name} net, batch {B}, {steps} timed steps after 1 warm-up, "
-                       f"{how} ({dt:.1f} s)")
+    med = statistics.median(times)
+    how = (f"GEMM row-parallel on {threads} OpenMP threads" if parallel
+           else f"GEMM single-threaded (reference-faithful), elementwise loops on {threads} "
+                f"OpenMP threads")
+    return dict(value=round(B / med, 3), unit="images/s", cores=threads,
+                gemm_threads=threads if parallel else 1, kind="port", build=build,
+                step_s=[round(v, 3) for v in times],
+                sample=f"oracle {name} net, batch {B}: 1 warm-up step, then the median of "
+                       f"{steps} timed steps ({med:.2f} s/step); {how}; built {build}")
 
 
 def main():
@@ -428,7 +605,15 @@ def main():
     ap.add_argument("--bandwidth-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=128)
-    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-faithful-batch", type=int, default=16)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 --pmc passes that measure roofline.traffic")
+    ap.add_argument("--traffic-probe", choices=sorted(PROBES),
+                    help="(internal) run one probe's traffic child under rocprofv3")
+    ap.add_argument("--sustain-s", type=float, default=10.0,
+                    help="seconds of further training after the timed steps, reported as the "
+                         "sustained rate (0 to skip)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -444,11 +629,16 @@ def main():
         sys.exit(1)
     aetcnn.check(ops.ach_set_device(0), "set_device")
 
+    if args.traffic_probe:
+        traffic_probe_main(aetcnn, args.traffic_probe)
+        return
     if args.roofline_only:
-        probe = roofline_phase(aetcnn, 128, args.roofline_reps)
+        rows = {}
+        for which in PROBES:
+            probe = roofline_phase(aetcnn, which, 128, args.roofline_reps)
+            rows[which] = {"ms": probe["ms"], "kernel": probe["kernel"], "shape": probe["shape"]}
         copy_calibration_phase(aetcnn)
-        print(json.dumps({"roofline_probe_ms": probe["ms"], "kernel": probe["kernel"],
-                          "shape": probe["shape"]}))
+        print(json.dumps({"roofline_probes": rows}))
         return
     if args.bandwidth_only:
         rows, softmax_us = bandwidth_phase(aetcnn, args.bandwidth_reps)
@@ -456,12 +646,16 @@ def main():
         return
 
     log(f"training phase: {args.config} b128, warmup {args.warmup}, steps {args.steps}")
-    tr = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None)
+    tr = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None,
+                     args.sustain_s)
     ms_step = tr["wall_s"] * 1e3 / args.steps
     ips = tr["batch"] * args.steps / tr["wall_s"]
     step_tflops = tr["gflop_step"] / (ms_step * 1e-3) / 1e3
     log(f"{ms_step:.3f} ms/step ({tr['gpu_ms'] / args.steps:.3f} GPU ms), {ips:.1f} img/s, "
         f"conv {step_tflops:.2f} TFLOP/s, loss {tr['first_loss']:.4f} -> {tr['loss']:.4f}")
+    if tr["sustained"]:
+        log(f"sustained over {tr['sustained']['seconds']} s: "
+            f"{tr['sustained']['images_per_s']} img/s")
 
     fed = None
     if not args.no_fed:
@@ -480,30 +674,54 @@ def main():
             log(f"bandwidth {r['op']}: {r['ms']:.4f} ms, {r['gbs']:.0f} GB/s "
                 f"({100 * r['frac']:.1f}% of HBM)")
         log(f"softmax+xent 512x1000: {softmax_us} us")
-    probe = roofline_phase(aetcnn, 128, args.roofline_reps)
-    copy_calibration_phase(aetcnn)
-    log(f"roofline probe {probe['shape']}: {probe['ms']:.4f} ms/launch over {probe['reps']}")
-
-    roofline = None
-    if probe:
+    rooflines = {}
+    for which in PROBES:
+        probe = roofline_phase(aetcnn, which, 128, args.roofline_reps)
+        log(f"roofline probe {which} {probe['shape']}: {probe['ms']:.4f} ms/launch over "
+            f"{probe['reps']}")
         ach = probe["flop"] / (probe["ms"] * 1e-3) / 1e12
-        roofline = dict(bound="mfma", achieved=round(ach, 3), peak=MFMA_FP32_PEAK_TFLOPS,
-                        unit="TFLOP/s", frac=round(ach / MFMA_FP32_PEAK_TFLOPS, 4),
-                        traffic=ROOFLINE_TRAFFIC_BYTES, kernel=probe["kernel"],
-                        shape=probe["shape"],
-                        avg_launch_ms=round(probe["ms"], 5), launches=probe["reps"],
-                        flop_per_launch=probe["flop"])
+        traffic, why = (None, "--no-traffic") if args.no_traffic else traffic_phase(which)
+        if traffic:
+            log(f"traffic {which}: {traffic['read_bytes'] / 1e6:.1f} MB read + "
+                f"{traffic['write_bytes'] / 1e6:.1f} MB written per call "
+                f"(algorithmic {algorithmic_bytes(which) / 1e6:.1f} MB)")
+        else:
+            log(f"traffic {which}: not measured ({why})")
+        rooflines[which] = dict(
+            bound="mfma", achieved=round(ach, 3), peak=MFMA_FP32_PEAK_TFLOPS, unit="TFLOP/s",
+            frac=round(ach / MFMA_FP32_PEAK_TFLOPS, 4),
+            traffic=traffic["bytes"] if traffic else None,
+            kernel=probe["kernel"], shape=probe["shape"], avg_launch_ms=round(probe["ms"], 5),
+            launches=probe["reps"], flop_per_launch=probe["flop"],
+            algorithmic_bytes=algorithmic_bytes(which),
+            traffic_detail=traffic if traffic else {"unmeasured": why})
 
     cpu = cpu_serial = None
+    host = host_cpu()
     if not args.no_cpu:
-        log("cpu baseline (oracle) ...")
+        log(f"cpu baseline (oracle) on {host['model']}, nproc {host['nproc']} ...")
+        so = None
         try:
-            cpu = cpu_phase(configs, args.config, args.cpu_batch, args.cpu_steps)
+            import oracle_lib
+            so, why = oracle_native_build()
+            build = "-O3 -ffast-math -march=native -fopenmp (the reference's flags)"
+            if so:
+                oracle_lib.set_library(so)
+            else:
+                build = f"-O3 -ffast-math -march=x86-64-v3 -fopenmp (prebuilt; {why})"
+            L = oracle_lib.lib()
+            cpu = cpu_phase(L, configs, args.config, args.cpu_batch, args.cpu_steps, True, build)
             log(f"cpu baseline: {cpu['value']} img/s on {cpu['cores']} threads")
-            cpu_serial = cpu_phase(configs, args.config, 16, 1, parallel=False)
+            cpu_serial = cpu_phase(L, configs, args.config, args.cpu_faithful_batch,
+                                   args.cpu_steps, False, build)
             log(f"cpu baseline (reference-faithful): {cpu_serial['value']} img/s")
         except Exception as e:  # the oracle is optional on the box
             log(f"cpu baseline skipped: {e}")
+        if so:  # loaded already; the scratch build directory can go
+            shutil.rmtree(os.path.dirname(so), ignore_errors=True)
+        for c in (cpu, cpu_serial):
+            if c:
+                c["host"] = host
 
     out = {
         "metric": "train images/s, fp32 32x32 13-conv net b=128; conv fwd+bwd TFLOP/s",
@@ -528,7 +746,9 @@ def main():
         "input_pipeline": fed,
         "bandwidth_ops": {"shape": "x[512][128][32][32] fp32 (config 2)", "ops": bw_rows,
                           "softmax_xent_512x1000_us": softmax_us},
-        "roofline": roofline,
+        "sustained": tr["sustained"],
+        "roofline": rooflines["fwd"],
+        "roofline_wgrad": rooflines["wgrad"],
         "cpu_baseline": cpu,
         "cpu_baseline_reference_faithful": cpu_serial,
     }

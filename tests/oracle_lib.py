@@ -89,6 +89,15 @@ _SIGS = {
 _lib = None
 
 
+def set_library(path: str):
+    """Use another build of the oracle (bench.py's CPU baseline compiles one
+    with -march=native on the host it runs on); before the first lib()."""
+    global ORACLE_SO
+    if _lib is not None and path != ORACLE_SO:
+        raise RuntimeError("oracle library already loaded from " + ORACLE_SO)
+    ORACLE_SO = path
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is None:
