@@ -24,6 +24,7 @@ ACH_EINVAL = -1
 ACH_EWORKSPACE = -2
 ACH_EHIP = -3
 ACH_EUNSUPPORTED = -4
+ACH_ENAN = -5
 
 LOGISTIC, RELU, LINEAR, LEAKY = 0, 1, 3, 7
 
@@ -50,6 +51,12 @@ class LayerOptions(C.Structure):
     """an_layer_options"""
     _fields_ = [("stopbackward", _i), ("onlyforward", _i), ("dontload", _i),
                 ("dontloadscales", _i), ("flipped", _i), ("learning_rate_scale", _f)]
+
+
+class Validation(C.Structure):
+    """an_validation: the result of an_validate_paths"""
+    _fields_ = [("images", _i), ("unlabeled", _i), ("topk", _i), ("top1_accuracy", _f),
+                ("topk_accuracy", _f)]
 
 
 class Augment(C.Structure):
@@ -148,6 +155,7 @@ _OPS = {
     "ach_dropout_fwd_dev": (_i, [_vp, _sz, _f, _u64, _vp, _u32, _vp]),
     "ach_dropout_bwd_dev": (_i, [_vp, _sz, _f, _u64, _vp, _u32, _vp]),
     "ach_counter_add": (_i, [_vp, _u32, _vp]),
+    "ach_nan_scan": (_i, [_vp, _i, _vp, _vp]),
     "ach_graph_capture_begin": (_i, [_vp]),
     "ach_graph_capture_end": (_i, [_vp, C.POINTER(_vp)]),
     "ach_graph_launch": (_i, [_vp, _vp]),
@@ -185,6 +193,7 @@ _NET = {
     "an_train_step": (_i, [_vp]),
     "an_set_graph": (_i, [_vp, _i]),
     "an_get_loss": (_i, [_vp, C.POINTER(_f)]),
+    "an_nan_status": (_i, [_vp, C.POINTER(_i), C.POINTER(_i)]),
     "an_train": (_i, [_vp, _vp, _vp, C.POINTER(_f)]),
     "an_forward": (_i, [_vp, _i]),
     "an_predict": (_i, [_vp, _vp, _vp]),
@@ -201,6 +210,12 @@ _NET = {
     "an_image_distort": (None, [_vp, _i, _i, _f, _f, _f]),
     "an_image_resize": (None, [_vp, _i, _i, _i, _i, _i, _vp]),
     "an_image_load": (_i, [C.c_char_p, _i, _i, _i, _vp]),
+    "an_image_read": (_i, [C.c_char_p, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_vp)]),
+    "an_image_free": (None, [_vp]),
+    "an_image_resize_min_size": (None, [_i, _i, _i, C.POINTER(_i), C.POINTER(_i)]),
+    "an_image_crop": (None, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "an_validation_image": (_i, [C.c_char_p, _i, _i, _i, _vp]),
+    "an_validate_paths": (_i, [_vp, C.c_char_p, _vp, _i, _i, C.POINTER(Validation)]),
     "an_label_from_path": (_i, [C.c_char_p, _vp, _i]),
     "an_feeder_next": (_i, [_vp]),
     "an_feeder_served": (_u64, [_vp]),
@@ -470,6 +485,15 @@ class Network:
         check(self.lib.an_predict(self.h, x.ctypes.data, out.ctypes.data), "an_predict")
         return out
 
+    def validate(self, list_file: str, labels, topk: int = 1) -> Validation:
+        """an_validate_paths (Classifier.validateSingle): top-1 / top-k
+        accuracy over an image list with labels from path substrings"""
+        arr = _cstrings(labels)
+        res = Validation()
+        check(self.lib.an_validate_paths(self.h, os.fsencode(list_file), C.cast(arr, _vp),
+                                         len(labels), topk, C.byref(res)), "an_validate_paths")
+        return res
+
     def fuse_conv_batchnorm(self):
         """NNetwork.fuseConvBatchnorm: fold the inference BN of every BN conv
         layer into its filters and biases (the layers become plain convs)"""
@@ -479,6 +503,16 @@ class Network:
         v = _f()
         check(self.lib.an_get_loss(self.h, C.byref(v)), "an_get_loss")
         return v.value
+
+    def nan_status(self):
+        """None while clean, else (layer, what) of the first batch-norm array
+        found holding a NaN: what 0 mean, 1 variance, 2 scales, 3 scale
+        updates (an_nan_status)."""
+        layer, what = _i(), _i()
+        rc = self.lib.an_nan_status(self.h, C.byref(layer), C.byref(what))
+        if rc < 0:
+            check(rc, "an_nan_status")
+        return (layer.value, what.value) if rc else None
 
     def forward(self, train=1):
         check(self.lib.an_forward(self.h, train), "an_forward")
@@ -539,6 +573,53 @@ class Network:
             self.close()
         except Exception:
             pass
+
+
+def image_read(path: str, c: int) -> np.ndarray:
+    """an_image_read: a file at its own size as float planes [c][h][w], with
+    c channels converted as the reference's stb_image load does"""
+    w, h, p = _i(), _i(), _vp()
+    lib = net_lib()
+    check(lib.an_image_read(os.fsencode(path), c, C.byref(w), C.byref(h), C.byref(p)),
+          "an_image_read")
+    try:
+        arr = np.ctypeslib.as_array(C.cast(p, C.POINTER(_f)), shape=(c, h.value, w.value)).copy()
+    finally:
+        lib.an_image_free(p)
+    return arr
+
+
+def resize_min_size(W: int, H: int, mn: int):
+    """an_image_resize_min_size: (w, h) of NImage.resizeMin"""
+    w, h = _i(), _i()
+    net_lib().an_image_resize_min_size(W, H, mn, C.byref(w), C.byref(h))
+    return w.value, h.value
+
+
+def image_crop(src: np.ndarray, dx: int, dy: int, w: int, h: int) -> np.ndarray:
+    """an_image_crop (NImage.crop) of host planes [c][H][W]"""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    c, H, W = src.shape
+    dst = np.empty((c, h, w), np.float32)
+    net_lib().an_image_crop(src.ctypes.data, W, H, c, dx, dy, w, h, dst.ctypes.data)
+    return dst
+
+
+def image_resize(src: np.ndarray, w: int, h: int) -> np.ndarray:
+    """an_image_resize (NImage.resizeImage) of host planes [c][H][W]"""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    c, H, W = src.shape
+    dst = np.empty((c, h, w), np.float32)
+    net_lib().an_image_resize(src.ctypes.data, W, H, c, w, h, dst.ctypes.data)
+    return dst
+
+
+def validation_image(path: str, w: int, h: int, c: int) -> np.ndarray:
+    """an_validation_image: read, resize-min, centre crop"""
+    dst = np.empty((c, h, w), np.float32)
+    check(net_lib().an_validation_image(os.fsencode(path), w, h, c, dst.ctypes.data),
+          "an_validation_image")
+    return dst
 
 
 def top_k(a: np.ndarray, k: int) -> np.ndarray:

@@ -1204,6 +1204,28 @@ int ach_counter_add(uint32_t *counter, uint32_t v, ach_stream_t s)
     return check_launch();
 }
 
+// ---- NaN scan: one workgroup per listed array ------------------------------
+__global__ void __launch_bounds__(256) k_nan_scan(const ach_nan_span *__restrict__ spans,
+                                                  int nspans, int32_t *flag)
+{
+    for (int s = blockIdx.x; s < nspans; s += gridDim.x) {
+        const float *p = spans[s].p;
+        const uint64_t n = spans[s].n;
+        int bad = 0;
+        for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) bad |= isnan(p[i]);
+        if (__syncthreads_or(bad) && threadIdx.x == 0) atomicMin(flag, spans[s].tag);
+    }
+}
+
+int ach_nan_scan(const ach_nan_span *spans, int nspans, int32_t *flag, ach_stream_t s)
+{
+    if (nspans <= 0) return ACH_OK;
+    if (!spans || !flag) return ACH_EINVAL;
+    const int grid = nspans < 1024 ? nspans : 1024;
+    hipLaunchKernelGGL(k_nan_scan, dim3(grid), dim3(256), 0, as_stream(s), spans, nspans, flag);
+    return check_launch();
+}
+
 // ---- HIP graphs: record a stream's work once, replay it -----------------
 int ach_graph_capture_begin(ach_stream_t s)
 {

@@ -80,9 +80,10 @@ static int paeth(int a, int b, int c)
 }
 
 /* PNG (ISO/IEC 15948): 8-bit samples, no interlace.  Native channels:
- * grey 1, RGB 3, palette 3 (4 with a tRNS chunk), grey+alpha 2, RGBA 4.   */
-static int load_png(const char *path, const unsigned char *buf, size_t len, int w, int h, int c,
-                    float *dst)
+ * grey 1, RGB 3, palette 3 (4 with a tRNS chunk), grey+alpha 2, RGBA 4.
+ * *px: W*H*chans interleaved 8-bit samples (malloc'd).                     */
+static int decode_png(const char *path, const unsigned char *buf, size_t len, int *Wp, int *Hp,
+                      int *chansp, unsigned char **px)
 {
     static const unsigned char sig[8] = {137, 80, 78, 71, 13, 10, 26, 10};
     if (len < 8 || memcmp(buf, sig, 8)) return fail(path, "not a PNG file");
@@ -144,9 +145,8 @@ static int load_png(const char *path, const unsigned char *buf, size_t len, int 
     }
     if (rc == ACH_OK && (depth != 8 || interlace != 0))
         rc = fail(path, "only 8-bit non-interlaced PNG is supported");
-    /* NImage.reload: the file must have the network's size and channels */
-    if (rc == ACH_OK && (W != w || H != h || chans != c))
-        rc = fail(path, "image size or channel count differs from the network input");
+    if (rc == ACH_OK && (W <= 0 || H <= 0 || W > (1 << 15) || H > (1 << 15)))
+        rc = fail(path, "image size out of range");
     if (rc == ACH_OK && !idat) rc = fail(path, "no image data");
     const int spp = ctype == 3 ? 1 : chans; /* bytes per pixel in the stream */
     const size_t stride = (size_t)W * spp;
@@ -186,36 +186,47 @@ static int load_png(const char *path, const unsigned char *buf, size_t len, int 
             }
         }
     }
+    unsigned char *out = NULL;
     if (rc == ACH_OK) {
-        const size_t plane = (size_t)W * H;
+        out = (unsigned char *)malloc((size_t)W * H * chans);
+        if (!out) rc = fail(path, "out of host memory");
+    }
+    if (rc == ACH_OK) {
         for (int y = 0; y < H; ++y) {
             const unsigned char *cur = raw + (size_t)y * (stride + 1) + 1;
+            unsigned char *o = out + (size_t)y * W * chans;
             for (int x = 0; x < W; ++x)
                 for (int k = 0; k < chans; ++k) {
-                    unsigned char v;
                     if (ctype == 3) {
                         const int idx = cur[x];
                         if (idx >= npal) {
                             rc = fail(path, "palette index out of range");
                             goto done;
                         }
-                        v = pal[idx][k];
+                        o[(size_t)x * chans + k] = pal[idx][k];
                     } else {
-                        v = cur[(size_t)x * chans + k];
+                        o[(size_t)x * chans + k] = cur[(size_t)x * chans + k];
                     }
-                    dst[k * plane + (size_t)y * W + x] = (float)v / 255.0f;
                 }
         }
     }
 done:
     free(raw);
     free(idat);
-    return rc;
+    if (rc != ACH_OK) {
+        free(out);
+        return rc;
+    }
+    *Wp = W;
+    *Hp = H;
+    *chansp = chans;
+    *px = out;
+    return ACH_OK;
 }
 
 /* binary PPM (P6, 3 channels) / PGM (P5, 1 channel), maxval 255 */
-static int load_pnm(const char *path, const unsigned char *buf, size_t len, int w, int h, int c,
-                    float *dst)
+static int decode_pnm(const char *path, const unsigned char *buf, size_t len, int *Wp, int *Hp,
+                      int *chansp, unsigned char **px)
 {
     const int chans = buf[1] == '6' ? 3 : 1;
     size_t pos = 2;
@@ -238,30 +249,151 @@ static int load_pnm(const char *path, const unsigned char *buf, size_t len, int 
     if (nv < 3 || pos >= len) return fail(path, "bad PNM header");
     ++pos; /* the single whitespace after maxval */
     if (vals[2] != 255) return fail(path, "only maxval 255 is supported");
-    if (vals[0] != w || vals[1] != h || chans != c)
-        return fail(path, "image size or channel count differs from the network input");
-    const size_t plane = (size_t)w * h;
-    if (len - pos < plane * chans) return fail(path, "truncated image data");
-    for (size_t p = 0; p < plane; ++p)
-        for (int k = 0; k < chans; ++k) dst[k * plane + p] = (float)buf[pos + p * chans + k] / 255.0f;
+    if (vals[0] <= 0 || vals[1] <= 0 || vals[0] > (1 << 15) || vals[1] > (1 << 15))
+        return fail(path, "image size out of range");
+    const size_t n = (size_t)vals[0] * vals[1] * chans;
+    if (len - pos < n) return fail(path, "truncated image data");
+    unsigned char *out = (unsigned char *)malloc(n);
+    if (!out) return fail(path, "out of host memory");
+    memcpy(out, buf + pos, n);
+    *Wp = vals[0];
+    *Hp = vals[1];
+    *chansp = chans;
+    *px = out;
     return ACH_OK;
 }
 
-int an_image_load(const char *path, int w, int h, int c, float *dst)
+/* the file's pixels at their native size and channel count */
+static int decode_file(const char *path, int *W, int *H, int *chans, unsigned char **px)
 {
-    if (!path || !dst || w <= 0 || h <= 0 || c <= 0) return ACH_EINVAL;
     size_t len = 0;
     unsigned char *buf = read_file(path, &len);
     if (!buf) return fail(path, "cannot read");
     int rc;
     if (len >= 8 && buf[0] == 137 && buf[1] == 'P' && buf[2] == 'N' && buf[3] == 'G')
-        rc = load_png(path, buf, len, w, h, c, dst);
+        rc = decode_png(path, buf, len, W, H, chans, px);
     else if (len >= 3 && buf[0] == 'P' && (buf[1] == '5' || buf[1] == '6'))
-        rc = load_pnm(path, buf, len, w, h, c, dst);
+        rc = decode_pnm(path, buf, len, W, H, chans, px);
     else
         rc = fail(path, "unsupported format (PNG, binary PPM / PGM)");
     free(buf);
     return rc;
+}
+
+/* interleaved 8-bit samples -> planar floats / 255 (NImage.reload's loop) */
+static void to_planes(const unsigned char *px, int W, int H, int c, float *dst)
+{
+    const size_t plane = (size_t)W * H;
+    for (size_t p = 0; p < plane; ++p)
+        for (int k = 0; k < c; ++k) dst[k * plane + p] = (float)px[p * c + k] / 255.0f;
+}
+
+int an_image_load(const char *path, int w, int h, int c, float *dst)
+{
+    if (!path || !dst || w <= 0 || h <= 0 || c <= 0) return ACH_EINVAL;
+    int W, H, chans;
+    unsigned char *px = NULL;
+    int rc = decode_file(path, &W, &H, &chans, &px);
+    if (rc) return rc;
+    /* NImage.reload: the file must have the network's size and channels */
+    if (W != w || H != h || chans != c)
+        rc = fail(path, "image size or channel count differs from the network input");
+    else
+        to_planes(px, W, H, c, dst);
+    free(px);
+    return rc;
+}
+
+/* The channel conversion of stb_image's loader when a channel count is
+ * requested (the reference's NImage.createImage asks for 3): grey is
+ * replicated, alpha dropped or set opaque, and RGB turns grey as
+ * (77 r + 150 g + 29 b) >> 8.                                               */
+static unsigned char luma(const unsigned char *p)
+{
+    return (unsigned char)((p[0] * 77 + p[1] * 150 + p[2] * 29) >> 8);
+}
+
+static void convert_channels(const unsigned char *in, int from, unsigned char *out, int to,
+                             size_t npix)
+{
+    for (size_t i = 0; i < npix; ++i) {
+        const unsigned char *s = in + i * from;
+        unsigned char *d = out + i * to;
+        unsigned char g, a = 255, rgb[3];
+        switch (from) {
+        case 1: g = s[0]; rgb[0] = rgb[1] = rgb[2] = g; break;
+        case 2: g = s[0]; a = s[1]; rgb[0] = rgb[1] = rgb[2] = g; break;
+        case 3: rgb[0] = s[0]; rgb[1] = s[1]; rgb[2] = s[2]; g = luma(s); break;
+        default: rgb[0] = s[0]; rgb[1] = s[1]; rgb[2] = s[2]; a = s[3]; g = luma(s); break;
+        }
+        switch (to) {
+        case 1: d[0] = g; break;
+        case 2: d[0] = g; d[1] = a; break;
+        case 3: d[0] = rgb[0]; d[1] = rgb[1]; d[2] = rgb[2]; break;
+        default: d[0] = rgb[0]; d[1] = rgb[1]; d[2] = rgb[2]; d[3] = a; break;
+        }
+    }
+}
+
+int an_image_read(const char *path, int c, int *w, int *h, float **dst)
+{
+    if (!path || !w || !h || !dst || c < 1 || c > 4) return ACH_EINVAL;
+    int W, H, chans;
+    unsigned char *px = NULL;
+    int rc = decode_file(path, &W, &H, &chans, &px);
+    if (rc) return rc;
+    unsigned char *cv = px;
+    if (chans != c) {
+        cv = (unsigned char *)malloc((size_t)W * H * c);
+        if (!cv) {
+            free(px);
+            return fail(path, "out of host memory");
+        }
+        convert_channels(px, chans, cv, c, (size_t)W * H);
+    }
+    float *out = (float *)malloc(sizeof(float) * (size_t)W * H * c);
+    if (!out) rc = fail(path, "out of host memory");
+    else to_planes(cv, W, H, c, out);
+    if (cv != px) free(cv);
+    free(px);
+    if (rc) return rc;
+    *w = W;
+    *h = H;
+    *dst = out;
+    return ACH_OK;
+}
+
+void an_image_free(float *im) { free(im); }
+
+/* NImage.resizeMin (NImage.c:1037-1051): the size whose smaller side is min,
+ * the other scaled in integer arithmetic                                     */
+void an_image_resize_min_size(int W, int H, int min, int *w, int *h)
+{
+    if (W < H) {
+        *h = (H * min) / W;
+        *w = min;
+    } else {
+        *w = (W * min) / H;
+        *h = min;
+    }
+}
+
+/* NImage.crop (NImage.c:439-458): the w x h window at (dx, dy), coordinates
+ * clamped to the image                                                      */
+void an_image_crop(const float *src, int W, int H, int c, int dx, int dy, int w, int h,
+                   float *dst)
+{
+    for (int k = 0; k < c; ++k)
+        for (int j = 0; j < h; ++j) {
+            int r = j + dy;
+            r = r < 0 ? 0 : (r > H - 1 ? H - 1 : r);
+            for (int i = 0; i < w; ++i) {
+                int cc = i + dx;
+                cc = cc < 0 ? 0 : (cc > W - 1 ? W - 1 : cc);
+                dst[(size_t)k * w * h + (size_t)j * w + i] =
+                    src[(size_t)k * W * H + (size_t)r * W + cc];
+            }
+        }
 }
 
 /* ---- labels from paths (ImageData.fillTruthSmooth, ImageData.c:80-104) ----- */

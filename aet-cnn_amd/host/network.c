@@ -88,6 +88,14 @@ struct an_network {
      * is frozen (train = 0): updates then run layer by layer after the
      * backward loop instead of the flat or early forms                     */
     int layer_opts;
+    /* the reference's NaN checks (NormData.c:273-276, ScaleData.c:51-54,
+     * 67-70) as one scan per step over every batch-norm layer's mean,
+     * variance, scales and scale updates (device table of spans); the flag
+     * keeps the smallest tag, layer * 4 + (0 mean, 1 variance, 2 scales,
+     * 3 scale updates), of an array holding a NaN, INT32_MAX while clean   */
+    ach_nan_span *d_nan_spans;
+    int n_nan_spans;
+    int32_t *d_nan_flag;
 };
 
 /* ---- randUniform over glibc rand() (DnnUtils.c:196-209) ------------------- */
@@ -775,6 +783,44 @@ int an_get_layer_options(const an_network *net, int layer, an_layer_options *opt
     return ACH_OK;
 }
 
+/* the NaN scan's span table and flag (their own small allocation) */
+static int setup_nan_scan(an_network *net)
+{
+    int nbn = 0;
+    for (int i = 0; i < net->n; ++i)
+        if (net->layers[i]->type == AN_CONVOLUTIONAL && net->layers[i]->batch_normalize) ++nbn;
+    if (!nbn) return ACH_OK;
+    ach_nan_span *h = (ach_nan_span *)calloc((size_t)nbn * 4, sizeof(ach_nan_span));
+    if (!h) return ACH_EINVAL;
+    int k = 0;
+    for (int i = 0; i < net->n; ++i) {
+        const an_layer *l = net->layers[i];
+        if (l->type != AN_CONVOLUTIONAL || !l->batch_normalize) continue;
+        const float *arr[4] = {l->mean, l->variance, l->scales, l->scale_updates};
+        for (int j = 0; j < 4; ++j, ++k) {
+            h[k].p = arr[j];
+            h[k].n = (uint64_t)l->n;
+            h[k].tag = i * 4 + j;
+        }
+    }
+    const size_t tb = (sizeof(ach_nan_span) * (size_t)k + 255) & ~(size_t)255;
+    void *mem = NULL;
+    int rc = ach_malloc(&mem, tb + 256);
+    const int32_t clean = INT32_MAX;
+    if (!rc) rc = ach_memcpy_h2d(mem, h, sizeof(ach_nan_span) * (size_t)k, net->stream);
+    if (!rc) rc = ach_memcpy_h2d((char *)mem + tb, &clean, sizeof(clean), net->stream);
+    if (!rc) rc = ach_stream_sync(net->stream);
+    free(h);
+    if (rc) {
+        ach_free(mem);
+        return rc;
+    }
+    net->d_nan_spans = (ach_nan_span *)mem;
+    net->d_nan_flag = (int32_t *)((char *)mem + tb);
+    net->n_nan_spans = k;
+    return ACH_OK;
+}
+
 int an_finalize(an_network *net)
 {
     if (!net || net->finalized || net->n == 0) return ACH_EINVAL;
@@ -895,6 +941,7 @@ int an_finalize(an_network *net)
         j->wt = l->weights_kmajor;
         j->wft = i > 0 ? l->weights_flipped : NULL;
     }
+    AN_CHECK(setup_nan_scan(net));
     /* zero everything once (momentum buffers, biases, stats, deltas) */
     AN_CHECK(ach_fill((float *)net->arena, net->arena_bytes / sizeof(float), 0.f, net->stream));
     for (int i = 0; i < net->n; ++i) {
@@ -938,6 +985,7 @@ void an_free(an_network *net)
         free(net->ev_dgrad);
     }
     if (net->ev_joined) ach_event_destroy(net->ev_joined);
+    ach_free(net->d_nan_spans);
     ach_free(net->arena);
     if (net->wstream) ach_stream_destroy(net->wstream);
     ach_stream_destroy(net->stream);
@@ -1169,6 +1217,7 @@ static int enqueue_step(an_network *net, int update, float rate)
     net->early_update = 0;
     AN_CHECK(rc);
     if (update && net->layer_opts) AN_CHECK(update_at_rate(net, rate));
+    AN_CHECK(ach_nan_scan(net->d_nan_spans, net->n_nan_spans, net->d_nan_flag, net->stream));
     return net->recording ? ach_counter_add(net->d_iter, 1u, net->stream) : ACH_OK;
 }
 
@@ -1213,9 +1262,30 @@ int an_train_step(an_network *net)
     return ACH_OK;
 }
 
+int an_nan_status(an_network *net, int *layer, int *what)
+{
+    if (!net || !net->finalized) return ACH_EINVAL;
+    int32_t f = INT32_MAX;
+    if (net->d_nan_flag) AN_CHECK(ach_memcpy_d2h(&f, net->d_nan_flag, sizeof(f), net->stream));
+    if (f == INT32_MAX) return 0;
+    if (layer) *layer = f / 4;
+    if (what) *what = f % 4;
+    return 1;
+}
+
 int an_get_loss(an_network *net, float *loss)
 {
     if (!net || !net->finalized || !loss) return ACH_EINVAL;
+    int nl = -1, nw = 0;
+    const int nan = an_nan_status(net, &nl, &nw);
+    if (nan < 0) return nan;
+    if (nan) {
+        static const char *what[4] = {"mean", "variance", "scales", "scale updates"};
+        fprintf(stderr, "an_get_loss: layer %d: NaN in its batch-norm %s (the reference's CPU "
+                "path exits here, %s)\n", nl, what[nw],
+                nw < 2 ? "NormData.c:273-276" : "ScaleData.c:51-54, 67-70");
+        return ACH_ENAN;
+    }
     float sum = 0;
     int count = 0;
     for (int i = 0; i < net->n; ++i) {
@@ -1229,7 +1299,7 @@ int an_get_loss(an_network *net, float *loss)
     /* getNetworkCost (NNetwork.c:611-624), then / (subdivisions*batch) */
     const float cost = count ? sum / count : 0.f;
     *loss = cost / net->batch;
-    if (isnan(*loss)) return ACH_EINVAL; /* the CPU path aborts on NaN */
+    if (isnan(*loss)) return ACH_ENAN; /* the CPU path aborts on NaN */
     return ACH_OK;
 }
 

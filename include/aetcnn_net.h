@@ -258,9 +258,42 @@ void an_image_resize(const float *src, int W, int H, int c, int w, int h, float 
  * pixels and c channels (else ACH_EINVAL with a message).  The reference
  * decodes through stb_image; JPEG and other formats are not supported.     */
 int an_image_load(const char *path, int w, int h, int c, float *dst);
+/* NImage.createImage (NImage.c:587-610): decodes a file at its own size
+ * into *dst = malloc'd planes [c][*h][*w] (free with an_image_free), with
+ * c (1-4) channels whatever the file holds, converted as stb_image does
+ * when the reference asks for a channel count: grey replicated, alpha
+ * dropped or opaque, RGB to grey as (77 r + 150 g + 29 b) >> 8.           */
+int an_image_read(const char *path, int c, int *w, int *h, float **dst);
+void an_image_free(float *im);
+/* NImage.resizeMin (NImage.c:1037-1051): the w x h whose smaller side is
+ * min (integer scaling of the other side); NImage.crop (NImage.c:439-458):
+ * the w x h window at (dx, dy) with coordinates clamped into the image     */
+void an_image_resize_min_size(int W, int H, int min, int *w, int *h);
+void an_image_crop(const float *src, int W, int H, int c, int dx, int dy, int w, int h,
+                   float *dst);
 /* ImageData.fillTruthSmooth (ImageData.c:80-104): the index of the one
  * label that occurs in path as a substring, or -1 for none or several     */
 int an_label_from_path(const char *path, const char *const *labels, int nlabels);
+
+/* ---- validation (Classifier.validateSingle, Classifier.c:359-464) ---------
+ * For every path of list_file: its class is the first label that occurs in
+ * it (-1, a miss, when none does); the image is read at its own size with
+ * the network's channel count, resized so its smaller side is the network
+ * width, cut to the network's w x h around its centre
+ * (an_validation_image), predicted (an_predict, the images filling the
+ * network's batch; a last partial batch padded with zero images) and its
+ * topk best classes taken (an_top_k; topk is clamped to the classes).
+ * top1_accuracy / topk_accuracy: the fraction of images whose class is the
+ * best / among the topk best.  The reference predicts one image at a time
+ * on a batch-1 network; inference is per image, so batching it changes
+ * only the rounding of the convolutions' sums.                              */
+typedef struct {
+    int images, unlabeled, topk;
+    float top1_accuracy, topk_accuracy;
+} an_validation;
+int an_validate_paths(an_network *net, const char *list_file, const char *const *labels,
+                      int nlabels, int topk, an_validation *result);
+int an_validation_image(const char *path, int w, int h, int c, float *dst);
 
 /* ---- input pipeline (ImageData.c:20-224, DstbCompute.c:60-216) ------------
  * Worker threads fill two pinned host batches; an_feeder_next copies the next
@@ -324,8 +357,18 @@ int an_train_step(an_network *net);
  * recorded one re-records it.  Needs subdivisions == 1 (ACH_EINVAL).      */
 int an_set_graph(an_network *net, int on);
 /* synchronises and returns sum(cost)/batch of the last minibatch (the
- * reference returns the mean of these over the subdivisions, NNetwork.c:804) */
+ * reference returns the mean of these over the subdivisions, NNetwork.c:804).
+ * Returns ACH_ENAN, with a message on stderr, where the reference's CPU path
+ * stops on a NaN: a NaN loss, or a NaN that a training step left in a
+ * batch-norm layer's mean or variance (NormData.normalize exits on a NaN
+ * normalized value, NormData.c:273-276) or in its scales or scale updates
+ * (ScaleData.c:51-54, 67-70).  Every step ends with one scan of those arrays
+ * (ach_nan_scan); the finding is sticky, as the state then holds the NaN.  */
 int an_get_loss(an_network *net, float *loss);
+/* synchronises; 0 while no step has left a NaN in those arrays, else 1 with
+ * *layer the first such layer and *what 0 mean, 1 variance, 2 scales,
+ * 3 scale updates.  No counterpart in the reference (it exits instead).   */
+int an_nan_status(an_network *net, int *layer, int *what);
 /* host-buffer convenience: set_input + train_step + get_loss               */
 int an_train(an_network *net, const float *host_input, const float *host_truth, float *loss);
 int an_forward(an_network *net, int train);

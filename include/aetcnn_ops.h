@@ -32,6 +32,7 @@ extern "C" {
 #define ACH_EWORKSPACE (-2) /* workspace missing or too small               */
 #define ACH_EHIP (-3)       /* HIP runtime error (ach_last_hip_error())     */
 #define ACH_EUNSUPPORTED (-4)
+#define ACH_ENAN (-5)       /* a NaN where the reference's CPU path exits    */
 
 /* Activation ids = the reference's ActivationType order (Activation.h). */
 #define ACH_LOGISTIC 0
@@ -326,6 +327,21 @@ int ach_dropout_bwd_dev(float *delta, size_t n, float probability, uint64_t seed
                         const uint32_t *iter, uint32_t layer, ach_stream_t stream);
 /* *counter += v on the stream (advances such a device-side step index).  */
 int ach_counter_add(uint32_t *counter, uint32_t v, ach_stream_t stream);
+
+/* ---- NaN scan (the reference's isnan checks: NormData.normalize exits on a
+ * NaN normalized value, NormData.c:273-276; ScaleData.addUpdatesToScale and
+ * scaleUpdates abort on a NaN scale or scale update, ScaleData.c:51-54,
+ * 67-70).  spans (device memory) lists nspans arrays; for every array that
+ * holds a NaN, *flag = min(*flag, its tag), so with tags in checking order
+ * *flag names the first offending array.  One launch for all the arrays;
+ * the caller initialises *flag (e.g. to INT32_MAX) and reads it later.     */
+typedef struct ach_nan_span {
+    const float *p;
+    uint64_t n;
+    int32_t tag;
+    int32_t reserved;
+} ach_nan_span;
+int ach_nan_scan(const ach_nan_span *spans, int nspans, int32_t *flag, ach_stream_t stream);
 
 /* ---- HIP graphs (no counterpart in the reference; the reference launches
  * every op eagerly).  capture_begin records the stream's work (and that of
