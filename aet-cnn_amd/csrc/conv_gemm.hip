@@ -1567,18 +1567,28 @@ static bool wgrad_chunked(const ConvGeom &g)
     return ACH_WGRAD_CHUNKED && wgrad_nchunks(g) * 16 - ohw <= ACH_WGRAD_PAD_WASTE * ohw;
 }
 
-// Grid cost model of the weight-gradient GEMM: all its workgroups do equal
-// work, so the kernel takes about ceil(workgroups / 256 CUs) times one
-// workgroup's work; below two workgroups per CU the matrix pipes idle.
-static double wgrad_cost(long long wgs, double work)
+// Cost model of the weight-gradient GEMM plus its split-K reduction, in CU
+// cycles.  All workgroups do equal work, so the GEMM takes about
+// ceil(workgroups / 256 CUs) times one workgroup's time: its MFMAs (a
+// 16-position chunk of `images` images, bm*bn*16 MACs per image at 128 fp32
+// MACs per CU cycle) and its epilogue, which writes bm*bn partial sums at a
+// CU's share of HBM bandwidth (~15 bytes per cycle); below two workgroups
+// per CU the matrix pipes idle (x1.25).  The reduction then reads every
+// partial once (~2300 bytes per cycle for the whole chip).  Without the
+// epilogue and reduction terms the model asks for tens of thousands of
+// workgroups of a few images each on small planes (AlexNet's 13x13 layers).
+static double wgrad_cost(long long wgs, int bm, int bn, int images)
 {
-    const double c = (double)((wgs + 255) / 256) * work;
-    return wgs < 512 ? c * 1.25 : c;
+    const double tile = (double)bm * bn;
+    const double per_wg = tile * (images * 16.0 / 128.0 + 4.0 / 15.0);
+    double c = (double)((wgs + 255) / 256) * per_wg;
+    if (wgs < 512) c *= 1.25;
+    return c + (double)wgs * tile * 4.0 / 2300.0;
 }
 
 // chunked split: spc splits per position chunk, nbs images each (>= 4 per
-// split), the count with the lowest grid cost (ties: fewer workgroups, so
-// fewer partial sums)
+// split), the count with the lowest modelled cost (ties: fewer workgroups,
+// so fewer partial sums)
 static double wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits, int &spc,
                                   int &nbs)
 {
@@ -1590,7 +1600,7 @@ static double wgrad_split_chunked(const ConvGeom &g, int bm, int bn, int &splits
         const int b = (g.B + want - 1) / want, s = (g.B + b - 1) / b;
         const long long wgs = tiles * nchunks * s;
         if (wgs > 65535LL * 1024) break;
-        const double c = wgrad_cost(wgs, (double)bm * bn * b);
+        const double c = wgrad_cost(wgs, bm, bn, b);
         if (best < 0 || c < best * (1 - 1e-9)) {
             best = c;
             nbs = b;
