@@ -42,7 +42,7 @@ SWEEP = [  # config 1: (C_in, C_out, H, k, pad)
 # the weight-gradient GEMM (the second most).
 PROBES = {
     "fwd": dict(shape=(256, 256, 16, 3, 1), op="fwd",
-                kernel="k_mfma_gemm<FwdProblem<256, BIm2col3F, true, false>> "
+                kernel="k_mfma_gemm<FwdProblem<128, BIm2col3F, true, false>> "
                        "(conv fwd / stride-1 dgrad implicit GEMM)"),
     "wgrad": dict(shape=(128, 128, 32, 3, 1), op="wgrad",
                   kernel="k_mfma_gemm<WgradProblemC<128, 96, 3>> (conv weight-gradient GEMM)"),
@@ -273,11 +273,10 @@ def probe_setup(aetcnn, which, batch):
 def roofline_phase(aetcnn, which, batch, reps):
     """A probe launched `reps` times back to back with HIP events around the
     run on the probe's stream.  The forward call is the filter transpose
-    (k_weights_kmajor, ~1%), the GEMM (256 x 128 tiles, K split in two
-    halves because the 256-tile grid is small) and the fixed-order split-K
-    reduction into NCHW (~6%); the weight-gradient call is the GEMM over
-    chunked K and its fixed-order split-K reduction.  The average is the
-    whole call, so it under-states the GEMM's own rate."""
+    (k_weights_kmajor, ~1.5%) and the GEMM (128 x 128 tiles, 512 of them,
+    K unsplit); the weight-gradient call is the GEMM over chunked K and its
+    fixed-order split-K reduction (~5%).  The average is the whole call, so
+    it under-states the GEMM's own rate."""
     ops = aetcnn.ops()
     call, stream, free, flop, shape = probe_setup(aetcnn, which, batch)
     ms = time_launch(ops, stream, call, reps)
