@@ -641,6 +641,7 @@ def main():
         return
     if args.bandwidth_only:
         rows, softmax_us = bandwidth_phase(aetcnn, args.bandwidth_reps)
+        copy_calibration_phase(aetcnn)  # scales rocprofv3 counter passes over this run
         print(json.dumps({"bandwidth_ops": rows, "softmax_xent_512x1000_us": softmax_us}))
         return
 
