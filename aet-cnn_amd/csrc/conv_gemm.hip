@@ -1155,6 +1155,204 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
         }
 }
 
+// ---- forward of a layer with a shallow im2col (K = C*KS*KS <= 32) ---------
+// A first layer on an RGB image (3x3: K = 27) has one k-tile of work per
+// output tile, so the tiled GEMM above pays its prologue, a padded second
+// k-tile and an epilogue that every workgroup reaches at once.  Here each
+// wave owns a 32 x 64 output tile and takes its whole K (16 MFMA k-steps,
+// K padded to 32 with zeros) straight from global memory into MFMA
+// registers: the filter fragments from the k-major copy Wt[K][M], the im2col
+// fragments gathered from x with out-of-range taps reading as zero.  No LDS
+// and no barrier; 64-column tiles give several waves per SIMD, so one
+// wave's output stores overlap another's MFMAs.  WM waves of a workgroup
+// split M (32 rows each), 4 / WM split N.  KS_ = 0: kernel size at run time.
+template <int WM, int KS_, bool EPI>
+__global__ void __launch_bounds__(GNT) k_conv_fwd_smallk(const float *__restrict__ x,
+                                                         const float *__restrict__ wt,
+                                                         float *__restrict__ y, ConvGeom g,
+                                                         FastDiv dohw, FastDiv dow, Epi e)
+{
+    constexpr int WN = 4 / WM;
+    const int KS = KS_ ? KS_ : g.KS, KK = KS * KS;
+    const int M = g.F, K = g.C * KK, ohw = (int)dohw.d, N = g.B * ohw;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lrow = lane >> 5, lcol = lane & 31;
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = (blockIdx.y * WM + wm) * 32;
+    const int n0 = (blockIdx.x * WN + wn) * 64;
+    if (m0 >= M || n0 >= N) return;
+
+    // A: lane holds Wt[2s + lrow][m0 + lcol] for the 16 k-steps s
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(wt, (unsigned)((size_t)M * K * 4));
+    const int m = m0 + lcol;
+    float a[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int k = 2 * s + lrow;
+        a[s] = bload(rw, boff(m < M && k < K, k * M + m));
+    }
+    // B: lane holds im2col(x)[2s + lrow][n0 + 32j + lcol].  The lane's k
+    // values are fixed, so their tap offsets (c*H*W + ky*W + kx) and tap
+    // coordinates are computed once; per output column only the base
+    // address and a validity bit per k-step remain.
+    const int HW = g.H * g.W;
+    int toff[16];
+    int tkyv[16], tkxv[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int k = 2 * s + lrow;
+        const int c = k / KK, r = k - c * KK, ky = r / KS, kx = r - ky * KS;
+        toff[s] = c * HW + ky * g.W + kx;
+        tkyv[s] = k < K ? ky : 1 << 20;  // a k past K is never in range
+        tkxv[s] = kx;
+    }
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x, (unsigned)((size_t)g.B * g.C * HW * 4));
+    float b[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + 32 * j + lcol;
+        const int bi = fdiv(n, dohw), p = n - bi * ohw;
+        const int oy = fdiv(p, dow), ox = p - oy * g.OW;
+        const int iy0 = oy * g.S - g.P, ix0 = ox * g.S - g.P;
+        const int base = bi * g.C * HW + iy0 * g.W + ix0;
+        // rows iy0 + ky and columns ix0 + kx inside the image: unsigned
+        // compares of the offsets from the image edges
+        const unsigned hy = (unsigned)g.H, hx = (unsigned)g.W;
+        const bool col_ok = n < N;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const bool ok = col_ok && (unsigned)(iy0 + tkyv[s]) < hy &&
+                            (unsigned)(ix0 + tkxv[s]) < hx;
+            b[j][s] = bload(rx, ok ? (base + toff[s]) * 4 : (int)kOOB);
+        }
+    }
+    v16f acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[j][s], acc[j], 0, 0, 0);
+
+    // D layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
+    // column l%32
+    const bool full_rows = m0 + 32 <= M;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + 32 * j + lcol;
+        if (n >= N) continue;
+        const int bi = fdiv(n, dohw), p = n - bi * ohw;
+        float *yb = y + ((size_t)bi * M + m0 + 4 * lrow) * ohw + p;
+        if (full_rows) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int mr = m0 + 8 * (r >> 2) + 4 * lrow + (r & 3);
+                yb[(size_t)(8 * (r >> 2) + (r & 3)) * ohw] = EPI ? e.apply(acc[j][r], mr) : acc[j][r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int mr = m0 + 8 * (r >> 2) + 4 * lrow + (r & 3);
+                if (mr < M)
+                    yb[(size_t)(8 * (r >> 2) + (r & 3)) * ohw] =
+                        EPI ? e.apply(acc[j][r], mr) : acc[j][r];
+            }
+        }
+    }
+}
+
+// The same with the input patch of the tile staged in LDS: a workgroup's
+// 64*WN output columns are consecutive positions of one image, which read
+// PR input rows (all channels, the full width plus the padding columns)
+// into patch[C][PR][PW], zero where the row or column lies outside the
+// image.  Each lane's im2col values are then LDS reads at offsets fixed for
+// the lane, with no bounds checks.  KST k-steps cover K (14 for 3x3x3).
+// The filter is read as Wt[K][M] or, with w_nat, in its own layout W[M][K]
+// (no transposed copy needed).  The host takes this kernel when the
+// positions of one image divide into whole tiles and the patch fits.
+template <int WM, int KS_, int KST, bool EPI>
+__global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__restrict__ x,
+                                                             const float *__restrict__ w,
+                                                             float *__restrict__ y, ConvGeom g,
+                                                             FastDiv dohw, FastDiv dow, Epi e,
+                                                             int PR, int PW, int w_nat)
+{
+    extern __shared__ float patch[];
+    constexpr int WN = 4 / WM, NT = 64 * WN;
+    const int KS = KS_ ? KS_ : g.KS, KK = KS * KS;
+    const int M = g.F, K = g.C * KK, ohw = (int)dohw.d;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lrow = lane >> 5, lcol = lane & 31;
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = (blockIdx.y * WM + wm) * 32;
+
+    // the tile's image and first output row; the patch starts at that row
+    const int nt0 = blockIdx.x * NT;
+    const int bi = fdiv(nt0, dohw), p0 = nt0 - bi * ohw;
+    const int oyf = fdiv(p0, dow);
+    const int iyf = oyf * g.S - g.P;
+    const float *xb = x + (size_t)bi * g.C * g.H * g.W;
+    const int plane = PR * PW, tot = g.C * plane;
+    for (int i = threadIdx.x; i < tot; i += GNT) {
+        const int c = i / plane, r0 = i - c * plane, r = r0 / PW, q = r0 - r * PW;
+        const int iy = iyf + r, ix = q - g.P;
+        patch[i] = (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W)
+                       ? xb[((size_t)c * g.H + iy) * g.W + ix] : 0.f;
+    }
+    // A: lane holds W(m0 + lcol, 2s + lrow) for the KST k-steps s
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (unsigned)((size_t)M * K * 4));
+    const int m = m0 + lcol;
+    float a[KST];
+    int toff[KST];
+#pragma unroll
+    for (int s = 0; s < KST; ++s) {
+        const int k = 2 * s + lrow;
+        a[s] = bload(rw, boff(m < M && k < K, w_nat ? m * K + k : k * M + m));
+        const int c = k / KK, r = k - c * KK, ky = r / KS, kx = r - ky * KS;
+        toff[s] = k < K ? (c * PR + ky) * PW + kx : -1;
+    }
+    __syncthreads();
+    float b[2][KST];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int p = p0 + wn * 64 + 32 * j + lcol;
+        const int oy = fdiv(p, dow), ox = p - oy * g.OW;
+        const int lb = (oy - oyf) * g.S * PW + ox * g.S;
+#pragma unroll
+        for (int s = 0; s < KST; ++s) b[j][s] = toff[s] >= 0 ? patch[lb + toff[s]] : 0.f;
+    }
+    v16f acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KST; ++s)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[j][s], acc[j], 0, 0, 0);
+
+    if (m0 >= M) return;
+    // D layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
+    // column l%32
+    const bool full_rows = m0 + 32 <= M;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int p = p0 + wn * 64 + 32 * j + lcol;
+        float *yb = y + ((size_t)bi * M + m0 + 4 * lrow) * ohw + p;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int mr = m0 + 8 * (r >> 2) + 4 * lrow + (r & 3);
+            if (full_rows || mr < M)
+                yb[(size_t)(8 * (r >> 2) + (r & 3)) * ohw] = EPI ? e.apply(acc[j][r], mr) : acc[j][r];
+        }
+    }
+}
+
 // Fixed-order split-K reduction: dw[i] += sum_z part[z][i], z ascending.
 __global__ void k_splitk_reduce(const float *__restrict__ part, float *__restrict__ dw,
                                 size_t mn, int splits)
@@ -1374,6 +1572,74 @@ static bool fc_geom(const ConvGeom &g) { return g.KS == 1 && g.H == 1 && g.W == 
 // loaders (BIm2colK<5> / AWeightsT4K)
 static bool fwd_padded_taps(const ConvGeom &g) { return g.KS == 5 && (g.F & 3) == 0; }
 
+// the shallow-im2col forward (k_conv_fwd_smallk) takes these geometries
+static bool fwd_small_k(const ConvGeom &g)
+{
+    return !fc_geom(g) && g.C * g.KS * g.KS <= 32;
+}
+
+template <int WM, int KS, bool EPI>
+static int smallk_launch(const ConvGeom &g, const float *x, const float *wt, float *y,
+                         const Epi &e, hipStream_t st)
+{
+    const int N = g.B * g.OH * g.OW;
+    const dim3 grid((N + 64 * (4 / WM) - 1) / (64 * (4 / WM)), (g.F + 32 * WM - 1) / (32 * WM));
+    if (grid.y > 65535) return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL((k_conv_fwd_smallk<WM, KS, EPI>), grid, dim3(GNT), 0, st, x, wt, y, g,
+                       make_fastdiv((unsigned)(g.OH * g.OW)), make_fastdiv((unsigned)g.OW), e);
+    return check_launch();
+}
+
+// the patch-staged kernel: returns ACH_EUNSUPPORTED when its conditions fail
+template <int WM, int KS, int KST, bool EPI>
+static int smallk_lds_launch(const ConvGeom &g, const float *x, const float *w, float *y,
+                             const Epi &e, bool w_nat, hipStream_t st)
+{
+    constexpr int NT = 64 * (4 / WM);
+    const int N = g.B * g.OH * g.OW, ohw = g.OH * g.OW;
+    const dim3 grid(N / NT, (g.F + 32 * WM - 1) / (32 * WM));
+    // the input rows of the output rows a tile spans
+    const int rows = (NT + g.OW - 2) / g.OW + 1;
+    const int PR = (rows - 1) * g.S + g.KS, PW = g.W + 2 * g.P;
+    const size_t lds = (size_t)g.C * PR * PW * sizeof(float);
+    if (ohw % NT != 0 || lds > 32768 || grid.y > 65535) return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL((k_conv_fwd_smallk_lds<WM, KS, KST, EPI>), grid, dim3(GNT), lds, st, x,
+                       w, y, g, make_fastdiv((unsigned)ohw), make_fastdiv((unsigned)g.OW), e, PR,
+                       PW, (int)w_nat);
+    return check_launch();
+}
+
+template <int WM, bool EPI>
+static int smallk_lds_ks(const ConvGeom &g, const float *x, const float *w, float *y,
+                         const Epi &e, bool w_nat, hipStream_t st)
+{
+    // 3x3 over 3 channels (K = 27): 14 k-steps; otherwise the full 16
+    if (g.KS == 3 && g.C == 3) return smallk_lds_launch<WM, 3, 14, EPI>(g, x, w, y, e, w_nat, st);
+    if (g.KS == 3) return smallk_lds_launch<WM, 3, 16, EPI>(g, x, w, y, e, w_nat, st);
+    return smallk_lds_launch<WM, 0, 16, EPI>(g, x, w, y, e, w_nat, st);
+}
+
+// w: Wt[K][M], or W[M][K] with w_nat (the patch-staged kernel reads either;
+// the register-gather fallback needs Wt and returns ACH_EUNSUPPORTED for w_nat)
+template <bool EPI>
+static int fwd_small_k_launch(const ConvGeom &g, const float *x, const float *w, float *y,
+                              const Epi &e, bool w_nat, hipStream_t st)
+{
+    // waves along M: 4 for more than 64 filters, 2 for 33-64, 1 for <= 32
+    int rc = g.F > 64 ? smallk_lds_ks<4, EPI>(g, x, w, y, e, w_nat, st)
+                      : (g.F > 32 ? smallk_lds_ks<2, EPI>(g, x, w, y, e, w_nat, st)
+                                  : smallk_lds_ks<1, EPI>(g, x, w, y, e, w_nat, st));
+    if (rc != ACH_EUNSUPPORTED || w_nat) return rc;
+    if (g.KS == 3) {
+        if (g.F > 64) return smallk_launch<4, 3, EPI>(g, x, w, y, e, st);
+        if (g.F > 32) return smallk_launch<2, 3, EPI>(g, x, w, y, e, st);
+        return smallk_launch<1, 3, EPI>(g, x, w, y, e, st);
+    }
+    if (g.F > 64) return smallk_launch<4, 0, EPI>(g, x, w, y, e, st);
+    if (g.F > 32) return smallk_launch<2, 0, EPI>(g, x, w, y, e, st);
+    return smallk_launch<1, 0, EPI>(g, x, w, y, e, st);
+}
+
 static FwdPlan fwd_plan(const ConvGeom &g)
 {
     FwdPlan pl;
@@ -1408,6 +1674,7 @@ static FwdPlan fwd_plan(const ConvGeom &g)
     }
     pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
     pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
+    if (fwd_small_k(g)) pl.splits = 1;  // k_conv_fwd_smallk: whole K per tile
     return pl;
 }
 
@@ -1507,6 +1774,9 @@ static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, c
 static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, float *part,
                     hipStream_t st, const Epi &e = Epi(), bool w_nat = false)
 {
+    if (fwd_small_k(g))
+        return e.active() ? fwd_small_k_launch<true>(g, x, w, y, e, w_nat, st)
+                          : fwd_small_k_launch<false>(g, x, w, y, e, w_nat, st);
     const FwdPlan pl = fwd_plan(g);
     const bool gemm_epi = e.active() && pl.splits == 1;
     int rc;
@@ -1759,8 +2029,13 @@ int ach_conv_fwd(const ach_conv_desc *d, const float *x, const float *w, float *
     const int M = g.F, K = g.C * g.KS * g.KS;
     float *wt = (float *)ws;
     float *part = (float *)((char *)ws + align256((size_t)M * K * sizeof(float)));
-    // a fully connected geometry reads the filter in its own layout
+    // a fully connected geometry reads the filter in its own layout, and so
+    // does the patch-staged shallow-im2col kernel
     if (fc_geom(g)) return fwd_impl(g, x, w, y, part, st, Epi(), true);
+    if (fwd_small_k(g)) {
+        const int rc0 = fwd_small_k_launch<false>(g, x, w, y, Epi(), true, st);
+        if (rc0 != ACH_EUNSUPPORTED) return rc0;
+    }
     hipLaunchKernelGGL(k_weights_kmajor, dim3((K + 31) / 32, (M + 31) / 32), dim3(256), 0, st, w,
                        wt, M, K);
     int rc = check_launch();

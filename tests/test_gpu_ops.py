@@ -110,6 +110,11 @@ CONV_SHAPES = [
     (2, 16, 8, 8, 80, 3, 1, 1),    # weight gradient 96 x 128 tiles, chunked K, 3x3
     (3, 4, 11, 11, 96, 4, 1, 0),   # weight gradient 96 x 128 tiles, chunked K, 4x4
     (8, 16, 5, 5, 24, 3, 1, 1),    # 25 positions: the (image, position) order
+    # shallow im2col (C*k*k <= 32: the whole K in MFMA registers, no LDS):
+    (3, 2, 9, 11, 40, 3, 2, 1),    # stride 2, 33-64 filters
+    (2, 1, 12, 10, 70, 5, 1, 2),   # 5x5 (kernel size at run time), ragged M
+    (3, 3, 7, 5, 16, 3, 1, 0),     # no padding, 45 output columns
+    (2, 32, 5, 5, 33, 1, 1, 0),    # K = 32 exactly, 33 filters
     # fully connected layers (1x1 of a 1x1 input, after flattening):
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
     (8, 64, 1, 1, 48, 1, 1, 0),    # 64 -> 48, 64-row tiles
@@ -531,8 +536,11 @@ def test_bias_ops(gpu, oracle, B, n, sp):
 
 
 @pytest.mark.parametrize("shape", [
-    (2, 128, 16, 16, 256, 3, 1, 1),   # 256-row tiles, split K (reduction epilogue)
+    (2, 128, 16, 16, 256, 3, 1, 1),   # no split (GEMM epilogue)
+    (2, 256, 8, 8, 512, 3, 1, 1),     # split K (reduction epilogue)
     (2, 128, 32, 32, 128, 3, 1, 1),   # no split (GEMM epilogue)
+    (2, 3, 32, 32, 128, 3, 1, 1),     # shallow im2col kernel
+    (2, 1, 12, 10, 70, 5, 1, 2),      # shallow im2col kernel, 5x5, ragged M
     (3, 5, 9, 7, 10, 3, 1, 1),        # scalar loaders, ragged tiles
     (2, 96, 9, 9, 80, 5, 1, 2),       # padded-tap 5x5, 96-row tiles
     (2, 16, 13, 13, 24, 5, 1, 2),
