@@ -1353,6 +1353,140 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__rest
     }
 }
 
+// ---- input gradient of a stride-1 layer with at most 4 input channels ------
+// dx[b][c][iy][ix] = sum_f sum_{ky,kx} W[f][c][ky][kx] * dy[b][f][iy+P-ky][ix+P-kx]
+// (ConvolutionalLayer.c:931-945 for stride 1).  As a GEMM its M is the
+// channel count: a 32-row MFMA tile would compute 29 rows of padding for an
+// RGB input, so this runs on the vector ALUs.  A workgroup of DG_WAVES waves
+// owns a DG_TH x DG_TW tile of one image; a lane computes 4 adjacent pixels
+// of one row for all C channels.  dy is staged in LDS DG_FC filters at a
+// time with the tile's halo (zero outside the image), together with those
+// filters' weights as wl[f][ky][kx][4 channels], so a lane's tap reads one
+// row segment (a float4 and a float2 for 3x3) and one float4 of weights per
+// tap for 4*C FMAs.  The next chunk's patch is loaded into registers while
+// the current one is computed.  The waves take every DG_WAVES-th filter of
+// a chunk and their partial sums are added in wave order through LDS (the
+// patch's space), so results do not depend on timing.  The filter is read
+// in its own layout W[F][C][KS][KS].
+constexpr int DG_TW = 32, DG_TH = 8, DG_FC = 16, DG_WAVES = 8, DG_NT = 64 * DG_WAVES;
+// patch rows a wave prefetches per chunk: 4*DG_ROWS, so DG_FC * PH must not
+// exceed 4*DG_ROWS*DG_WAVES (kernels up to 9 wide)
+constexpr int DG_ROWS = 8;
+template <int NC, int KS_>
+__global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__restrict__ dy,
+                                                             const float *__restrict__ w,
+                                                             float *__restrict__ dx, ConvGeom g,
+                                                             int tiles_x)
+{
+    extern __shared__ float4 smem4[];
+    float *smem = reinterpret_cast<float *>(smem4);
+    const int KS = KS_ ? KS_ : g.KS;
+    // patch rows padded to a multiple of 4 floats (16-byte aligned segments)
+    const int PH = DG_TH + KS - 1, PWd = (DG_TW + KS - 1 + 3) & ~3, pplane = PH * PWd;
+    float *patch = smem;                                   // [DG_FC][PH][PWd]
+    float4 *wl = reinterpret_cast<float4 *>(smem + DG_FC * pplane);  // [DG_FC][KS*KS]
+    float *red = smem;  // after the last chunk: [DG_WAVES-1][NC][4][64]
+    const int b = blockIdx.y;
+    const int tx0 = (blockIdx.x % tiles_x) * DG_TW, ty0 = (blockIdx.x / tiles_x) * DG_TH;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ty = lane >> 3, tx = (lane & 7) * 4;   // the lane's first pixel in the tile
+    // patch row r is dy row oy0 + r, column q is dy column ox0 + q
+    const int oy0 = ty0 + g.P - (KS - 1), ox0 = tx0 + g.P - (KS - 1);
+    const float *dyb = dy + (size_t)b * g.F * g.OH * g.OW;
+    float acc[NC][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[c][q] = 0.f;
+    const int taps = KS * KS;
+    // a chunk's patch rows rr = wave + DG_WAVES*u, one column per lane
+    float pre[DG_ROWS * 4];
+    const int prow = DG_FC * PH;  // at most DG_ROWS*4*DG_WAVES rows (host check)
+    auto load_chunk = [&](int f0) {
+        const int fc = min(DG_FC, g.F - f0);
+#pragma unroll
+        for (int u = 0; u < DG_ROWS * 4; ++u) {
+            const int rr = wave + DG_WAVES * u;
+            const int f = rr / PH, r = rr - f * PH, oy = oy0 + r, ox = ox0 + lane;
+            pre[u] = (rr < fc * PH && lane < PWd && oy >= 0 && oy < g.OH && ox >= 0 &&
+                      ox < g.OW)
+                         ? dyb[((size_t)(f0 + f) * g.OH + oy) * g.OW + ox]
+                         : 0.f;
+        }
+    };
+    load_chunk(0);
+    for (int f0 = 0; f0 < g.F; f0 += DG_FC) {
+        const int fc = min(DG_FC, g.F - f0);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < DG_ROWS * 4; ++u) {
+            const int rr = wave + DG_WAVES * u;
+            if (rr < prow && lane < PWd) patch[rr * PWd + lane] = pre[u];
+        }
+        for (int i = threadIdx.x; i < fc * taps; i += DG_NT) {
+            const int f = i / taps, tap = i - f * taps;
+            const float *wf = w + (size_t)(f0 + f) * NC * taps + tap;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            v.x = wf[0];
+            if (NC > 1) v.y = wf[taps];
+            if (NC > 2) v.z = wf[2 * taps];
+            if (NC > 3) v.w = wf[3 * taps];
+            wl[i] = v;
+        }
+        __syncthreads();
+        if (f0 + DG_FC < g.F) load_chunk(f0 + DG_FC);  // in flight while this chunk computes
+        for (int f = wave; f < fc; f += DG_WAVES) {
+            const float *pf = patch + f * pplane;
+            const float4 *wf = wl + f * taps;
+            for (int ky = 0; ky < KS; ++ky) {
+                // row segment: columns tx .. tx + 3 + KS - 1
+                const float *row = pf + (ty + KS - 1 - ky) * PWd + tx;
+                float v[4 + (KS_ ? KS_ : 16) - 1];
+                if (KS_ == 3) {
+                    const float4 v0 = *reinterpret_cast<const float4 *>(row);
+                    const float2 v1 = *reinterpret_cast<const float2 *>(row + 4);
+                    v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+                    v[4] = v1.x; v[5] = v1.y;
+                } else {
+                    for (int j = 0; j < 4 + KS - 1; ++j) v[j] = row[j];
+                }
+#pragma unroll
+                for (int kx = 0; kx < (KS_ ? KS_ : 16); ++kx) {
+                    if (!KS_ && kx >= KS) break;
+                    const float4 wv = wf[ky * KS + kx];
+                    const float wc[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float val = v[q + KS - 1 - kx];
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) acc[c][q] = __fmaf_rn(wc[c], val, acc[c][q]);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with the last chunk's patch
+    if (wave > 0) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) red[(((wave - 1) * NC + c) * 4 + q) * 64 + lane] = acc[c][q];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int iy = ty0 + ty;
+    if (iy >= g.H) return;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int ix = tx0 + tx + q;
+            float s = acc[c][q];
+            for (int v = 0; v < DG_WAVES - 1; ++v) s += red[((v * NC + c) * 4 + q) * 64 + lane];
+            if (ix < g.W) dx[((size_t)(b * NC + c) * g.H + iy) * g.W + ix] = s;
+        }
+}
+
 // Fixed-order split-K reduction: dw[i] += sum_z part[z][i], z ascending.
 __global__ void k_splitk_reduce(const float *__restrict__ part, float *__restrict__ dw,
                                 size_t mn, int splits)
@@ -2000,6 +2134,51 @@ static int fc_wgrad_launch(const ConvGeom &g, const float *x, const float *dy, f
     return fc_wgrad_bm<128>(g, x, dy, dw, part, splits, kchunk, st);
 }
 
+// the small-channel input gradient: stride 1, at most 4 input channels,
+// kernels up to 16 wide, a staged chunk that fits LDS
+static size_t dgrad_small_c_lds(const ConvGeom &g, int nc)
+{
+    const int PH = DG_TH + g.KS - 1, PWd = (DG_TW + g.KS - 1 + 3) & ~3;
+    const size_t stage = (size_t)DG_FC * PH * PWd + 4 * DG_FC * g.KS * g.KS;
+    const size_t red = (size_t)(DG_WAVES - 1) * nc * 4 * 64;
+    return (stage > red ? stage : red) * sizeof(float);
+}
+static bool dgrad_small_c(const ConvGeom &g)
+{
+    // the chunk's patch rows fit the per-wave register prefetch
+    const int PH = DG_TH + g.KS - 1;
+    return g.S == 1 && g.P <= g.KS - 1 && g.C <= 4 && g.KS <= 16 &&
+           DG_FC * PH <= DG_ROWS * 4 * DG_WAVES && dgrad_small_c_lds(g, 4) <= 65536;
+}
+
+template <int NC>
+static int dgrad_small_c_nc(const ConvGeom &g, const float *dy, const float *w, float *dx,
+                            hipStream_t st)
+{
+    const size_t lds = dgrad_small_c_lds(g, NC);
+    const int tiles_x = (g.W + DG_TW - 1) / DG_TW, tiles_y = (g.H + DG_TH - 1) / DG_TH;
+    const dim3 grid(tiles_x * tiles_y, g.B);
+    if (grid.y > 65535) return ACH_EUNSUPPORTED;
+    if (g.KS == 3)
+        hipLaunchKernelGGL((k_conv_dgrad_smallc<NC, 3>), grid, dim3(DG_NT), lds, st, dy, w, dx, g,
+                           tiles_x);
+    else
+        hipLaunchKernelGGL((k_conv_dgrad_smallc<NC, 0>), grid, dim3(DG_NT), lds, st, dy, w, dx, g,
+                           tiles_x);
+    return check_launch();
+}
+
+static int dgrad_small_c_launch(const ConvGeom &g, const float *dy, const float *w, float *dx,
+                                hipStream_t st)
+{
+    switch (g.C) {
+    case 1: return dgrad_small_c_nc<1>(g, dy, w, dx, st);
+    case 2: return dgrad_small_c_nc<2>(g, dy, w, dx, st);
+    case 3: return dgrad_small_c_nc<3>(g, dy, w, dx, st);
+    default: return dgrad_small_c_nc<4>(g, dy, w, dx, st);
+    }
+}
+
 }  // namespace ach
 
 using namespace ach;
@@ -2073,6 +2252,7 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
     if (!ws || ws_bytes < need) return ACH_EWORKSPACE;
     const ConvGeom g = geom(d);
     hipStream_t st = as_stream(stream);
+    if (dgrad_small_c(g) && !fc_geom(g)) return dgrad_small_c_launch(g, dy, w, dx, st);
     if (g.S == 1 && g.P <= g.KS - 1) {
         const size_t tot = (size_t)g.F * g.C * g.KS * g.KS;
         float *part = (float *)((char *)ws + align256(tot * sizeof(float)));
@@ -2185,6 +2365,7 @@ int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const fl
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
     if (!(g.S == 1 && g.P <= g.KS - 1)) return ACH_EUNSUPPORTED;  // strided: ach_conv_bwd_data
+    if (dgrad_small_c(g) && !fc_geom(g)) return dgrad_small_c_launch(g, dy, w, dx, as_stream(stream));
     if (g.KS > 1 && !wft) return ACH_EINVAL;
     const ConvGeom t = dgrad_as_fwd(g);
     const size_t need = fwd_part_bytes(t);
