@@ -190,7 +190,7 @@ def config1_inputs(rng, batch, ci, co, hw, k, p):
     return x, w, dy
 
 
-def sweep_phase(aetcnn, batch, reps):
+def sweep_phase(aetcnn, batch, reps, shapes=None):
     ops = aetcnn.ops()
     D = aetcnn.DeviceArray
     stream = C.c_void_p()
@@ -198,7 +198,7 @@ def sweep_phase(aetcnn, batch, reps):
     rng = np.random.default_rng(0)
     rows = []
     tot_flop = tot_ms = 0.0
-    for (ci, co, hw, k, p) in SWEEP:
+    for (ci, co, hw, k, p) in (SWEEP if shapes is None else [SWEEP[i] for i in shapes]):
         d = aetcnn.ConvDesc(batch, ci, hw, hw, co, k, 1, p)
         oh = (hw + 2 * p - k) + 1
         xh, wh, dyh = config1_inputs(rng, batch, ci, co, hw, k, p)
@@ -592,6 +592,10 @@ def main():
     ap.add_argument("--config", default="darknet", choices=["darknet", "tiny", "alexnet"])
     ap.add_argument("--sweep-reps", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="run only the config-1 sweep and print its rows (for rocprofv3)")
+    ap.add_argument("--sweep-shapes", default=None,
+                    help="comma-separated indices into the config-1 sweep (default: all)")
     ap.add_argument("--roofline-reps", type=int, default=20)
     ap.add_argument("--no-bandwidth", action="store_true")
     ap.add_argument("--no-fed", action="store_true",
@@ -638,6 +642,11 @@ def main():
             rows[which] = {"ms": probe["ms"], "kernel": probe["kernel"], "shape": probe["shape"]}
         copy_calibration_phase(aetcnn)
         print(json.dumps({"roofline_probes": rows}))
+        return
+    if args.sweep_only:
+        shapes = None if args.sweep_shapes is None else [int(s) for s in args.sweep_shapes.split(",")]
+        rows, tf = sweep_phase(aetcnn, 128, args.sweep_reps, shapes)
+        print(json.dumps({"conv_sweep": rows, "conv_sweep_tflops": round(tf, 3)}))
         return
     if args.bandwidth_only:
         rows, softmax_us = bandwidth_phase(aetcnn, args.bandwidth_reps)
