@@ -56,9 +56,10 @@ def log(msg):
 
 def train_phase(aetcnn, configs, name, steps, warmup, batch, sustain_s=0.0):
     """Warm-up, then exactly `steps` timed steps between two device
-    synchronisations (the headline); then, untimed for the headline, steps in
-    blocks of 50 until `sustain_s` seconds have passed, reported as the
-    sustained rate (clock and thermal behaviour under load)."""
+    synchronisations (the headline).  With sustain_s > 0 (the separate
+    sustained phase) the same network then trains on in blocks of 50 steps
+    until sustain_s seconds have passed, reported as the sustained rate
+    (clock and thermal behaviour under load)."""
     lib = aetcnn.net_lib()
     lib.an_rand_seed(1)
     B, h, w, c = configs.dims(name, batch)
@@ -655,23 +656,14 @@ def main():
         return
 
     log(f"training phase: {args.config} b128, warmup {args.warmup}, steps {args.steps}")
-    tr = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None,
-                     args.sustain_s)
+    tr = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None)
     ms_step = tr["wall_s"] * 1e3 / args.steps
     ips = tr["batch"] * args.steps / tr["wall_s"]
     step_tflops = tr["gflop_step"] / (ms_step * 1e-3) / 1e3
     log(f"{ms_step:.3f} ms/step ({tr['gpu_ms'] / args.steps:.3f} GPU ms), {ips:.1f} img/s, "
         f"conv {step_tflops:.2f} TFLOP/s, loss {tr['first_loss']:.4f} -> {tr['loss']:.4f}")
-    if tr["sustained"]:
-        log(f"sustained over {tr['sustained']['seconds']} s: "
-            f"{tr['sustained']['images_per_s']} img/s")
-
-    fed = None
-    if not args.no_fed:
-        fed = fed_phase(aetcnn, configs, args.config, args.steps, args.warmup, 8)
-        log(f"fed by the input pipeline: {fed['ms_per_step']:.3f} ms/step, "
-            f"{fed['images_per_s']:.1f} img/s")
-
+    # kernel measurements next, before the long fed and sustained runs heat the
+    # GPU and lower its clocks
     sweep_rows, sweep_tflops = [], None
     if not args.no_sweep:
         sweep_rows, sweep_tflops = sweep_phase(aetcnn, 128, args.sweep_reps)
@@ -704,6 +696,17 @@ def main():
             launches=probe["reps"], flop_per_launch=probe["flop"],
             algorithmic_bytes=algorithmic_bytes(which),
             traffic_detail=traffic if traffic else {"unmeasured": why})
+
+    fed = None
+    if not args.no_fed:
+        fed = fed_phase(aetcnn, configs, args.config, args.steps, args.warmup, 8)
+        log(f"fed by the input pipeline: {fed['ms_per_step']:.3f} ms/step, "
+            f"{fed['images_per_s']:.1f} img/s")
+    sustained = None
+    if args.sustain_s > 0:
+        sustained = train_phase(aetcnn, configs, args.config, args.steps, args.warmup, None,
+                                args.sustain_s)["sustained"]
+        log(f"sustained over {sustained['seconds']} s: {sustained['images_per_s']} img/s")
 
     cpu = cpu_serial = None
     host = host_cpu()
@@ -755,7 +758,7 @@ def main():
         "input_pipeline": fed,
         "bandwidth_ops": {"shape": "x[512][128][32][32] fp32 (config 2)", "ops": bw_rows,
                           "softmax_xent_512x1000_us": softmax_us},
-        "sustained": tr["sustained"],
+        "sustained": sustained,
         "roofline": rooflines["fwd"],
         "roofline_wgrad": rooflines["wgrad"],
         "cpu_baseline": cpu,
