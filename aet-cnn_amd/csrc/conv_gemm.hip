@@ -1265,27 +1265,35 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk(const float *__restrict
     }
 }
 
-// The same with the input patch of the tile staged in LDS: a workgroup's
-// 64*WN output columns are consecutive positions of one image, which read
-// PR input rows (all channels, the full width plus the padding columns)
-// into patch[C][PR][PW], zero where the row or column lies outside the
-// image.  Each lane's im2col values are then LDS reads at offsets fixed for
-// the lane, with no bounds checks.  KST k-steps cover K (14 for 3x3x3).
-// The filter is read as Wt[K][M] or, with w_nat, in its own layout W[M][K]
-// (no transposed copy needed).  The host takes this kernel when the
-// positions of one image divide into whole tiles and the patch fits.
-template <int WM, int KS_, int KST, bool EPI>
+// The same with the input patch of the tile staged in LDS.  A workgroup's
+// NT = 32*TPW*WN output columns are consecutive positions of one image, which
+// read PR input rows (all channels, the full width plus the padding columns)
+// into patch[C][PR][PW], zero where the row or column lies outside the image;
+// the patch's global loads are all issued before the first LDS write.  Each
+// lane's im2col values are then LDS reads at offsets fixed for the lane, with
+// no bounds checks.  KST k-steps cover K (14 for 3x3x3).  Each wave owns 32
+// filters and TPW tiles of 32 consecutive positions and walks them in order:
+// the MFMAs of tile t+1 issue while the stores of tile t drain, so the
+// output's HBM writes overlap the matrix work (one tile per MFMA chain, k in
+// order, as the single-tile form).  The filter is read as Wt[K][M] or, with
+// w_nat, in its own layout W[M][K] (no transposed copy needed).  The host
+// takes this kernel when the positions of one image divide into whole tiles
+// and the patch fits.
+template <int WM, int KS_, int KST, bool EPI, int TPW>
 __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__restrict__ x,
                                                              const float *__restrict__ w,
                                                              float *__restrict__ y, ConvGeom g,
                                                              FastDiv dohw, FastDiv dow, Epi e,
-                                                             int PR, int PW, int w_nat)
+                                                             int PR, FastDiv dpw, FastDiv dplane,
+                                                             int w_nat)
 {
     extern __shared__ float patch[];
-    constexpr int WN = 4 / WM, NT = 64 * WN;
+    constexpr int WN = 4 / WM, NT = 32 * TPW * WN, U = 8;
+    const int PW = (int)dpw.d;
     const int KS = KS_ ? KS_ : g.KS, KK = KS * KS;
     const int M = g.F, K = g.C * KK, ohw = (int)dohw.d;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lrow = lane >> 5, lcol = lane & 31;
     const int wm = wave / WN, wn = wave % WN;
     const int m0 = (blockIdx.y * WM + wm) * 32;
@@ -1295,13 +1303,26 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__rest
     const int bi = fdiv(nt0, dohw), p0 = nt0 - bi * ohw;
     const int oyf = fdiv(p0, dow);
     const int iyf = oyf * g.S - g.P;
-    const float *xb = x + (size_t)bi * g.C * g.H * g.W;
-    const int plane = PR * PW, tot = g.C * plane;
-    for (int i = threadIdx.x; i < tot; i += GNT) {
-        const int c = i / plane, r0 = i - c * plane, r = r0 / PW, q = r0 - r * PW;
-        const int iy = iyf + r, ix = q - g.P;
-        patch[i] = (iy >= 0 && iy < g.H && ix >= 0 && ix < g.W)
-                       ? xb[((size_t)c * g.H + iy) * g.W + ix] : 0.f;
+    // the image's planes through a buffer resource: taps outside the image
+    // take the out-of-range offset and read as zero
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x + (size_t)bi * g.C * g.H * g.W, (unsigned)(g.C * g.H * g.W) * 4u);
+    const int plane = (int)dplane.d, tot = g.C * plane;
+    for (int base = 0; base < tot; base += GNT * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = base + u * GNT + (int)threadIdx.x;
+            const int c = fdiv(i, dplane), r0 = i - c * plane, r = fdiv(r0, dpw), q = r0 - r * PW;
+            const int iy = iyf + r, ix = q - g.P;
+            v[u] = bload(rx, boff(i < tot && iy >= 0 && iy < g.H && ix >= 0 && ix < g.W,
+                                  (c * g.H + iy) * g.W + ix));
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = base + u * GNT + (int)threadIdx.x;
+            if (i < tot) patch[i] = v[u];
+        }
     }
     // A: lane holds W(m0 + lcol, 2s + lrow) for the KST k-steps s
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (unsigned)((size_t)M * K * 4));
@@ -1313,44 +1334,77 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__rest
         const int k = 2 * s + lrow;
         a[s] = bload(rw, boff(m < M && k < K, w_nat ? m * K + k : k * M + m));
         const int c = k / KK, r = k - c * KK, ky = r / KS, kx = r - ky * KS;
-        toff[s] = k < K ? (c * PR + ky) * PW + kx : -1;
+        toff[s] = k < K ? (c * PR + ky) * PW + kx : 0;  // k >= K: read anything, use 0
     }
-    __syncthreads();
-    float b[2][KST];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int p = p0 + wn * 64 + 32 * j + lcol;
+    __syncthreads();  // the only barrier: waves past it may leave early
+    if (m0 >= M) return;
+
+    const int pw0 = p0 + wn * 32 * TPW;  // the wave's first position
+    auto fetch = [&](int t, float (&bb)[KST]) {
+        const int p = pw0 + 32 * t + lcol;
         const int oy = fdiv(p, dow), ox = p - oy * g.OW;
         const int lb = (oy - oyf) * g.S * PW + ox * g.S;
 #pragma unroll
-        for (int s = 0; s < KST; ++s) b[j][s] = toff[s] >= 0 ? patch[lb + toff[s]] : 0.f;
-    }
-    v16f acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-#pragma unroll
-    for (int s = 0; s < KST; ++s)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[j][s], acc[j], 0, 0, 0);
-
-    if (m0 >= M) return;
+        for (int s = 0; s < KST; ++s) {
+            const float v = patch[lb + toff[s]];
+            bb[s] = 2 * s + lrow < K ? v : 0.f;
+        }
+    };
     // D layout: lane l, register r holds row 8*(r/4) + 4*(l/32) + r%4,
-    // column l%32
-    const bool full_rows = m0 + 32 <= M;
+    // column l%32.  Buffer stores into the wave's rows m0 .. min(m0 + 32, M)
+    // - 1 of image bi: the range check of the resource drops the rows past M,
+    // each store takes the lane's row offset and the tile's offset (the host
+    // keeps 32 rows of a plane below 2^31 bytes).
+    const int rows = M - m0 < 32 ? M - m0 : 32;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(y + ((size_t)bi * M + m0) * ohw, (unsigned)(rows * ohw) * 4u);
+    unsigned rowv[16];  // the lane's byte offset of each row at the wave's first position
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int p = p0 + wn * 64 + 32 * j + lcol;
-        float *yb = y + ((size_t)bi * M + m0 + 4 * lrow) * ohw + p;
+    for (int r = 0; r < 16; ++r)
+        rowv[r] = (unsigned)((4 * lrow + 8 * (r >> 2) + (r & 3)) * ohw + pw0 + lcol) * 4u;
+    float bv[16];  // the rows' biases (rows past M: any valid row, never stored)
+    if constexpr (EPI) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int mr = m0 + 8 * (r >> 2) + 4 * lrow + (r & 3);
-            if (full_rows || mr < M)
-                yb[(size_t)(8 * (r >> 2) + (r & 3)) * ohw] = EPI ? e.apply(acc[j][r], mr) : acc[j][r];
+            bv[r] = e.bias ? e.bias[mr < M ? mr : M - 1] : -0.0f;
         }
     }
+    auto val = [&](const v16f &acc, int r) -> float {
+        if constexpr (EPI) {  // Epi::apply with the row's bias preloaded
+            const float v = acc[r] + bv[r];
+            return v > 0.f ? v : (float)(e.slope * (double)v);
+        } else {
+            return acc[r];
+        }
+    };
+    auto put = [&](int t, const v16f &acc) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val(acc, r)), ry, (int)rowv[r],
+                                                  128 * t, 0);
+    };
+    float b0[KST], b1[KST];
+    v16f acc0, acc1;
+    fetch(0, b0);
+#pragma unroll
+    for (int t = 0; t < TPW; t += 2) {  // TPW even: tiles t (acc0) and t+1 (acc1)
+        fetch(t + 1, b1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc0[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KST; ++s)
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b0[s], acc0, 0, 0, 0);
+        if (t > 0) put(t - 1, acc1);
+        if (t + 2 < TPW) fetch(t + 2, b0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc1[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KST; ++s)
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b1[s], acc1, 0, 0, 0);
+        put(t, acc0);
+    }
+    put(TPW - 1, acc1);
 }
 
 // ---- input gradient of a stride-1 layer with at most 4 input channels ------
@@ -1724,23 +1778,46 @@ static int smallk_launch(const ConvGeom &g, const float *x, const float *wt, flo
     return check_launch();
 }
 
-// the patch-staged kernel: returns ACH_EUNSUPPORTED when its conditions fail
-template <int WM, int KS, int KST, bool EPI>
-static int smallk_lds_launch(const ConvGeom &g, const float *x, const float *w, float *y,
-                             const Epi &e, bool w_nat, hipStream_t st)
+// the patch-staged kernel: returns ACH_EUNSUPPORTED when its conditions fail.
+// Tiles per wave: the most of 8, 4, 2 whose workgroup span divides the
+// positions of an image and still leaves 512 workgroups (fewer tiles per
+// wave when the grid would not fill the GPU twice over).
+template <int WM, int KS, int KST, bool EPI, int TPW>
+static int smallk_lds_go(const ConvGeom &g, const float *x, const float *w, float *y,
+                         const Epi &e, bool w_nat, hipStream_t st)
 {
-    constexpr int NT = 64 * (4 / WM);
+    constexpr int NT = 32 * TPW * (4 / WM);
     const int N = g.B * g.OH * g.OW, ohw = g.OH * g.OW;
     const dim3 grid(N / NT, (g.F + 32 * WM - 1) / (32 * WM));
     // the input rows of the output rows a tile spans
     const int rows = (NT + g.OW - 2) / g.OW + 1;
     const int PR = (rows - 1) * g.S + g.KS, PW = g.W + 2 * g.P;
     const size_t lds = (size_t)g.C * PR * PW * sizeof(float);
-    if (ohw % NT != 0 || lds > 32768 || grid.y > 65535) return ACH_EUNSUPPORTED;
-    hipLaunchKernelGGL((k_conv_fwd_smallk_lds<WM, KS, KST, EPI>), grid, dim3(GNT), lds, st, x,
-                       w, y, g, make_fastdiv((unsigned)ohw), make_fastdiv((unsigned)g.OW), e, PR,
-                       PW, (int)w_nat);
+    if (ohw % NT != 0 || lds > 32768 || grid.y > 65535 || (size_t)ohw * 32 * 4 >= (1u << 31))
+        return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL((k_conv_fwd_smallk_lds<WM, KS, KST, EPI, TPW>), grid, dim3(GNT), lds, st,
+                       x, w, y, g, make_fastdiv((unsigned)ohw), make_fastdiv((unsigned)g.OW), e,
+                       PR, make_fastdiv((unsigned)PW), make_fastdiv((unsigned)(PR * PW)),
+                       (int)w_nat);
     return check_launch();
+}
+
+template <int WM, int KS, int KST, bool EPI>
+static int smallk_lds_launch(const ConvGeom &g, const float *x, const float *w, float *y,
+                             const Epi &e, bool w_nat, hipStream_t st)
+{
+    constexpr int WN = 4 / WM;
+    const long long N = (long long)g.B * g.OH * g.OW;
+    const long long fb = (g.F + 32 * WM - 1) / (32 * WM);
+    if (N / (32 * 8 * WN) * fb >= 512) {
+        const int rc = smallk_lds_go<WM, KS, KST, EPI, 8>(g, x, w, y, e, w_nat, st);
+        if (rc != ACH_EUNSUPPORTED) return rc;
+    }
+    if (N / (32 * 4 * WN) * fb >= 512) {
+        const int rc = smallk_lds_go<WM, KS, KST, EPI, 4>(g, x, w, y, e, w_nat, st);
+        if (rc != ACH_EUNSUPPORTED) return rc;
+    }
+    return smallk_lds_go<WM, KS, KST, EPI, 2>(g, x, w, y, e, w_nat, st);
 }
 
 template <int WM, bool EPI>

@@ -583,6 +583,41 @@ def test_conv_fwd_bias_act_fused(gpu, shape, act):
 
 
 @pytest.mark.parametrize("shape", [
+    (512, 3, 16, 8, 128, 3, 1, 1),    # 128 filters per workgroup, 4 tiles per wave
+    (256, 3, 32, 32, 48, 3, 1, 1),    # 64 filters per workgroup, 8 tiles per wave, ragged M
+    (512, 3, 32, 32, 16, 3, 1, 1),    # 32 filters per workgroup, 8 tiles per wave
+    (512, 1, 16, 16, 40, 5, 1, 2),    # 5x5 (kernel size at run time), 4 tiles per wave
+], ids=lambda s: "x".join(map(str, s)))
+def test_conv_fwd_shallow_tile_counts(gpu, oracle, shape):
+    """The patch-staged shallow-im2col forward walks 4 or 8 tiles per wave
+    only when the grid is large: forward against the oracle, and the fused
+    bias + leaky epilogue bit-equal to the separate passes."""
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, _ = _conv_inputs(shape, 21)
+    ref = oracle.conv_forward(x, w, F, k, s, p)
+    d = conv_desc(*shape)
+    ws = gpu.ach_conv_fwd_workspace(C.byref(d))
+    dws = dev(np.zeros(ws // 4 + 64, np.float32))
+    dx, dw = dev(x), dev(w)
+    y = D(ref.shape)
+    check(gpu.ach_fill(y.ptr, ref.size, 123.0, None))  # must be overwritten
+    check(gpu.ach_conv_fwd(C.byref(d), dx.ptr, dw.ptr, y.ptr, dws.ptr, ws, None))
+    assert rel_err(y.numpy(), ref) < TOL
+    bias = dev(np.random.default_rng(22).standard_normal(F).astype(np.float32))
+    wt = dev(np.zeros(w.size, np.float32))
+    job = aetcnn.FilterJob(d, dw.ptr, wt.ptr, None)
+    check(gpu.ach_conv_prepare_filters(1, C.byref(job), None))
+    y0, y1 = D(ref.shape), D(ref.shape)
+    oh, ow = gpu.ach_conv_out_h(C.byref(d)), gpu.ach_conv_out_w(C.byref(d))
+    check(gpu.ach_conv_fwd_prepared(C.byref(d), dx.ptr, wt.ptr, y0.ptr, dws.ptr, ws, None))
+    check(gpu.ach_add_bias(y0.ptr, bias.ptr, B, F, oh * ow, None))
+    check(gpu.ach_activate(y0.ptr, ref.size, aetcnn.LEAKY, None))
+    check(gpu.ach_conv_fwd_bias_act_prepared(C.byref(d), dx.ptr, wt.ptr, bias.ptr, aetcnn.LEAKY,
+                                             y1.ptr, dws.ptr, ws, None))
+    assert np.array_equal(y0.numpy().view(np.uint32), y1.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [
     (2, 128, 16, 16, 256, 3, 1, 1),   # 3x3, 256-row tiles, split K
     (3, 5, 9, 7, 10, 3, 1, 1),
     (2, 16, 13, 13, 24, 5, 1, 2),     # generic kernel size
