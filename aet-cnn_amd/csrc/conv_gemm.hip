@@ -838,6 +838,46 @@ struct FwdProblem {
         if constexpr (EPI) v = e.apply(v, m);
         y[((size_t)b * M + m) * ohw + p] = v;
     }
+    // The 16 values of one lane of a 32x32 accumulator tile: rows mb +
+    // 8*(r/4) + r%4, column n.  The column's image and position (one
+    // division) and the base address are computed once per tile, each row
+    // is an offset from it.  full: every row of the workgroup's tile is
+    // below M (no per-row test).
+    __device__ __forceinline__ void store_tile(int mb, int n, const v16f &acc, int z,
+                                               bool full) const
+    {
+        if (n >= N) return;
+        float *base;
+        int stride;
+        if (splits > 1) {
+            base = part + ((size_t)z * M + mb) * N + n;
+            stride = N;
+        } else {
+            const int ohw = g.OH * g.OW;
+            const int b = n / ohw, p = n - b * ohw;
+            base = y + ((size_t)b * M + mb) * ohw + p;
+            stride = ohw;
+        }
+        if (full) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                float v = acc[r];
+                if constexpr (EPI) v = e.apply(v, mb + dm);
+                base[(size_t)dm * stride] = v;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                if (mb + dm < M) {
+                    float v = acc[r];
+                    if constexpr (EPI) v = e.apply(v, mb + dm);
+                    base[(size_t)dm * stride] = v;
+                }
+            }
+        }
+    }
 };
 
 template <int BM_, int BN_, int KS_T>
@@ -1010,6 +1050,10 @@ struct FcWgradProblem {
 // ===========================================================================
 template <class P, class = void> struct is_rmw : std::false_type {};
 template <class P> struct is_rmw<P, std::void_t<decltype(P::RMW)>> : std::true_type {};
+template <class P, class = void> struct has_store_tile : std::false_type {};
+template <class P>
+struct has_store_tile<P, std::void_t<decltype(std::declval<const P &>().store_tile(
+                             0, 0, std::declval<const v16f &>(), 0, false))>> : std::true_type {};
 
 
 template <class P>
@@ -1139,7 +1183,9 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
         for (int j = 0; j < TN; ++j) {
             const int n = n0 + wn * (BN / WN) + j * 32 + lcol;
             const int mb = m0 + wm * (BM / WM) + i * 32 + 4 * lrow;
-            if constexpr (is_rmw<P>::value) {
+            if constexpr (has_store_tile<P>::value) {
+                p.store_tile(mb, n, acc[i][j], z, m0 + BM <= p.M);
+            } else if constexpr (is_rmw<P>::value) {
                 // all 16 prior values in flight before the first store
                 float old[16];
 #pragma unroll
