@@ -948,6 +948,42 @@ struct WgradProblemC {
         else
             part[((size_t)z * M + m) * N + n] = v;
     }
+    // One lane's 16 values of a 32x32 tile (rows mb + 8*(r/4) + r%4, column
+    // n): the base address once per tile, rows at a stride of N; dw += acc
+    // with all 16 prior values loaded before the first store, or the K
+    // slice's partial sums.  full: every row of the workgroup's tile is
+    // below M.
+    __device__ __forceinline__ void store_tile(int mb, int n, const v16f &acc, int z,
+                                               bool full) const
+    {
+        if (n >= N) return;
+        if (splits == 1) {
+            float *base = dw + (size_t)mb * N + n;
+            float old[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                old[r] = (full || mb + dm < M) ? base[(size_t)dm * N] : 0.f;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                if (full || mb + dm < M) base[(size_t)dm * N] = old[r] + acc[r];
+            }
+        } else {
+            float *base = part + ((size_t)z * M + mb) * N + n;
+            if (full) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) base[(size_t)(8 * (r >> 2) + (r & 3)) * N] = acc[r];
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int dm = 8 * (r >> 2) + (r & 3);
+                    if (mb + dm < M) base[(size_t)dm * N] = acc[r];
+                }
+            }
+        }
+    }
 };
 
 template <bool TA, bool TB>
