@@ -38,6 +38,14 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int GNT = 256;     // threads per workgroup
 constexpr int GBN = 128;     // N tile
 constexpr int LDP = 4;       // LDS row padding (floats)
+// The 3x3 forward's operand rows (AWeightsT4, BIm2col3) are unpadded: 128
+// floats, so every k-step's fragment pair sits a whole number of 64-float
+// units from one base and one ds_read2st64 reads it without address
+// arithmetic.  Their stores write whole 64-lane row segments (no conflicts).
+#ifndef ACH_LDP_FWD
+#define ACH_LDP_FWD 0
+#endif
+constexpr int LDP_FWD = ACH_LDP_FWD;
 constexpr unsigned kOOB = 0x80000000u;  // buffer offset that reads as 0
 #ifndef ACH_WGRAD_BK
 #define ACH_WGRAD_BK 16
@@ -151,8 +159,8 @@ template <int BM, int BK>
 struct AWeightsT4 {
     static constexpr int C4 = BM / 4;                      // float4 per tile row
     static constexpr int NV = (BK * C4 + GNT - 1) / GNT;   // float4 per thread
-    static constexpr int RA = 4 * NV, PAD = LDP;
-    static_assert(BM % 4 == 0 && ((BM + LDP) % 4) == 0, "16-byte LDS rows");
+    static constexpr int RA = 4 * NV, PAD = LDP_FWD;
+    static_assert(BM % 4 == 0 && ((BM + PAD) % 4) == 0, "16-byte LDS rows");
     __amdgpu_buffer_rsrc_t rs;
     int M, m0;
     __device__ __forceinline__ void init(const float *wt, int M_, int K_, int m0_, int)
@@ -291,7 +299,7 @@ struct AWeightsT4F : AWeightsT4<BM, BK> {
 struct BIm2col3 {
     static constexpr int CH = ACH_FWD_CH, HC = CH / 2;
     static_assert(CH % 2 == 0, "channel groups split over two thread halves");
-    static constexpr int BK = 9 * CH, RB = 9 * HC, PAD = LDP;
+    static constexpr int BK = 9 * CH, RB = 9 * HC, PAD = LDP_FWD;
     __amdgpu_buffer_rsrc_t rs;
     int base;      // b*C*H*W + (oh*S-P)*W + (ow*S-P) + kr*H*W
     int HW, W, K, kr;
@@ -1101,6 +1109,9 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     constexpr int WM = BN <= 32 ? 4 : (BN % 64 != 0 && BM % 128 == 0 ? 4 : (BM % 64 == 0 ? 2 : 1));
     constexpr int WN = 4 / WM;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;      // MFMA tiles per wave
+    // a wave's tiles interleave with the other waves' (rows (i*WM + wm)*32,
+    // columns (j*WN + wn)*32): its two fragments of a k-step lie 64 floats
+    // apart, which one ds_read2st64 fetches
     static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
     constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
     __shared__ __attribute__((aligned(16))) float As[2][BK][LA];
@@ -1159,19 +1170,19 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
         // k-step kk issue, so the LDS latency hides behind the matrix pipe
         float a[2][TM], b[2][TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[0][i] = As[cur][lrow][wm * (BM / WM) + i * 32 + lcol];
+        for (int i = 0; i < TM; ++i) a[0][i] = As[cur][lrow][(i * WM + wm) * 32 + lcol];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[0][j] = Bs[cur][lrow][wn * (BN / WN) + j * 32 + lcol];
+        for (int j = 0; j < TN; ++j) b[0][j] = Bs[cur][lrow][(j * WN + wn) * 32 + lcol];
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
             const int s = (kk >> 1) & 1;
             if (kk + 2 < BK) {
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    a[s ^ 1][i] = As[cur][kk + 2 + lrow][wm * (BM / WM) + i * 32 + lcol];
+                    a[s ^ 1][i] = As[cur][kk + 2 + lrow][(i * WM + wm) * 32 + lcol];
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    b[s ^ 1][j] = Bs[cur][kk + 2 + lrow][wn * (BN / WN) + j * 32 + lcol];
+                    b[s ^ 1][j] = Bs[cur][kk + 2 + lrow][(j * WN + wn) * 32 + lcol];
             }
             // keep the scheduler from sinking those reads below the MFMAs
             __builtin_amdgcn_sched_barrier(0);
@@ -1217,8 +1228,8 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn * (BN / WN) + j * 32 + lcol;
-            const int mb = m0 + wm * (BM / WM) + i * 32 + 4 * lrow;
+            const int n = n0 + (j * WN + wn) * 32 + lcol;
+            const int mb = m0 + (i * WM + wm) * 32 + 4 * lrow;
             if constexpr (has_store_tile<P>::value) {
                 p.store_tile(mb, n, acc[i][j], z, m0 + BM <= p.M);
             } else if constexpr (is_rmw<P>::value) {
