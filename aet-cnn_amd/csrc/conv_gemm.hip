@@ -652,9 +652,14 @@ struct BWgrad {
 // for the whole split: the byte offsets are computed once and a k-tile (one
 // image) only adds the uniform image stride.  Offsets of invalid elements
 // are >= 2^31 and stay out of range after the addition (operands < 2 GiB).
+// Both operands are staged K-contiguous (KC: S[row][position], rows of 17
+// floats): a thread writes its 16-position run along one row, and a
+// fragment's two k-steps are a fixed small offset apart, so the loop reads
+// them without address arithmetic.
 template <int BM, int BK_>
 struct AWgradC {
     static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = WG_PAD;
+    static constexpr bool KC = true;  // stored as S[m][k]
     static_assert(BK == 16, "one 16-position chunk per k-tile");
     __amdgpu_buffer_rsrc_t rs;
     unsigned voff[RA];
@@ -687,13 +692,14 @@ struct AWgradC {
     {
         const int r = threadIdx.x / BK, kc = threadIdx.x % BK;
 #pragma unroll
-        for (int i = 0; i < RA; ++i) S[kc][r + RPI * i] = ra[i];
+        for (int i = 0; i < RA; ++i) S[r + RPI * i][kc] = ra[i];
     }
 };
 
 template <int BN, int BK_, int KS_T>
 struct BWgradC {
     static constexpr int BK = BK_, RPI = GNT / BK, RB = BN / RPI, PAD = WG_PAD;
+    static constexpr bool KC = true;  // stored as S[n][k]
     static_assert(BK == 16, "one 16-position chunk per k-tile");
     __amdgpu_buffer_rsrc_t rs;
     unsigned voff[RB];
@@ -732,7 +738,7 @@ struct BWgradC {
     {
         const int r = threadIdx.x / BK, kc = threadIdx.x % BK;
 #pragma unroll
-        for (int i = 0; i < RB; ++i) S_[kc][r + RPI * i] = rb[i];
+        for (int i = 0; i < RB; ++i) S_[r + RPI * i][kc] = rb[i];
     }
 };
 
@@ -1094,6 +1100,8 @@ struct FcWgradProblem {
 // ===========================================================================
 template <class P, class = void> struct is_rmw : std::false_type {};
 template <class P> struct is_rmw<P, std::void_t<decltype(P::RMW)>> : std::true_type {};
+template <class L, class = void> struct kc_layout : std::false_type {};
+template <class L> struct kc_layout<L, std::void_t<decltype(L::KC)>> : std::bool_constant<L::KC> {};
 template <class P, class = void> struct has_store_tile : std::false_type {};
 template <class P>
 struct has_store_tile<P, std::void_t<decltype(std::declval<const P &>().store_tile(
@@ -1113,9 +1121,22 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     // columns (j*WN + wn)*32): its two fragments of a k-step lie 64 floats
     // apart, which one ds_read2st64 fetches
     static_assert(TM >= 1 && TN >= 1, "tile too small for the wave grid");
-    constexpr int LA = BM + P::AL::PAD, LB = BN + P::BLd::PAD;
-    __shared__ __attribute__((aligned(16))) float As[2][BK][LA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LB];
+    // LDS stages: k-major [BK][rows + PAD], or [rows][BK + 1] for loaders
+    // that store a row's K positions contiguously (KC): the odd row length
+    // keeps a fragment's 32 rows on 32 banks, and two k-steps of a fragment
+    // are a few floats apart (one ds_read2 from a fixed base)
+    constexpr bool AKC = kc_layout<typename P::AL>::value, BKC = kc_layout<typename P::BLd>::value;
+    constexpr int LA = AKC ? BK + 1 : BM + P::AL::PAD, LB = BKC ? BK + 1 : BN + P::BLd::PAD;
+    __shared__ __attribute__((aligned(16))) float As[2][AKC ? BM : BK][LA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BKC ? BN : BK][LB];
+    auto rda = [&](int c, int k, int m) -> float {
+        if constexpr (AKC) return As[c][m][k];
+        else return As[c][k][m];
+    };
+    auto rdb = [&](int c, int k, int n) -> float {
+        if constexpr (BKC) return Bs[c][n][k];
+        else return Bs[c][k][n];
+    };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -1170,19 +1191,19 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
         // k-step kk issue, so the LDS latency hides behind the matrix pipe
         float a[2][TM], b[2][TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[0][i] = As[cur][lrow][(i * WM + wm) * 32 + lcol];
+        for (int i = 0; i < TM; ++i) a[0][i] = rda(cur, lrow, (i * WM + wm) * 32 + lcol);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[0][j] = Bs[cur][lrow][(j * WN + wn) * 32 + lcol];
+        for (int j = 0; j < TN; ++j) b[0][j] = rdb(cur, lrow, (j * WN + wn) * 32 + lcol);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
             const int s = (kk >> 1) & 1;
             if (kk + 2 < BK) {
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    a[s ^ 1][i] = As[cur][kk + 2 + lrow][(i * WM + wm) * 32 + lcol];
+                    a[s ^ 1][i] = rda(cur, kk + 2 + lrow, (i * WM + wm) * 32 + lcol);
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    b[s ^ 1][j] = Bs[cur][kk + 2 + lrow][(j * WN + wn) * 32 + lcol];
+                    b[s ^ 1][j] = rdb(cur, kk + 2 + lrow, (j * WN + wn) * 32 + lcol);
             }
             // keep the scheduler from sinking those reads below the MFMAs
             __builtin_amdgcn_sched_barrier(0);
