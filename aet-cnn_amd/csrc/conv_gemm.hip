@@ -38,10 +38,11 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int GNT = 256;     // threads per workgroup
 constexpr int GBN = 128;     // N tile
 constexpr int LDP = 4;       // LDS row padding (floats)
-// The 3x3 forward's operand rows (AWeightsT4, BIm2col3) are unpadded: 128
-// floats, so every k-step's fragment pair sits a whole number of 64-float
-// units from one base and one ds_read2st64 reads it without address
-// arithmetic.  Their stores write whole 64-lane row segments (no conflicts).
+// The forward loaders' operand rows (AWeightsT, AWeightsT4, BIm2col3,
+// BIm2colK, BIm2colAny) are unpadded: 128 floats, so every k-step's fragment
+// pair sits a whole number of 64-float units from one base and one
+// ds_read2st64 reads it without address arithmetic.  Their stores write whole
+// 64-lane row segments (no conflicts).
 #ifndef ACH_LDP_FWD
 #define ACH_LDP_FWD 0
 #endif
@@ -108,7 +109,7 @@ struct ConvGeom {
 template <int BM, int BK>
 struct AWeightsT {
     static constexpr int RPI = GNT / BM;                 // rows per step
-    static constexpr int RA = (BK + RPI - 1) / RPI, PAD = LDP;
+    static constexpr int RA = (BK + RPI - 1) / RPI, PAD = LDP_FWD;
     __amdgpu_buffer_rsrc_t rs;
     int M, mok, kr, col;
     __device__ __forceinline__ void init(const float *wt, int M_, int K_, int m0, int tid)
@@ -389,7 +390,7 @@ struct BIm2col3F : BIm2col3 {
 // LDS stages per CU.
 template <int KS>
 struct BIm2colK {
-    static constexpr int T = KS * KS, BK = T + 1, HALF = BK / 2, RB = HALF, PAD = LDP;
+    static constexpr int T = KS * KS, BK = T + 1, HALF = BK / 2, RB = HALF, PAD = LDP_FWD;
     static_assert(T % 2 == 1, "odd kernel: one zero row completes the k-step");
     __amdgpu_buffer_rsrc_t rs;
     unsigned voff[HALF];
@@ -479,7 +480,7 @@ template <int KS> struct PaddedTaps<BIm2colK<KS>> {
 // n0 + tid%128, rows tid/128 + 2*i.
 template <int KS_T>
 struct BIm2colAny {
-    static constexpr int BK = 16, RB = 8, PAD = LDP;
+    static constexpr int BK = 16, RB = 8, PAD = LDP_FWD;
     __amdgpu_buffer_rsrc_t rs;
     int xoff, ihb, iwb, kr, ok, H, W, KS;
     FastDiv dkk, dks;
