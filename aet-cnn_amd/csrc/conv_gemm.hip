@@ -489,7 +489,9 @@ struct BIm2colAny {
     {
         rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
         const int n = n0 + tid % GBN;
-        kr = tid / GBN;
+        // the same for the 128 threads of two waves: the rows' (c, ki, kj)
+        // are then scalar arithmetic
+        kr = __builtin_amdgcn_readfirstlane(tid / GBN);
         ok = n < N;
         H = g.H;
         W = g.W;
