@@ -751,17 +751,28 @@ template <bool T, int BR>
 struct PlainOperand {
     // element (r, k) of op(X) where X is [R][K] (T = 0) or [K][R] (T = 1);
     // thread map: T = 0 -> k fastest (k = tid%16), T = 1 -> r fastest.
+    // Each element's byte offset at k0 = 0 is fixed (rows past R clamped to
+    // R-1: they feed only output rows / columns that are never stored); a
+    // k-tile adds one uniform offset, and only a k-tile that reaches past
+    // the end of its K range tests k per element (zero past the end).
     static constexpr int BK = 16, RN = BR * BK / GNT, RA = RN, RB = RN, PAD = T ? LDP : 1;
     __amdgpu_buffer_rsrc_t rs;
-    int R, K, ld, r0;
+    int K, ld, r0;
+    unsigned voff[RN];
     __device__ __forceinline__ void init(const float *X, int R_, int K_, int ld_, size_t bytes,
                                          int r0_)
     {
         rs = make_rsrc(X, (unsigned)bytes);
-        R = R_;
         K = K_;
         ld = ld_;
         r0 = r0_;
+#pragma unroll
+        for (int i = 0; i < RN; ++i) {
+            int r, k;
+            coords(i, 0, r, k);
+            r = r < R_ ? r : R_ - 1;
+            voff[i] = (unsigned)(T ? k * ld + r : r * ld + k) * 4u;
+        }
     }
     __device__ __forceinline__ void coords(int i, int k0, int &r, int &k) const
     {
@@ -770,11 +781,17 @@ struct PlainOperand {
     }
     __device__ __forceinline__ void load(int k0, int ke, float *v) const
     {
+        const unsigned d = (T ? (unsigned)k0 * (unsigned)ld : (unsigned)k0) * 4u;
+        if (k0 + BK <= ke) {
 #pragma unroll
-        for (int i = 0; i < RN; ++i) {
-            int r, k;
-            coords(i, k0, r, k);
-            v[i] = bload(rs, boff(r < R && k < ke, T ? k * ld + r : r * ld + k));
+            for (int i = 0; i < RN; ++i) v[i] = bload_so(rs, voff[i], d);
+        } else {
+#pragma unroll
+            for (int i = 0; i < RN; ++i) {
+                int r, k;
+                coords(i, k0, r, k);
+                v[i] = k < ke ? bload_so(rs, voff[i], d) : 0.f;
+            }
         }
     }
     template <int LD>
