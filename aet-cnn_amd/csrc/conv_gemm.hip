@@ -1413,7 +1413,13 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk(const float *__restrict
 // w_nat, in its own layout W[M][K] (no transposed copy needed).  The host
 // takes this kernel when the positions of one image divide into whole tiles
 // and the patch fits.
-template <int WM, int KS_, int KST, bool EPI, int TPW>
+// OWC != 0 (output rows exactly OWC = 32 wide, stride 1, KS_ x KS_): every
+// tile is one output row and the patch pitch is OWC + KS_ - 1, so tile t of
+// a wave reads t patch rows below tile 0.  The lane's KST LDS addresses are
+// then computed once, each tile's reads add only a compile-time offset (no
+// address arithmetic or k < K selects per tile), and the k-steps past K
+// read a zeroed block after the patch.
+template <int WM, int KS_, int KST, bool EPI, int TPW, int OWC = 0>
 __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__restrict__ x,
                                                              const float *__restrict__ w,
                                                              float *__restrict__ y, ConvGeom g,
@@ -1423,6 +1429,8 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__rest
 {
     extern __shared__ float patch[];
     constexpr int WN = 4 / WM, NT = 32 * TPW * WN, U = 8;
+    static_assert(OWC == 0 || (OWC == 32 && KS_ > 0), "row tiles need 32-wide rows, fixed KS");
+    constexpr int PWC = OWC ? OWC + KS_ - 1 : 0;  // the patch pitch of row tiles
     const int PW = (int)dpw.d;
     const int KS = KS_ ? KS_ : g.KS, KK = KS * KS;
     const int M = g.F, K = g.C * KK, ohw = (int)dohw.d;
@@ -1458,6 +1466,9 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__rest
             if (i < tot) patch[i] = v[u];
         }
     }
+    if constexpr (OWC != 0) {  // the zero block: TPW patch rows
+        for (int i = (int)threadIdx.x; i < TPW * PWC; i += GNT) patch[tot + i] = 0.f;
+    }
     // A: lane holds W(m0 + lcol, 2s + lrow) for the KST k-steps s
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (unsigned)((size_t)M * K * 4));
     const int m = m0 + lcol;
@@ -1474,7 +1485,18 @@ __global__ void __launch_bounds__(GNT) k_conv_fwd_smallk_lds(const float *__rest
     if (m0 >= M) return;
 
     const int pw0 = p0 + wn * 32 * TPW;  // the wave's first position
+    int vb[KST];  // row tiles: the lane's patch index of each k-step in tile 0
+    if constexpr (OWC != 0) {
+        const int lb0 = (pw0 / OWC - oyf) * PWC + lcol;
+#pragma unroll
+        for (int s = 0; s < KST; ++s) vb[s] = 2 * s + lrow < K ? lb0 + toff[s] : tot;
+    }
     auto fetch = [&](int t, float (&bb)[KST]) {
+        if constexpr (OWC != 0) {
+#pragma unroll
+            for (int s = 0; s < KST; ++s) bb[s] = patch[vb[s] + t * PWC];
+            return;
+        }
         const int p = pw0 + 32 * t + lcol;
         const int oy = fdiv(p, dow), ox = p - oy * g.OW;
         const int lb = (oy - oyf) * g.S * PW + ox * g.S;
@@ -1916,7 +1938,7 @@ static int smallk_launch(const ConvGeom &g, const float *x, const float *wt, flo
 // Tiles per wave: the most of 8, 4, 2 whose workgroup span divides the
 // positions of an image and still leaves 512 workgroups (fewer tiles per
 // wave when the grid would not fill the GPU twice over).
-template <int WM, int KS, int KST, bool EPI, int TPW>
+template <int WM, int KS, int KST, bool EPI, int TPW, int OWC>
 static int smallk_lds_go(const ConvGeom &g, const float *x, const float *w, float *y,
                          const Epi &e, bool w_nat, hipStream_t st)
 {
@@ -1926,17 +1948,21 @@ static int smallk_lds_go(const ConvGeom &g, const float *x, const float *w, floa
     // the input rows of the output rows a tile spans
     const int rows = (NT + g.OW - 2) / g.OW + 1;
     const int PR = (rows - 1) * g.S + g.KS, PW = g.W + 2 * g.P;
-    const size_t lds = (size_t)g.C * PR * PW * sizeof(float);
+    // row tiles add a zero block of TPW patch rows
+    const size_t lds = ((size_t)g.C * PR * PW + (OWC ? (size_t)TPW * PW : 0)) * sizeof(float);
     if (ohw % NT != 0 || lds > 32768 || grid.y > 65535 || (size_t)ohw * 32 * 4 >= (1u << 31))
         return ACH_EUNSUPPORTED;
-    hipLaunchKernelGGL((k_conv_fwd_smallk_lds<WM, KS, KST, EPI, TPW>), grid, dim3(GNT), lds, st,
+    if (OWC && (g.OW != OWC || g.S != 1 || g.KS != KS || PW != OWC + KS - 1))
+        return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL((k_conv_fwd_smallk_lds<WM, KS, KST, EPI, TPW, OWC>), grid, dim3(GNT), lds,
+                       st,
                        x, w, y, g, make_fastdiv((unsigned)ohw), make_fastdiv((unsigned)g.OW), e,
                        PR, make_fastdiv((unsigned)PW), make_fastdiv((unsigned)(PR * PW)),
                        (int)w_nat);
     return check_launch();
 }
 
-template <int WM, int KS, int KST, bool EPI>
+template <int WM, int KS, int KST, bool EPI, int OWC = 0>
 static int smallk_lds_launch(const ConvGeom &g, const float *x, const float *w, float *y,
                              const Epi &e, bool w_nat, hipStream_t st)
 {
@@ -1944,21 +1970,26 @@ static int smallk_lds_launch(const ConvGeom &g, const float *x, const float *w, 
     const long long N = (long long)g.B * g.OH * g.OW;
     const long long fb = (g.F + 32 * WM - 1) / (32 * WM);
     if (N / (32 * 8 * WN) * fb >= 512) {
-        const int rc = smallk_lds_go<WM, KS, KST, EPI, 8>(g, x, w, y, e, w_nat, st);
+        const int rc = smallk_lds_go<WM, KS, KST, EPI, 8, OWC>(g, x, w, y, e, w_nat, st);
         if (rc != ACH_EUNSUPPORTED) return rc;
     }
     if (N / (32 * 4 * WN) * fb >= 512) {
-        const int rc = smallk_lds_go<WM, KS, KST, EPI, 4>(g, x, w, y, e, w_nat, st);
+        const int rc = smallk_lds_go<WM, KS, KST, EPI, 4, OWC>(g, x, w, y, e, w_nat, st);
         if (rc != ACH_EUNSUPPORTED) return rc;
     }
-    return smallk_lds_go<WM, KS, KST, EPI, 2>(g, x, w, y, e, w_nat, st);
+    return smallk_lds_go<WM, KS, KST, EPI, 2, OWC>(g, x, w, y, e, w_nat, st);
 }
 
 template <int WM, bool EPI>
 static int smallk_lds_ks(const ConvGeom &g, const float *x, const float *w, float *y,
                          const Epi &e, bool w_nat, hipStream_t st)
 {
-    // 3x3 over 3 channels (K = 27): 14 k-steps; otherwise the full 16
+    // 3x3 over 3 channels (K = 27): 14 k-steps, in row tiles for 32-wide
+    // stride-1 outputs; otherwise the full 16
+    if (g.KS == 3 && g.C == 3 && g.OW == 32 && g.S == 1) {
+        const int rc = smallk_lds_launch<WM, 3, 14, EPI, 32>(g, x, w, y, e, w_nat, st);
+        if (rc != ACH_EUNSUPPORTED) return rc;
+    }
     if (g.KS == 3 && g.C == 3) return smallk_lds_launch<WM, 3, 14, EPI>(g, x, w, y, e, w_nat, st);
     if (g.KS == 3) return smallk_lds_launch<WM, 3, 16, EPI>(g, x, w, y, e, w_nat, st);
     return smallk_lds_launch<WM, 0, 16, EPI>(g, x, w, y, e, w_nat, st);
