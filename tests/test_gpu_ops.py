@@ -586,6 +586,7 @@ def test_conv_fwd_bias_act_fused(gpu, shape, act):
     (512, 3, 16, 8, 128, 3, 1, 1),    # 128 filters per workgroup, 4 tiles per wave
     (256, 3, 32, 32, 48, 3, 1, 1),    # 64 filters per workgroup, 8 tiles per wave, ragged M
     (512, 3, 32, 32, 16, 3, 1, 1),    # 32 filters per workgroup, 8 tiles per wave
+    (256, 3, 34, 34, 64, 3, 1, 0),    # 32-wide output rows without padding (row tiles)
     (512, 1, 16, 16, 40, 5, 1, 2),    # 5x5 (kernel size at run time), 4 tiles per wave
 ], ids=lambda s: "x".join(map(str, s)))
 def test_conv_fwd_shallow_tile_counts(gpu, oracle, shape):
