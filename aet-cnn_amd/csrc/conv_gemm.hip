@@ -36,6 +36,9 @@ namespace ach {
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int GNT = 256;     // threads per workgroup
+// thread index within a GNT-thread group: a GEMM workgroup may hold
+// several groups, each loading its own operand tiles
+__device__ __forceinline__ int ltid() { return (int)(threadIdx.x & (GNT - 1)); }
 constexpr int GBN = 128;     // N tile
 constexpr int LDP = 4;       // LDS row padding (floats)
 // The forward loaders' operand rows (AWeightsT, AWeightsT4, BIm2col3,
@@ -174,7 +177,7 @@ struct AWeightsT4 {
     {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int f = threadIdx.x + GNT * i;
+            const int f = ltid() + GNT * i;
             const int row = f / C4, m = m0 + 4 * (f % C4), k = k0 + row;
             const bool ok = f < BK * C4 && k < ke && m < M;
             const float4 v = bload4(rs, boff(ok, k * M + m));
@@ -193,7 +196,7 @@ struct AWeightsT4 {
     {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int f = threadIdx.x + GNT * i;
+            const int f = ltid() + GNT * i;
             if (i + 1 < NV || NV * GNT <= BK * C4 || f < BK * C4)
                 *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
                     make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
@@ -274,7 +277,7 @@ struct AWeightsT4F : AWeightsT4<BM, BK> {
         M4 = M_ * 4;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int f = threadIdx.x + GNT * i;
+            const int f = ltid() + GNT * i;
             const int row = f / C4, m = m0_ + 4 * (f % C4);
             voff[i] = (f < BK * C4 && m < M_) ? (unsigned)(row * M_ + m) * 4u : kOOB;
         }
@@ -345,7 +348,7 @@ struct BIm2col3 {
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
     {
-        const int nc = threadIdx.x % GBN;
+        const int nc = ltid() % GBN;
 #pragma unroll
         for (int j = 0; j < HC; ++j)
 #pragma unroll
@@ -1128,10 +1131,16 @@ struct has_store_tile<P, std::void_t<decltype(std::declval<const P &>().store_ti
                              0, 0, std::declval<const v16f &>(), 0, false))>> : std::true_type {};
 
 
-template <class P>
-__global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
+// KG > 1: KG groups of GNT threads share one output tile, group g taking
+// the K slice z*KG + g of the problem's K split; at the end each group adds
+// the other groups' accumulators of the fragments it stores, through LDS.
+// With KG = 2 the sum is slice 0 + slice 1, the value a separate reduction
+// of the two slices' partials would produce, without writing them.
+template <class P, int KG = 1>
+__global__ void __launch_bounds__(GNT * KG) k_mfma_gemm(P p, int mt, int nt)
 {
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK;
+    static_assert(KG == 1 || KG == 2, "one or two K groups per workgroup");
     // wave grid: 2x2 for 64+ x 128 tiles, 1x4 for 32-row, 4x1 for 32-column
     // and for 128 x 96 tiles (each wave 32 x 96)
     constexpr int WM = BN <= 32 ? 4 : (BN % 64 != 0 && BM % 128 == 0 ? 4 : (BM % 64 == 0 ? 2 : 1));
@@ -1147,8 +1156,11 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     // are a few floats apart (one ds_read2 from a fixed base)
     constexpr bool AKC = kc_layout<typename P::AL>::value, BKC = kc_layout<typename P::BLd>::value;
     constexpr int LA = AKC ? BK + 1 : BM + P::AL::PAD, LB = BKC ? BK + 1 : BN + P::BLd::PAD;
-    __shared__ __attribute__((aligned(16))) float As[2][AKC ? BM : BK][LA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BKC ? BN : BK][LB];
+    __shared__ __attribute__((aligned(16))) float Ash[KG][2][AKC ? BM : BK][LA];
+    __shared__ __attribute__((aligned(16))) float Bsh[KG][2][BKC ? BN : BK][LB];
+    const int grp = KG > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x / GNT)) : 0;
+    auto &As = Ash[grp];
+    auto &Bs = Bsh[grp];
     auto rda = [&](int c, int k, int m) -> float {
         if constexpr (AKC) return As[c][m][k];
         else return As[c][k][m];
@@ -1158,7 +1170,7 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
         else return Bs[c][k][n];
     };
 
-    const int tid = threadIdx.x;
+    const int tid = (int)threadIdx.x - grp * GNT;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
 
@@ -1176,7 +1188,7 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
     const int m0 = (tile % mt) * BM, n0 = (tile / mt) * BN;
 
     int kb, ke;
-    p.krange(z, kb, ke);
+    p.krange(z * KG + grp, kb, ke);
     typename P::AL al;
     typename P::BLd bl;
     p.init_a(al, m0, tid, kb);
@@ -1191,7 +1203,17 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     float ra[P::AL::RA], rb[P::BLd::RB];
-    const int nkt = (ke - kb + BK - 1) / BK;
+    int nkt = (ke - kb + BK - 1) / BK;
+    if constexpr (KG > 1) {
+        // every group runs the longest slice's k-tile count (the barriers
+        // are shared); past its own end a group's loads read zeros
+#pragma unroll
+        for (int q = 0; q < KG; ++q) {
+            int qb, qe;
+            p.krange(z * KG + q, qb, qe);
+            nkt = max(nkt, (qe - qb + BK - 1) / BK);
+        }
+    }
     if (nkt > 0) {
         al.load(kb, ke, ra);
         bl.load(kb, ke, rb);
@@ -1263,12 +1285,55 @@ __global__ void __launch_bounds__(GNT) k_mfma_gemm(P p, int mt, int nt)
         __syncthreads();
     }
 
+    if constexpr (KG > 1) {
+        // group g stores the fragments f = i*TN + j with f % KG == g: it
+        // hands the others' fragments over and adds what it receives.  The
+        // stages are free after the loop's last barrier: fragments 0 and 1
+        // go through the A stages, 2 and 3 through the B stages, each as
+        // [register / 4][thread][4]
+        static_assert(KG == 2 && TM * TN == 4, "two K groups exchange 4 fragments per wave");
+        static_assert(sizeof(Ash) >= 2 * 16 * GNT * sizeof(float) &&
+                          sizeof(Bsh) >= 2 * 16 * GNT * sizeof(float),
+                      "each stage array holds two exchanged fragments");
+        auto xslot = [&](int f, int r4) -> float4 * {
+            float4 *base = reinterpret_cast<float4 *>(f < 2 ? &Ash[0][0][0][0] : &Bsh[0][0][0][0]);
+            return base + ((f & 1) * 4 + r4) * GNT + tid;
+        };
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int f = i * TN + j;
+                if (f % KG == grp) continue;
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    *xslot(f, r4) = make_float4(acc[i][j][4 * r4], acc[i][j][4 * r4 + 1],
+                                                acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int f = i * TN + j;
+                if (f % KG != grp) continue;
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const float4 o = *xslot(f, r4);
+                    acc[i][j][4 * r4] += o.x;
+                    acc[i][j][4 * r4 + 1] += o.y;
+                    acc[i][j][4 * r4 + 2] += o.z;
+                    acc[i][j][4 * r4 + 3] += o.w;
+                }
+            }
+    }
     // D layout of v_mfma_f32_32x32x2f32: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
+            if (KG > 1 && (i * TN + j) % KG != grp) continue;
             const int n = n0 + (j * WN + wn) * 32 + lcol;
             const int mb = m0 + (i * WM + wm) * 32 + 4 * lrow;
             if constexpr (has_store_tile<P>::value) {
@@ -1815,12 +1880,15 @@ __global__ void __launch_bounds__(256) k_prepare_filters(PrepTable tab)
 }
 
 // ---------------------------------------------------------------------------
-template <class P>
+// splits: the problem's K slices; KG of them share a workgroup
+template <class P, int KG = 1>
 static int launch_gemm(const P &p, int M, int N, int splits, hipStream_t st)
 {
     const int mt = (M + P::BM - 1) / P::BM, nt = (N + P::BN - 1) / P::BN;
-    if ((long long)mt * nt * splits > 0x7fffffffLL || splits > 65535) return ACH_EINVAL;
-    hipLaunchKernelGGL(k_mfma_gemm<P>, dim3(mt * nt, splits), dim3(GNT), 0, st, p, mt, nt);
+    if ((long long)mt * nt * splits > 0x7fffffffLL || splits > 65535 || splits % KG != 0)
+        return ACH_EINVAL;
+    hipLaunchKernelGGL((k_mfma_gemm<P, KG>), dim3(mt * nt, splits / KG), dim3(GNT * KG), 0, st, p,
+                       mt, nt);
     return check_launch();
 }
 
@@ -1906,6 +1974,7 @@ __global__ void __launch_bounds__(256) k_splitk_rows(const float *__restrict__ p
 // reproducible run to run.
 struct FwdPlan {
     int bm, bk, splits, kchunk;
+    int kg;  // K slices per workgroup (kg == splits: no partial sums)
 };
 
 // a 1x1 convolution of a 1x1 input (the fully connected layers once geom()
@@ -2016,7 +2085,9 @@ static int fwd_small_k_launch(const ConvGeom &g, const float *x, const float *w,
     return smallk_launch<1, 0, EPI>(g, x, w, y, e, st);
 }
 
-static FwdPlan fwd_plan(const ConvGeom &g)
+// kg_ok: the call may run both K slices of a tile in one workgroup (forward
+// passes; input gradients keep the separate reduction, below)
+static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
 {
     FwdPlan pl;
     const int M = g.F, N = g.B * g.OH * g.OW;
@@ -2051,13 +2122,24 @@ static FwdPlan fwd_plan(const ConvGeom &g)
     pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
     pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
     if (fwd_small_k(g)) pl.splits = 1;  // k_conv_fwd_smallk: whole K per tile
+    // a 3x3 forward split in two (the 8x8 layers of darknet: 256 tiles)
+    // runs both slices of a tile in one 512-thread workgroup and adds them in
+    // LDS: the same sums, without the partials' HBM round trip and the
+    // reduction pass (filter counts divisible by 4: the two float4-filter
+    // loaders of fwd_bm).  Input gradients run beside the weight-gradient
+    // GEMMs of the second stream, where 8-wave workgroups with 72 KB of LDS
+    // find fewer free slots: measured on the darknet step, 6.855 ms without,
+    // 6.827 with forward passes only, 6.961 with input gradients only.
+    pl.kg = (kg_ok && pl.splits == 2 && pl.bm == 128 && g.KS == 3 && (g.F & 3) == 0 &&
+             !fc_geom(g))
+                ? 2 : 1;
     return pl;
 }
 
-static size_t fwd_part_bytes(const ConvGeom &g)
+static size_t fwd_part_bytes(const ConvGeom &g, bool kg_ok = true)
 {
-    const FwdPlan pl = fwd_plan(g);
-    if (pl.splits <= 1) return 0;
+    const FwdPlan pl = fwd_plan(g, kg_ok);
+    if (pl.splits <= 1 || pl.kg == pl.splits) return 0;
     return (size_t)pl.splits * g.F * g.B * g.OH * g.OW * sizeof(float);
 }
 
@@ -2068,14 +2150,21 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
                   float *y, float *part, const Epi &e, bool w_nat, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW, K = g.C * g.KS * g.KS;
+    // both K slices in one workgroup: the problem stores finished outputs
+    const bool kg2 = BM == 128 && pl.kg == 2;
+    const int psplits = kg2 ? 1 : pl.splits;
     if (g.KS == 3 && (M & 3) == 0 && (g.C & 1) == 0) {
-        FwdProblem<BM, BIm2col3F, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        FwdProblem<BM, BIm2col3F, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, psplits};
         p.e = e;
+        if constexpr (BM == 128)
+            if (kg2) return launch_gemm<decltype(p), 2>(p, M, N, pl.splits, st);
         return launch_gemm(p, M, N, pl.splits, st);
     }
     if (g.KS == 3 && (M & 3) == 0) {
-        FwdProblem<BM, BIm2col3, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
+        FwdProblem<BM, BIm2col3, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, psplits};
         p.e = e;
+        if constexpr (BM == 128)
+            if (kg2) return launch_gemm<decltype(p), 2>(p, M, N, pl.splits, st);
         return launch_gemm(p, M, N, pl.splits, st);
     }
     if (g.KS == 3) {
@@ -2148,13 +2237,14 @@ static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, c
 // is not split, or in the split-K reduction.
 // w_nat: a fully connected geometry's w is the filter itself (W[F][K]).
 static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y, float *part,
-                    hipStream_t st, const Epi &e = Epi(), bool w_nat = false)
+                    hipStream_t st, const Epi &e = Epi(), bool w_nat = false, bool kg_ok = true)
 {
     if (fwd_small_k(g))
         return e.active() ? fwd_small_k_launch<true>(g, x, w, y, e, w_nat, st)
                           : fwd_small_k_launch<false>(g, x, w, y, e, w_nat, st);
-    const FwdPlan pl = fwd_plan(g);
-    const bool gemm_epi = e.active() && pl.splits == 1;
+    const FwdPlan pl = fwd_plan(g, kg_ok);
+    const bool unsplit = pl.splits == 1 || pl.kg == pl.splits;  // no partial sums
+    const bool gemm_epi = e.active() && unsplit;
     int rc;
     if (gemm_epi) {
         if (pl.bm == 32) rc = fwd_bm<32, true>(g, pl, x, w, y, part, e, w_nat, st);
@@ -2167,7 +2257,7 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
     else if (pl.bm == 96) rc = fwd_bm_padded<96, false>(g, pl, x, w, y, part, e, st);
     else if (pl.bm == 64) rc = fwd_bm<64, false>(g, pl, x, w, y, part, e, w_nat, st);
     else rc = fwd_bm<128, false>(g, pl, x, w, y, part, e, w_nat, st);
-    if (rc || pl.splits == 1) return rc;
+    if (rc || unsplit) return rc;
     const int M = g.F, N = g.B * g.OH * g.OW;
     const size_t mn = (size_t)M * N;
     if (fc_geom(g)) {  // FcProblem partials: [z][b][m]
@@ -2480,7 +2570,7 @@ size_t ach_conv_bwd_data_workspace(const ach_conv_desc *d)
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
     size_t wf = (size_t)g.F * g.C * g.KS * g.KS * sizeof(float);
-    if (g.S == 1 && g.P <= g.KS - 1) return align256(wf) + fwd_part_bytes(dgrad_as_fwd(g));
+    if (g.S == 1 && g.P <= g.KS - 1) return align256(wf) + fwd_part_bytes(dgrad_as_fwd(g), false);
     // strided fallback: one image's column buffer
     return (size_t)g.C * g.KS * g.KS * g.OH * g.OW * sizeof(float);
 }
@@ -2499,13 +2589,13 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
         const size_t tot = (size_t)g.F * g.C * g.KS * g.KS;
         float *part = (float *)((char *)ws + align256(tot * sizeof(float)));
         // 1x1: the flipped k-major filter Wft[f][c] is W itself
-        if (g.KS == 1) return fwd_impl(dgrad_as_fwd(g), dy, w, dx, part, st);
+        if (g.KS == 1) return fwd_impl(dgrad_as_fwd(g), dy, w, dx, part, st, Epi(), false, false);
         float *wf = (float *)ws;
         hipLaunchKernelGGL(k_weights_flip_kmajor, dim3(grid_for(tot, 256)), dim3(256), 0, st, w,
                            wf, g.F, g.C, g.KS * g.KS);
         int rc = check_launch();
         if (rc) return rc;
-        return fwd_impl(dgrad_as_fwd(g), dy, wf, dx, part, st);
+        return fwd_impl(dgrad_as_fwd(g), dy, wf, dx, part, st, Epi(), false, false);
     }
     // Strided convolution: the reference's per-image TN GEMM + col2im
     // (ConvolutionalLayer.c:933-945).  Not on any benchmark path.
@@ -2610,9 +2700,10 @@ int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const fl
     if (dgrad_small_c(g) && !fc_geom(g)) return dgrad_small_c_launch(g, dy, w, dx, as_stream(stream));
     if (g.KS > 1 && !wft) return ACH_EINVAL;
     const ConvGeom t = dgrad_as_fwd(g);
-    const size_t need = fwd_part_bytes(t);
+    const size_t need = fwd_part_bytes(t, false);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
-    return fwd_impl(t, dy, g.KS == 1 ? w : wft, dx, (float *)ws, as_stream(stream));
+    return fwd_impl(t, dy, g.KS == 1 ? w : wft, dx, (float *)ws, as_stream(stream), Epi(), false,
+                    false);
 }
 
 size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)

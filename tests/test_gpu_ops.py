@@ -547,6 +547,7 @@ def test_bias_ops(gpu, oracle, B, n, sp):
     (2, 3, 35, 35, 8, 11, 4, 0),      # generic loader, stride 4
     (2, 3, 35, 35, 96, 11, 4, 0),     # generic loader, 96-row tiles
     (2, 512, 8, 8, 10, 1, 1, 0),      # 1x1
+    (128, 256, 8, 8, 512, 3, 1, 1),   # K split in two inside one workgroup
     (8, 64, 1, 1, 48, 1, 1, 0),       # fully connected GEMM
     (4, 300, 1, 1, 64, 1, 1, 0),      # fully connected, split K
 ], ids=lambda s: "x".join(map(str, s)))
