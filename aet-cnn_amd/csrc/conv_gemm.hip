@@ -2122,16 +2122,19 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
     pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
     pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
     if (fwd_small_k(g)) pl.splits = 1;  // k_conv_fwd_smallk: whole K per tile
-    // a 3x3 forward split in two (the 8x8 layers of darknet: 256 tiles)
-    // runs both slices of a tile in one 512-thread workgroup and adds them in
-    // LDS: the same sums, without the partials' HBM round trip and the
-    // reduction pass (filter counts divisible by 4: the two float4-filter
-    // loaders of fwd_bm).  Input gradients run beside the weight-gradient
-    // GEMMs of the second stream, where 8-wave workgroups with 72 KB of LDS
-    // find fewer free slots: measured on the darknet step, 6.855 ms without,
-    // 6.827 with forward passes only, 6.961 with input gradients only.
-    pl.kg = (kg_ok && pl.splits == 2 && pl.bm == 128 && g.KS == 3 && (g.F & 3) == 0 &&
-             !fc_geom(g))
+    // a 3x3 forward split in two whose tiles fit one per CU (the 8x8 layers
+    // of darknet: 256 tiles on 256 CUs) runs both slices of a tile in one
+    // 512-thread workgroup and adds them in LDS: the same sums, without the
+    // partials' HBM round trip and the reduction pass (filter counts
+    // divisible by 4: the two float4-filter loaders of fwd_bm).  With more
+    // tiles the 2-per-CU workgroups (72 KB of LDS each) balance worse than
+    // twice as many 256-thread ones (AlexNet's 338-tile conv5 forward: step
+    // 7.81 -> 7.91 ms).  Input gradients run beside the weight-gradient GEMMs
+    // of the second stream, where 8-wave workgroups find fewer free slots:
+    // measured on the darknet step, 6.855 ms without, 6.827 with forward
+    // passes only, 6.961 with input gradients only.
+    pl.kg = (kg_ok && pl.splits == 2 && tiles <= 256 && pl.bm == 128 && g.KS == 3 &&
+             (g.F & 3) == 0 && !fc_geom(g))
                 ? 2 : 1;
     return pl;
 }
