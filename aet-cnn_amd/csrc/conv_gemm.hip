@@ -2119,23 +2119,29 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
         if (s > ktiles / 8) s = ktiles / 8;  // keep >= 8 k-tiles per slice
         if (s < 1) s = 1;
     }
+    // Two K groups per 512-thread workgroup (k_mfma_gemm<P, 2>) for 3x3
+    // forward passes whose grid gives one or two such workgroups per CU on
+    // 256 CUs (filter counts divisible by 4: the two float4-filter loaders of
+    // fwd_bm):
+    //  - 256 tiles split in two (the 8x8 layers of darknet): both slices of
+    //    a tile in one workgroup, added in LDS -- the same sums, without the
+    //    partials' HBM round trip and the reduction pass;
+    //  - 512 tiles not split (the 16x16 layers): K is halved between the two
+    //    groups, doubling the waves per SIMD at the same 64 x 64 wave tile
+    //    (256->256@16 forward 134 -> 137 TF/s; the sums become two halves
+    //    added, a different but fixed order).
+    // Grids in between balance worse than twice as many 256-thread
+    // workgroups (AlexNet's 338-tile conv5 forward: step 7.81 -> 7.91 ms).
+    // Input gradients (kg_ok false) run beside the weight-gradient GEMMs of
+    // the second stream, where 8-wave workgroups find fewer free slots:
+    // measured on the darknet step, 6.855 ms without, 6.827 with forward
+    // passes only, 6.961 with input gradients only.
+    const bool kg_shape = kg_ok && pl.bm == 128 && g.KS == 3 && (g.F & 3) == 0 && !fc_geom(g);
+    if (kg_shape && s == 1 && tiles == 512 && ktiles >= 16) s = 2;
     pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
     pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
     if (fwd_small_k(g)) pl.splits = 1;  // k_conv_fwd_smallk: whole K per tile
-    // a 3x3 forward split in two whose tiles fit one per CU (the 8x8 layers
-    // of darknet: 256 tiles on 256 CUs) runs both slices of a tile in one
-    // 512-thread workgroup and adds them in LDS: the same sums, without the
-    // partials' HBM round trip and the reduction pass (filter counts
-    // divisible by 4: the two float4-filter loaders of fwd_bm).  With more
-    // tiles the 2-per-CU workgroups (72 KB of LDS each) balance worse than
-    // twice as many 256-thread ones (AlexNet's 338-tile conv5 forward: step
-    // 7.81 -> 7.91 ms).  Input gradients run beside the weight-gradient GEMMs
-    // of the second stream, where 8-wave workgroups find fewer free slots:
-    // measured on the darknet step, 6.855 ms without, 6.827 with forward
-    // passes only, 6.961 with input gradients only.
-    pl.kg = (kg_ok && pl.splits == 2 && tiles <= 256 && pl.bm == 128 && g.KS == 3 &&
-             (g.F & 3) == 0 && !fc_geom(g))
-                ? 2 : 1;
+    pl.kg = (kg_shape && pl.splits == 2 && (tiles <= 256 || tiles == 512)) ? 2 : 1;
     return pl;
 }
 

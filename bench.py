@@ -42,8 +42,9 @@ SWEEP = [  # config 1: (C_in, C_out, H, k, pad)
 # the weight-gradient GEMM (the second most).
 PROBES = {
     "fwd": dict(shape=(256, 256, 16, 3, 1), op="fwd",
-                kernel="k_mfma_gemm<FwdProblem<128, BIm2col3F, true, false>> "
-                       "(conv fwd / stride-1 dgrad implicit GEMM)"),
+                kernel="k_mfma_gemm<FwdProblem<128, BIm2col3F, true, false>, 2> "
+                       "(conv fwd implicit GEMM, two K groups per workgroup; the stride-1 "
+                       "dgrad runs the same loop with one)"),
     "wgrad": dict(shape=(128, 128, 32, 3, 1), op="wgrad",
                   kernel="k_mfma_gemm<WgradProblemC<128, 96, 3>> (conv weight-gradient GEMM)"),
 }
