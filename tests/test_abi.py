@@ -51,11 +51,16 @@ def test_conv_shape_and_workspace_queries():
     assert ops.ach_conv_fwd_workspace(C.byref(d)) >= 96 * 3 * 121 * 4
     bad = aetcnn.ConvDesc(1, 3, 2, 2, 4, 5, 1, 0)  # kernel larger than padded input
     assert ops.ach_conv_out_h(C.byref(bad)) == -1
-    # split-K partial buffers appear only when the tile grid is small
+    # split-K partial buffers appear only when the tile grid is small, and
+    # not for a forward whose two K slices share one workgroup (256 tiles)
     small = aetcnn.ConvDesc(128, 512, 8, 8, 512, 3, 1, 1)
     big = aetcnn.ConvDesc(128, 128, 32, 32, 128, 3, 1, 1)
-    assert ops.ach_conv_fwd_workspace(C.byref(small)) > 512 * 512 * 9 * 4
+    filt = 512 * 512 * 9 * 4
+    assert ops.ach_conv_bwd_data_workspace(C.byref(small)) > filt + 512
+    assert filt <= ops.ach_conv_fwd_workspace(C.byref(small)) < filt + 512
     assert ops.ach_conv_fwd_workspace(C.byref(big)) < 128 * 128 * 9 * 4 + 512
+    fewer = aetcnn.ConvDesc(64, 512, 8, 8, 512, 3, 1, 1)  # 128 tiles: split in four
+    assert ops.ach_conv_fwd_workspace(C.byref(fewer)) > filt + 512
     assert ops.ach_conv_bwd_filter_workspace(C.byref(big)) > 0
     assert ops.ach_maxpool_out(32, 2, 2, 1) == 16  # darknet default padding = size-1
     assert ops.ach_maxpool_out(55, 3, 2, 0) == 27
