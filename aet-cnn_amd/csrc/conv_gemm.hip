@@ -1762,15 +1762,53 @@ __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__rest
         }
 }
 
-// Fixed-order split-K reduction: dw[i] += sum_z part[z][i], z ascending.
-__global__ void k_splitk_reduce(const float *__restrict__ part, float *__restrict__ dw,
-                                size_t mn, int splits)
+__device__ __forceinline__ void addto(float &a, float b) { a += b; }
+__device__ __forceinline__ void addto(float4 &a, const float4 &b)
 {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < mn;
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+}
+
+// sum of part[z][i] over z in [z0, z1), in z order from 0: eight slices'
+// loads are issued before their (in-order) adds
+template <class T>
+__device__ __forceinline__ T slice_sum(const T *__restrict__ p, size_t n, size_t i, int z0, int z1)
+{
+    T s;
+    if constexpr (std::is_same<T, float4>::value) s = make_float4(0.f, 0.f, 0.f, 0.f);
+    else s = 0.f;
+    int z = z0;
+    for (; z + 8 <= z1; z += 8) {
+        T v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(size_t)(z + u) * n + i];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) addto(s, v[u]);
+    }
+    for (; z < z1; ++z) addto(s, p[(size_t)z * n + i]);
+    return s;
+}
+
+// Fixed-order split-K reduction: dw[i] += sum_z part[z][i], z ascending.
+// V4: four consecutive outputs per thread as float4 (mn % 4 == 0, 16-byte
+// aligned operands); the same additions in the same order.
+template <bool V4>
+__global__ void __launch_bounds__(256) k_splitk_reduce(const float *__restrict__ part,
+                                                       float *__restrict__ dw, size_t mn,
+                                                       int splits)
+{
+    typedef typename std::conditional<V4, float4, float>::type T;
+    const size_t n = V4 ? mn / 4 : mn;
+    const T *p = reinterpret_cast<const T *>(part);
+    T *d = reinterpret_cast<T *>(dw);
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x) {
-        float s = 0.f;
-        for (int z = 0; z < splits; ++z) s += part[(size_t)z * mn + i];
-        dw[i] += s;
+        const T s = slice_sum(p, n, i, 0, splits);
+        T o = d[i];
+        addto(o, s);
+        d[i] = o;
     }
 }
 
@@ -1778,17 +1816,20 @@ __global__ void k_splitk_reduce(const float *__restrict__ part, float *__restric
 // SPLIT_GROUP consecutive z of group c (z ascending); the second level is
 // k_splitk_reduce over the groups.  Keeps every output's sum order fixed.
 constexpr int SPLIT_GROUP = 32;
-__global__ void k_splitk_group(const float *__restrict__ part, float *__restrict__ tmp, size_t mn,
-                               int splits)
+template <bool V4>
+__global__ void __launch_bounds__(256) k_splitk_group(const float *__restrict__ part,
+                                                      float *__restrict__ tmp, size_t mn,
+                                                      int splits)
 {
+    typedef typename std::conditional<V4, float4, float>::type T;
+    const size_t n = V4 ? mn / 4 : mn;
+    const T *p = reinterpret_cast<const T *>(part);
+    T *t = reinterpret_cast<T *>(tmp);
     const int c = blockIdx.y;
     const int z0 = c * SPLIT_GROUP, z1 = min(splits, z0 + SPLIT_GROUP);
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < mn;
-         i += (size_t)gridDim.x * blockDim.x) {
-        float s = 0.f;
-        for (int z = z0; z < z1; ++z) s += part[(size_t)z * mn + i];
-        tmp[(size_t)c * mn + i] = s;
-    }
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        t[(size_t)c * n + i] = slice_sum(p, n, i, z0, z1);
 }
 
 // Wt[k][m] = W[m][k]: the k-major copy of the filter the forward GEMM reads
@@ -2750,19 +2791,35 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
     else rc = wgrad_launch<128, 128>(g, x, dy, dw, part, splits, kchunk, st);
     if (rc || splits == 1) return rc;
     const size_t mn = (size_t)g.F * g.C * g.KS * g.KS;
+    // float4 when every slice starts 16-byte aligned (part is a workspace)
+    const bool v4 = (mn & 3) == 0 && ((reinterpret_cast<uintptr_t>(part) |
+                                       reinterpret_cast<uintptr_t>(dw)) & 15) == 0;
+    const size_t nt = v4 ? mn / 4 : mn;  // threads' outputs
     if (splits > 2 * SPLIT_GROUP) {
         const int groups = (splits + SPLIT_GROUP - 1) / SPLIT_GROUP;
         float *tmp = part + (size_t)splits * mn;
-        hipLaunchKernelGGL(k_splitk_group, dim3(grid_for(mn, 256, 1024), groups), dim3(256), 0, st,
-                           part, tmp, mn, splits);
+        if (v4)
+            hipLaunchKernelGGL(k_splitk_group<true>, dim3(grid_for(nt, 256, 1024), groups),
+                               dim3(256), 0, st, part, tmp, mn, splits);
+        else
+            hipLaunchKernelGGL(k_splitk_group<false>, dim3(grid_for(nt, 256, 1024), groups),
+                               dim3(256), 0, st, part, tmp, mn, splits);
         rc = check_launch();
         if (rc) return rc;
-        hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(mn, 256)), dim3(256), 0, st, tmp, dw,
-                           mn, groups);
+        if (v4)
+            hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(grid_for(nt, 256)), dim3(256), 0, st,
+                               tmp, dw, mn, groups);
+        else
+            hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(grid_for(nt, 256)), dim3(256), 0, st,
+                               tmp, dw, mn, groups);
         return check_launch();
     }
-    hipLaunchKernelGGL(k_splitk_reduce, dim3(grid_for(mn, 256)), dim3(256), 0, st, part, dw,
-                       mn, splits);
+    if (v4)
+        hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(grid_for(nt, 256)), dim3(256), 0, st, part,
+                           dw, mn, splits);
+    else
+        hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(grid_for(nt, 256)), dim3(256), 0, st, part,
+                           dw, mn, splits);
     return check_launch();
 }
 
