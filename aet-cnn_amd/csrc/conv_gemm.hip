@@ -1974,38 +1974,71 @@ static bool fits_int(const ach_conv_desc *d)
 }
 
 // y[b][m][p] = sum_z part[z][m][b*OHW+p], z ascending (fixed order), then
-// the epilogue.
-template <bool EPI>
+// the epilogue.  V4: four consecutive positions of one plane per thread as
+// float4 (OHW % 4 == 0, 16-byte aligned operands); the same additions.
+template <bool EPI, bool V4>
 __global__ void __launch_bounds__(256) k_splitk_to_nchw(const float *__restrict__ part,
                                                         float *__restrict__ y, int M, int N,
                                                         FastDiv dohw, FastDiv dM, int splits,
                                                         Epi e)
 {
     // M*N < 2^29 (operands below 2 GiB): 32-bit indices, magic-number division
+    constexpr int V = V4 ? 4 : 1;
+    typedef typename std::conditional<V4, float4, float>::type T;
     const int mn = M * N, ohw = (int)dohw.d;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += gridDim.x * blockDim.x) {
+    const T *pt = reinterpret_cast<const T *>(part);
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < mn / V;
+         q += gridDim.x * blockDim.x) {
+        const int i = q * V;
         const int bm = fdiv(i, dohw), p = i - bm * ohw;
         const int b = fdiv(bm, dM), m = bm - b * M;
         const int n = b * ohw + p;
-        float s = 0.f;
-        for (int z = 0; z < splits; ++z) s += part[((size_t)z * M + m) * N + n];
-        y[i] = EPI ? e.apply(s, m) : s;
+        T s = slice_sum(pt, (size_t)mn / V, (size_t)(m * N + n) / V, 0, splits);
+        if constexpr (V4) {
+            if constexpr (EPI) {
+                s.x = e.apply(s.x, m);
+                s.y = e.apply(s.y, m);
+                s.z = e.apply(s.z, m);
+                s.w = e.apply(s.w, m);
+            }
+            reinterpret_cast<float4 *>(y)[q] = s;
+        } else {
+            y[i] = EPI ? e.apply(s, m) : s;
+        }
     }
 }
 
 // The same reduction for partials already in the output's layout (the
 // fully connected GEMMs): y[i] = sum_z part[z][i], z ascending, then the
-// epilogue with m = i mod M.
-template <bool EPI>
+// epilogue with m = i mod M.  V4 as above (mn % 4 == 0).
+template <bool EPI, bool V4>
 __global__ void __launch_bounds__(256) k_splitk_rows(const float *__restrict__ part,
                                                      float *__restrict__ y, int mn, FastDiv dM,
                                                      int splits, Epi e)
 {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += gridDim.x * blockDim.x) {
-        float s = 0.f;
-        for (int z = 0; z < splits; ++z) s += part[(size_t)z * mn + i];
-        if constexpr (EPI) s = e.apply(s, i - fdiv(i, dM) * (int)dM.d);
-        y[i] = s;
+    constexpr int V = V4 ? 4 : 1;
+    typedef typename std::conditional<V4, float4, float>::type T;
+    const T *pt = reinterpret_cast<const T *>(part);
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < mn / V;
+         q += gridDim.x * blockDim.x) {
+        T s = slice_sum(pt, (size_t)mn / V, (size_t)q, 0, splits);
+        if constexpr (V4) {
+            if constexpr (EPI) {
+                const int M = (int)dM.d;
+                int m = 4 * q - fdiv(4 * q, dM) * M;
+                s.x = e.apply(s.x, m);
+                m = m + 1 == M ? 0 : m + 1;
+                s.y = e.apply(s.y, m);
+                m = m + 1 == M ? 0 : m + 1;
+                s.z = e.apply(s.z, m);
+                m = m + 1 == M ? 0 : m + 1;
+                s.w = e.apply(s.w, m);
+            }
+            reinterpret_cast<float4 *>(y)[q] = s;
+        } else {
+            if constexpr (EPI) s = e.apply(s, q - fdiv(q, dM) * (int)dM.d);
+            y[q] = s;
+        }
     }
 }
 
@@ -2310,23 +2343,41 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
     if (rc || unsplit) return rc;
     const int M = g.F, N = g.B * g.OH * g.OW;
     const size_t mn = (size_t)M * N;
+    const bool al16 = ((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+    const FastDiv dM = make_fastdiv((unsigned)M);
     if (fc_geom(g)) {  // FcProblem partials: [z][b][m]
-        if (e.active())
-            hipLaunchKernelGGL(k_splitk_rows<true>, dim3(grid_for(mn, 256, 1u << 20)), dim3(256),
-                               0, st, part, y, (int)mn, make_fastdiv((unsigned)M), pl.splits, e);
+        const bool v4 = al16 && (mn & 3) == 0;
+        const dim3 grid(grid_for(v4 ? mn / 4 : mn, 256, 1u << 20));
+        if (e.active() && v4)
+            hipLaunchKernelGGL((k_splitk_rows<true, true>), grid, dim3(256), 0, st, part, y,
+                               (int)mn, dM, pl.splits, e);
+        else if (e.active())
+            hipLaunchKernelGGL((k_splitk_rows<true, false>), grid, dim3(256), 0, st, part, y,
+                               (int)mn, dM, pl.splits, e);
+        else if (v4)
+            hipLaunchKernelGGL((k_splitk_rows<false, true>), grid, dim3(256), 0, st, part, y,
+                               (int)mn, dM, pl.splits, e);
         else
-            hipLaunchKernelGGL(k_splitk_rows<false>, dim3(grid_for(mn, 256, 1u << 20)), dim3(256),
-                               0, st, part, y, (int)mn, make_fastdiv((unsigned)M), pl.splits, e);
+            hipLaunchKernelGGL((k_splitk_rows<false, false>), grid, dim3(256), 0, st, part, y,
+                               (int)mn, dM, pl.splits, e);
         return check_launch();
     }
-    if (e.active())
-        hipLaunchKernelGGL(k_splitk_to_nchw<true>, dim3(grid_for(mn, 256, 1u << 20)), dim3(256),
-                           0, st, part, y, M, N, make_fastdiv((unsigned)(g.OH * g.OW)),
-                           make_fastdiv((unsigned)M), pl.splits, e);
+    const int ohw = g.OH * g.OW;
+    const FastDiv dohw = make_fastdiv((unsigned)ohw);
+    const bool v4 = al16 && (ohw & 3) == 0;  // four positions never straddle a plane
+    const dim3 grid(grid_for(v4 ? mn / 4 : mn, 256, 1u << 20));
+    if (e.active() && v4)
+        hipLaunchKernelGGL((k_splitk_to_nchw<true, true>), grid, dim3(256), 0, st, part, y, M, N,
+                           dohw, dM, pl.splits, e);
+    else if (e.active())
+        hipLaunchKernelGGL((k_splitk_to_nchw<true, false>), grid, dim3(256), 0, st, part, y, M, N,
+                           dohw, dM, pl.splits, e);
+    else if (v4)
+        hipLaunchKernelGGL((k_splitk_to_nchw<false, true>), grid, dim3(256), 0, st, part, y, M, N,
+                           dohw, dM, pl.splits, e);
     else
-        hipLaunchKernelGGL(k_splitk_to_nchw<false>, dim3(grid_for(mn, 256, 1u << 20)), dim3(256),
-                           0, st, part, y, M, N, make_fastdiv((unsigned)(g.OH * g.OW)),
-                           make_fastdiv((unsigned)M), pl.splits, e);
+        hipLaunchKernelGGL((k_splitk_to_nchw<false, false>), grid, dim3(256), 0, st, part, y, M,
+                           N, dohw, dM, pl.splits, e);
     return check_launch();
 }
 
