@@ -15,6 +15,7 @@
 // is bit-reproducible.
 #include "common.hpp"
 
+#include <algorithm>
 #include <float.h>
 #include <stdio.h>
 #include <string.h>
@@ -411,38 +412,45 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
     din[p] = gi.apply(v, (size_t)p);
 }
 
-// The same gather for output planes that fit in LDS: one workgroup per
-// (image, channel) plane first stages the plane's argmax indices and output
-// gradients in LDS (each read from HBM once, coalesced), then every input
-// pixel of the plane takes its candidates from LDS in ascending output
-// order -- the sums of k_maxpool_bwd, bit for bit, without its eight
-// dependent global loads per pixel (which stall when the kernel shares the
-// CUs with a GEMM).  Dynamic LDS: 8 bytes per output position.
-constexpr int POOL_PLANE_MAX = 4096;  // output positions of a plane staged in LDS
+// The same gather for output planes that fit in LDS: a workgroup takes ppw
+// consecutive (image, channel) planes (several when planes are small, so
+// that a workgroup has about a thousand input pixels), first stages their
+// argmax indices and output gradients in LDS (each read from HBM once,
+// coalesced), then every input pixel takes its candidates from its plane's
+// LDS copy in ascending output order -- the sums of k_maxpool_bwd, bit for
+// bit, without its eight dependent global loads per pixel (which stall when
+// the kernel shares the CUs with a GEMM).  Dynamic LDS: 8 bytes per staged
+// output position.
+constexpr int POOL_PLANE_MAX = 4096;  // output positions staged in LDS per workgroup
+constexpr int POOL_PIX_PER_WG = 1024; // input pixels a workgroup aims at
 template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restrict__ dout,
                                                            const int32_t *__restrict__ idx,
-                                                           FastDiv dW, int H, int size_,
+                                                           FastDiv dW, FastDiv dHW, int size_,
                                                            int stride_, int pad, int OH, int OW,
-                                                           float *din, int accumulate, GradIn gi)
+                                                           int planes, int ppw, float *din,
+                                                           int accumulate, GradIn gi)
 {
     extern __shared__ int32_t pool_lds[];
     const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
-    const int ohw = OH * OW, W = (int)dW.d, hw = H * W;
+    const int ohw = OH * OW, W = (int)dW.d, hw = (int)dHW.d;
+    const int bc0 = blockIdx.x * ppw, np = min(ppw, planes - bc0);
     int32_t *six = pool_lds;
-    float *sg = reinterpret_cast<float *>(pool_lds + ohw);
-    const int bc = blockIdx.x;
-    const size_t obase = (size_t)bc * ohw;
-    for (int q = threadIdx.x; q < ohw; q += blockDim.x) {
+    float *sg = reinterpret_cast<float *>(pool_lds + ppw * ohw);
+    const size_t obase = (size_t)bc0 * ohw;
+    for (int q = threadIdx.x; q < np * ohw; q += blockDim.x) {
         six[q] = idx[obase + q];
         sg[q] = dout[obase + q];
     }
     __syncthreads();
     const int off = -pad / 2;
-    const int pbase = bc * hw;  // < 2^31: the caller's pool_ok
-    for (int r = threadIdx.x; r < hw; r += blockDim.x) {
-        const int h = fdiv(r, dW), w = r - h * W;
+    const int pbase = bc0 * hw;  // < 2^31: the caller's pool_ok
+    for (int r = threadIdx.x; r < np * hw; r += blockDim.x) {
+        const int pl = fdiv(r, dHW), rr = r - pl * hw;
+        const int h = fdiv(rr, dW), w = rr - h * W;
         const int p = pbase + r;
+        const int32_t *pix = six + pl * ohw;
+        const float *pg = sg + pl * ohw;
         const int i0 = max(floor_div(h - off - size, stride) + 1, 0);
         const int i1 = min(floor_div(h - off, stride), OH - 1);
         const int j0 = max(floor_div(w - off - size, stride) + 1, 0);
@@ -457,14 +465,14 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
                     const int i = i0 + a, j = j0 + c;
                     if (i <= i1 && j <= j1) {
                         const int o = i * OW + j;
-                        if (six[o] == p) v += sg[o];
+                        if (pix[o] == p) v += pg[o];
                     }
                 }
         } else {
             for (int i = i0; i <= i1; ++i)
                 for (int j = j0; j <= j1; ++j) {
                     const int o = i * OW + j;
-                    if (six[o] == p) v += sg[o];
+                    if (pix[o] == p) v += pg[o];
                 }
         }
         din[p] = gi.apply(v, (size_t)p);
@@ -1055,18 +1063,22 @@ static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, 
     const int total = batch * c * h * w;  // < 2^31: pool_ok
     const dim3 grid((total + 255) / 256);
     const FastDiv dH = make_fastdiv((unsigned)h), dW = make_fastdiv((unsigned)w);
-    if (OH * OW <= POOL_PLANE_MAX) {  // one workgroup per plane, outputs staged in LDS
-        const dim3 pg((unsigned)(batch * c));
-        const size_t lds = (size_t)OH * OW * 8;
+    if (OH * OW <= POOL_PLANE_MAX) {  // planes staged in LDS, ppw per workgroup
+        const int planes = batch * c;
+        const int ppw = std::max(1, std::min({POOL_PIX_PER_WG / (h * w),
+                                              POOL_PLANE_MAX / (OH * OW), planes}));
+        const dim3 pg((unsigned)((planes + ppw - 1) / ppw));
+        const size_t lds = (size_t)ppw * OH * OW * 8;
+        const FastDiv dHW = make_fastdiv((unsigned)(h * w));
         if (size == 3 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<3, 2>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, h, size, stride, pad, OH, OW, din, acc, gi);
+                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi);
         else if (size == 2 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<2, 2>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, h, size, stride, pad, OH, OW, din, acc, gi);
+                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi);
         else
             hipLaunchKernelGGL((k_maxpool_bwd_plane<0, 0>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, h, size, stride, pad, OH, OW, din, acc, gi);
+                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi);
         return check_launch();
     }
     if (size == 3 && stride == 2)

@@ -339,6 +339,8 @@ def test_activation_bit_exact(gpu, oracle, act):
     (4, 3, 32, 32, 2, 2, 1),      # darknet default padding = size-1
     (2, 5, 55, 55, 3, 2, 0),      # AlexNet overlapping 3x3/2
     (2, 4, 13, 13, 3, 2, 2),
+    (3, 7, 13, 13, 3, 2, 0),      # 6 planes per workgroup, partial last workgroup
+    (2, 5, 27, 27, 3, 2, 0),      # one 729-pixel plane per workgroup
     (3, 2, 7, 9, 2, 1, 1),
     (2, 3, 16, 16, 2, 2, 0),
     (2, 3, 8, 12, 2, 2, 1),       # 2x2/2 fast path, non-square
@@ -375,6 +377,7 @@ def test_maxpool_bit_exact(gpu, oracle, B, Cc, H, W, size, stride, pad):
 
 @pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [
     (2, 5, 55, 55, 3, 2, 0),      # LDS-staged plane kernel
+    (3, 7, 13, 13, 3, 2, 0),      # several planes per workgroup
     (4, 3, 32, 32, 2, 2, 1),      # 2x2/2 fast path (float4 y loads)
     (1, 2, 140, 140, 3, 2, 0),    # gather kernel (plane above the LDS limit)
     (3, 2, 7, 9, 2, 1, 1),        # generic window
