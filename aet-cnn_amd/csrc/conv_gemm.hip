@@ -2008,6 +2008,33 @@ __global__ void __launch_bounds__(256) k_splitk_to_nchw(const float *__restrict_
     }
 }
 
+// The same reduction walked in the partials' order for planes whose size is
+// not a multiple of 4 (N % 4 == 0, 16-byte aligned part): four consecutive
+// n of one filter row per thread, loaded as float4, summed in the same
+// order, stored one by one (they may cross an image boundary).
+template <bool EPI>
+__global__ void __launch_bounds__(256) k_splitk_to_nchw_pv(const float *__restrict__ part,
+                                                           float *__restrict__ y, int M, int N,
+                                                           FastDiv dohw, FastDiv dN, int splits,
+                                                           Epi e)
+{
+    const int mn = M * N, ohw = (int)dohw.d;
+    const float4 *pt = reinterpret_cast<const float4 *>(part);
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < mn / 4;
+         q += gridDim.x * blockDim.x) {
+        const int i = q * 4;
+        const int m = fdiv(i, dN), n = i - m * N;
+        int b = fdiv(n, dohw), pp = n - b * ohw;
+        const float4 s = slice_sum(pt, (size_t)mn / 4, (size_t)q, 0, splits);
+        const float v[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            y[((size_t)b * M + m) * ohw + pp] = EPI ? e.apply(v[j], m) : v[j];
+            if (++pp == ohw) { pp = 0; ++b; }
+        }
+    }
+}
+
 // The same reduction for partials already in the output's layout (the
 // fully connected GEMMs): y[i] = sum_z part[z][i], z ascending, then the
 // epilogue with m = i mod M.  V4 as above (mn % 4 == 0).
@@ -2366,6 +2393,17 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
     const FastDiv dohw = make_fastdiv((unsigned)ohw);
     const bool v4 = al16 && (ohw & 3) == 0;  // four positions never straddle a plane
     const dim3 grid(grid_for(v4 ? mn / 4 : mn, 256, 1u << 20));
+    if (!v4 && al16 && (N & 3) == 0) {  // float4 loads in the partials' order
+        const dim3 g4(grid_for(mn / 4, 256, 1u << 20));
+        const FastDiv dN = make_fastdiv((unsigned)N);
+        if (e.active())
+            hipLaunchKernelGGL((k_splitk_to_nchw_pv<true>), g4, dim3(256), 0, st, part, y, M, N,
+                               dohw, dN, pl.splits, e);
+        else
+            hipLaunchKernelGGL((k_splitk_to_nchw_pv<false>), g4, dim3(256), 0, st, part, y, M, N,
+                               dohw, dN, pl.splits, e);
+        return check_launch();
+    }
     if (e.active() && v4)
         hipLaunchKernelGGL((k_splitk_to_nchw<true, true>), grid, dim3(256), 0, st, part, y, M, N,
                            dohw, dM, pl.splits, e);
