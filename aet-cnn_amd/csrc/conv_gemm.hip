@@ -2209,12 +2209,20 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
     const int ktiles = (K + pl.bk - 1) / pl.bk;
     int s = 1;
     // the padded-tap kernel fits two workgroups per CU: aim at two rounds
-    // (measured 0.5% faster on AlexNet than one)
-    const int target = fwd_padded_taps(g) ? 1024 : 512;
+    // (measured 0.5% faster on AlexNet than one).  Input gradients (kg_ok
+    // false) whose grid gives one to two workgroups per CU (257-511 tiles:
+    // AlexNet's 13x13 layers, 338 and 507 tiles) aim there too, since they
+    // share the CUs with the weight-gradient GEMMs (AlexNet step 7.78 ->
+    // 7.73 ms, three A/B pairs); a 1024 target for every input gradient
+    // (or 768) made darknet's 128- and 256-tile ones 1.2-1.4% slower on the
+    // step, and 256 or 128 made them 6.5% slower.
+    const bool mid_dgrad = !kg_ok && tiles > 256 && tiles < 512;
+    const int target = (fwd_padded_taps(g) || mid_dgrad) ? 1024 : 512;
     if (tiles < target) {
         // rounded, not raised: a grid just short of the target (AlexNet's
-        // 13x13 input gradients, 507 tiles) runs unsplit rather than paying
-        // a reduction pass for a 2x grid (measured 2.4% on AlexNet)
+        // 13x13 forwards with 384 filters, 507 tiles) runs unsplit rather
+        // than paying a reduction pass for a 2x grid (measured 2.4% on
+        // AlexNet when its input gradients ran the same rule)
         s = (target + tiles / 2) / tiles;
         if (s > 32) s = 32;
         if (s > ktiles / 8) s = ktiles / 8;  // keep >= 8 k-tiles per slice
