@@ -341,6 +341,8 @@ def test_activation_bit_exact(gpu, oracle, act):
     (2, 4, 13, 13, 3, 2, 2),
     (3, 7, 13, 13, 3, 2, 0),      # 6 planes per workgroup, partial last workgroup
     (2, 5, 27, 27, 3, 2, 0),      # one 729-pixel plane per workgroup
+    (2, 3, 50, 50, 3, 2, 2),      # LDS-staged forward with padded windows (625 outputs)
+    (3, 5, 33, 65, 3, 2, 0),      # staged forward, 2 planes per workgroup, partial last
     (3, 2, 7, 9, 2, 1, 1),
     (2, 3, 16, 16, 2, 2, 0),
     (2, 3, 8, 12, 2, 2, 1),       # 2x2/2 fast path, non-square
