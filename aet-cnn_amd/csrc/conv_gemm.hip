@@ -954,6 +954,7 @@ struct WgradProblem {
 // chunk z / spc and images [(z % spc)*nbs, min(B, (z % spc + 1)*nbs)).
 template <int BM_, int BN_, int KS_T>
 struct WgradProblemC {
+    static constexpr int kWPE = 4;  // waves per SIMD (k_mfma_gemm)
     static constexpr int BM = BM_, BN = BN_, BK = WGRAD_BK;
     using AL = AWgradC<BM, BK>;
     using BLd = BWgradC<BN, BK, KS_T>;
@@ -1136,8 +1137,21 @@ struct has_store_tile<P, std::void_t<decltype(std::declval<const P &>().store_ti
 // the other groups' accumulators of the fragments it stores, through LDS.
 // With KG = 2 the sum is slice 0 + slice 1, the value a separate reduction
 // of the two slices' partials would produce, without writing them.
+// Waves per SIMD the compiler must leave room for (P::kWPE, default 1 = no
+// constraint).  The weight-gradient problems ask for 4: the compiler then
+// keeps the accumulators in ordinary VGPRs (103 registers in all instead of
+// 103 VGPRs + 48 AGPRs), so a CU running three of their workgroups keeps
+// about 200 registers per SIMD free for the memory-bound kernels of the
+// other stream (batch-norm backward reduction: 44 VGPRs, one wave per SIMD
+// beside the 152-register waves before); darknet step 6.69 -> 6.64 ms,
+// AlexNet 7.69 -> 7.65 ms, the GEMM alone unchanged.
+template <class P, class = void> struct WavesPerEU { static constexpr int v = 1; };
+template <class P> struct WavesPerEU<P, std::void_t<decltype(P::kWPE)>> {
+    static constexpr int v = P::kWPE;
+};
 template <class P, int KG = 1>
-__global__ void __launch_bounds__(GNT * KG) k_mfma_gemm(P p, int mt, int nt)
+__global__ void __launch_bounds__(GNT * KG) __attribute__((amdgpu_waves_per_eu(WavesPerEU<P>::v)))
+k_mfma_gemm(P p, int mt, int nt)
 {
     constexpr int BM = P::BM, BN = P::BN, BK = P::BK;
     static_assert(KG == 1 || KG == 2, "one or two K groups per workgroup");
