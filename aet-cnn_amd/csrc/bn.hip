@@ -39,11 +39,17 @@ constexpr int BN_U = 4;     // elements (float or float4) per thread in apply
 constexpr int BN_FWD_APPLY_BLOCKS = 2048;
 constexpr int BN_BWD_APPLY_BLOCKS = 1536;
 
-// reduction blocks: about 4096 (channel, image chunk) blocks in all
-// (measured 1-2% faster than 1024 or 2048 on config 2)
-static int bn_chunks(int batch, int c)
+// reduction blocks: about BN_BWD_RED_BLOCKS (channel, image chunk) blocks
+// in all for the backward reduction (config 2, 256 MiB tensors: 74.8% of
+// HBM against 72.8% with 2048 or 1024; 2048 made the darknet step 0.2-0.4%
+// faster, 8192 2.2% slower), BN_FWD_RED_BLOCKS for the forward statistics
+// (config 2: 75.1-75.5% against 73.9-74.5% with 4096; the darknet step
+// unchanged).  The workspace holds the larger.
+constexpr int BN_BWD_RED_BLOCKS = 4096;
+constexpr int BN_FWD_RED_BLOCKS = 2048;
+static int bn_chunks(int batch, int c, int blocks = BN_BWD_RED_BLOCKS)
 {
-    int nch = (4096 + c - 1) / c;
+    int nch = (blocks + c - 1) / c;
     if (nch > batch) nch = batch;
     if (nch < 1) nch = 1;
     return nch;
@@ -434,12 +440,13 @@ struct BnPlan {
     dim3 reduce_grid, apply_grid;
 };
 
-static BnPlan bn_plan(int batch, int C, int HW, bool vec_ok, int apply_blocks)
+static BnPlan bn_plan(int batch, int C, int HW, bool vec_ok, int apply_blocks,
+                      int red_blocks = BN_BWD_RED_BLOCKS)
 {
     BnPlan p;
     p.vec = vec_ok && (HW & 3) == 0;
     p.hwv = p.vec ? HW / 4 : HW;
-    const int nch = bn_chunks(batch, C);
+    const int nch = bn_chunks(batch, C, red_blocks);
     p.per = (batch + nch - 1) / nch;
     p.nch = (batch + p.per - 1) / p.per;
     p.reduce_grid = dim3(C, p.nch);
@@ -468,7 +475,7 @@ static int bn_fwd(const float *src, float *xcopy, float *xnorm, float *out, int 
     const BnPlan p = bn_plan(batch, C, HW,
                              aligned16(src) && aligned16(out) && aligned16(xcopy) &&
                                  aligned16(xnorm),
-                             BN_FWD_APPLY_BLOCKS);
+                             BN_FWD_APPLY_BLOCKS, BN_FWD_RED_BLOCKS);
     if (p.vec)
         hipLaunchKernelGGL(k_bn_stats<true>, p.reduce_grid, dim3(BN_NT), 0, st, src, batch, C,
                            p.hwv, p.per, part);
