@@ -40,13 +40,16 @@ constexpr int BN_FWD_APPLY_BLOCKS = 2048;
 constexpr int BN_BWD_APPLY_BLOCKS = 1536;
 
 // reduction blocks: about BN_BWD_RED_BLOCKS (channel, image chunk) blocks
-// in all for the backward reduction (config 2, 256 MiB tensors: 74.8% of
-// HBM against 72.8% with 2048 or 1024; 2048 made the darknet step 0.2-0.4%
-// faster, 8192 2.2% slower), BN_FWD_RED_BLOCKS for the forward statistics
-// (config 2: 75.1-75.5% against 73.9-74.5% with 4096; the darknet step
-// unchanged).  The workspace holds the larger.
+// in all for the backward reduction of tensors above BN_SMALL_ELEMS
+// elements (config 2, 256 MiB tensors: 74.8% of HBM against 72.8% with 2048
+// or 1024) and BN_FWD_RED_BLOCKS for smaller ones (darknet's, up to 64 MiB,
+// which reduce beside the weight-gradient GEMMs: step 0.2-0.4% faster than
+// with 4096, 2.2% slower with 8192); BN_FWD_RED_BLOCKS for every forward
+// statistics pass (config 2: 75.1-75.5% against 73.9-74.5% with 4096; the
+// darknet step unchanged).  The workspace holds the larger.
 constexpr int BN_BWD_RED_BLOCKS = 4096;
 constexpr int BN_FWD_RED_BLOCKS = 2048;
+constexpr long long BN_SMALL_ELEMS = 1ll << 24;
 static int bn_chunks(int batch, int c, int blocks = BN_BWD_RED_BLOCKS)
 {
     int nch = (blocks + c - 1) / c;
@@ -640,8 +643,9 @@ int ach_bn_bwd(float *delta, int batch, int C, int HW, const float *x, const flo
     if (!ws || ws_bytes < bn_ws_bytes(batch, C)) return ACH_EWORKSPACE;
     hipStream_t st = as_stream(stream);
     double *part = (double *)ws;
+    const bool small = (long long)batch * C * HW <= BN_SMALL_ELEMS;
     const BnPlan p = bn_plan(batch, C, HW, aligned16(delta) && aligned16(x) && aligned16(x_norm),
-                             BN_BWD_APPLY_BLOCKS);
+                             BN_BWD_APPLY_BLOCKS, small ? BN_FWD_RED_BLOCKS : BN_BWD_RED_BLOCKS);
     const int act = fused ? activation : ACH_LINEAR;
     if (p.vec)
         hipLaunchKernelGGL(k_bn_bwd_reduce<true>, p.reduce_grid, dim3(BN_NT), 0, st, delta, x,
