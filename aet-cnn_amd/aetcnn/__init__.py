@@ -208,7 +208,7 @@ _NET = {
     "an_image_rotate_crop": (None, [_vp, _i, _i, _i, _f, _f, _i, _i, _f, _f, _f, _vp]),
     "an_image_flip": (None, [_vp, _i, _i, _i]),
     "an_image_distort": (None, [_vp, _i, _i, _f, _f, _f]),
-    "an_image_resize": (None, [_vp, _i, _i, _i, _i, _i, _vp]),
+    "an_image_resize": (_i, [_vp, _i, _i, _i, _i, _i, _vp]),
     "an_image_load": (_i, [C.c_char_p, _i, _i, _i, _vp]),
     "an_image_read": (_i, [C.c_char_p, _i, C.POINTER(_i), C.POINTER(_i), C.POINTER(_vp)]),
     "an_image_free": (None, [_vp]),
@@ -610,7 +610,8 @@ def image_resize(src: np.ndarray, w: int, h: int) -> np.ndarray:
     src = np.ascontiguousarray(src, dtype=np.float32)
     c, H, W = src.shape
     dst = np.empty((c, h, w), np.float32)
-    net_lib().an_image_resize(src.ctypes.data, W, H, c, w, h, dst.ctypes.data)
+    check(net_lib().an_image_resize(src.ctypes.data, W, H, c, w, h, dst.ctypes.data),
+          "an_image_resize")
     return dst
 
 

@@ -1222,8 +1222,10 @@ k_mfma_gemm(P p, int mt, int nt)
     float ra[P::AL::RA], rb[P::BLd::RB];
     int nkt = (ke - kb + BK - 1) / BK;
     if constexpr (KG > 1) {
-        // every group runs the longest slice's k-tile count (the barriers
-        // are shared); past its own end a group's loads read zeros
+        // the groups share the barriers, so each runs the longest slice's
+        // k-tile count; the host launches KG > 1 only for slices of equal
+        // k-tile counts (a group running past its own end would add the
+        // re-read last tile of its slice a second time)
 #pragma unroll
         for (int q = 0; q < KG; ++q) {
             int qb, qe;
@@ -1243,8 +1245,9 @@ k_mfma_gemm(P p, int mt, int nt)
     constexpr int KB_LOAD = BK > 2 ? 2 : 0;  // k-step that issues the B loads
     for (int kt = 0; kt < nkt; ++kt) {
         const int cur = kt & 1;
-        // next k-tile (past ke on the last tile: every load reads as zero and
-        // the stores go to the stage nobody reads again)
+        // next k-tile (past ke on the last tile: the loaders read zeros or
+        // re-read the last tile, and the stores go to the stage nobody reads
+        // again)
         const int k0n = kb + (kt + 1) * BK;
         // fragments of k-step kk+2 are read from LDS while the MFMAs of
         // k-step kk issue, so the LDS latency hides behind the matrix pipe
@@ -1733,25 +1736,43 @@ __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__rest
             for (int ky = 0; ky < KS; ++ky) {
                 // row segment: columns tx .. tx + 3 + KS - 1
                 const float *row = pf + (ty + KS - 1 - ky) * PWd + tx;
-                float v[4 + (KS_ ? KS_ : 16) - 1];
-                if (KS_ == 3) {
-                    const float4 v0 = *reinterpret_cast<const float4 *>(row);
-                    const float2 v1 = *reinterpret_cast<const float2 *>(row + 4);
-                    v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
-                    v[4] = v1.x; v[5] = v1.y;
+                if constexpr (KS_ != 0) {
+                    // compile-time kernel width: the segment in registers
+                    float v[4 + KS_ - 1];
+                    if constexpr (KS_ == 3) {
+                        const float4 v0 = *reinterpret_cast<const float4 *>(row);
+                        const float2 v1 = *reinterpret_cast<const float2 *>(row + 4);
+                        v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+                        v[4] = v1.x; v[5] = v1.y;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4 + KS_ - 1; ++j) v[j] = row[j];
+                    }
+#pragma unroll
+                    for (int kx = 0; kx < KS_; ++kx) {
+                        const float4 wv = wf[ky * KS_ + kx];
+                        const float wc[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float val = v[q + KS_ - 1 - kx];
+#pragma unroll
+                            for (int c = 0; c < NC; ++c)
+                                acc[c][q] = __fmaf_rn(wc[c], val, acc[c][q]);
+                        }
+                    }
                 } else {
-                    for (int j = 0; j < 4 + KS - 1; ++j) v[j] = row[j];
-                }
+                    // run-time width: each tap value read from LDS (a register
+                    // array indexed at run time would live in scratch)
+                    for (int kx = 0; kx < KS; ++kx) {
+                        const float4 wv = wf[ky * KS + kx];
+                        const float wc[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-                for (int kx = 0; kx < (KS_ ? KS_ : 16); ++kx) {
-                    if (!KS_ && kx >= KS) break;
-                    const float4 wv = wf[ky * KS + kx];
-                    const float wc[4] = {wv.x, wv.y, wv.z, wv.w};
+                        for (int q = 0; q < 4; ++q) {
+                            const float val = row[q + KS - 1 - kx];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float val = v[q + KS - 1 - kx];
-#pragma unroll
-                        for (int c = 0; c < NC; ++c) acc[c][q] = __fmaf_rn(wc[c], val, acc[c][q]);
+                            for (int c = 0; c < NC; ++c)
+                                acc[c][q] = __fmaf_rn(wc[c], val, acc[c][q]);
+                        }
                     }
                 }
             }
@@ -2262,12 +2283,18 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
     // the second stream, where 8-wave workgroups find fewer free slots:
     // measured on the darknet step, 6.855 ms without, 6.827 with forward
     // passes only, 6.961 with input gradients only.
-    const bool kg_shape = kg_ok && pl.bm == 128 && g.KS == 3 && (g.F & 3) == 0 && !fc_geom(g);
+    // The two groups share the loop's barriers, so they must run the same
+    // number of k-tiles: with an odd k-tile count the shorter slice's group
+    // would run one tile past its end, where the 3x3 loaders re-read its last
+    // tile.  Such shapes keep one group per workgroup.
+    const bool kg_shape = kg_ok && pl.bm == 128 && g.KS == 3 && (g.F & 3) == 0 && !fc_geom(g) &&
+                          (ktiles & 1) == 0;
     if (kg_shape && s == 1 && tiles == 512 && ktiles >= 16) s = 2;
     pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
     pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
     if (fwd_small_k(g)) pl.splits = 1;  // k_conv_fwd_smallk: whole K per tile
-    pl.kg = (kg_shape && pl.splits == 2 && (tiles <= 256 || tiles == 512)) ? 2 : 1;
+    pl.kg = (kg_shape && pl.splits == 2 && 2 * (pl.kchunk / pl.bk) == ktiles &&
+             (tiles <= 256 || tiles == 512)) ? 2 : 1;
     return pl;
 }
 
@@ -2288,6 +2315,9 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     // both K slices in one workgroup: the problem stores finished outputs
     const bool kg2 = BM == 128 && pl.kg == 2;
     const int psplits = kg2 ? 1 : pl.splits;
+    // the two groups run k-tile counts that must match (fwd_plan)
+    if (kg2 && (pl.splits != 2 || 2 * pl.kchunk != ((K + pl.bk - 1) / pl.bk) * pl.bk))
+        return ACH_EINVAL;
     if (g.KS == 3 && (M & 3) == 0 && (g.C & 1) == 0) {
         FwdProblem<BM, BIm2col3F, true, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, psplits};
         p.e = e;
@@ -2657,6 +2687,9 @@ static int dgrad_small_c_nc(const ConvGeom &g, const float *dy, const float *w, 
     if (grid.y > 65535) return ACH_EUNSUPPORTED;
     if (g.KS == 3)
         hipLaunchKernelGGL((k_conv_dgrad_smallc<NC, 3>), grid, dim3(DG_NT), lds, st, dy, w, dx, g,
+                           tiles_x);
+    else if (g.KS == 5)
+        hipLaunchKernelGGL((k_conv_dgrad_smallc<NC, 5>), grid, dim3(DG_NT), lds, st, dy, w, dx, g,
                            tiles_x);
     else
         hipLaunchKernelGGL((k_conv_dgrad_smallc<NC, 0>), grid, dim3(DG_NT), lds, st, dy, w, dx, g,

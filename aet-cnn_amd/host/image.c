@@ -574,16 +574,20 @@ void an_image_distort(float *im, int w, int h, float hue, float sat, float val)
     }
 }
 
-void an_image_resize(const float *src, int W, int H, int c, int w, int h, float *dst)
+int an_image_resize(const float *src, int W, int H, int c, int w, int h, float *dst)
 {
     /* NImage.resizeImage (NImage.c:474-530): rows first, then columns */
+    if (!src || !dst || W <= 0 || H <= 0 || c <= 0 || w <= 0 || h <= 0) return ACH_EINVAL;
     if (W == w && H == h) {
         memcpy(dst, src, sizeof(float) * (size_t)w * h * c);
-        return;
+        return ACH_OK;
     }
     float *part = (float *)malloc(sizeof(float) * (size_t)w * H * c);
-    if (!part) return;
-    const float w_scale = (float)(W - 1) / (w - 1), h_scale = (float)(H - 1) / (h - 1);
+    if (!part) return ACH_EINVAL;
+    /* a one-pixel output side samples source row / column 0 (the
+     * reference's (H-1)/(h-1) would divide by zero there) */
+    const float w_scale = w > 1 ? (float)(W - 1) / (w - 1) : 0.f;
+    const float h_scale = h > 1 ? (float)(H - 1) / (h - 1) : 0.f;
     for (int k = 0; k < c; ++k)
         for (int r = 0; r < H; ++r)
             for (int x = 0; x < w; ++x) {
@@ -611,6 +615,7 @@ void an_image_resize(const float *src, int W, int H, int c, int w, int h, float 
             for (int x = 0; x < w; ++x) out[x] += dy * p0[x + w];
         }
     free(part);
+    return ACH_OK;
 }
 
 int an_augment_image(const float *src, int w, int h, int c, const an_augment *a, uint64_t seed,
@@ -643,7 +648,7 @@ int an_augment_image(const float *src, int w, int h, int c, const an_augment *a,
         const float dexp = rand_scale(&r, SALT_EXP, SALT_EXP_INV, a->exposure);
         an_image_distort(tmp, size, size, dhue, dsat, dexp);
     }
-    an_image_resize(tmp, size, size, c, w, h, dst);
+    const int rc = an_image_resize(tmp, size, size, c, w, h, dst);
     free(tmp);
-    return ACH_OK;
+    return rc;
 }

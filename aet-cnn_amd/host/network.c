@@ -761,7 +761,7 @@ int an_set_layer_options(an_network *net, int layer, const an_layer_options *opt
     an_layer *l = an_get_layer(net, layer);
     if (!l || !opt || net->finalized) return ACH_EINVAL;
     if (opt->flipped && l->type != AN_CONVOLUTIONAL) return ACH_EINVAL;
-    l->stopbackward = opt->stopbackward ? 1 : 0;
+    l->stopbackward = opt->stopbackward; /* raw: only 1 freezes the layers below */
     l->onlyforward = opt->onlyforward ? 1 : 0;
     l->dontload = opt->dontload ? 1 : 0;
     l->dontloadscales = opt->dontloadscales ? 1 : 0;
@@ -826,11 +826,13 @@ int an_finalize(an_network *net)
     if (!net || net->finalized || net->n == 0) return ACH_EINVAL;
     an_layer *last = net->layers[net->n - 1];
     net->classes = last->outputs;
-    /* the layers below the last stopbackward layer run forward only and are
-     * not updated (NetworkFactory.c:881-893, 981-991) */
+    /* the layers below the last layer with stopbackward = 1 run forward only
+     * and are not updated (NetworkFactory.c:881-893, 981-991: only the value
+     * 1 counts there, while the backward loop stops at any nonzero value,
+     * NNetwork.c:648) */
     int last_stop = -1;
     for (int i = 0; i < net->n; ++i)
-        if (net->layers[i]->stopbackward) last_stop = i;
+        if (net->layers[i]->stopbackward == 1) last_stop = i;
     for (int k = 0; k < last_stop; ++k) {
         net->layers[k]->onlyforward = 1;
         net->layers[k]->train = 0;

@@ -87,11 +87,11 @@ int an_validation_image(const char *path, int w, int h, int c, float *dst)
         an_image_free(im);
         return ACH_EINVAL;
     }
-    an_image_resize(im, W, H, c, rw, rh, rs);
-    an_image_crop(rs, rw, rh, c, (rw - w) / 2, (rh - h) / 2, w, h, dst);
+    const int rc = an_image_resize(im, W, H, c, rw, rh, rs);
+    if (rc == ACH_OK) an_image_crop(rs, rw, rh, c, (rw - w) / 2, (rh - h) / 2, w, h, dst);
     free(rs);
     an_image_free(im);
-    return ACH_OK;
+    return rc;
 }
 
 int an_validate_paths(an_network *net, const char *list_file, const char *const *labels,

@@ -83,9 +83,9 @@ struct an_layer {
     /* common */
     float *output, *delta;
     /* per-layer options (NLayer.h:115-125; NetworkFactory.c:656-663,
-     * 926-935, 981-991): stopbackward ends the backward loop at this layer,
+     * 926-935, 981-991): stopbackward (nonzero) ends the backward loop at this layer,
      * onlyforward skips its backward, train = 0 skips its update (set for
-     * every layer below the last stopbackward layer), learning_rate_scale
+     * every layer below the last layer whose stopbackward is 1), learning_rate_scale
      * multiplies the rate of its update, dontload / dontloadscales /
      * flipped shape how a .weights file is read into it                   */
     int stopbackward, onlyforward, train;
@@ -153,10 +153,11 @@ int an_set_subdivisions(an_network *net, int subdivisions);
 /* The per-layer cfg options the reference's CPU path acts on (NLayer.h:
  * 115-125, read by NetworkFactory.createLayer / createNetwork,
  * NetworkFactory.c:656-663, 926-935):
- *   stopbackward        NNetwork.backward (NNetwork.c:648) stops before this
- *                       layer's backward; an_finalize also freezes every
- *                       layer below the last such layer (train = 0,
- *                       onlyforward = 1; NetworkFactory.c:981-991)
+ *   stopbackward        nonzero: NNetwork.backward (NNetwork.c:648) stops
+ *                       before this layer's backward; exactly 1: an_finalize
+ *                       also freezes every layer below the last such layer
+ *                       (train = 0, onlyforward = 1; NetworkFactory.c:
+ *                       887-892, 981-991)
  *   onlyforward         the backward loop skips the layer (NNetwork.c:650)
  *   learning_rate_scale the layer's update runs at rate * scale
  *                       (ConvolutionalLayer.c:960)
@@ -251,7 +252,9 @@ void an_image_rotate_crop(const float *src, int W, int H, int c, float rad, floa
                           float dx, float dy, float aspect, float *dst);
 void an_image_flip(float *im, int w, int h, int c);
 void an_image_distort(float *im, int w, int h, float hue, float sat, float val);
-void an_image_resize(const float *src, int W, int H, int c, int w, int h, float *dst);
+/* resizeImage returns ACH_EINVAL (dst unwritten) for a bad size or when
+ * its row buffer cannot be allocated                                       */
+int an_image_resize(const float *src, int W, int H, int c, int w, int h, float *dst);
 /* NImage.reload (NImage.c:638-658): decodes a PNG (8-bit, non-interlaced;
  * grey, RGB, palette, grey+alpha, RGBA) or binary PPM / PGM file into host
  * planes dst[c][h][w] = sample / 255; the file must have exactly w x h

@@ -970,11 +970,13 @@ void or_net_set_layer_options(or_net *net, int i, int stopbackward, int onlyforw
 
 int or_net_finalize(or_net *net)
 {
-    /* NetworkFactory.c:881-893, 981-991: every layer below the last
-     * stopbackward layer runs forward only and is not updated */
+    /* NetworkFactory.c:881-893, 981-991: every layer below the last layer
+     * whose stopbackward is exactly 1 (atoi(value) == 1 at :889-890) runs
+     * forward only and is not updated; the backward loop stops at any
+     * nonzero value (NNetwork.c:648) */
     int last_stop = -1;
     for (int i = 0; i < net->n; ++i)
-        if (net->layers[i].stopbackward) last_stop = i;
+        if (net->layers[i].stopbackward == 1) last_stop = i;
     for (int k = 0; k < last_stop; ++k) {
         net->layers[k].onlyforward = 1;
         net->layers[k].train = 0;

@@ -61,6 +61,12 @@ def test_conv_shape_and_workspace_queries():
     assert ops.ach_conv_fwd_workspace(C.byref(big)) < 128 * 128 * 9 * 4 + 512
     fewer = aetcnn.ConvDesc(64, 512, 8, 8, 512, 3, 1, 1)  # 128 tiles: split in four
     assert ops.ach_conv_fwd_workspace(C.byref(fewer)) > filt + 512
+    # an odd k-tile count (34 channels: 17 tiles) splits into 9 + 8 tiles,
+    # which keep separate workgroups and partial sums
+    odd = aetcnn.ConvDesc(2, 34, 8, 8, 128, 3, 1, 1)
+    even = aetcnn.ConvDesc(2, 36, 8, 8, 128, 3, 1, 1)
+    assert ops.ach_conv_fwd_workspace(C.byref(odd)) >= 34 * 128 * 9 * 4 + 2 * 128 * 2 * 64 * 4
+    assert ops.ach_conv_fwd_workspace(C.byref(even)) < 36 * 128 * 9 * 4 + 512
     assert ops.ach_conv_bwd_filter_workspace(C.byref(big)) > 0
     assert ops.ach_maxpool_out(32, 2, 2, 1) == 16  # darknet default padding = size-1
     assert ops.ach_maxpool_out(55, 3, 2, 0) == 27

@@ -231,11 +231,16 @@ def test_distort_closed_forms():
 def test_resize_closed_form():
     src = np.array([[[1.0, 3.0], [5.0, 9.0]]], np.float32)  # 1 x 2 x 2
     dst = np.empty((1, 3, 3), np.float32)
-    lib().an_image_resize(src.ctypes.data, 2, 2, 1, 3, 3, dst.ctypes.data)
+    assert lib().an_image_resize(src.ctypes.data, 2, 2, 1, 3, 3, dst.ctypes.data) == 0
     assert np.array_equal(dst[0], [[1, 2, 3], [3, 4.5, 6], [5, 7, 9]])
     same = np.empty_like(src)
-    lib().an_image_resize(src.ctypes.data, 2, 2, 1, 2, 2, same.ctypes.data)
+    assert lib().an_image_resize(src.ctypes.data, 2, 2, 1, 2, 2, same.ctypes.data) == 0
     assert np.array_equal(same, src)
+    # a one-pixel side samples row / column 0; bad sizes are refused
+    one = np.empty((1, 1, 3), np.float32)
+    assert lib().an_image_resize(src.ctypes.data, 2, 2, 1, 3, 1, one.ctypes.data) == 0
+    assert np.array_equal(one[0, 0], [1, 2, 3])
+    assert lib().an_image_resize(src.ctypes.data, 2, 2, 1, 0, 3, one.ctypes.data) < 0
 
 
 # ---- the whole augmentation -----------------------------------------------------

@@ -199,6 +199,38 @@ def test_oracle_stopbackward_freezes_layers_below(oracle):
         n.close()
 
 
+def test_oracle_stopbackward_two_freezes_nothing(oracle):
+    """stopbackward=2 on layer 2: the backward loop stops there as for 1
+    (NNetwork.c:648 tests nonzero), but only the value 1 freezes the layers
+    below (NetworkFactory.c:889-891), so layer 0 keeps train = 1 and takes
+    its decay-only update: W += lr/B * (-decay*B*W), no longer its initial
+    value, while layer 2's update equals the stopbackward=1 case."""
+    one, two = (_tiny_pair(oracle, lambda n, v=v: n.set_layer_options(2, stopbackward=v))[1]
+                for v in (1, 2))
+    x, t, _ = configs.synthetic_batch("tiny", 3, 8)
+    w0 = two.buffer(0, 2).copy()
+    one.train(x, t)
+    two.train(x, t)
+    assert np.array_equal(one.buffer(0, 2), w0)           # frozen by 1
+    B, lr, decay = 8, np.float32(0.01), np.float32(5e-4)
+    a1, a2 = np.float32(-decay * np.float32(B)), np.float32(lr / np.float32(B))
+    want = (w0 + a2 * (a1 * w0).astype(np.float32)).astype(np.float32)
+    got = two.buffer(0, 2)
+    assert not np.array_equal(got, w0)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1
+    assert np.array_equal(two.buffer(2, 2), one.buffer(2, 2))
+    assert np.array_equal(two.buffer(4, 2), one.buffer(4, 2))
+    for n in (one, two):
+        n.close()
+
+
+def test_stopbackward_value_kept(tmp_path):
+    net = parse(tmp_path, NET + CONV + CONV + "stopbackward=2\n" + TAIL)
+    assert net is not None and opts(net, 1)["stopbackward"] == 2
+    net.close()
+
+
 def test_oracle_onlyforward_skips_one_layer(oracle):
     """onlyforward on the max-pool (layer 3): its backward is skipped, so the
     conv layer below gets a zero delta (deltas are zeroed in forward) and

@@ -533,6 +533,9 @@ def test_train_step_updates_like_separate_update(gpu, name, batch, steps):
     # a dropout after a 2x2 max-pool skipped in backward: the pool must not
     # apply its mask either
     ("darknet", 8, {4: dict(onlyforward=1)}),
+    # stopbackward = 2 stops the backward loop but freezes nothing: the
+    # layers below get their decay / momentum updates
+    ("darknet", 8, {5: dict(stopbackward=2)}),
 ])
 def test_layer_options_match_oracle(gpu, oracle, name, batch, options):
     """stopbackward / onlyforward / learning_rate (NNetwork.c:648-651,
@@ -558,7 +561,7 @@ def test_layer_options_match_oracle(gpu, oracle, name, batch, options):
         onet.set_layer_options(i, **o)
     net.finalize()
     onet.finalize()
-    stop = max([i for i, o in options.items() if o.get("stopbackward")], default=-1)
+    stop = max([i for i, o in options.items() if o.get("stopbackward") == 1], default=-1)
     init = {i: net.buffer(i, 2).copy() for i in conv_layers(onet) if i < stop}
     for step in range(3):
         for i in conv_layers(onet):  # teacher forcing, as in the teacher-forced steps

@@ -118,6 +118,10 @@ CONV_SHAPES = [
     # fully connected layers (1x1 of a 1x1 input, after flattening):
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
     (8, 64, 1, 1, 48, 1, 1, 0),    # 64 -> 48, 64-row tiles
+    # 3x3 forwards with an odd k-tile count (C/2 = 17): the K split gives
+    # slices of 9 and 8 tiles, which must not share one workgroup
+    (2, 34, 8, 8, 128, 3, 1, 1),   # one tile split in two
+    (16, 34, 32, 32, 512, 3, 1, 1),  # 512 tiles
 ]
 
 
