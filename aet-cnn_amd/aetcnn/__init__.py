@@ -119,6 +119,7 @@ _OPS = {
     "ach_add_bias": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "ach_bias_grad_workspace": (_sz, [_i, _i, _i]),
     "ach_bias_grad": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "ach_bias_grad_planes": (_i, [_vp, _vp, _i, _i, _vp]),
     "ach_bn_workspace": (_sz, [_i, _i, _i]),
     "ach_bn_train_fwd": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                               _vp, _sz, _vp]),
@@ -137,10 +138,13 @@ _OPS = {
                         _vp, _sz, _vp]),
     "ach_activate": (_i, [_vp, _sz, _i, _vp]),
     "ach_gradient": (_i, [_vp, _sz, _i, _vp, _vp]),
+    "ach_gradient_planes": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ach_maxpool_out": (_i, [_i, _i, _i, _i]),
     "ach_maxpool_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ach_maxpool_bwd": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp]),
     "ach_maxpool_bwd_act": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
+    "ach_maxpool_bwd_act_planes": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp,
+                                        _vp]),
     "ach_maxpool_fwd_dropout": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _f, _u64, _u32,
                                      _vp, _u32, _vp]),
     "ach_maxpool_bwd_dropout": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _u64,

@@ -237,6 +237,114 @@ __global__ void k_gradient(const float *__restrict__ y, size_t n, int act, float
     for (size_t i = done + gid; i < n; i += stride) d[i] *= act_gradient(y[i], act);
 }
 
+// Per-plane sums of what a plane-walking kernel writes (the bias gradient's
+// per-(image, channel) sums, BiasData.calcGrad BiasData.c:40-57), for a
+// workgroup of 256 threads over np <= PSUM_PLANES consecutive planes walked
+// flat (pixel r of the workgroup's planes at r = tid, tid + 256, ...): a
+// thread's plane index never decreases, so it keeps one running double sum
+// and parks it in its LDS slot red[plane][tid] when the plane changes; at
+// the end one wave per plane adds the 256 slots (four per lane in order,
+// then a fixed xor tree).  Deterministic.
+constexpr int PSUM_PLANES = 8;
+struct PlaneSum {
+    double *red;  // LDS [np][256], zeroed before the walk
+    int cur = -1;
+    double s = 0;
+    __device__ __forceinline__ void add(int pl, float v)
+    {
+        if (pl != cur) {
+            if (cur >= 0) red[cur * 256 + threadIdx.x] = s;
+            cur = pl;
+            s = 0;
+        }
+        s += (double)v;
+    }
+    // every thread calls it; psum[plane0 + k] for k < np
+    __device__ __forceinline__ void finish(int np, double *psum, size_t plane0)
+    {
+        if (cur >= 0) red[cur * 256 + threadIdx.x] = s;
+        __syncthreads();
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        for (int k = wave; k < np; k += 4) {
+            const double *r = red + k * 256 + lane;
+            double t = ((r[0] + r[64]) + r[128]) + r[192];
+            t = wave_sum(t);
+            if (lane == 0) psum[plane0 + k] = t;
+        }
+    }
+};
+__device__ __forceinline__ void psum_clear(double *red, int np)
+{
+    for (int q = threadIdx.x; q < np * 256; q += 256) red[q] = 0.0;
+}
+
+// The activation gradient (as k_gradient) of [planes][hw], one plane per
+// wave, with each plane's sum of the result in psum[plane] (the bias
+// gradient's per-(image, channel) sums, taken while the delta is written):
+// lane l adds positions l, l + 64, ... in order (four loads in flight),
+// then a fixed xor tree.  No LDS, so it fits beside the GEMMs' workgroups.
+__global__ void __launch_bounds__(256) k_gradient_planes(const float *__restrict__ y, int planes,
+                                                         int hw, int act, float *__restrict__ d,
+                                                         double *__restrict__ psum)
+{
+    const int lane = threadIdx.x & 63;
+    const int pl = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pl >= planes) return;
+    const size_t base = (size_t)pl * hw;
+    double s = 0;
+    for (int q0 = lane; q0 < hw; q0 += 4 * 64) {
+        float yv[4], dv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * 64;
+            yv[u] = q < hw ? y[base + q] : 0.f;
+            dv[u] = q < hw ? d[base + q] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * 64;
+            if (q >= hw) break;
+            const float v = dv[u] * act_gradient(yv[u], act);
+            d[base + q] = v;
+            s += (double)v;
+        }
+    }
+    s = wave_sum(s);
+    if (lane == 0) psum[pl] = s;
+}
+
+// bias_updates[c] += sum over images b of psum[b][c] (BiasData.calcGrad's
+// sums of each image's plane, BiasData.c:52-56), in double: a block takes 32
+// channels, its 8 thread groups the images b = g, g + 8, ... (their loads in
+// flight together), and the 8 group sums are added in group order.
+constexpr int BFP_G = 8;
+__global__ void __launch_bounds__(256) k_bias_from_planes(const double *__restrict__ psum,
+                                                          int batch, int n, float *updates)
+{
+    __shared__ double sh[BFP_G][32];
+    const int cl = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int c = blockIdx.x * 32 + cl;
+    double s = 0;
+    if (c < n) {
+        int b = g;
+        for (; b + 3 * BFP_G < batch; b += 4 * BFP_G) {
+            const double v0 = psum[(size_t)b * n + c], v1 = psum[(size_t)(b + BFP_G) * n + c];
+            const double v2 = psum[(size_t)(b + 2 * BFP_G) * n + c];
+            const double v3 = psum[(size_t)(b + 3 * BFP_G) * n + c];
+            s = (((s + v0) + v1) + v2) + v3;
+        }
+        for (; b < batch; b += BFP_G) s += psum[(size_t)b * n + c];
+    }
+    sh[g][cl] = s;
+    __syncthreads();
+    if (g == 0 && c < n) {
+        double t = 0;
+#pragma unroll
+        for (int k = 0; k < BFP_G; ++k) t += sh[k][cl];
+        updates[c] += (float)t;
+    }
+}
+
 // ---- max-pool --------------------------------------------------------------------
 // Input element counts are below 2^31 (the indexes are int32), so all index
 // arithmetic is 32-bit.
@@ -483,13 +591,15 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
 // output position.
 constexpr int POOL_PLANE_MAX = 4096;  // output positions staged in LDS per workgroup
 constexpr int POOL_PIX_PER_WG = 1024; // input pixels a workgroup aims at
+
 template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restrict__ dout,
                                                            const int32_t *__restrict__ idx,
                                                            FastDiv dW, FastDiv dHW, int size_,
                                                            int stride_, int pad, int OH, int OW,
                                                            int planes, int ppw, float *din,
-                                                           int accumulate, GradIn gi)
+                                                           int accumulate, GradIn gi,
+                                                           double *psum)
 {
     extern __shared__ int32_t pool_lds[];
     const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
@@ -497,6 +607,11 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
     const int bc0 = blockIdx.x * ppw, np = min(ppw, planes - bc0);
     int32_t *six = pool_lds;
     float *sg = reinterpret_cast<float *>(pool_lds + ppw * ohw);
+    // psum (optional): the sums of each input plane written, after the
+    // staged planes (8-byte aligned: 8 bytes per staged output position)
+    PlaneSum ps;
+    ps.red = reinterpret_cast<double *>(pool_lds + 2 * ppw * ohw);
+    if (psum) psum_clear(ps.red, np);
     const size_t obase = (size_t)bc0 * ohw;
     for (int q = threadIdx.x; q < np * ohw; q += blockDim.x) {
         six[q] = idx[obase + q];
@@ -535,8 +650,11 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
                     if (pix[o] == p) v += pg[o];
                 }
         }
-        din[p] = gi.apply(v, (size_t)p);
+        v = gi.apply(v, (size_t)p);
+        din[p] = v;
+        if (psum) ps.add(pl, v);
     }
+    if (psum) ps.finish(np, psum, (size_t)bc0);
 }
 
 // Backward of k_maxpool2_fwd: every input pixel lies in exactly one window.
@@ -1116,14 +1234,30 @@ int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w, int
     return maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, dr, s);
 }
 
+// the planes per workgroup of k_maxpool_bwd_plane (0: output planes too
+// large to stage)
+static int pool_bwd_ppw(int batch, int c, int h, int w, int OH, int OW)
+{
+    if (OH * OW > POOL_PLANE_MAX) return 0;
+    return std::max(1, std::min({POOL_PIX_PER_WG / (h * w), POOL_PLANE_MAX / (OH * OW),
+                                 batch * c}));
+}
+
+// psum (optional): per-(image, channel) sums of din as written, double
+// [batch][c]; only the plane-staged kernel with at most PSUM_PLANES planes
+// per workgroup takes it (else ACH_EUNSUPPORTED, nothing launched)
 static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
                        int size, int stride, int pad, float *din, int accumulate, GradIn gi,
-                       DropIn dr, ach_stream_t s)
+                       DropIn dr, ach_stream_t s, double *psum = nullptr)
 {
     if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
     const int acc = accumulate ? 1 : 0;
-    const bool fast2 = pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
+    if (psum) {
+        const int ppw = pool_bwd_ppw(batch, c, h, w, OH, OW);
+        if (ppw == 0 || ppw > PSUM_PLANES || dr.on) return ACH_EUNSUPPORTED;
+    }
+    const bool fast2 = !psum && pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
                        (reinterpret_cast<uintptr_t>(idx) & 7) == 0 &&
                        (reinterpret_cast<uintptr_t>(gi.y) & 15) == 0;
     if (dr.on && !fast2) {  // the dropout backward in place on dout first
@@ -1143,20 +1277,22 @@ static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, 
     const FastDiv dH = make_fastdiv((unsigned)h), dW = make_fastdiv((unsigned)w);
     if (OH * OW <= POOL_PLANE_MAX) {  // planes staged in LDS, ppw per workgroup
         const int planes = batch * c;
-        const int ppw = std::max(1, std::min({POOL_PIX_PER_WG / (h * w),
-                                              POOL_PLANE_MAX / (OH * OW), planes}));
+        const int ppw = pool_bwd_ppw(batch, c, h, w, OH, OW);
         const dim3 pg((unsigned)((planes + ppw - 1) / ppw));
-        const size_t lds = (size_t)ppw * OH * OW * 8;
+        const size_t lds = (size_t)ppw * OH * OW * 8 + (psum ? (size_t)ppw * 256 * 8 : 0);
         const FastDiv dHW = make_fastdiv((unsigned)(h * w));
         if (size == 3 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<3, 2>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi);
+                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi,
+                               psum);
         else if (size == 2 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<2, 2>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi);
+                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi,
+                               psum);
         else
             hipLaunchKernelGGL((k_maxpool_bwd_plane<0, 0>), pg, dim3(256), lds, as_stream(s), dout,
-                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi);
+                               idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi,
+                               psum);
         return check_launch();
     }
     if (size == 3 && stride == 2)
@@ -1198,6 +1334,40 @@ int ach_maxpool_bwd_act(const float *dout, const int32_t *idx, int batch, int c,
         return ACH_EINVAL;
     return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
                        GradIn{y_in, act_in}, DropIn{}, s);
+}
+
+int ach_maxpool_bwd_act_planes(const float *dout, const int32_t *idx, int batch, int c, int h,
+                               int w, int size, int stride, int pad, float *din,
+                               const float *y_in, int act_in, double *plane_sums,
+                               ach_stream_t s)
+{
+    if (!plane_sums || (y_in && act_in != ACH_LOGISTIC && act_in != ACH_RELU &&
+                        act_in != ACH_LINEAR && act_in != ACH_LEAKY))
+        return ACH_EINVAL;
+    return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, 0,
+                       GradIn{y_in, y_in ? act_in : ACH_LINEAR}, DropIn{}, s, plane_sums);
+}
+
+int ach_gradient_planes(const float *y, int batch, int n, int spatial, int act, float *delta,
+                        double *plane_sums, ach_stream_t s)
+{
+    if (!y || !delta || !plane_sums || batch <= 0 || n <= 0 || spatial <= 0) return ACH_EINVAL;
+    if (act != ACH_LEAKY && act != ACH_RELU && act != ACH_LOGISTIC && act != ACH_LINEAR)
+        return ACH_EUNSUPPORTED;
+    const long long planes = (long long)batch * n;
+    if (planes * spatial >= 0x7fffffffll) return ACH_EUNSUPPORTED;
+    hipLaunchKernelGGL(k_gradient_planes, dim3((unsigned)((planes + 3) / 4)), dim3(256), 0,
+                       as_stream(s), y, (int)planes, spatial, act, delta, plane_sums);
+    return check_launch();
+}
+
+int ach_bias_grad_planes(float *bias_updates, const double *plane_sums, int batch, int n,
+                         ach_stream_t s)
+{
+    if (!bias_updates || !plane_sums || batch <= 0 || n <= 0) return ACH_EINVAL;
+    hipLaunchKernelGGL(k_bias_from_planes, dim3((n + 31) / 32), dim3(256), 0, as_stream(s),
+                       plane_sums, batch, n, bias_updates);
+    return check_launch();
 }
 
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out, ach_stream_t s)

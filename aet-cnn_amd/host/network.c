@@ -255,6 +255,11 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
                             st.workspace_bytes, s));
     } else if (l->grad_applied) {
         l->grad_applied = 0; /* the max-pool above applied f'(y) already */
+    } else if (l->bias_planes && l->activation != ACH_LINEAR) {
+        /* the gradient pass also takes the bias gradient's plane sums */
+        AN_CHECK(ach_gradient_planes(l->output, l->batch, l->n, spatial, l->activation, l->delta,
+                                     l->bias_planes, s));
+        l->planes_ready = 1;
     } else {
         AN_CHECK(ach_gradient(l->output, nout, l->activation, l->delta, s));
     }
@@ -273,9 +278,13 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
         gws = net->wgrad_ws;
         gws_bytes = net->wgrad_ws_bytes;
     }
-    if (!l->batch_normalize)
+    if (!l->batch_normalize && l->planes_ready) {
+        l->planes_ready = 0;
+        AN_CHECK(ach_bias_grad_planes(l->bias_updates, l->bias_planes, l->batch, l->n, gs));
+    } else if (!l->batch_normalize) {
         AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial, gws,
                                gws_bytes, gs));
+    }
     AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, gws, gws_bytes,
                                  gs));
     if (st.delta)
@@ -404,6 +413,19 @@ static int maxpool_backward(an_network *net, an_layer *l, an_state st)
      * BN, which fuses its gradient itself), the layer's activation gradient
      * is applied here and the conv layer's backward skips it.              */
     an_layer *p = pool_act_target(net, l, st.delta);
+    if (p && p->bias_planes) {
+        /* ... and takes that layer's bias-gradient plane sums as it writes */
+        const int rc = ach_maxpool_bwd_act_planes(l->delta, l->indexes, l->batch, l->c, l->h,
+                                                  l->w, l->size, l->stride, l->pad, st.delta,
+                                                  p->output, p->activation, p->bias_planes,
+                                                  net->stream);
+        if (rc == ACH_OK) {
+            p->grad_applied = 1;
+            p->planes_ready = 1;
+            return ACH_OK;
+        }
+        if (rc != ACH_EUNSUPPORTED) return rc;
+    }
     if (p) {
         AN_CHECK(ach_maxpool_bwd_act(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size,
                                      l->stride, l->pad, st.delta, 0, p->output, p->activation,
@@ -726,6 +748,8 @@ static void layout(an_network *net, bump *b)
             l->variance_delta = (float *)take(b, sizeof(float) * l->n);
         } else if (l->type == AN_MAXPOOL) {
             l->indexes = (int32_t *)take(b, sizeof(int32_t) * bo);
+        } else if (l->type == AN_CONVOLUTIONAL && l->out_h * l->out_w >= 128) {
+            l->bias_planes = (double *)take(b, sizeof(double) * B * l->n);
         } else if (l->type == AN_SOFTMAX) {
             l->loss = (float *)take(b, sizeof(float) * bo);
             l->cost = (float *)take(b, sizeof(float) * 4);
@@ -1085,7 +1109,10 @@ int an_backward(an_network *net)
         rc = l->backward(net, l, backward_state(net, i));
     }
     net->in_chain = 0;
-    for (int i = 0; i < net->n; ++i) net->layers[i]->grad_applied = 0;
+    for (int i = 0; i < net->n; ++i) {
+        net->layers[i]->grad_applied = 0;
+        net->layers[i]->planes_ready = 0;
+    }
     AN_CHECK(rc);
     return join_wgrad(net);
 }

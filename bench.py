@@ -627,6 +627,8 @@ def main():
                          "(for rocprofv3 counter passes)")
     ap.add_argument("--bandwidth-reps", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the full-step timing of the two configs besides --config")
     ap.add_argument("--cpu-batch", type=int, default=128)
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--cpu-faithful-batch", type=int, default=16)
@@ -681,6 +683,24 @@ def main():
     step_tflops = tr["gflop_step"] / (ms_step * 1e-3) / 1e3
     log(f"{ms_step:.3f} ms/step ({tr['gpu_ms'] / args.steps:.3f} GPU ms), {ips:.1f} img/s, "
         f"conv {step_tflops:.2f} TFLOP/s, loss {tr['first_loss']:.4f} -> {tr['loss']:.4f}")
+    # the other two full-step configs (BASELINE configs 0 / 3 / 4), each timed
+    # the same way at batch 128: the headline stays --config's
+    other_steps = {}
+    if not args.no_other_configs:
+        for name in ("tiny", "darknet", "alexnet"):
+            if name == args.config:
+                continue
+            o = train_phase(aetcnn, configs, name, args.steps, args.warmup, None)
+            oms = o["wall_s"] * 1e3 / args.steps
+            otf = o["gflop_step"] / (oms * 1e-3) / 1e3
+            other_steps[f"{name}_step"] = dict(
+                ms_per_step=round(oms, 4), images_per_s=round(o["batch"] * args.steps / o["wall_s"], 1),
+                gpu_ms_per_step=round(o["gpu_ms"] / args.steps, 4), batch=o["batch"],
+                steps=args.steps, warmup=args.warmup, conv_gflop_per_step=round(o["gflop_step"], 2),
+                conv_tflops=round(otf, 3), frac_of_fp32_mfma_peak=round(otf / MFMA_FP32_PEAK_TFLOPS, 4),
+                loss_first_last=[round(o["first_loss"], 5), round(o["loss"], 5)])
+            log(f"{name} b{o['batch']}: {oms:.3f} ms/step, "
+                f"{other_steps[name + '_step']['images_per_s']} img/s, conv {otf:.2f} TFLOP/s")
     # kernel measurements next, before the long fed and sustained runs heat the
     # GPU and lower its clocks
     sweep_rows, sweep_tflops = [], None
@@ -778,6 +798,7 @@ def main():
         "bandwidth_ops": {"shape": "x[512][128][32][32] fp32 (config 2)", "ops": bw_rows,
                           "softmax_xent_512x1000_us": softmax_us},
         "sustained": sustained,
+        **other_steps,
         "roofline": rooflines["fwd"],
         "roofline_wgrad": rooflines["wgrad"],
         "cpu_baseline": cpu,

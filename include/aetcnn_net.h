@@ -93,6 +93,10 @@ struct an_layer {
     float learning_rate_scale;
     int zero_delta;         /* delta is accumulated into by the next layer */
     int grad_applied;       /* this step's f'(y) already applied to delta   */
+    double *bias_planes;    /* conv without BN, planes of 128+ positions:
+                               per-(image, filter) sums of delta, written by
+                               the pass that writes delta [batch][n]     */
+    int planes_ready;       /* bias_planes hold this step's sums           */
     int (*forward)(an_network *net, an_layer *l, an_state st);
     int (*backward)(an_network *net, an_layer *l, an_state st);
     int (*update)(an_network *net, an_layer *l, int batch, float lr, float momentum,

@@ -168,6 +168,14 @@ int ach_add_bias(float *out, const float *biases, int batch, int n, int spatial,
 size_t ach_bias_grad_workspace(int batch, int n, int spatial);
 int ach_bias_grad(float *bias_updates, const float *delta, int batch, int n, int spatial,
                   void *ws, size_t ws_bytes, ach_stream_t stream);
+/* The same gradient in two halves, for a pass that already writes the delta
+ * (the activation gradient below, or a max-pool's input gradient): that
+ * pass stores plane_sums[b][c] = sum over positions of delta[b][c][:]
+ * (double [batch][n]: DnnUtils.sum of each image's plane, BiasData.c:
+ * 52-56), and this call adds bias_updates[c] += sum over b ascending of
+ * plane_sums[b][c] (in double, rounded once).                             */
+int ach_bias_grad_planes(float *bias_updates, const double *plane_sums, int batch, int n,
+                         ach_stream_t stream);
 
 /* ---- batch-norm, training mode ------------------------------------------
  * Forward (forwardNormCPU NLayer.c:141-162 = NormData.calcVarianceAndMean
@@ -246,6 +254,11 @@ int ach_bn_bwd(float *delta, int batch, int c, int spatial,
 int ach_activate(float *x, size_t n, int activation, ach_stream_t stream);
 int ach_gradient(const float *y, size_t n, int activation, float *delta,
                  ach_stream_t stream);
+/* ach_gradient of a [batch][n][spatial] tensor (the same products, ACH_LINEAR
+ * included: delta unchanged) that also stores the bias gradient's
+ * plane_sums[b][c] of the result (ach_bias_grad_planes)                    */
+int ach_gradient_planes(const float *y, int batch, int n, int spatial, int activation,
+                        float *delta, double *plane_sums, ach_stream_t stream);
 
 /* ---- max-pool (MaxPoolLayer.c:237-272 forward, :318-331 backward) --------
  * out size = (in + padding - size)/stride + 1, window offset -padding/2,
@@ -292,6 +305,16 @@ int ach_maxpool_bwd_act(const float *delta_out, const int32_t *indexes,
                         int batch, int c, int h, int w, int size, int stride, int padding,
                         float *delta_in, int accumulate, const float *y_in, int act_in,
                         ach_stream_t stream);
+/* ach_maxpool_bwd_act with accumulate = 0 (y_in may be NULL: no gradient)
+ * that also stores the bias gradient's plane_sums[b][c] of the delta_in it
+ * writes (ach_bias_grad_planes; double [batch][c]).  For pools whose output
+ * planes are staged in LDS with at most 8 planes per workgroup (input
+ * planes of 128+ pixels, output planes of at most 4096): ACH_EUNSUPPORTED
+ * otherwise, with nothing launched.                                       */
+int ach_maxpool_bwd_act_planes(const float *delta_out, const int32_t *indexes, int batch, int c,
+                               int h, int w, int size, int stride, int padding, float *delta_in,
+                               const float *y_in, int act_in, double *plane_sums,
+                               ach_stream_t stream);
 
 /* ---- global average pool (AvgPoolLayer.c:29-46, 73-88) ----------------- */
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out,

@@ -413,6 +413,74 @@ def test_maxpool_bwd_act_fused(gpu, oracle, B, Cc, H, W, size, stride, pad, act)
 
 
 @pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [
+    (3, 5, 55, 55, 3, 2, 0),      # AlexNet pool 1: one plane per workgroup
+    (3, 7, 27, 27, 3, 2, 0),      # pool 2
+    (5, 7, 13, 13, 3, 2, 0),      # pool 5: six planes per workgroup, partial last
+    (2, 3, 20, 20, 2, 2, 1),      # 2x2/2 through the staged kernel
+])
+@pytest.mark.parametrize("act", [aetcnn.RELU, aetcnn.LEAKY, aetcnn.LINEAR])
+def test_maxpool_bwd_act_planes(gpu, oracle, B, Cc, H, W, size, stride, pad, act):
+    """ach_maxpool_bwd_act_planes writes the delta of ach_maxpool_bwd_act
+    bit for bit and each (image, channel) plane's sum of it in double; the
+    bias gradient from those sums (ach_bias_grad_planes) equals
+    ach_bias_grad over the delta (BiasData.c:40-57)."""
+    rng = np.random.default_rng(H + 3 * act)
+    x = rng.integers(-3, 4, (B, Cc, H, W)).astype(np.float32)
+    out, idx = oracle.maxpool_forward(x, size, stride, pad)
+    y = rng.standard_normal(x.shape).astype(np.float32)
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    dg, di, dy_ = dev(g), dev(idx.astype(np.int32)), dev(y)
+    ref = dev(np.zeros(x.shape, np.float32))
+    check(gpu.ach_maxpool_bwd_act(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, ref.ptr, 0,
+                                  dy_.ptr, act, None))
+    got = dev(np.full(x.shape, np.nan, np.float32))
+    ps = dev(np.full(B * Cc, np.nan))
+    check(gpu.ach_maxpool_bwd_act_planes(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, got.ptr,
+                                         dy_.ptr, act, ps.ptr, None))
+    a, b = ref.numpy(), got.numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    sums = b.astype(np.float64).sum(axis=(2, 3)).reshape(-1)
+    assert np.allclose(ps.numpy(), sums, rtol=1e-12, atol=1e-12)
+    u0 = rng.standard_normal(Cc).astype(np.float32)
+    ua, ub = dev(u0), dev(u0)
+    ws = gpu.ach_bias_grad_workspace(B, Cc, H * W)
+    dws = D(ws // 4 + 1)
+    check(gpu.ach_bias_grad(ua.ptr, got.ptr, B, Cc, H * W, dws.ptr, ws, None))
+    check(gpu.ach_bias_grad_planes(ub.ptr, ps.ptr, B, Cc, None))
+    assert rel_err(ub.numpy(), ua.numpy()) < 1e-7
+
+
+def test_maxpool_bwd_act_planes_unsupported(gpu):
+    """Small input planes (more than 8 per workgroup) keep the separate bias
+    gradient: nothing is launched."""
+    B, Cc, H, W = 4, 8, 8, 8  # 16 planes of 64 pixels per workgroup
+    g, idx = dev(np.zeros(B * Cc * 16, np.float32)), dev(np.zeros(B * Cc * 16, np.int32))
+    din, ps = dev(np.zeros(B * Cc * H * W, np.float32)), dev(np.zeros(B * Cc))
+    assert gpu.ach_maxpool_bwd_act_planes(g.ptr, idx.ptr, B, Cc, H, W, 2, 2, 1, din.ptr, None,
+                                          aetcnn.LINEAR, ps.ptr, None) == aetcnn.ACH_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("B,n,sp", [(3, 5, 169), (2, 4, 3025), (4, 3, 130), (2, 3, 2000)])
+@pytest.mark.parametrize("act", [aetcnn.RELU, aetcnn.LEAKY, aetcnn.LOGISTIC, aetcnn.LINEAR])
+def test_gradient_planes(gpu, B, n, sp, act):
+    """ach_gradient_planes: the products of ach_gradient bit for bit, plus
+    the per-plane sums of the result."""
+    rng = np.random.default_rng(sp + act)
+    y = rng.standard_normal((B, n, sp)).astype(np.float32)
+    if act == aetcnn.LOGISTIC:
+        y = (1 / (1 + np.exp(-y))).astype(np.float32)
+    d = rng.standard_normal(y.shape).astype(np.float32)
+    dy_, da, db = dev(y), dev(d), dev(d)
+    check(gpu.ach_gradient(dy_.ptr, y.size, act, da.ptr, None))
+    ps = dev(np.full(B * n, np.nan))
+    check(gpu.ach_gradient_planes(dy_.ptr, B, n, sp, act, db.ptr, ps.ptr, None))
+    a, b = da.numpy(), db.numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.allclose(ps.numpy(), b.astype(np.float64).sum(axis=2).reshape(-1), rtol=1e-12,
+                       atol=1e-12)
+
+
+@pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [
     (4, 3, 32, 32, 2, 2, 1),      # 2x2/2 kernels: mask applied inside
     (2, 5, 55, 55, 3, 2, 0),      # other windows: two steps inside the call
 ])
