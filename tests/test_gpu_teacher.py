@@ -11,7 +11,8 @@ NNetwork.c:740-805; ConvolutionalLayer.update, ConvolutionalLayer.c:959-980).
 
 Config 3 (darknet-style) runs all 100 steps at batch 128, in ten tests of ten
 steps that share one pair of networks, so progress shows per ten steps;
-config 4 (AlexNet-style) runs 5 steps at batch 128."""
+config 4 (AlexNet-style) runs 30 steps at batch 128 the same way (three
+tests of ten), printing every step's |dloss| and worst parameter error."""
 import numpy as np
 import pytest
 
@@ -164,19 +165,35 @@ def test_darknet_teacher_forced_100_steps(darknet_run, chunk):
           f"max |dloss| {max(r['dloss']):.3g}")
 
 
-def test_alexnet_teacher_forced_steps(gpu, oracle):
-    """Config 4 at batch 128: 5 teacher-forced steps (strided 11x11 conv,
-    5x5 conv, overlapping 3x3 pools, FC layers, dropout)."""
+ALEXNET_STEPS = 30
+
+
+@pytest.fixture(scope="module")
+def alexnet_run(gpu, oracle):
     oracle.lib().or_set_gemm_parallel(1)
     net, onet = make_pair(oracle, "alexnet", 128)
-    dls, pes = [], []
-    try:
-        for step in range(5):
-            dl, pe = teacher_step(net, onet, "alexnet", step, 128)
-            dls.append(dl)
-            pes.append(pe)
-    finally:
-        net.close()
-        onet.close()
-    print(f"alexnet b128 teacher-forced 5 steps: |dloss| {[f'{v:.2g}' for v in dls]}, "
-          f"max parameter error {max(pes):.3g}")
+    run = dict(net=net, onet=onet, done=0, dloss=[], perr=[])
+    yield run
+    net.close()
+    onet.close()
+
+
+@pytest.mark.parametrize("chunk", range(ALEXNET_STEPS // CHUNK))
+def test_alexnet_teacher_forced_steps(alexnet_run, chunk):
+    """Steps [10*chunk, 10*chunk + 10) of config 4 at batch 128 (strided
+    11x11 conv, 5x5 conv, overlapping 3x3 pools, FC layers, dropout), with
+    the per-step bars of teacher_step."""
+    r = alexnet_run
+    end = (chunk + 1) * CHUNK
+    while r["done"] < end:
+        dl, pe = teacher_step(r["net"], r["onet"], "alexnet", r["done"], 128)
+        print(f"alexnet b128 teacher-forced step {r['done']}: |dloss| {dl:.3g}, "
+              f"worst parameter error {pe:.3g}")
+        r["dloss"].append(dl)
+        r["perr"].append(pe)
+        r["done"] += 1
+    dl = np.array(r["dloss"][end - CHUNK:end])
+    pe = np.array(r["perr"][end - CHUNK:end])
+    print(f"alexnet b128 teacher-forced steps {end - CHUNK}-{end - 1}: max |dloss| "
+          f"{dl.max():.3g}, max parameter error {pe.max():.3g}; over steps 0-{end - 1}: "
+          f"max |dloss| {max(r['dloss']):.3g}, max parameter error {max(r['perr']):.3g}")
