@@ -116,6 +116,9 @@ _OPS = {
     "ach_conv_bwd_data": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _sz, _vp]),
     "ach_conv_bwd_filter_workspace": (_sz, [C.POINTER(ConvDesc)]),
     "ach_conv_bwd_filter": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ach_conv_bwd_filter_sgd": (_i, [C.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _f, _f, _f, _vp, _sz,
+                                    _vp]),
+    "ach_conv_bwd_data_reads_w": (_i, [C.POINTER(ConvDesc)]),
     "ach_add_bias": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "ach_bias_grad_workspace": (_sz, [_i, _i, _i]),
     "ach_bias_grad": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),

@@ -113,6 +113,26 @@ __device__ __forceinline__ float act_gradient(float y, int act)
     return 1.f;
 }
 
+// One SGD step of a parameter a and its update accumulator u
+// (ConvolutionalLayer.update, ConvolutionalLayer.c:959-980, via WeightData
+// addWeightToUpdates / addUpdatesToWeight / scaleUpdates):
+// u += dc*a (dc = -decay*batch); a += lc*u (lc = lr/batch); u *= mom.
+// Shared by the flat update and the weight-gradient passes that apply it
+// where dW is final, so both compile to the same arithmetic.
+__device__ __forceinline__ void sgd_step(float &a, float &u, float dc, float lc, float mom)
+{
+    u += dc * a;
+    a += lc * u;
+    u *= mom;
+}
+
+// The update a weight-gradient pass applies to (w, dW) once dW is final
+// (w == nullptr: none).
+struct Sgd {
+    float *w = nullptr;
+    float dc = 0.f, lc = 0.f, mom = 0.f;
+};
+
 // Counter-based uniform in [0,1): SplitMix64 finaliser over
 // (seed, iteration, layer, index); top 24 bits.
 __host__ __device__ __forceinline__ float dropout_uniform(uint64_t seed, uint32_t iter,

@@ -917,6 +917,66 @@ struct FwdProblem {
     }
 };
 
+// dW tile stores of the weight-gradient problems (dw[m][n] row-major, one
+// lane's 16 values of a 32x32 tile: rows mb + 8*(r/4) + r%4, column n).
+// Unsplit: dw += acc with all 16 prior values loaded before the first store;
+// with sgd.w the weights are loaded with them and every (w, dw) pair then
+// takes the SGD step (sgd_step) on the new dw, so the update costs no pass
+// of its own.  Split K: the slice's partial sums.  full: every row of the
+// workgroup's tile is below M.
+__device__ __forceinline__ void wgrad_store_tile(float *dw, float *part, const Sgd &sgd, int M,
+                                                 int N, int splits, int mb, int n,
+                                                 const v16f &acc, int z, bool full)
+{
+    if (n >= N) return;
+    if (splits == 1) {
+        float *base = dw + (size_t)mb * N + n;
+        float old[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int dm = 8 * (r >> 2) + (r & 3);
+            old[r] = (full || mb + dm < M) ? base[(size_t)dm * N] : 0.f;
+        }
+        if (sgd.w) {
+            float *wb = sgd.w + (size_t)mb * N + n;
+            float wv[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                wv[r] = (full || mb + dm < M) ? wb[(size_t)dm * N] : 0.f;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                if (full || mb + dm < M) {
+                    float a = wv[r], u = old[r] + acc[r];
+                    sgd_step(a, u, sgd.dc, sgd.lc, sgd.mom);
+                    wb[(size_t)dm * N] = a;
+                    base[(size_t)dm * N] = u;
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int dm = 8 * (r >> 2) + (r & 3);
+            if (full || mb + dm < M) base[(size_t)dm * N] = old[r] + acc[r];
+        }
+    } else {
+        float *base = part + ((size_t)z * M + mb) * N + n;
+        if (full) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) base[(size_t)(8 * (r >> 2) + (r & 3)) * N] = acc[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dm = 8 * (r >> 2) + (r & 3);
+                if (mb + dm < M) base[(size_t)dm * N] = acc[r];
+            }
+        }
+    }
+}
+
 template <int BM_, int BN_, int KS_T>
 struct WgradProblem {
     static constexpr int BM = BM_, BN = BN_, BK = WGRAD_BK;
@@ -963,6 +1023,7 @@ struct WgradProblemC {
     ConvGeom g;
     WgradDivs dv;
     int M, N, spc, nbs, splits;
+    Sgd sgd;  // the weights' SGD step in the unsplit epilogue (w == nullptr: none)
     __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
     {
         const int chunk = z / spc, j = z - chunk * spc;
@@ -986,41 +1047,10 @@ struct WgradProblemC {
         else
             part[((size_t)z * M + m) * N + n] = v;
     }
-    // One lane's 16 values of a 32x32 tile (rows mb + 8*(r/4) + r%4, column
-    // n): the base address once per tile, rows at a stride of N; dw += acc
-    // with all 16 prior values loaded before the first store, or the K
-    // slice's partial sums.  full: every row of the workgroup's tile is
-    // below M.
     __device__ __forceinline__ void store_tile(int mb, int n, const v16f &acc, int z,
                                                bool full) const
     {
-        if (n >= N) return;
-        if (splits == 1) {
-            float *base = dw + (size_t)mb * N + n;
-            float old[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dm = 8 * (r >> 2) + (r & 3);
-                old[r] = (full || mb + dm < M) ? base[(size_t)dm * N] : 0.f;
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dm = 8 * (r >> 2) + (r & 3);
-                if (full || mb + dm < M) base[(size_t)dm * N] = old[r] + acc[r];
-            }
-        } else {
-            float *base = part + ((size_t)z * M + mb) * N + n;
-            if (full) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) base[(size_t)(8 * (r >> 2) + (r & 3)) * N] = acc[r];
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int dm = 8 * (r >> 2) + (r & 3);
-                    if (mb + dm < M) base[(size_t)dm * N] = acc[r];
-                }
-            }
-        }
+        wgrad_store_tile(dw, part, sgd, M, N, splits, mb, n, acc, z, full);
     }
 };
 
@@ -1102,6 +1132,7 @@ struct FcWgradProblem {
     float *dw, *part;
     int M, N, K, kchunk, splits;
     size_t xbytes;
+    Sgd sgd;  // the weights' SGD step in the unsplit epilogue (w == nullptr: none)
     __device__ __forceinline__ void krange(int z, int &kb, int &ke) const
     {
         kb = z * kchunk;
@@ -1109,18 +1140,10 @@ struct FcWgradProblem {
     }
     __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(dy, M, K, m0, tid); }
     __device__ __forceinline__ void init_b(BLd &b, int n0, int, int) const { b.init(x, N, K, N, xbytes, n0); }
-    static constexpr bool RMW = true;
-    __device__ __forceinline__ float prior(int m, int n, int) const
+    __device__ __forceinline__ void store_tile(int mb, int n, const v16f &acc, int z,
+                                               bool full) const
     {
-        return (m < M && n < N && splits == 1) ? dw[(size_t)m * N + n] : 0.f;
-    }
-    __device__ __forceinline__ void store(int m, int n, float v, float old, int z) const
-    {
-        if (m >= M || n >= N) return;
-        if (splits == 1)
-            dw[(size_t)m * N + n] = old + v;
-        else
-            part[((size_t)z * M + m) * N + n] = v;
+        wgrad_store_tile(dw, part, sgd, M, N, splits, mb, n, acc, z, full);
     }
 };
 
@@ -1831,21 +1854,36 @@ __device__ __forceinline__ T slice_sum(const T *__restrict__ p, size_t n, size_t
 
 // Fixed-order split-K reduction: dw[i] += sum_z part[z][i], z ascending.
 // V4: four consecutive outputs per thread as float4 (mn % 4 == 0, 16-byte
-// aligned operands); the same additions in the same order.
+// aligned operands); the same additions in the same order.  With sg.w the
+// weights' SGD step (sgd_step) follows on each (w[i], dw[i]) in the same
+// pass, the values of ach_sgd_update over dw afterwards.
 template <bool V4>
 __global__ void __launch_bounds__(256) k_splitk_reduce(const float *__restrict__ part,
                                                        float *__restrict__ dw, size_t mn,
-                                                       int splits)
+                                                       int splits, Sgd sg)
 {
     typedef typename std::conditional<V4, float4, float>::type T;
     const size_t n = V4 ? mn / 4 : mn;
     const T *p = reinterpret_cast<const T *>(part);
     T *d = reinterpret_cast<T *>(dw);
+    T *w = reinterpret_cast<T *>(sg.w);
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x) {
         const T s = slice_sum(p, n, i, 0, splits);
         T o = d[i];
         addto(o, s);
+        if (w) {
+            T a = w[i];
+            if constexpr (V4) {
+                sgd_step(a.x, o.x, sg.dc, sg.lc, sg.mom);
+                sgd_step(a.y, o.y, sg.dc, sg.lc, sg.mom);
+                sgd_step(a.z, o.z, sg.dc, sg.lc, sg.mom);
+                sgd_step(a.w, o.w, sg.dc, sg.lc, sg.mom);
+            } else {
+                sgd_step(a, o, sg.dc, sg.lc, sg.mom);
+            }
+            w[i] = a;
+        }
         d[i] = o;
     }
 }
@@ -2602,9 +2640,12 @@ static int wgrad_bn(const ConvGeom &g)
     return best_bn;
 }
 
+// sgd: the weights' update for the unsplit chunked and fully connected
+// problems (their epilogue applies it); *sgd_done tells the caller
 template <int BM, int BN>
 static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, float *dw,
-                        float *part, int splits, int kchunk, hipStream_t st)
+                        float *part, int splits, int kchunk, hipStream_t st, const Sgd &sgd,
+                        bool &sgd_done)
 {
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
     WgradDivs dv;
@@ -2615,15 +2656,17 @@ static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, floa
         int spc, nbs;
         wgrad_split_chunked(g, BM, BN, splits, spc, nbs);
         if (splits > 65535) return ACH_EUNSUPPORTED;
+        const Sgd s1 = splits == 1 ? sgd : Sgd();
+        sgd_done = s1.w != nullptr;
         if (g.KS == 3) {
-            WgradProblemC<BM, BN, 3> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits};
+            WgradProblemC<BM, BN, 3> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits, s1};
             return launch_gemm(p, M, N, splits, st);
         }
         if (g.KS == 1) {
-            WgradProblemC<BM, BN, 1> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits};
+            WgradProblemC<BM, BN, 1> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits, s1};
             return launch_gemm(p, M, N, splits, st);
         }
-        WgradProblemC<BM, BN, 0> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits};
+        WgradProblemC<BM, BN, 0> p{x, dy, dw, part, g, dv, M, N, spc, nbs, splits, s1};
         return launch_gemm(p, M, N, splits, st);
     }
     if (g.KS == 3) {
@@ -2640,24 +2683,27 @@ static int wgrad_launch(const ConvGeom &g, const float *x, const float *dy, floa
 
 template <int BM>
 static int fc_wgrad_bm(const ConvGeom &g, const float *x, const float *dy, float *dw,
-                       float *part, int splits, int kchunk, hipStream_t st)
+                       float *part, int splits, int kchunk, hipStream_t st, const Sgd &sgd)
 {
     const int M = g.F, N = g.C, K = g.B;
     const size_t xb = (size_t)K * N * sizeof(float);
     if ((M & 3) == 0) {
-        FcWgradProblem<BM, true> p{x, dy, dw, part, M, N, K, kchunk, splits, xb};
+        FcWgradProblem<BM, true> p{x, dy, dw, part, M, N, K, kchunk, splits, xb, sgd};
         return launch_gemm(p, M, N, splits, st);
     }
-    FcWgradProblem<BM, false> p{x, dy, dw, part, M, N, K, kchunk, splits, xb};
+    FcWgradProblem<BM, false> p{x, dy, dw, part, M, N, K, kchunk, splits, xb, sgd};
     return launch_gemm(p, M, N, splits, st);
 }
 
 static int fc_wgrad_launch(const ConvGeom &g, const float *x, const float *dy, float *dw,
-                           float *part, int bm, int splits, int kchunk, hipStream_t st)
+                           float *part, int bm, int splits, int kchunk, hipStream_t st,
+                           const Sgd &sgd, bool &sgd_done)
 {
-    if (bm == 32) return fc_wgrad_bm<32>(g, x, dy, dw, part, splits, kchunk, st);
-    if (bm == 64) return fc_wgrad_bm<64>(g, x, dy, dw, part, splits, kchunk, st);
-    return fc_wgrad_bm<128>(g, x, dy, dw, part, splits, kchunk, st);
+    const Sgd s1 = splits == 1 ? sgd : Sgd();
+    sgd_done = s1.w != nullptr;
+    if (bm == 32) return fc_wgrad_bm<32>(g, x, dy, dw, part, splits, kchunk, st, s1);
+    if (bm == 64) return fc_wgrad_bm<64>(g, x, dy, dw, part, splits, kchunk, st, s1);
+    return fc_wgrad_bm<128>(g, x, dy, dw, part, splits, kchunk, st, s1);
 }
 
 // the small-channel input gradient: stride 1, at most 4 input channels,
@@ -2914,8 +2960,11 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)
     return (size_t)(splits + groups) * g.F * g.C * g.KS * g.KS * sizeof(float);
 }
 
-int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
-                        void *ws, size_t ws_bytes, ach_stream_t stream)
+// dw += the weight gradient; with sgd.w, then the weights' SGD step on
+// (w, dw) in the pass that finishes dw (the GEMM's unsplit epilogue or the
+// split-K reduction), else by ach_sgd_update after it
+static int bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
+                      void *ws, size_t ws_bytes, ach_stream_t stream, const Sgd &sgd)
 {
     if (!conv_ok(d) || !x || !dy || !dw) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
@@ -2928,19 +2977,26 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
     hipStream_t st = as_stream(stream);
     float *part = (float *)ws;
     int rc;
-    if (fc_geom(g)) rc = fc_wgrad_launch(g, x, dy, dw, part, bm, splits, kchunk, st);
-    else if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st);
-    else if (bn == 64) rc = wgrad_launch<128, 64>(g, x, dy, dw, part, splits, kchunk, st);
-    else if (bn == 96) rc = wgrad_launch<128, 96>(g, x, dy, dw, part, splits, kchunk, st);
-    else if (bm == 96) rc = wgrad_launch<96, 128>(g, x, dy, dw, part, splits, kchunk, st);
-    else if (bm == 32) rc = wgrad_launch<32, 128>(g, x, dy, dw, part, splits, kchunk, st);
-    else if (bm == 64) rc = wgrad_launch<64, 128>(g, x, dy, dw, part, splits, kchunk, st);
-    else rc = wgrad_launch<128, 128>(g, x, dy, dw, part, splits, kchunk, st);
-    if (rc || splits == 1) return rc;
+    bool done = false;  // the update was applied in the GEMM's epilogue
+    if (fc_geom(g)) rc = fc_wgrad_launch(g, x, dy, dw, part, bm, splits, kchunk, st, sgd, done);
+    else if (bn == 32) rc = wgrad_launch<128, 32>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    else if (bn == 64) rc = wgrad_launch<128, 64>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    else if (bn == 96) rc = wgrad_launch<128, 96>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    else if (bm == 96) rc = wgrad_launch<96, 128>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    else if (bm == 32) rc = wgrad_launch<32, 128>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    else if (bm == 64) rc = wgrad_launch<64, 128>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    else rc = wgrad_launch<128, 128>(g, x, dy, dw, part, splits, kchunk, st, sgd, done);
+    if (rc) return rc;
+    if (splits == 1) {
+        if (!sgd.w || done) return ACH_OK;
+        return ach_sgd_update((size_t)g.F * g.C * g.KS * g.KS, sgd.w, dw, sgd.dc, sgd.lc, sgd.mom,
+                              stream);
+    }
     const size_t mn = (size_t)g.F * g.C * g.KS * g.KS;
     // float4 when every slice starts 16-byte aligned (part is a workspace)
     const bool v4 = (mn & 3) == 0 && ((reinterpret_cast<uintptr_t>(part) |
-                                       reinterpret_cast<uintptr_t>(dw)) & 15) == 0;
+                                       reinterpret_cast<uintptr_t>(dw) |
+                                       reinterpret_cast<uintptr_t>(sgd.w)) & 15) == 0;
     const size_t nt = v4 ? mn / 4 : mn;  // threads' outputs
     if (splits > 2 * SPLIT_GROUP) {
         const int groups = (splits + SPLIT_GROUP - 1) / SPLIT_GROUP;
@@ -2955,19 +3011,47 @@ int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy,
         if (rc) return rc;
         if (v4)
             hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(grid_for(nt, 256)), dim3(256), 0, st,
-                               tmp, dw, mn, groups);
+                               tmp, dw, mn, groups, sgd);
         else
             hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(grid_for(nt, 256)), dim3(256), 0, st,
-                               tmp, dw, mn, groups);
+                               tmp, dw, mn, groups, sgd);
         return check_launch();
     }
     if (v4)
         hipLaunchKernelGGL(k_splitk_reduce<true>, dim3(grid_for(nt, 256)), dim3(256), 0, st, part,
-                           dw, mn, splits);
+                           dw, mn, splits, sgd);
     else
         hipLaunchKernelGGL(k_splitk_reduce<false>, dim3(grid_for(nt, 256)), dim3(256), 0, st, part,
-                           dw, mn, splits);
+                           dw, mn, splits, sgd);
     return check_launch();
+}
+
+int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
+                        void *ws, size_t ws_bytes, ach_stream_t stream)
+{
+    return bwd_filter(d, x, dy, dw, ws, ws_bytes, stream, Sgd());
+}
+
+int ach_conv_bwd_filter_sgd(const ach_conv_desc *d, const float *x, const float *dy, float *w,
+                            float *dw, float decay_coef, float lr_coef, float momentum, void *ws,
+                            size_t ws_bytes, ach_stream_t stream)
+{
+    if (!w) return ACH_EINVAL;
+    Sgd sgd;
+    sgd.w = w;
+    sgd.dc = decay_coef;
+    sgd.lc = lr_coef;
+    sgd.mom = momentum;
+    return bwd_filter(d, x, dy, dw, ws, ws_bytes, stream, sgd);
+}
+
+int ach_conv_bwd_data_reads_w(const ach_conv_desc *d)
+{
+    if (!conv_ok(d)) return 1;
+    const ConvGeom g = geom(d);
+    // ach_conv_bwd_data_prepared reads wft only for the GEMM path of a
+    // stride-1 layer whose filter is wider than 1x1
+    return !(g.S == 1 && g.P <= g.KS - 1 && g.KS > 1 && !fc_geom(g) && !dgrad_small_c(g));
 }
 
 int ach_gemm(int TA, int TB, int M, int N, int K, float ALPHA, const float *A, int lda,

@@ -873,9 +873,7 @@ __global__ void k_dropout(float *x, size_t n, float p, float scale, uint64_t see
 // v += decay_coef*w; w += lr_coef*v; v *= momentum  (WeightData.c:45-78)
 __device__ __forceinline__ void sgd1(float &a, float &u, float dc, float lc, float mom)
 {
-    u += dc * a;
-    a += lc * u;
-    u *= mom;
+    sgd_step(a, u, dc, lc, mom);
 }
 
 __global__ void k_sgd(size_t n, float *__restrict__ w, float *__restrict__ v, float dc,

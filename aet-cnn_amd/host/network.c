@@ -236,6 +236,19 @@ static int output_masked_unreverted(const an_network *net, const an_layer *l)
     return d->type == AN_DROPOUT && d->shares_prev && d->onlyforward;
 }
 
+/* ConvolutionalLayer.backward's input gradient into state.delta
+ * (ConvolutionalLayer.c:931-945): the GEMM path for stride 1, the
+ * reference's per-image GEMM + col2im otherwise                          */
+static int conv_input_gradient(const an_layer *l, const ach_conv_desc *d, an_state st,
+                               ach_stream_t s)
+{
+    return l->stride == 1
+               ? ach_conv_bwd_data_prepared(d, l->delta, l->weights, l->weights_flipped, st.delta,
+                                            st.workspace, st.workspace_bytes, s)
+               : ach_conv_bwd_data(d, l->delta, l->weights, st.delta, st.workspace,
+                                   st.workspace_bytes, s);
+}
+
 static int conv_backward(an_network *net, an_layer *l, an_state st)
 {
     ach_conv_desc d = conv_desc(l);
@@ -285,30 +298,35 @@ static int conv_backward(an_network *net, an_layer *l, an_state st)
         AN_CHECK(ach_bias_grad(l->bias_updates, l->delta, l->batch, l->n, spatial, gws,
                                gws_bytes, gs));
     }
+    const int ub = net->batch * net->subdivisions;
+    if (net->early_update) {
+        /* The layer's SGD update (ConvolutionalLayer.update, the per-layer
+         * step of NNetwork.updateCPU) as soon as nothing else reads its
+         * parameters: the weights' step rides on the pass that finishes
+         * the weight gradient (ach_conv_bwd_filter_sgd), after the input
+         * gradient when that reads W (otherwise it reads the flipped copy
+         * made at the forward); biases and scales follow on the same
+         * stream.  The same arithmetic as an_update; it overlaps the
+         * backward of the layers below instead of ending the step
+         * (AlexNet's FC weights are 94% of its parameters).               */
+        const int reads_w = st.delta && ach_conv_bwd_data_reads_w(&d);
+        if (reads_w) {
+            AN_CHECK(conv_input_gradient(l, &d, st, s));
+            AN_CHECK(ach_event_record(net->ev_dgrad[l->index], s));
+            AN_CHECK(ach_stream_wait_event(gs, net->ev_dgrad[l->index]));
+        }
+        AN_CHECK(ach_conv_bwd_filter_sgd(&d, st.input, l->delta, l->weights, l->weight_updates,
+                                         -net->decay * ub, net->early_rate / ub, net->momentum,
+                                         gws, gws_bytes, gs));
+        if (st.delta && !reads_w) AN_CHECK(conv_input_gradient(l, &d, st, s));
+        return ach_conv_update(0, NULL, NULL, (size_t)l->n, l->biases, l->bias_updates,
+                               l->scales, l->scale_updates, ub, net->early_rate, net->momentum,
+                               net->decay, gs);
+    }
     AN_CHECK(ach_conv_bwd_filter(&d, st.input, l->delta, l->weight_updates, gws, gws_bytes,
                                  gs));
-    if (st.delta)
-        AN_CHECK(l->stride == 1
-                     ? ach_conv_bwd_data_prepared(&d, l->delta, l->weights, l->weights_flipped,
-                                                  st.delta, st.workspace, st.workspace_bytes, s)
-                     : ach_conv_bwd_data(&d, l->delta, l->weights, st.delta, st.workspace,
-                                         st.workspace_bytes, s));
-    if (!net->early_update) return ACH_OK;
-    /* The layer's SGD update (ConvolutionalLayer.update, the per-layer step
-     * of NNetwork.updateCPU) as soon as nothing else reads its parameters:
-     * after its gradients (stream gs) and, on the other stream, after its
-     * input gradient, which reads W (or, for stride 1 and k > 1, the
-     * flipped copy made at the forward).  The same arithmetic as an_update;
-     * it overlaps the backward of the layers below instead of ending the
-     * step (AlexNet's FC weights are 94% of its parameters).               */
-    if (gs != s) {
-        AN_CHECK(ach_event_record(net->ev_dgrad[l->index], s));
-        AN_CHECK(ach_stream_wait_event(gs, net->ev_dgrad[l->index]));
-    }
-    return ach_conv_update((size_t)l->nweights, l->weights, l->weight_updates, (size_t)l->n,
-                           l->biases, l->bias_updates, l->scales, l->scale_updates,
-                           net->batch * net->subdivisions, net->early_rate, net->momentum,
-                           net->decay, gs);
+    if (st.delta) AN_CHECK(conv_input_gradient(l, &d, st, s));
+    return ACH_OK;
 }
 
 /* per-layer update for callers that drive layers one by one; an_update

@@ -114,6 +114,21 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
 size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d);
 int ach_conv_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
                         void *ws, size_t ws_bytes, ach_stream_t stream);
+/* ach_conv_bwd_filter, then the weights' step of ConvolutionalLayer.update
+ * (ConvolutionalLayer.c:959-980) on (w, dw): dw += decay_coef*w;
+ * w += lr_coef*dw; dw *= momentum -- the results of ach_conv_bwd_filter
+ * followed by ach_sgd_update(F*C*k*k, w, dw, ...), bit for bit, with the
+ * update done in the pass that finishes dw (no pass of its own).  The
+ * caller orders it after every reader of w: ach_conv_bwd_data_reads_w(d)
+ * tells whether this layer's _prepared input gradient is one.  Same
+ * workspace as ach_conv_bwd_filter.                                       */
+int ach_conv_bwd_filter_sgd(const ach_conv_desc *d, const float *x, const float *dy, float *w,
+                            float *dw, float decay_coef, float lr_coef, float momentum, void *ws,
+                            size_t ws_bytes, ach_stream_t stream);
+/* 1 if ach_conv_bwd_data_prepared (or ach_conv_bwd_data) reads w, 0 if it
+ * reads only the flipped copy wft (stride 1, filters wider than 1x1, more
+ * than 4 input channels)                                                   */
+int ach_conv_bwd_data_reads_w(const ach_conv_desc *d);
 
 /* ---- prepared filters -------------------------------------------------------
  * The conv GEMMs read the filter k-major (Wt[C*k*k][n]) and, for the stride-1

@@ -162,6 +162,31 @@ def test_conv_bwd_data(gpu, oracle, shape):
     assert rel_err(ddx.numpy(), ref) < TOL
 
 
+@pytest.mark.parametrize("shape", CONV_SHAPES + [(2, 3, 227, 227, 96, 11, 4, 0)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_conv_bwd_filter_sgd(gpu, shape):
+    """ach_conv_bwd_filter_sgd == ach_conv_bwd_filter + ach_sgd_update over
+    the weights, bit for bit, whether the update runs in the unsplit GEMM's
+    epilogue, the split-K reduction (one or two levels) or a pass of its own
+    (ConvolutionalLayer.c:913-929, 959-980)."""
+    B, Cc, H, W, F, k, s, p = shape
+    x, w, dy = _conv_inputs(shape, 41)
+    rng = np.random.default_rng(42)
+    dw0 = (rng.standard_normal(w.shape) * 0.1).astype(np.float32)
+    d = conv_desc(*shape)
+    ws = gpu.ach_conv_bwd_filter_workspace(C.byref(d))
+    dws = D(max(ws, 4) // 4)
+    dc, lc, mom = np.float32(-5e-4 * B), np.float32(0.01 / B), np.float32(0.9)
+    dx_, ddy = dev(x), dev(dy)
+    wa, dwa, wb, dwb = dev(w), dev(dw0), dev(w), dev(dw0)
+    check(gpu.ach_conv_bwd_filter(C.byref(d), dx_.ptr, ddy.ptr, dwa.ptr, dws.ptr, ws, None))
+    check(gpu.ach_sgd_update(w.size, wa.ptr, dwa.ptr, dc, lc, mom, None))
+    check(gpu.ach_conv_bwd_filter_sgd(C.byref(d), dx_.ptr, ddy.ptr, wb.ptr, dwb.ptr, dc, lc, mom,
+                                      dws.ptr, ws, None))
+    assert np.array_equal(wa.numpy().view(np.uint32), wb.numpy().view(np.uint32)), shape
+    assert np.array_equal(dwa.numpy().view(np.uint32), dwb.numpy().view(np.uint32)), shape
+
+
 @pytest.mark.parametrize("shape", CONV_SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_conv_bwd_filter(gpu, oracle, shape):
     B, Cc, H, W, F, k, s, p = shape
