@@ -149,9 +149,9 @@ _OPS = {
     "ach_maxpool_bwd_act_planes": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp,
                                         _vp]),
     "ach_maxpool_fwd_dropout": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _f, _u64, _u32,
-                                     _vp, _u32, _vp]),
+                                     _u32, _vp]),
     "ach_maxpool_bwd_dropout": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _u64,
-                                     _u32, _vp, _u32, _vp]),
+                                     _u32, _u32, _vp]),
     "ach_avgpool_fwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "ach_avgpool_bwd": (_i, [_vp, _i, _i, _i, _vp, _vp]),
     "ach_softmax_workspace": (_sz, [_i, _i]),
@@ -159,14 +159,7 @@ _OPS = {
     "ach_dropout_uniform": (_f, [_u64, _u32, _u32, _u32]),
     "ach_dropout_fwd": (_i, [_vp, _sz, _f, _u64, _u32, _u32, _vp]),
     "ach_dropout_bwd": (_i, [_vp, _sz, _f, _u64, _u32, _u32, _vp]),
-    "ach_dropout_fwd_dev": (_i, [_vp, _sz, _f, _u64, _vp, _u32, _vp]),
-    "ach_dropout_bwd_dev": (_i, [_vp, _sz, _f, _u64, _vp, _u32, _vp]),
-    "ach_counter_add": (_i, [_vp, _u32, _vp]),
     "ach_nan_scan": (_i, [_vp, _i, _vp, _vp]),
-    "ach_graph_capture_begin": (_i, [_vp]),
-    "ach_graph_capture_end": (_i, [_vp, C.POINTER(_vp)]),
-    "ach_graph_launch": (_i, [_vp, _vp]),
-    "ach_graph_destroy": (_i, [_vp]),
     "ach_conv_update": (_i, [_sz, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _i, _f, _f, _f, _vp]),
     "ach_sgd_update": (_i, [_sz, _vp, _vp, _f, _f, _f, _vp]),
 }
@@ -198,7 +191,6 @@ _NET = {
     "an_set_input": (_i, [_vp, _vp, _vp]),
     "an_set_input_device": (_i, [_vp, _vp, _vp]),
     "an_train_step": (_i, [_vp]),
-    "an_set_graph": (_i, [_vp, _i]),
     "an_get_loss": (_i, [_vp, C.POINTER(_f)]),
     "an_nan_status": (_i, [_vp, C.POINTER(_i), C.POINTER(_i)]),
     "an_train": (_i, [_vp, _vp, _vp, C.POINTER(_f)]),
@@ -479,11 +471,6 @@ class Network:
 
     def train_step(self):
         check(self.lib.an_train_step(self.h), "an_train_step")
-
-    def set_graph(self, on=True):
-        """Replay the training step from a recorded HIP graph (same results
-        as eager steps); hyper/seed/weight-load/fuse changes re-record it."""
-        check(self.lib.an_set_graph(self.h, 1 if on else 0), "an_set_graph")
 
     def predict(self, x: np.ndarray) -> np.ndarray:
         """NNetwork.predict: inference forward, returns [batch][classes]"""

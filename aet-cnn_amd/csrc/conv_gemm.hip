@@ -46,18 +46,12 @@ constexpr int LDP = 4;       // LDS row padding (floats)
 // pair sits a whole number of 64-float units from one base and one
 // ds_read2st64 reads it without address arithmetic.  Their stores write whole
 // 64-lane row segments (no conflicts).
-#ifndef ACH_LDP_FWD
-#define ACH_LDP_FWD 0
-#endif
-constexpr int LDP_FWD = ACH_LDP_FWD;
+constexpr int LDP_FWD = 0;
 constexpr unsigned kOOB = 0x80000000u;  // buffer offset that reads as 0
-#ifndef ACH_WGRAD_BK
-#define ACH_WGRAD_BK 16
-#endif
-constexpr int WGRAD_BK = ACH_WGRAD_BK;  // k-tile of the weight-gradient GEMM
-#ifndef ACH_WGRAD_TARGET
-#define ACH_WGRAD_TARGET 2048  // weight-gradient workgroups aimed for (tiles x splits)
-#endif
+constexpr int WGRAD_BK = 16;            // k-tile of the weight-gradient GEMM
+// weight-gradient workgroups aimed for (tiles x splits) in the (image,
+// position) K order
+constexpr int WGRAD_TARGET = 2048;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p, unsigned bytes)
 {
@@ -297,11 +291,8 @@ struct AWeightsT4F : AWeightsT4<BM, BK> {
 // per k-tile): thread -> column n = n0 + tid%128 and channel group
 // kr = tid/128 (channels kr*CH/2 .. +CH/2-1 of the tile); the 9 rows of a
 // channel are (ki, kj) = (i/3, i%3), i = 0..8, all compile-time.
-#ifndef ACH_FWD_CH
-#define ACH_FWD_CH 2
-#endif
 struct BIm2col3 {
-    static constexpr int CH = ACH_FWD_CH, HC = CH / 2;
+    static constexpr int CH = 2, HC = CH / 2;
     static_assert(CH % 2 == 0, "channel groups split over two thread halves");
     static constexpr int BK = 9 * CH, RB = 9 * HC, PAD = LDP_FWD;
     __amdgpu_buffer_rsrc_t rs;
@@ -2514,21 +2505,16 @@ static int fwd_impl(const ConvGeom &g, const float *x, const float *w, float *y,
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Split count of the weight gradient in the (image, position) K order: aim
-// for ~ACH_WGRAD_TARGET workgroups, K chunks a multiple of the k-tile.
-#ifndef ACH_WGRAD_CHUNKED
-#define ACH_WGRAD_CHUNKED 1
-#endif
-#ifndef ACH_WGRAD_PAD_WASTE
-#define ACH_WGRAD_PAD_WASTE 0.0625  // largest padded fraction of a plane taken
-#endif
-// the chunked K order applies when padding the output plane to whole
-// 16-position chunks wastes at most ACH_WGRAD_PAD_WASTE of the work
+// The chunked K order of the weight gradient applies when padding the
+// output plane to whole 16-position chunks wastes at most WGRAD_PAD_WASTE of
+// the work; otherwise the (image, position) order splits K to aim at
+// ~WGRAD_TARGET workgroups, K chunks a multiple of the k-tile.
+constexpr double WGRAD_PAD_WASTE = 0.0625;
 static int wgrad_nchunks(const ConvGeom &g) { return (g.OH * g.OW + 15) / 16; }
 static bool wgrad_chunked(const ConvGeom &g)
 {
     const int ohw = g.OH * g.OW;
-    return ACH_WGRAD_CHUNKED && wgrad_nchunks(g) * 16 - ohw <= ACH_WGRAD_PAD_WASTE * ohw;
+    return wgrad_nchunks(g) * 16 - ohw <= WGRAD_PAD_WASTE * ohw;
 }
 
 // Cost model of the weight-gradient GEMM plus its split-K reduction, in CU
@@ -2586,7 +2572,7 @@ static void wgrad_split(const ConvGeom &g, int bm, int bn, int &splits, int &kch
     const int M = g.F, N = g.C * g.KS * g.KS, K = g.B * g.OH * g.OW;
     const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int bk = WGRAD_BK;
-    int s = (ACH_WGRAD_TARGET + tiles - 1) / tiles;
+    int s = (WGRAD_TARGET + tiles - 1) / tiles;
     const int max_s = (K + 4 * bk - 1) / (4 * bk);  // >= 4 k-tiles per split
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;

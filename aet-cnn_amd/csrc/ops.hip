@@ -455,22 +455,20 @@ __device__ __forceinline__ void max4(float a, float b, float c, float d, int ia,
 // (DropoutLayer.c:55-86, NetworkFactory.c:644-650) can run inside the pool
 // kernels: the forward writes r < p ? 0 : v * scale for pooled element e,
 // the backward applies the same mask to the output gradient it reads
-// (r = dropout_uniform(seed, iter, layer, e), iter from device memory when
-// iter_ptr is set) -- the values k_dropout would leave, bit for bit.
+// (r = dropout_uniform(seed, iter, layer, e)) -- the values k_dropout would
+// leave, bit for bit.
 struct DropIn {
     float p, scale;
     uint64_t seed;
-    uint32_t iter0;
-    const uint32_t *iter_ptr;
+    uint32_t iter;
     uint32_t layer;
     int on;
     __device__ __forceinline__ float2 apply(float2 v, unsigned t) const
     {
         if (!on) return v;
-        const uint32_t it = iter_ptr ? *iter_ptr : iter0;
         const uint32_t e = 2u * t;
-        const float r0 = dropout_uniform(seed, it, layer, e);
-        const float r1 = dropout_uniform(seed, it, layer, e + 1);
+        const float r0 = dropout_uniform(seed, iter, layer, e);
+        const float r1 = dropout_uniform(seed, iter, layer, e + 1);
         v.x = (r0 < p) ? 0.f : v.x * scale;
         v.y = (r1 < p) ? 0.f : v.y * scale;
         return v;
@@ -837,17 +835,9 @@ __device__ __forceinline__ float drop1(float v, float r, float p, float scale)
     return (r < p) ? 0.f : v * scale;
 }
 
-// counter += v (a device-side step index advanced inside a replayed graph)
-__global__ void k_counter_add(uint32_t *counter, uint32_t v)
-{
-    if (threadIdx.x == 0) counter[0] += v;
-}
-
 __global__ void k_dropout(float *x, size_t n, float p, float scale, uint64_t seed,
-                          uint32_t iter0, const uint32_t *__restrict__ iter_ptr, uint32_t layer)
+                          uint32_t iter, uint32_t layer)
 {
-    // the step index comes from device memory when a replayed graph supplies it
-    const uint32_t iter = iter_ptr ? *iter_ptr : iter0;
     const size_t gid = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     size_t done = 0;
@@ -1158,7 +1148,7 @@ static bool pool2_fast(const void *a, const void *b, int h, int w, int size, int
 }
 
 static int dropout_launch(float *x, size_t n, float p, uint64_t seed, uint32_t iter,
-                          const uint32_t *iter_ptr, uint32_t layer, ach_stream_t s);
+                          uint32_t layer, ach_stream_t s);
 
 // dr.on: the following dropout runs in the 2x2 kernel, or after the pool
 // on the other paths
@@ -1179,8 +1169,8 @@ static int maxpool_fwd(const float *in, int batch, int c, int h, int w, int size
         none.on = 0;
         const int rc = maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, none, s);
         if (rc) return rc;
-        return dropout_launch(out, (size_t)batch * c * OH * OW, dr.p, dr.seed, dr.iter0,
-                              dr.iter_ptr, dr.layer, s);
+        return dropout_launch(out, (size_t)batch * c * OH * OW, dr.p, dr.seed, dr.iter,
+                              dr.layer, s);
     }
     const int total = batch * c * OH * OW;
     const dim3 grid((total + 255) / 256);
@@ -1224,11 +1214,10 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
 
 int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w, int size,
                             int stride, int pad, float *out, int32_t *idx, float probability,
-                            uint64_t seed, uint32_t iter, const uint32_t *iter_ptr,
-                            uint32_t layer, ach_stream_t s)
+                            uint64_t seed, uint32_t iter, uint32_t layer, ach_stream_t s)
 {
     if (!(probability >= 0.f && probability < 1.f)) return ACH_EINVAL;
-    const DropIn dr{probability, (float)(1. / (1.0 - probability)), seed, iter, iter_ptr, layer, 1};
+    const DropIn dr{probability, (float)(1. / (1.0 - probability)), seed, iter, layer, 1};
     return maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, dr, s);
 }
 
@@ -1260,7 +1249,7 @@ static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, 
                        (reinterpret_cast<uintptr_t>(gi.y) & 15) == 0;
     if (dr.on && !fast2) {  // the dropout backward in place on dout first
         const int rc = dropout_launch(const_cast<float *>(dout), (size_t)batch * c * OH * OW,
-                                      dr.p, dr.seed, dr.iter0, dr.iter_ptr, dr.layer, s);
+                                      dr.p, dr.seed, dr.iter, dr.layer, s);
         if (rc) return rc;
         dr.on = 0;
     }
@@ -1315,10 +1304,10 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
 int ach_maxpool_bwd_dropout(float *dout, const int32_t *idx, int batch, int c, int h, int w,
                             int size, int stride, int pad, float *din, int accumulate,
                             float probability, uint64_t seed, uint32_t iter,
-                            const uint32_t *iter_ptr, uint32_t layer, ach_stream_t s)
+                            uint32_t layer, ach_stream_t s)
 {
     if (!(probability >= 0.f && probability < 1.f)) return ACH_EINVAL;
-    const DropIn dr{probability, (float)(1. / (1.0 - probability)), seed, iter, iter_ptr, layer, 1};
+    const DropIn dr{probability, (float)(1. / (1.0 - probability)), seed, iter, layer, 1};
     return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
                        GradIn{nullptr, 0}, dr, s);
 }
@@ -1419,47 +1408,26 @@ float ach_dropout_uniform(uint64_t seed, uint32_t iter, uint32_t layer, uint32_t
 }
 
 static int dropout_launch(float *x, size_t n, float p, uint64_t seed, uint32_t iter,
-                          const uint32_t *iter_ptr, uint32_t layer, ach_stream_t s)
+                          uint32_t layer, ach_stream_t s)
 {
     if (n == 0) return ACH_OK;
     if (!x || !(p >= 0.f && p < 1.f) || n > 0xffffffffull) return ACH_EINVAL;
     const float scale = (float)(1. / (1.0 - p));
     hipLaunchKernelGGL(k_dropout, dim3(grid_stream(n)), dim3(256), 0, as_stream(s), x, n, p,
-                       scale, seed, iter, iter_ptr, layer);
+                       scale, seed, iter, layer);
     return check_launch();
 }
 
 int ach_dropout_fwd(float *x, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
                     ach_stream_t s)
 {
-    return dropout_launch(x, n, p, seed, iter, nullptr, layer, s);
+    return dropout_launch(x, n, p, seed, iter, layer, s);
 }
 
 int ach_dropout_bwd(float *d, size_t n, float p, uint64_t seed, uint32_t iter, uint32_t layer,
                     ach_stream_t s)
 {
-    return dropout_launch(d, n, p, seed, iter, nullptr, layer, s);
-}
-
-int ach_dropout_fwd_dev(float *x, size_t n, float p, uint64_t seed, const uint32_t *iter,
-                        uint32_t layer, ach_stream_t s)
-{
-    if (!iter) return ACH_EINVAL;
-    return dropout_launch(x, n, p, seed, 0, iter, layer, s);
-}
-
-int ach_dropout_bwd_dev(float *d, size_t n, float p, uint64_t seed, const uint32_t *iter,
-                        uint32_t layer, ach_stream_t s)
-{
-    if (!iter) return ACH_EINVAL;
-    return dropout_launch(d, n, p, seed, 0, iter, layer, s);
-}
-
-int ach_counter_add(uint32_t *counter, uint32_t v, ach_stream_t s)
-{
-    if (!counter) return ACH_EINVAL;
-    hipLaunchKernelGGL(k_counter_add, dim3(1), dim3(64), 0, as_stream(s), counter, v);
-    return check_launch();
+    return dropout_launch(d, n, p, seed, iter, layer, s);
 }
 
 // ---- NaN scan: one workgroup per listed array ------------------------------
@@ -1482,38 +1450,6 @@ int ach_nan_scan(const ach_nan_span *spans, int nspans, int32_t *flag, ach_strea
     const int grid = nspans < 1024 ? nspans : 1024;
     hipLaunchKernelGGL(k_nan_scan, dim3(grid), dim3(256), 0, as_stream(s), spans, nspans, flag);
     return check_launch();
-}
-
-// ---- HIP graphs: record a stream's work once, replay it -----------------
-int ach_graph_capture_begin(ach_stream_t s)
-{
-    return check(hipStreamBeginCapture(as_stream(s), hipStreamCaptureModeThreadLocal));
-}
-
-int ach_graph_capture_end(ach_stream_t s, void **exec)
-{
-    if (!exec) return ACH_EINVAL;
-    *exec = nullptr;
-    hipGraph_t g = nullptr;
-    int rc = check(hipStreamEndCapture(as_stream(s), &g));
-    if (rc) return rc;
-    hipGraphExec_t e = nullptr;
-    rc = check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
-    (void)hipGraphDestroy(g);
-    if (rc) return rc;
-    *exec = (void *)e;
-    return ACH_OK;
-}
-
-int ach_graph_launch(void *exec, ach_stream_t s)
-{
-    if (!exec) return ACH_EINVAL;
-    return check(hipGraphLaunch((hipGraphExec_t)exec, as_stream(s)));
-}
-
-int ach_graph_destroy(void *exec)
-{
-    return exec ? check(hipGraphExecDestroy((hipGraphExec_t)exec)) : ACH_OK;
 }
 
 int ach_sgd_update(size_t n, float *w, float *v, float dc, float lc, float mom, ach_stream_t s)

@@ -75,13 +75,6 @@ struct an_network {
     int njobs;
     float *zero_region;            /* deltas that need zeroing per forward */
     size_t zero_floats;
-    /* graph replay of the training step (an_set_graph): the recorded step,
-     * and the device copy of cur_iteration its dropout kernels read and its
-     * last kernel advances                                                  */
-    int graph_on, recording;
-    void *graph_exec;
-    float graph_rate;              /* the learning rate recorded in it      */
-    uint32_t *d_iter;
     /* host copies of initial parameters until finalize */
     float **init_w;
     /* some layer sets stopbackward / onlyforward / a learning-rate scale, or
@@ -507,15 +500,10 @@ int an_add_avgpool(an_network *net)
 /* ======================================================================== */
 /* Dropout: DropoutLayer.c:55-86; shares the previous layer's output and
  * delta (NetworkFactory.c:644-650).                                        */
-/* In a recorded step the step index comes from the device copy
- * (net->d_iter), so every replay of it draws its own masks.               */
 static int dropout_forward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.train) return ACH_OK;
     const size_t n = (size_t)l->batch * l->inputs;
-    if (net->recording)
-        return ach_dropout_fwd_dev((float *)st.input, n, l->probability, net->dropout_seed,
-                                   net->d_iter, (uint32_t)l->index, net->stream);
     return ach_dropout_fwd((float *)st.input, n, l->probability, net->dropout_seed,
                            net->dropout_step, (uint32_t)l->index, net->stream);
 }
@@ -524,9 +512,6 @@ static int dropout_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
     const size_t n = (size_t)l->batch * l->inputs;
-    if (net->recording)
-        return ach_dropout_bwd_dev(st.delta, n, l->probability, net->dropout_seed, net->d_iter,
-                                   (uint32_t)l->index, net->stream);
     return ach_dropout_bwd(st.delta, n, l->probability, net->dropout_seed,
                            net->dropout_step, (uint32_t)l->index, net->stream);
 }
@@ -584,28 +569,16 @@ int an_add_softmax(an_network *net, int groups, float temperature)
     return net->n++;
 }
 
-/* a recorded step holds the hyper-parameters, the dropout seed and the
- * layer functions as they were: any change drops it (re-recorded lazily) */
-static void drop_graph(an_network *net)
-{
-    if (net->graph_exec) {
-        ach_graph_destroy(net->graph_exec);
-        net->graph_exec = NULL;
-    }
-}
-
 void an_set_hyper(an_network *net, float learning_rate, float momentum, float decay)
 {
     net->learning_rate = learning_rate;
     net->momentum = momentum;
     net->decay = decay;
-    drop_graph(net);
 }
 
 void an_set_dropout_seed(an_network *net, uint64_t seed)
 {
     net->dropout_seed = seed;
-    drop_graph(net);
 }
 
 int an_set_policy(an_network *net, int policy, int burn_in, float power, float gamma,
@@ -641,7 +614,6 @@ int an_set_policy(an_network *net, int policy, int burn_in, float power, float g
     net->scale = scale;
     net->step = step;
     net->max_batches = max_batches;
-    drop_graph(net);
     return ACH_OK;
 }
 
@@ -649,7 +621,6 @@ int an_set_subdivisions(an_network *net, int subdivisions)
 {
     if (!net || subdivisions < 1) return ACH_EINVAL;
     net->subdivisions = subdivisions;
-    drop_graph(net);
     return ACH_OK;
 }
 
@@ -681,14 +652,6 @@ float an_rate(an_network *net, uint64_t batch_num64)
         return lr * (1. / (1. + exp(net->gamma * (float)(batch_num - (size_t)net->step))));
     default: return lr;
     }
-}
-
-int an_set_graph(an_network *net, int on)
-{
-    if (!net) return ACH_EINVAL;
-    if (!on) drop_graph(net);
-    net->graph_on = on ? 1 : 0;
-    return ACH_OK;
 }
 
 /* ======================================================================== */
@@ -795,7 +758,6 @@ static void layout(an_network *net, bump *b)
     }
     net->wgrad_ws_bytes = wws;
     net->wgrad_ws = (float *)take(b, wws ? wws : 256);
-    net->d_iter = (uint32_t *)take(b, sizeof(uint32_t));
 }
 
 int an_set_layer_options(an_network *net, int layer, const an_layer_options *opt)
@@ -1015,7 +977,6 @@ void an_free(an_network *net)
     free(net->jobs);
     if (net->wstream) ach_stream_sync(net->wstream);
     if (net->stream) ach_stream_sync(net->stream);
-    drop_graph(net);
     free(net->steps);
     free(net->scales);
     if (net->ev_ready) {
@@ -1221,7 +1182,6 @@ int an_predict(an_network *net, const float *host_input, float *host_output)
 int an_fuse_conv_batchnorm(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
-    drop_graph(net);
     for (int i = 0; i < net->n; ++i) {
         an_layer *l = net->layers[i];
         if (l->type != AN_CONVOLUTIONAL || !l->batch_normalize) continue;
@@ -1250,8 +1210,8 @@ void an_top_k(const float *a, int n, int k, int *index)
     }
 }
 
-/* the kernels of one training step: forward, both backward streams, update
- * and, in graph mode, the device step index advanced                       */
+/* the kernels of one training step: forward, both backward streams and
+ * the update                                                               */
 static int enqueue_step(an_network *net, int update, float rate)
 {
     AN_CHECK(an_forward(net, 1));
@@ -1264,32 +1224,7 @@ static int enqueue_step(an_network *net, int update, float rate)
     net->early_update = 0;
     AN_CHECK(rc);
     if (update && net->layer_opts) AN_CHECK(update_at_rate(net, rate));
-    AN_CHECK(ach_nan_scan(net->d_nan_spans, net->n_nan_spans, net->d_nan_flag, net->stream));
-    return net->recording ? ach_counter_add(net->d_iter, 1u, net->stream) : ACH_OK;
-}
-
-/* Graph mode records enqueue_step once (after copying cur_iteration to the
- * device) and replays it; every replay is the same kernel sequence with the
- * same arguments, reading the current input, weights and step index.      */
-static int train_step_graph(an_network *net, float rate)
-{
-    if (net->graph_exec && rate != net->graph_rate) drop_graph(net);
-    if (!net->graph_exec) {
-        AN_CHECK(ach_memcpy_h2d(net->d_iter, &net->dropout_step, sizeof(uint32_t), net->stream));
-        AN_CHECK(ach_graph_capture_begin(net->stream));
-        net->recording = 1;
-        const int rc = enqueue_step(net, 1, rate);
-        net->recording = 0;
-        void *exec = NULL;
-        const int rc2 = ach_graph_capture_end(net->stream, &exec);
-        if (rc || rc2) {
-            ach_graph_destroy(exec);
-            return rc ? rc : rc2;
-        }
-        net->graph_exec = exec;
-        net->graph_rate = rate;
-    }
-    return ach_graph_launch(net->graph_exec, net->stream);
+    return ach_nan_scan(net->d_nan_spans, net->n_nan_spans, net->d_nan_flag, net->stream);
 }
 
 /* One minibatch of NNetwork.train(ImageData) (NNetwork.c:762-805, with
@@ -1299,12 +1234,11 @@ static int train_step_graph(an_network *net, float rate)
 int an_train_step(an_network *net)
 {
     if (!net || !net->finalized) return ACH_EINVAL;
-    if (net->graph_on && net->subdivisions != 1) return ACH_EINVAL;
     net->dropout_step = (uint32_t)(net->seen / (uint64_t)net->batch);
     net->seen += (uint64_t)net->batch;
     const int update = (net->seen / (uint64_t)net->batch) % (uint64_t)net->subdivisions == 0;
     const float rate = update ? an_current_rate(net) : 0.f;
-    AN_CHECK(net->graph_on ? train_step_graph(net, rate) : enqueue_step(net, update, rate));
+    AN_CHECK(enqueue_step(net, update, rate));
     if (update) net->cur_iteration += 1;
     return ACH_OK;
 }
@@ -1551,7 +1485,6 @@ int an_load_weights(an_network *net, const char *path)
     }
     const int transpose = hdr[0] > 1000 || hdr[1] > 1000;
     net->cur_iteration = (int)(net->seen / ((uint64_t)net->batch * net->subdivisions));
-    drop_graph(net); /* the recorded step's device step index is stale */
     int rc = ACH_OK;
     float *host = NULL;
     size_t host_cap = 0;

@@ -351,18 +351,6 @@ int an_set_input_device(an_network *net, const float *dev_input, const float *de
  * stays on the device until an_get_loss.  Dropout masks use the index
  * seen/batch of the minibatch (before the increment) as their step.       */
 int an_train_step(an_network *net);
-/* Graph replay of an_train_step; no counterpart in the reference (its
- * training loop calls the layers one by one, NNetwork.c:740-805).  For
- * callers whose step is launch-bound (small batches, small images).  With
- * on != 0 the next an_train_step records the step's kernels (both streams)
- * into a HIP graph and every step replays it: the same kernels and
- * arguments, reading the current input, truth and weights, and a device
- * copy of the iteration for the dropout masks, so results are the same as
- * eager steps.  an_set_hyper, an_set_dropout_seed, an_set_policy,
- * an_set_subdivisions, an_load_weights, an_fuse_conv_batchnorm and
- * on == 0 drop the recording; a step whose learning rate differs from the
- * recorded one re-records it.  Needs subdivisions == 1 (ACH_EINVAL).      */
-int an_set_graph(an_network *net, int on);
 /* synchronises and returns sum(cost)/batch of the last minibatch (the
  * reference returns the mean of these over the subdivisions, NNetwork.c:804).
  * Returns ACH_ENAN, with a message on stderr, where the reference's CPU path

@@ -296,20 +296,18 @@ int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
  * the forward writes the masked output (ach_maxpool_fwd + ach_dropout_fwd on
  * out), the backward masks delta_out as it reads it (ach_dropout_bwd on
  * delta_out + ach_maxpool_bwd; delta_out itself may be left unmasked) --
- * the same values bit for bit.  iter_ptr, when set, supplies the step index
- * from device memory (as ach_dropout_fwd_dev).  Fused into the 2x2 / stride
+ * the same values bit for bit.  Fused into the 2x2 / stride
  * 2 kernels; other windows run the two steps inside the call.  (The network
  * loops of aetcnn_net.h run pool and dropout as separate layers, as the
  * reference does, so the shared delta is masked in place.)                */
 int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w,
                             int size, int stride, int padding, float *out, int32_t *indexes,
-                            float probability, uint64_t seed, uint32_t iter,
-                            const uint32_t *iter_ptr, uint32_t layer, ach_stream_t stream);
+                            float probability, uint64_t seed, uint32_t iter, uint32_t layer,
+                            ach_stream_t stream);
 int ach_maxpool_bwd_dropout(float *delta_out, const int32_t *indexes,
                             int batch, int c, int h, int w, int size, int stride, int padding,
                             float *delta_in, int accumulate, float probability, uint64_t seed,
-                            uint32_t iter, const uint32_t *iter_ptr, uint32_t layer,
-                            ach_stream_t stream);
+                            uint32_t iter, uint32_t layer, ach_stream_t stream);
 /* ach_maxpool_bwd, then delta_in *= f'(y_in) with the previous layer's
  * output y_in and activation act_in (Activation.gradientArray,
  * Activation.c:233-239, the first step of that layer's backward,
@@ -356,15 +354,6 @@ int ach_dropout_fwd(float *x, size_t n, float probability, uint64_t seed,
                     uint32_t iter, uint32_t layer, ach_stream_t stream);
 int ach_dropout_bwd(float *delta, size_t n, float probability, uint64_t seed,
                     uint32_t iter, uint32_t layer, ach_stream_t stream);
-/* The same with the step index read from device memory (*iter) when the
- * kernel runs, for work recorded once into a HIP graph and replayed every
- * step.  No counterpart in the reference (its dropout is a host loop). */
-int ach_dropout_fwd_dev(float *x, size_t n, float probability, uint64_t seed,
-                        const uint32_t *iter, uint32_t layer, ach_stream_t stream);
-int ach_dropout_bwd_dev(float *delta, size_t n, float probability, uint64_t seed,
-                        const uint32_t *iter, uint32_t layer, ach_stream_t stream);
-/* *counter += v on the stream (advances such a device-side step index).  */
-int ach_counter_add(uint32_t *counter, uint32_t v, ach_stream_t stream);
 
 /* ---- NaN scan (the reference's isnan checks: NormData.normalize exits on a
  * NaN normalized value, NormData.c:273-276; ScaleData.addUpdatesToScale and
@@ -380,17 +369,6 @@ typedef struct ach_nan_span {
     int32_t reserved;
 } ach_nan_span;
 int ach_nan_scan(const ach_nan_span *spans, int nspans, int32_t *flag, ach_stream_t stream);
-
-/* ---- HIP graphs (no counterpart in the reference; the reference launches
- * every op eagerly).  capture_begin records the stream's work (and that of
- * streams forked from it by events) instead of running it, in the calling
- * thread's capture mode; capture_end instantiates the recording into
- * *exec; launch replays it on a stream; destroy frees it.  Recorded work
- * must not allocate, copy to or from the host, or synchronise.            */
-int ach_graph_capture_begin(ach_stream_t stream);
-int ach_graph_capture_end(ach_stream_t stream, void **exec);
-int ach_graph_launch(void *exec, ach_stream_t stream);
-int ach_graph_destroy(void *exec);
 
 /* ---- SGD momentum / weight-decay update ----------------------------------
  * ConvolutionalLayer.update (ConvolutionalLayer.c:959-980):

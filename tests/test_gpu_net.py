@@ -383,42 +383,6 @@ def _twin_nets(name, batch, seed=3, dropout_seed=0xd00d):
     return nets
 
 
-@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("fcnet", 16)])
-def test_graph_replay_matches_eager(gpu, name, batch):
-    """an_set_graph: replayed steps give bit-identical losses and parameters to
-    eager steps, with eager copies and reads between the replays, a new batch
-    every step, dropout masks advancing with the iteration, and a re-record
-    after a hyper-parameter change."""
-    eager, graph = _twin_nets(name, batch)
-    graph.set_graph(True)
-    n = eager.n_layers()
-    for step in range(6):
-        if step == 3:
-            for net in (eager, graph):
-                net.hyper(0.0005, 0.8, 0.001)
-        x, truth, _ = configs.synthetic_batch(name, 40 + step, batch)
-        losses = []
-        for net in (eager, graph):
-            net.set_input(x, truth)
-            net.train_step()
-            losses.append(net.loss())
-            # eager work between replays: a device read of a live buffer
-            net.buffer(0, 0)
-        assert losses[0] == losses[1], (name, step, losses)
-        assert eager.iteration() == graph.iteration() == step + 1
-        assert eager.seen() == graph.seen()
-    for i in range(n):
-        for which in (0, 2, 3, 4, 5, 6, 8, 9):
-            a, b = eager.buffer(i, which), graph.buffer(i, which)
-            if a is None:
-                continue
-            assert np.array_equal(a, b), (name, i, which)
-    # switching back to eager steps continues from the same state
-    graph.set_graph(False)
-    x, truth, _ = configs.synthetic_batch(name, 99, batch)
-    assert eager.train(x, truth) == graph.train(x, truth)
-
-
 def test_policy_and_subdivisions_match_oracle(gpu, oracle):
     """Config 3 at minibatch 8 with subdivisions = 2 (BN, dropout), a burn-in
     ramp and the poly policy.  At the start of each iteration the GPU network
@@ -455,26 +419,6 @@ def test_policy_and_subdivisions_match_oracle(gpu, oracle):
                 v = onet.buffer(i, code)
                 if v is not None and v.size:
                     assert rel_err(net.buffer(i, code), v) < TOL, (step, i, code)
-
-
-def test_graph_replay_with_changing_rate(gpu):
-    """A policy whose rate changes every update re-records the graph each
-    step; the replays still equal eager steps bit for bit.  Graph mode
-    refuses subdivisions > 1."""
-    eager, graph = _twin_nets("darknet", 8)
-    for net in (eager, graph):
-        net.policy(aetcnn.POLICY_EXP, gamma=0.9)
-    graph.set_graph(True)
-    for step in range(3):
-        x, truth, _ = configs.synthetic_batch("darknet", 70 + step, 8)
-        assert eager.train(x, truth) == graph.train(x, truth), step
-    for i in range(eager.n_layers()):
-        for which in (2, 4, 6, 8, 9):
-            a, b = eager.buffer(i, which), graph.buffer(i, which)
-            if a is not None:
-                assert np.array_equal(a, b), (i, which)
-    graph.subdivisions(2)
-    assert aetcnn.net_lib().an_train_step(graph.h) == aetcnn.ACH_EINVAL
 
 
 def test_cfg_policy_keys(gpu, oracle, tmp_path):

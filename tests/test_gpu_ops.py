@@ -512,8 +512,7 @@ def test_gradient_planes(gpu, B, n, sp, act):
 def test_maxpool_dropout_fused(gpu, B, Cc, H, W, size, stride, pad):
     """ach_maxpool_fwd_dropout == ach_maxpool_fwd + ach_dropout_fwd on the
     output; ach_maxpool_bwd_dropout == ach_dropout_bwd on delta_out +
-    ach_maxpool_bwd; bit for bit, with the step index from the host or from
-    device memory."""
+    ach_maxpool_bwd; bit for bit."""
     rng = np.random.default_rng(H + size)
     x = rng.standard_normal((B, Cc, H, W)).astype(np.float32)
     OH = gpu.ach_maxpool_out(H, size, stride, pad)
@@ -524,27 +523,22 @@ def test_maxpool_dropout_fused(gpu, B, Cc, H, W, size, stride, pad):
     o0, i0 = D((n,)), D((n,), np.int32)
     check(gpu.ach_maxpool_fwd(dx.ptr, B, Cc, H, W, size, stride, pad, o0.ptr, i0.ptr, None))
     check(gpu.ach_dropout_fwd(o0.ptr, n, p, seed, it, layer, None))
-    dit = dev(np.array([it], np.uint32))
-    for iter_ptr in (None, dit.ptr):
-        o1, i1 = D((n,)), D((n,), np.int32)
-        check(gpu.ach_maxpool_fwd_dropout(dx.ptr, B, Cc, H, W, size, stride, pad, o1.ptr,
-                                          i1.ptr, p, seed, 0 if iter_ptr else it, iter_ptr,
-                                          layer, None))
-        assert np.array_equal(o0.numpy().view(np.uint32), o1.numpy().view(np.uint32))
-        assert np.array_equal(i0.numpy(), i1.numpy())
+    o1, i1 = D((n,)), D((n,), np.int32)
+    check(gpu.ach_maxpool_fwd_dropout(dx.ptr, B, Cc, H, W, size, stride, pad, o1.ptr, i1.ptr, p,
+                                      seed, it, layer, None))
+    assert np.array_equal(o0.numpy().view(np.uint32), o1.numpy().view(np.uint32))
+    assert np.array_equal(i0.numpy(), i1.numpy())
     g = rng.standard_normal(n).astype(np.float32)
     gd = dev(g)
     check(gpu.ach_dropout_bwd(gd.ptr, n, p, seed, it, layer, None))
     ref = D(x.shape)
     check(gpu.ach_maxpool_bwd(gd.ptr, i0.ptr, B, Cc, H, W, size, stride, pad, ref.ptr, 0, None))
-    for iter_ptr in (None, dit.ptr):
-        got = dev(np.full(x.shape, np.nan, np.float32))
-        check(gpu.ach_maxpool_bwd_dropout(dev(g).ptr, i0.ptr, B, Cc, H, W, size, stride, pad,
-                                          got.ptr, 0, p, seed, 0 if iter_ptr else it, iter_ptr,
-                                          layer, None))
-        assert np.array_equal(ref.numpy().view(np.uint32), got.numpy().view(np.uint32))
+    got = dev(np.full(x.shape, np.nan, np.float32))
+    check(gpu.ach_maxpool_bwd_dropout(dev(g).ptr, i0.ptr, B, Cc, H, W, size, stride, pad,
+                                      got.ptr, 0, p, seed, it, layer, None))
+    assert np.array_equal(ref.numpy().view(np.uint32), got.numpy().view(np.uint32))
     assert gpu.ach_maxpool_fwd_dropout(dx.ptr, B, Cc, H, W, size, stride, pad, o0.ptr, i0.ptr,
-                                       1.0, seed, it, None, layer, None) == aetcnn.ACH_EINVAL
+                                       1.0, seed, it, layer, None) == aetcnn.ACH_EINVAL
 
 
 def test_avgpool_bit_exact(gpu, oracle):
