@@ -118,6 +118,7 @@ CONV_SHAPES = [
     # fully connected layers (1x1 of a 1x1 input, after flattening):
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
     (8, 64, 1, 1, 48, 1, 1, 0),    # 64 -> 48, 64-row tiles
+    (16, 2048, 1, 1, 8192, 1, 1, 0),  # pairs of K slices per workgroup (fwd and dgrad)
     # 3x3 forwards with an odd k-tile count (C/2 = 17): the K split gives
     # slices of 9 and 8 tiles, which must not share one workgroup
     (2, 34, 8, 8, 128, 3, 1, 1),   # one tile split in two
@@ -646,6 +647,7 @@ def test_bias_ops(gpu, oracle, B, n, sp):
     (128, 256, 8, 8, 512, 3, 1, 1),   # K split in two inside one workgroup
     (8, 64, 1, 1, 48, 1, 1, 0),       # fully connected GEMM
     (4, 300, 1, 1, 64, 1, 1, 0),      # fully connected, split K
+    (16, 2048, 1, 1, 8192, 1, 1, 0),  # fully connected, pairs of K slices per workgroup
 ], ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("act", [aetcnn.LEAKY, aetcnn.RELU, aetcnn.LINEAR, aetcnn.LOGISTIC])
 def test_conv_fwd_bias_act_fused(gpu, shape, act):
