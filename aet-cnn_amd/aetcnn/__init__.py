@@ -148,6 +148,8 @@ _OPS = {
     "ach_maxpool_bwd_act": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
     "ach_maxpool_bwd_act_planes": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp,
                                         _vp]),
+    "ach_maxpool_bwd_act_pooled": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp,
+                                        _vp]),
     "ach_maxpool_fwd_dropout": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _f, _u64, _u32,
                                      _u32, _vp]),
     "ach_maxpool_bwd_dropout": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _u64,

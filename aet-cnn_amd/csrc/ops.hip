@@ -587,8 +587,23 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ d
 // bit, without its eight dependent global loads per pixel (which stall when
 // the kernel shares the CUs with a GEMM).  Dynamic LDS: 8 bytes per staged
 // output position.
+// With yout (the pool's forward output, unmodified since), the activation
+// gradient of the layer below is taken from it: a pixel that receives a sum
+// is the argmax of each window it matches, and that window's output is the
+// pixel's own value, so act_gradient(yout[o]) equals act_gradient(y[p]) bit
+// for bit, and a pixel that receives nothing is +0 either way (relu and
+// leaky, whose gradients are finite for every input).  It reads the pooled
+// tensor (a quarter of the input's size for a 3x3/2 window) instead of the
+// input.  12 bytes of LDS per staged output position.
 constexpr int POOL_PLANE_MAX = 4096;  // output positions staged in LDS per workgroup
 constexpr int POOL_PIX_PER_WG = 1024; // input pixels a workgroup aims at
+// int32 offset of k_maxpool_bwd_plane's plane-sum scratch behind its staged
+// arrays of n positions (indices, gradients, and with yout the gradients of
+// the activation), rounded up to 8 bytes
+__host__ __device__ constexpr int pool_psum_offset(int n, bool yout)
+{
+    return ((yout ? 3 : 2) * n + 1) & ~1;
+}
 
 template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restrict__ dout,
@@ -597,7 +612,7 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
                                                            int stride_, int pad, int OH, int OW,
                                                            int planes, int ppw, float *din,
                                                            int accumulate, GradIn gi,
-                                                           double *psum)
+                                                           double *psum, const float *yout)
 {
     extern __shared__ int32_t pool_lds[];
     const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
@@ -605,15 +620,19 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
     const int bc0 = blockIdx.x * ppw, np = min(ppw, planes - bc0);
     int32_t *six = pool_lds;
     float *sg = reinterpret_cast<float *>(pool_lds + ppw * ohw);
+    // yout (optional): the pool's own output; its activation gradients are
+    // staged after the gradients
+    float *sgr = sg + ppw * ohw;
     // psum (optional): the sums of each input plane written, after the
-    // staged planes (8-byte aligned: 8 bytes per staged output position)
+    // staged arrays (rounded up to 8 bytes)
     PlaneSum ps;
-    ps.red = reinterpret_cast<double *>(pool_lds + 2 * ppw * ohw);
+    ps.red = reinterpret_cast<double *>(pool_lds + pool_psum_offset(ppw * ohw, yout != nullptr));
     if (psum) psum_clear(ps.red, np);
     const size_t obase = (size_t)bc0 * ohw;
     for (int q = threadIdx.x; q < np * ohw; q += blockDim.x) {
         six[q] = idx[obase + q];
         sg[q] = dout[obase + q];
+        if (yout) sgr[q] = act_gradient(yout[obase + q], gi.act);
     }
     __syncthreads();
     const int off = -pad / 2;
@@ -624,11 +643,13 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
         const int p = pbase + r;
         const int32_t *pix = six + pl * ohw;
         const float *pg = sg + pl * ohw;
+        const float *pgr = sgr + pl * ohw;
         const int i0 = max(floor_div(h - off - size, stride) + 1, 0);
         const int i1 = min(floor_div(h - off, stride), OH - 1);
         const int j0 = max(floor_div(w - off - size, stride) + 1, 0);
         const int j1 = min(floor_div(w - off, stride), OW - 1);
         float v = accumulate ? din[p] : 0.f;
+        float g = 0.f;  // with yout: the gradient at a window whose argmax is p
         if constexpr (SIZE > 0 && STRIDE > 0) {
             constexpr int NC = (SIZE + STRIDE - 1) / STRIDE;
 #pragma unroll
@@ -638,17 +659,23 @@ __global__ void __launch_bounds__(256) k_maxpool_bwd_plane(const float *__restri
                     const int i = i0 + a, j = j0 + c;
                     if (i <= i1 && j <= j1) {
                         const int o = i * OW + j;
-                        if (pix[o] == p) v += pg[o];
+                        if (pix[o] == p) {
+                            v += pg[o];
+                            if (yout) g = pgr[o];
+                        }
                     }
                 }
         } else {
             for (int i = i0; i <= i1; ++i)
                 for (int j = j0; j <= j1; ++j) {
                     const int o = i * OW + j;
-                    if (pix[o] == p) v += pg[o];
+                    if (pix[o] == p) {
+                        v += pg[o];
+                        if (yout) g = pgr[o];
+                    }
                 }
         }
-        v = gi.apply(v, (size_t)p);
+        v = yout ? v * g : gi.apply(v, (size_t)p);
         din[p] = v;
         if (psum) ps.add(pl, v);
     }
@@ -1232,19 +1259,25 @@ static int pool_bwd_ppw(int batch, int c, int h, int w, int OH, int OW)
 
 // psum (optional): per-(image, channel) sums of din as written, double
 // [batch][c]; only the plane-staged kernel with at most PSUM_PLANES planes
-// per workgroup takes it (else ACH_EUNSUPPORTED, nothing launched)
+// per workgroup takes it (else ACH_EUNSUPPORTED, nothing launched).
+// yout (optional): the pool's output, from which the plane-staged kernel
+// takes gi's activation gradient (relu / leaky, accumulate 0; else
+// ACH_EUNSUPPORTED, nothing launched)
 static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
                        int size, int stride, int pad, float *din, int accumulate, GradIn gi,
-                       DropIn dr, ach_stream_t s, double *psum = nullptr)
+                       DropIn dr, ach_stream_t s, double *psum = nullptr,
+                       const float *yout = nullptr)
 {
     if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, stride, pad)) return ACH_EINVAL;
     const int OH = ach_maxpool_out(h, size, stride, pad), OW = ach_maxpool_out(w, size, stride, pad);
     const int acc = accumulate ? 1 : 0;
-    if (psum) {
+    if (psum || yout) {
         const int ppw = pool_bwd_ppw(batch, c, h, w, OH, OW);
-        if (ppw == 0 || ppw > PSUM_PLANES || dr.on) return ACH_EUNSUPPORTED;
+        if (ppw == 0 || (psum && ppw > PSUM_PLANES) || dr.on) return ACH_EUNSUPPORTED;
+        if (yout && (acc || (gi.act != ACH_RELU && gi.act != ACH_LEAKY)))
+            return ACH_EUNSUPPORTED;
     }
-    const bool fast2 = !psum && pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
+    const bool fast2 = !psum && !yout && pool2_fast(din, dout, h, w, size, stride, pad, OH, OW) &&
                        (reinterpret_cast<uintptr_t>(idx) & 7) == 0 &&
                        (reinterpret_cast<uintptr_t>(gi.y) & 15) == 0;
     if (dr.on && !fast2) {  // the dropout backward in place on dout first
@@ -1266,20 +1299,21 @@ static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, 
         const int planes = batch * c;
         const int ppw = pool_bwd_ppw(batch, c, h, w, OH, OW);
         const dim3 pg((unsigned)((planes + ppw - 1) / ppw));
-        const size_t lds = (size_t)ppw * OH * OW * 8 + (psum ? (size_t)ppw * 256 * 8 : 0);
+        const size_t lds = (size_t)pool_psum_offset(ppw * OH * OW, yout != nullptr) * 4 +
+                           (psum ? (size_t)ppw * 256 * 8 : 0);
         const FastDiv dHW = make_fastdiv((unsigned)(h * w));
         if (size == 3 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<3, 2>), pg, dim3(256), lds, as_stream(s), dout,
                                idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi,
-                               psum);
+                               psum, yout);
         else if (size == 2 && stride == 2)
             hipLaunchKernelGGL((k_maxpool_bwd_plane<2, 2>), pg, dim3(256), lds, as_stream(s), dout,
                                idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi,
-                               psum);
+                               psum, yout);
         else
             hipLaunchKernelGGL((k_maxpool_bwd_plane<0, 0>), pg, dim3(256), lds, as_stream(s), dout,
                                idx, dW, dHW, size, stride, pad, OH, OW, planes, ppw, din, acc, gi,
-                               psum);
+                               psum, yout);
         return check_launch();
     }
     if (size == 3 && stride == 2)
@@ -1333,6 +1367,16 @@ int ach_maxpool_bwd_act_planes(const float *dout, const int32_t *idx, int batch,
         return ACH_EINVAL;
     return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, 0,
                        GradIn{y_in, y_in ? act_in : ACH_LINEAR}, DropIn{}, s, plane_sums);
+}
+
+int ach_maxpool_bwd_act_pooled(const float *dout, const int32_t *idx, int batch, int c, int h,
+                               int w, int size, int stride, int pad, float *din,
+                               const float *pooled, int act_in, double *plane_sums,
+                               ach_stream_t s)
+{
+    if (!pooled || (act_in != ACH_RELU && act_in != ACH_LEAKY)) return ACH_EINVAL;
+    return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, 0,
+                       GradIn{nullptr, act_in}, DropIn{}, s, plane_sums, pooled);
 }
 
 int ach_gradient_planes(const float *y, int batch, int n, int spatial, int act, float *delta,

@@ -424,6 +424,22 @@ static int maxpool_backward(an_network *net, an_layer *l, an_state st)
      * BN, which fuses its gradient itself), the layer's activation gradient
      * is applied here and the conv layer's backward skips it.              */
     an_layer *p = pool_act_target(net, l, st.delta);
+    const int out_kept = l->index + 1 >= net->n || !net->layers[l->index + 1]->shares_prev;
+    if (p && out_kept && (p->activation == ACH_RELU || p->activation == ACH_LEAKY)) {
+        /* ... from the pool's own output, which a following layer has not
+         * masked in place: the gradient at each argmax pixel, read from the
+         * pooled tensor instead of the conv output                          */
+        const int rc = ach_maxpool_bwd_act_pooled(l->delta, l->indexes, l->batch, l->c, l->h,
+                                                  l->w, l->size, l->stride, l->pad, st.delta,
+                                                  l->output, p->activation, p->bias_planes,
+                                                  net->stream);
+        if (rc == ACH_OK) {
+            p->grad_applied = 1;
+            p->planes_ready = p->bias_planes != NULL;
+            return ACH_OK;
+        }
+        if (rc != ACH_EUNSUPPORTED) return rc;
+    }
     if (p && p->bias_planes) {
         /* ... and takes that layer's bias-gradient plane sums as it writes */
         const int rc = ach_maxpool_bwd_act_planes(l->delta, l->indexes, l->batch, l->c, l->h,

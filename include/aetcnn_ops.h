@@ -328,6 +328,19 @@ int ach_maxpool_bwd_act_planes(const float *delta_out, const int32_t *indexes, i
                                int h, int w, int size, int stride, int padding, float *delta_in,
                                const float *y_in, int act_in, double *plane_sums,
                                ach_stream_t stream);
+/* ach_maxpool_bwd_act_planes (plane_sums may be NULL here) for a relu or
+ * leaky layer below, with the activation gradient taken from the pool's
+ * own forward output `pooled` instead of the layer's output: a pixel that
+ * receives a sum is the argmax of its windows and the window's output is
+ * its value, so the results equal ach_maxpool_bwd_act_planes' bit for bit
+ * while reading the pooled tensor instead of the pool's input.  `pooled`
+ * must hold what ach_maxpool_fwd wrote (not masked in place since).
+ * ACH_EINVAL for another activation; ACH_EUNSUPPORTED, with nothing
+ * launched, for pools the plane-staged kernel does not take (as above).   */
+int ach_maxpool_bwd_act_pooled(const float *delta_out, const int32_t *indexes, int batch, int c,
+                               int h, int w, int size, int stride, int padding, float *delta_in,
+                               const float *pooled, int act_in, double *plane_sums,
+                               ach_stream_t stream);
 
 /* ---- global average pool (AvgPoolLayer.c:29-46, 73-88) ----------------- */
 int ach_avgpool_fwd(const float *in, int batch, int c, int spatial, float *out,

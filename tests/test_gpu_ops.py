@@ -476,6 +476,46 @@ def test_maxpool_bwd_act_planes(gpu, oracle, B, Cc, H, W, size, stride, pad, act
     assert rel_err(ub.numpy(), ua.numpy()) < 1e-7
 
 
+@pytest.mark.parametrize("B,Cc,H,W,size,stride,pad,sums", [
+    (3, 5, 55, 55, 3, 2, 0, True),    # AlexNet pool 1
+    (3, 7, 27, 27, 3, 2, 0, True),    # pool 2
+    (5, 7, 13, 13, 3, 2, 0, True),    # pool 5: six planes per workgroup
+    (2, 3, 20, 20, 2, 2, 1, True),    # padded 2x2/2 windows
+    (4, 8, 8, 8, 2, 2, 1, False),     # 16 planes per workgroup: no plane sums
+    (2, 3, 9, 11, 3, 1, 1, False),    # overlapping stride-1 windows, odd sizes
+])
+@pytest.mark.parametrize("act", [aetcnn.RELU, aetcnn.LEAKY])
+def test_maxpool_bwd_act_pooled(gpu, oracle, B, Cc, H, W, size, stride, pad, sums, act):
+    """ach_maxpool_bwd_act_pooled takes the activation gradient from the
+    pool's output: the delta (and plane sums) of ach_maxpool_bwd_act(_planes)
+    with the layer's output, bit for bit.  The layer's output is an
+    activated tensor with ties (integers, zeros from relu)."""
+    rng = np.random.default_rng(H + 5 * act + size)
+    z = rng.integers(-4, 5, (B, Cc, H, W)).astype(np.float32)
+    x = np.where(z > 0, z, np.float32(0) if act == aetcnn.RELU else np.float32(0.1) * z)
+    x = x.astype(np.float32)
+    out, idx = oracle.maxpool_forward(x, size, stride, pad)
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    dg, di, dx, dout = dev(g), dev(idx.astype(np.int32)), dev(x), dev(out)
+    ref = dev(np.zeros(x.shape, np.float32))
+    check(gpu.ach_maxpool_bwd_act(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, ref.ptr, 0,
+                                  dx.ptr, act, None))
+    got = dev(np.full(x.shape, np.nan, np.float32))
+    ps = dev(np.full(B * Cc, np.nan)) if sums else None
+    check(gpu.ach_maxpool_bwd_act_pooled(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad, got.ptr,
+                                         dout.ptr, act, ps.ptr if sums else None, None))
+    a, b = ref.numpy(), got.numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    if sums:
+        ps2 = dev(np.full(B * Cc, np.nan))
+        check(gpu.ach_maxpool_bwd_act_planes(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad,
+                                             ref.ptr, dx.ptr, act, ps2.ptr, None))
+        assert np.array_equal(ps.numpy().view(np.uint64), ps2.numpy().view(np.uint64))
+    assert gpu.ach_maxpool_bwd_act_pooled(dg.ptr, di.ptr, B, Cc, H, W, size, stride, pad,
+                                          got.ptr, dout.ptr, aetcnn.LOGISTIC, None,
+                                          None) == aetcnn.ACH_EINVAL
+
+
 def test_maxpool_bwd_act_planes_unsupported(gpu):
     """Small input planes (more than 8 per workgroup) keep the separate bias
     gradient: nothing is launched."""
