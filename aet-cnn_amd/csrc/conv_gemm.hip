@@ -1681,6 +1681,11 @@ constexpr int DG_TW = 32, DG_TH = 8, DG_FC = 16, DG_WAVES = 8, DG_NT = 64 * DG_W
 // patch rows a wave prefetches per chunk: 4*DG_ROWS, so DG_FC * PH must not
 // exceed 4*DG_ROWS*DG_WAVES (kernels up to 9 wide)
 constexpr int DG_ROWS = 8;
+// 3x3 kernels (the compile-time KS = 3 instance) stage 32 filters per chunk
+// (10 prefetched rows per wave): each chunk's compute then covers more of
+// the next chunk's load latency, with half as many chunks and barriers
+__host__ __device__ constexpr int dg_fc(int ks) { return ks == 3 ? 32 : DG_FC; }
+__host__ __device__ constexpr int dg_rows(int ks) { return ks == 3 ? 10 : DG_ROWS; }
 template <int NC, int KS_>
 __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__restrict__ dy,
                                                              const float *__restrict__ w,
@@ -1692,8 +1697,9 @@ __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__rest
     const int KS = KS_ ? KS_ : g.KS;
     // patch rows padded to a multiple of 4 floats (16-byte aligned segments)
     const int PH = DG_TH + KS - 1, PWd = (DG_TW + KS - 1 + 3) & ~3, pplane = PH * PWd;
-    float *patch = smem;                                   // [DG_FC][PH][PWd]
-    float4 *wl = reinterpret_cast<float4 *>(smem + DG_FC * pplane);  // [DG_FC][KS*KS]
+    constexpr int FC = dg_fc(KS_), ROWS = dg_rows(KS_);
+    float *patch = smem;                                   // [FC][PH][PWd]
+    float4 *wl = reinterpret_cast<float4 *>(smem + FC * pplane);  // [FC][KS*KS]
     float *red = smem;  // after the last chunk: [DG_WAVES-1][NC][4][64]
     const int b = blockIdx.y;
     const int tx0 = (blockIdx.x % tiles_x) * DG_TW, ty0 = (blockIdx.x / tiles_x) * DG_TH;
@@ -1708,45 +1714,57 @@ __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__rest
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[c][q] = 0.f;
     const int taps = KS * KS;
-    // a chunk's patch rows rr = wave + DG_WAVES*u, one column per lane
-    float pre[DG_ROWS * 4];
-    const int prow = DG_FC * PH;  // at most DG_ROWS*4*DG_WAVES rows (host check)
+    // slot u of a wave's prefetch holds patch row r = u % PH of the chunk's
+    // filter wvu + DG_WAVES * (u / PH), one column per lane: the row's offset
+    // is wave-uniform (the loads' scalar operand) and the lane's column
+    // offset is fixed, so the loads take no per-slot address registers;
+    // columns and rows outside dy read as zero
+    constexpr int NU = ROWS * 4;
+    const int used = (FC / DG_WAVES) * PH;  // slots in use (host check: <= NU)
+    float pre[NU];
+    const int wvu = __builtin_amdgcn_readfirstlane(wave);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(dyb, (unsigned)((size_t)g.F * g.OH * g.OW * 4));
+    const int oxl = ox0 + lane;
+    const unsigned voff = (lane < PWd && oxl >= 0 && oxl < g.OW) ? (unsigned)oxl * 4u : kOOB;
     auto load_chunk = [&](int f0) {
-        const int fc = min(DG_FC, g.F - f0);
+        const int fc = min(FC, g.F - f0);
 #pragma unroll
-        for (int u = 0; u < DG_ROWS * 4; ++u) {
-            const int rr = wave + DG_WAVES * u;
-            const int f = rr / PH, r = rr - f * PH, oy = oy0 + r, ox = ox0 + lane;
-            pre[u] = (rr < fc * PH && lane < PWd && oy >= 0 && oy < g.OH && ox >= 0 &&
-                      ox < g.OW)
-                         ? dyb[((size_t)(f0 + f) * g.OH + oy) * g.OW + ox]
-                         : 0.f;
+        for (int u = 0; u < NU; ++u) {
+            const int fl = wvu + DG_WAVES * (u / PH), oy = oy0 + u % PH;
+            const bool ok = u < used && fl < fc && oy >= 0 && oy < g.OH;
+            const unsigned soff = ok ? (unsigned)(((f0 + fl) * g.OH + oy) * g.OW) * 4u : 0u;
+            pre[u] = bload_so(rs, ok ? voff : kOOB, soff);
         }
     };
     load_chunk(0);
-    for (int f0 = 0; f0 < g.F; f0 += DG_FC) {
-        const int fc = min(DG_FC, g.F - f0);
+    for (int f0 = 0; f0 < g.F; f0 += FC) {
+        const int fc = min(FC, g.F - f0);
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < DG_ROWS * 4; ++u) {
-            const int rr = wave + DG_WAVES * u;
-            if (rr < prow && lane < PWd) patch[rr * PWd + lane] = pre[u];
+        for (int u = 0; u < NU; ++u) {
+            const int fl = wvu + DG_WAVES * (u / PH);
+            if (u < used && lane < PWd) patch[(fl * PH + u % PH) * PWd + lane] = pre[u];
         }
-        for (int i = threadIdx.x; i < fc * taps; i += DG_NT) {
-            const int f = i / taps, tap = i - f * taps;
-            const float *wf = w + (size_t)(f0 + f) * NC * taps + tap;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            v.x = wf[0];
-            if (NC > 1) v.y = wf[taps];
-            if (NC > 2) v.z = wf[2 * taps];
-            if (NC > 3) v.w = wf[3 * taps];
-            wl[i] = v;
+        if constexpr (KS_ == 0) {
+            for (int i = threadIdx.x; i < fc * taps; i += DG_NT) {
+                const int f = i / taps, tap = i - f * taps;
+                const float *wf = w + (size_t)(f0 + f) * NC * taps + tap;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                v.x = wf[0];
+                if (NC > 1) v.y = wf[taps];
+                if (NC > 2) v.z = wf[2 * taps];
+                if (NC > 3) v.w = wf[3 * taps];
+                wl[i] = v;
+            }
         }
         __syncthreads();
-        if (f0 + DG_FC < g.F) load_chunk(f0 + DG_FC);  // in flight while this chunk computes
-        for (int f = wave; f < fc; f += DG_WAVES) {
+        if (f0 + FC < g.F) load_chunk(f0 + FC);  // in flight while this chunk computes
+        for (int f = wvu; f < fc; f += DG_WAVES) {
             const float *pf = patch + f * pplane;
             const float4 *wf = wl + f * taps;
+            // compile-time widths read the (wave-uniform) filter's weights
+            // straight from W through the scalar cache
+            const float *wg = w + (size_t)(f0 + f) * NC * taps;
             for (int ky = 0; ky < KS; ++ky) {
                 // row segment: columns tx .. tx + 3 + KS - 1
                 const float *row = pf + (ty + KS - 1 - ky) * PWd + tx;
@@ -1764,8 +1782,9 @@ __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__rest
                     }
 #pragma unroll
                     for (int kx = 0; kx < KS_; ++kx) {
-                        const float4 wv = wf[ky * KS_ + kx];
-                        const float wc[4] = {wv.x, wv.y, wv.z, wv.w};
+                        float wc[NC];
+#pragma unroll
+                        for (int c = 0; c < NC; ++c) wc[c] = wg[c * taps + ky * KS_ + kx];
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             const float val = v[q + KS_ - 1 - kx];
@@ -2716,8 +2735,8 @@ static int fc_wgrad_launch(const ConvGeom &g, const float *x, const float *dy, f
 // kernels up to 16 wide, a staged chunk that fits LDS
 static size_t dgrad_small_c_lds(const ConvGeom &g, int nc)
 {
-    const int PH = DG_TH + g.KS - 1, PWd = (DG_TW + g.KS - 1 + 3) & ~3;
-    const size_t stage = (size_t)DG_FC * PH * PWd + 4 * DG_FC * g.KS * g.KS;
+    const int PH = DG_TH + g.KS - 1, PWd = (DG_TW + g.KS - 1 + 3) & ~3, FC = dg_fc(g.KS);
+    const size_t stage = (size_t)FC * PH * PWd + 4 * FC * g.KS * g.KS;
     const size_t red = (size_t)(DG_WAVES - 1) * nc * 4 * 64;
     return (stage > red ? stage : red) * sizeof(float);
 }
@@ -2725,8 +2744,10 @@ static bool dgrad_small_c(const ConvGeom &g)
 {
     // the chunk's patch rows fit the per-wave register prefetch
     const int PH = DG_TH + g.KS - 1;
+    // (and one image's dy addressable by 32-bit buffer offsets)
     return g.S == 1 && g.P <= g.KS - 1 && g.C <= 4 && g.KS <= 16 &&
-           DG_FC * PH <= DG_ROWS * 4 * DG_WAVES && dgrad_small_c_lds(g, 4) <= 65536;
+           (dg_fc(g.KS) / DG_WAVES) * PH <= dg_rows(g.KS) * 4 &&
+           dgrad_small_c_lds(g, 4) <= 65536 && (long long)g.F * g.OH * g.OW * 4 < (1ll << 31);
 }
 
 template <int NC>
