@@ -1833,6 +1833,83 @@ __global__ void __launch_bounds__(DG_NT) k_conv_dgrad_smallc(const float *__rest
         }
 }
 
+// ---- weight gradient of a 1x1 stride-1 layer with few filters -------------
+// dW[f][c] += sum over (b, p) of dy[b][f][p] * x[b][c][p]
+// (ConvolutionalLayer.c:913-929 for k = 1).  As a GEMM its M is the filter
+// count (10 for a classifier's last 1x1 layer) and its K = B*HW is long, so
+// the tiled GEMM needs a deep K split and a separate reduction pass.  Here a
+// workgroup of WG1_NT threads owns CB channels for every filter and walks
+// the whole K in one pass, four positions per float4: thread t takes
+// position quads t, t + WG1_NT, ... (x read once; dy read by every
+// workgroup, from L2), all of a step's loads in flight together.  Its
+// F x CB partial sums are added over the wave (xor tree), then over the
+// waves in wave order, and one thread per output adds the total to dW (then
+// the weights' SGD step when sg.w is set, as the GEMM epilogues do).  Fixed
+// order, no workspace.
+constexpr int WG1_NT = 1024;
+template <int FMAX, int CB>
+__global__ void __launch_bounds__(WG1_NT) k_wgrad_1x1_smallf(const float *__restrict__ x,
+                                                             const float *__restrict__ dy,
+                                                             float *__restrict__ dw, int B,
+                                                             int C, int F, int HW, Sgd sg)
+{
+    constexpr int NW = WG1_NT / 64;
+    __shared__ float red[NW][FMAX * CB];
+    const int c0 = blockIdx.x * CB, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float acc[FMAX][CB];
+#pragma unroll
+    for (int f = 0; f < FMAX; ++f)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[f][cb] = 0.f;
+    const int hw4 = HW >> 2, k4n = B * hw4;
+    for (int k4 = threadIdx.x; k4 < k4n; k4 += WG1_NT) {
+        const int b = k4 / hw4, p = (k4 - b * hw4) * 4;
+        float4 xv[CB], dv[FMAX];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            xv[cb] = c0 + cb < C ? *reinterpret_cast<const float4 *>(
+                                       x + ((size_t)b * C + c0 + cb) * HW + p)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float *dyb = dy + (size_t)b * F * HW + p;
+#pragma unroll
+        for (int f = 0; f < FMAX; ++f)
+            dv[f] = f < F ? *reinterpret_cast<const float4 *>(dyb + (size_t)f * HW)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int f = 0; f < FMAX; ++f)
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                float a = acc[f][cb];
+                a = __fmaf_rn(dv[f].x, xv[cb].x, a);
+                a = __fmaf_rn(dv[f].y, xv[cb].y, a);
+                a = __fmaf_rn(dv[f].z, xv[cb].z, a);
+                a = __fmaf_rn(dv[f].w, xv[cb].w, a);
+                acc[f][cb] = a;
+            }
+    }
+#pragma unroll
+    for (int f = 0; f < FMAX; ++f) {
+        if (f >= F) break;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            const float v = wave_sum(acc[f][cb]);
+            if (lane == 0) red[wave][f * CB + cb] = v;
+        }
+    }
+    __syncthreads();
+    const int i = threadIdx.x;
+    if (i >= F * CB) return;
+    const int f = i / CB, c = c0 + (i - f * CB);
+    if (c >= C) return;
+    float t = red[0][i];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w][i];
+    const size_t o = (size_t)f * C + c;
+    float u = dw[o] + t;
+    if (sg.w) sgd_step(sg.w[o], u, sg.dc, sg.lc, sg.mom);
+    dw[o] = u;
+}
+
 __device__ __forceinline__ void addto(float &a, float b) { a += b; }
 __device__ __forceinline__ void addto(float4 &a, const float4 &b)
 {
@@ -2731,6 +2808,24 @@ static int fc_wgrad_launch(const ConvGeom &g, const float *x, const float *dy, f
     return fc_wgrad_bm<128>(g, x, dy, dw, part, splits, kchunk, st, s1);
 }
 
+// the one-pass weight gradient of 1x1 stride-1 layers (not fully connected)
+// with at most 16 filters on planes of at most 256 positions, a multiple of
+// 4 (a classifier's last layer): every workgroup reads dy (F/2 times the
+// bytes of x in all, from L2), x is read once
+constexpr int WG1_FMAX = 16, WG1_CB = 2;
+static bool wgrad_1x1_smallf(const ConvGeom &g)
+{
+    return g.KS == 1 && g.S == 1 && g.P == 0 && !fc_geom(g) && g.F <= WG1_FMAX &&
+           g.OH * g.OW <= 256 && (g.OH * g.OW) % 4 == 0;
+}
+static int wgrad_1x1_smallf_launch(const ConvGeom &g, const float *x, const float *dy, float *dw,
+                                   const Sgd &sg, hipStream_t st)
+{
+    hipLaunchKernelGGL((k_wgrad_1x1_smallf<WG1_FMAX, WG1_CB>), dim3((g.C + WG1_CB - 1) / WG1_CB),
+                       dim3(WG1_NT), 0, st, x, dy, dw, g.B, g.C, g.F, g.OH * g.OW, sg);
+    return check_launch();
+}
+
 // the small-channel input gradient: stride 1, at most 4 input channels,
 // kernels up to 16 wide, a staged chunk that fits LDS
 static size_t dgrad_small_c_lds(const ConvGeom &g, int nc)
@@ -2980,6 +3075,8 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)
 {
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
+    // (the one-pass 1x1 kernel needs none, but unaligned operands take the
+    // GEMM, so its workspace is reported)
     int splits, kchunk;
     wgrad_split(g, wgrad_bm(g), wgrad_bn(g), splits, kchunk);
     if (splits <= 1) return 0;
@@ -2996,6 +3093,10 @@ static int bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, f
     if (!conv_ok(d) || !x || !dy || !dw) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
+    // (float4 loads: 16-byte aligned operands; planes are multiples of 4)
+    if (wgrad_1x1_smallf(g) &&
+        ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy)) & 15) == 0)
+        return wgrad_1x1_smallf_launch(g, x, dy, dw, sgd, as_stream(stream));
     const int bm = wgrad_bm(g), bn = wgrad_bn(g);
     int splits, kchunk;
     wgrad_split(g, bm, bn, splits, kchunk);
