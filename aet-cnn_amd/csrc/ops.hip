@@ -920,6 +920,24 @@ __global__ void k_sgd(size_t n, float *__restrict__ w, float *__restrict__ v, fl
     }
 }
 
+// A layer's biases and BN scales in one launch (the two small updates of
+// ConvolutionalLayer.update, ConvolutionalLayer.c:959-980, without decay):
+// element i < n of (w0, v0), else element i - n of (w1, v1); the arithmetic
+// of k_sgd with dc = 0.
+__global__ void k_sgd_pair(int n, float *__restrict__ w0, float *__restrict__ v0,
+                           float *__restrict__ w1, float *__restrict__ v1, float lc, float mom)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < 2 * n; i += gridDim.x * blockDim.x) {
+        const bool first = i < n;
+        const int j = first ? i : i - n;
+        float *w = first ? w0 : w1, *v = first ? v0 : v1;
+        float a = w[j], u = v[j];
+        sgd1(a, u, 0.f, lc, mom);
+        w[j] = a;
+        v[j] = u;
+    }
+}
+
 }  // namespace ach
 
 using namespace ach;
@@ -1515,6 +1533,14 @@ int ach_conv_update(size_t nweights, float *weights, float *weight_updates, size
     const float a2 = lr / batch;
     int rc = ach_sgd_update(nweights, weights, weight_updates, a1, a2, momentum, s);
     if (rc) return rc;
+    if (scales && n > 0 && n <= (1u << 20)) {  // both small arrays in one launch
+        if (!biases || !bias_updates) return ACH_EINVAL;
+        const int n2 = (int)(2 * n);
+        hipLaunchKernelGGL(k_sgd_pair, dim3((unsigned)((n2 + 255) / 256)), dim3(256), 0,
+                           as_stream(s), (int)n, biases, bias_updates, scales, scale_updates, a2,
+                           momentum);
+        return check_launch();
+    }
     rc = ach_sgd_update(n, biases, bias_updates, 0.f, a2, momentum, s);
     if (rc || !scales) return rc;
     return ach_sgd_update(n, scales, scale_updates, 0.f, a2, momentum, s);

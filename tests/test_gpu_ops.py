@@ -652,6 +652,24 @@ def test_conv_update(gpu, oracle):
         assert rel_err(a.numpy(), r) < 1e-6
 
 
+@pytest.mark.parametrize("n", [1, 64, 1000, 4099])
+def test_conv_update_pair_matches_sgd(gpu, n):
+    """ach_conv_update with BN scales (biases and scales in one launch)
+    equals ach_sgd_update on each array, bit for bit."""
+    rng = np.random.default_rng(n)
+    b, db = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    s, ds = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    got = [dev(a) for a in (b, db, s, ds)]
+    ref = [dev(a) for a in (b, db, s, ds)]
+    check(gpu.ach_conv_update(0, None, None, n, got[0].ptr, got[1].ptr, got[2].ptr, got[3].ptr,
+                              64, 0.1, 0.9, 5e-4, None))
+    lc = np.float32(0.1) / np.float32(64)
+    check(gpu.ach_sgd_update(n, ref[0].ptr, ref[1].ptr, 0.0, lc, 0.9, None))
+    check(gpu.ach_sgd_update(n, ref[2].ptr, ref[3].ptr, 0.0, lc, 0.9, None))
+    for a, r in zip(got, ref):
+        assert np.array_equal(a.numpy().view(np.uint32), r.numpy().view(np.uint32))
+
+
 @pytest.mark.parametrize("B,n,sp", [(16, 10, 64), (8, 300, 1), (5, 40, 12), (9, 6, 169)])
 def test_bias_ops(gpu, oracle, B, n, sp):
     """add_bias bit-exact; bias gradient (large planes: two-pass partials;
