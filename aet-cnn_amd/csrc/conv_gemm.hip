@@ -1889,11 +1889,12 @@ __global__ void __launch_bounds__(WG1_NT) k_wgrad_1x1_smallf(const float *__rest
     }
 #pragma unroll
     for (int f = 0; f < FMAX; ++f) {
-        if (f >= F) break;
+        if (f < F) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-            const float v = wave_sum(acc[f][cb]);
-            if (lane == 0) red[wave][f * CB + cb] = v;
+            for (int cb = 0; cb < CB; ++cb) {
+                const float v = wave_sum(acc[f][cb]);
+                if (lane == 0) red[wave][f * CB + cb] = v;
+            }
         }
     }
     __syncthreads();

@@ -119,6 +119,9 @@ CONV_SHAPES = [
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
     (8, 64, 1, 1, 48, 1, 1, 0),    # 64 -> 48, 64-row tiles
     (16, 2048, 1, 1, 8192, 1, 1, 0),  # pairs of K slices per workgroup (fwd and dgrad)
+    # split K on 169-position planes with N % 4 == 0: partials reduced in
+    # their own order, four sums of one plane stored at once
+    (4, 64, 13, 13, 96, 3, 1, 1),
     # one-pass 1x1 weight gradient (at most 16 filters, planes of <= 256):
     (3, 37, 7, 9, 16, 1, 1, 0),    # channels not a multiple of 4, odd plane
     (2, 5, 16, 16, 1, 1, 1, 0),    # one filter, a 256-position plane
