@@ -461,6 +461,105 @@ struct AWeightsT4K : AWeightsT4<BM, KS * KS + 1> {
     }
 };
 
+// B for the forward pass of a wide KS x KS kernel (KS odd) without padding:
+// k-tile t holds two filter rows r = 2t, 2t + 1 of the C*KS rows (channel
+// c = r / KS, kernel row ki = r % KS), each as its KS taps and a zero tap,
+// BK = 2*(KS + 1); the GEMM runs over K = ceil(C*KS/2) * BK.  Thread ->
+// column n0 + tid%128 and row kr = tid/128 of the pair (wave-uniform).  With
+// no padding every tap of a valid column lies inside the image, so a
+// thread's KS byte offsets are loop-invariant and a k-tile adds the uniform
+// (c*H + ki)*W*4 of its row; a row past the last (c >= C) reads zeros.  No
+// per-element arithmetic (the generic loader spent about 8 VALU per element
+// on the tap's channel, row, column and bounds).
+template <int KS>
+struct BIm2colRow {
+    static constexpr int BK = 2 * (KS + 1), RB = KS + 1, PAD = LDP_FWD;
+    static_assert(KS % 2 == 1, "odd kernel: a zero tap completes each row");
+    __amdgpu_buffer_rsrc_t rs;
+    unsigned voff[KS];
+    int kr, C, H, W;
+    __device__ __forceinline__ void init(const float *x, const ConvGeom &g, int N, int n0,
+                                         int tid)
+    {
+        rs = make_rsrc(x, (unsigned)((size_t)g.B * g.C * g.H * g.W * 4));
+        const int n = n0 + tid % GBN;
+        kr = __builtin_amdgcn_readfirstlane(tid / GBN);
+        C = g.C;
+        H = g.H;
+        W = g.W;
+        const int ohw = g.OH * g.OW;
+        const bool nok = n < N;
+        const int nn = nok ? n : 0;
+        const int b = nn / ohw, p = nn - b * ohw;
+        const int oh = p / g.OW, ow = p - oh * g.OW;
+        const int base = b * g.C * g.H * g.W + oh * g.S * g.W + ow * g.S;
+#pragma unroll
+        for (int j = 0; j < KS; ++j) voff[j] = nok ? (unsigned)(base + j) * 4u : kOOB;
+    }
+    __device__ __forceinline__ void load(int k0, int, float *rb) const
+    {
+        const int r = 2 * (k0 / BK) + kr, c = r / KS, ki = r - c * KS;
+        const bool rok = c < C;  // uniform: the row exists
+        const unsigned d = rok ? (unsigned)((c * H + ki) * W) * 4u : 0u;
+#pragma unroll
+        for (int j = 0; j < KS; ++j) rb[j] = bload_so(rs, rok ? voff[j] : kOOB, d);
+        rb[KS] = 0.f;
+    }
+    template <int LD>
+    __device__ __forceinline__ void store(float (*S)[LD], const float *rb) const
+    {
+        const int nc = ltid() % GBN;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) S[kr * RB + j][nc] = rb[j];
+    }
+};
+
+// The k-major weights Wt[C*KS*KS][M] for BIm2colRow: local row kr*(KS+1) + j
+// of k-tile t is weight row (2t + kr)*KS + j (j < KS), or zero for the pad
+// tap and for rows past the last; float4 loads with loop-invariant offsets
+// and the uniform 2t*KS*M*4 per k-tile.
+template <int BM, int KS>
+struct AWeightsT4Row : AWeightsT4<BM, 2 * (KS + 1)> {
+    static constexpr int BK = 2 * (KS + 1);
+    using Base = AWeightsT4<BM, BK>;
+    using Base::NV;
+    using Base::C4;
+    unsigned voff[NV];
+    int wrow[NV];  // each float4's weight row at t = 0 (-1: a pad tap)
+    int KM4, kw;   // 2*KS*M*4 per k-tile; the weight rows, C*KS*KS
+    __device__ __forceinline__ void init_rows(const float *wt, int M_, int kw_, int m0_)
+    {
+        Base::init(wt, M_, kw_, m0_, 0);
+        kw = kw_;
+        KM4 = 2 * KS * M_ * 4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int f = ltid() + GNT * i;
+            const int lr = f / C4, m = m0_ + 4 * (f % C4);
+            const int half = lr / (KS + 1), j = lr - half * (KS + 1);
+            const bool ok = f < BK * C4 && j < KS && m < M_;
+            wrow[i] = ok ? half * KS + j : -1;
+            voff[i] = ok ? (unsigned)(wrow[i] * M_ + m) * 4u : kOOB;
+        }
+    }
+    __device__ __forceinline__ void load(int k0, int, float *ra) const
+    {
+        const int t = k0 / BK;
+        const unsigned d = (unsigned)t * (unsigned)KM4;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            // rows past the filter's (the second row of a last, odd pair,
+            // and the prefetch past the last k-tile) read as zero
+            const bool ok = wrow[i] >= 0 && 2 * t * KS + wrow[i] < kw;
+            const float4 v = bload4_so(this->rs, ok ? voff[i] : kOOB, ok ? d : 0u);
+            ra[4 * i] = v.x; ra[4 * i + 1] = v.y; ra[4 * i + 2] = v.z; ra[4 * i + 3] = v.w;
+        }
+    }
+};
+
+template <class BL> struct RowTaps : std::false_type { static constexpr int ks = 11; };
+template <int KS> struct RowTaps<BIm2colRow<KS>> : std::true_type { static constexpr int ks = KS; };
+
 template <class BL> struct PaddedTaps {
     static constexpr bool value = false;
     static constexpr int ks = 5;
@@ -835,12 +934,14 @@ struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
     // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
     using AL = typename std::conditional<
-        PaddedTaps<BL>::value, AWeightsT4K<BM, PaddedTaps<BL>::ks>,
+        RowTaps<BL>::value, AWeightsT4Row<BM, RowTaps<BL>::ks>,
         typename std::conditional<
-            VECA,
-            typename std::conditional<std::is_same<BL, BIm2col3F>::value, AWeightsT4F<BM, BK>,
-                                      AWeightsT4<BM, BK>>::type,
-            AWeightsT<BM, BK>>::type>::type;
+            PaddedTaps<BL>::value, AWeightsT4K<BM, PaddedTaps<BL>::ks>,
+            typename std::conditional<
+                VECA,
+                typename std::conditional<std::is_same<BL, BIm2col3F>::value,
+                                          AWeightsT4F<BM, BK>, AWeightsT4<BM, BK>>::type,
+                AWeightsT<BM, BK>>::type>::type>::type;
     using BLd = BL;
     const float *x, *w;
     float *y, *part;
@@ -852,7 +953,11 @@ struct FwdProblem {
         kb = z * kchunk;
         ke = min(K, kb + kchunk);
     }
-    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const { a.init(w, M, K, m0, tid); }
+    __device__ __forceinline__ void init_a(AL &a, int m0, int tid, int) const
+    {
+        if constexpr (RowTaps<BL>::value) a.init_rows(w, M, g.C * g.KS * g.KS, m0);
+        else a.init(w, M, K, m0, tid);
+    }
     __device__ __forceinline__ void init_b(BL &b, int n0, int tid, int) const { b.init(x, g, N, n0, tid); }
     __device__ __forceinline__ void store(int m, int n, float v, int z) const
     {
@@ -2251,6 +2356,17 @@ static bool fc_geom(const ConvGeom &g) { return g.KS == 1 && g.H == 1 && g.W == 
 // 5x5 filters with a filter count divisible by 4 take the padded-tap
 // loaders (BIm2colK<5> / AWeightsT4K)
 static bool fwd_padded_taps(const ConvGeom &g) { return g.KS == 5 && (g.F & 3) == 0; }
+// 11x11 filters without padding (AlexNet's first layer), a filter count
+// divisible by 4: the row-tap loaders (k-tiles of two filter rows)
+constexpr int ROW_KS = 11;
+static bool fwd_row_taps(const ConvGeom &g)
+{
+    return g.KS == ROW_KS && g.P == 0 && (g.F & 3) == 0 && !fc_geom(g);
+}
+static int fwd_row_k(const ConvGeom &g)
+{
+    return (g.C * g.KS + 1) / 2 * BIm2colRow<ROW_KS>::BK;
+}
 
 // the shallow-im2col forward (k_conv_fwd_smallk) takes these geometries
 static bool fwd_small_k(const ConvGeom &g)
@@ -2368,6 +2484,10 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
         pl.bk = BIm2colK<5>::BK;
         K = g.C * pl.bk;
         if (M > 64 && M <= 96) pl.bm = 96;  // three 32-row MFMA tiles per wave
+    } else if (fwd_row_taps(g)) {  // 11x11: two filter rows per k-tile
+        pl.bk = BIm2colRow<ROW_KS>::BK;
+        K = fwd_row_k(g);
+        if (M > 64 && M <= 96) pl.bm = 96;
     } else if (M > 64 && M <= 96 && (M & 3) == 0 && g.KS != 3 && g.KS != 1) {
         pl.bm = 96;  // generic loader, 65-96 filters (AlexNet conv1: 96 of 128 rows)
     }
@@ -2515,6 +2635,12 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
             p.e = e;
             return launch_gemm(p, M, N, pl.splits, st);
         }
+        if (fwd_row_taps(g)) {
+            FwdProblem<BM, BIm2colRow<ROW_KS>, true, EPI> p{x, w, y, part, g, M, N,
+                                                             fwd_row_k(g), pl.kchunk, pl.splits};
+            p.e = e;
+            return launch_gemm(p, M, N, pl.splits, st);
+        }
     }
     FwdProblem<BM, BIm2colAny<0>, false, EPI> p{x, w, y, part, g, M, N, K, pl.kchunk, pl.splits};
     p.e = e;
@@ -2530,6 +2656,12 @@ static int fwd_bm_padded(const ConvGeom &g, const FwdPlan &pl, const float *x, c
                          float *y, float *part, const Epi &e, hipStream_t st)
 {
     const int M = g.F, N = g.B * g.OH * g.OW;
+    if (fwd_row_taps(g)) {
+        FwdProblem<BM, BIm2colRow<ROW_KS>, true, EPI> p{x, w, y, part, g, M, N, fwd_row_k(g),
+                                                         pl.kchunk, pl.splits};
+        p.e = e;
+        return launch_gemm(p, M, N, pl.splits, st);
+    }
     if (!fwd_padded_taps(g)) {
         FwdProblem<BM, BIm2colAny<0>, true, EPI> p{x, w, y, part, g, M, N, g.C * g.KS * g.KS,
                                                    pl.kchunk, pl.splits};

@@ -122,6 +122,9 @@ CONV_SHAPES = [
     # split K on 169-position planes with N % 4 == 0: partials reduced in
     # their own order, four sums of one plane stored at once
     (4, 64, 13, 13, 96, 3, 1, 1),
+    # 11x11 without padding: k-tiles of two filter rows (row-tap loaders)
+    (2, 4, 23, 23, 64, 11, 2, 0),  # 44 filter rows: 22 pairs
+    (3, 5, 21, 21, 12, 11, 1, 0),  # 55 rows: the last pair half empty
     # one-pass 1x1 weight gradient (at most 16 filters, planes of <= 256):
     (3, 37, 7, 9, 16, 1, 1, 0),    # channels not a multiple of 4, odd plane
     (2, 5, 16, 16, 1, 1, 1, 0),    # one filter, a 256-position plane
@@ -705,8 +708,10 @@ def test_bias_ops(gpu, oracle, B, n, sp):
     (3, 5, 9, 7, 10, 3, 1, 1),        # scalar loaders, ragged tiles
     (2, 96, 9, 9, 80, 5, 1, 2),       # padded-tap 5x5, 96-row tiles
     (2, 16, 13, 13, 24, 5, 1, 2),
-    (2, 3, 35, 35, 8, 11, 4, 0),      # generic loader, stride 4
-    (2, 3, 35, 35, 96, 11, 4, 0),     # generic loader, 96-row tiles
+    (2, 3, 35, 35, 8, 11, 4, 0),      # row-tap loaders (11x11, no padding), stride 4
+    (2, 3, 35, 35, 96, 11, 4, 0),     # row-tap loaders, 96-row tiles
+    (4, 3, 227, 227, 96, 11, 4, 0),   # AlexNet conv1 at batch 4
+    (2, 3, 35, 35, 96, 7, 4, 0),      # generic loader, 96-row tiles
     (2, 512, 8, 8, 10, 1, 1, 0),      # 1x1
     (128, 256, 8, 8, 512, 3, 1, 1),   # K split in two inside one workgroup
     (8, 64, 1, 1, 48, 1, 1, 0),       # fully connected GEMM
