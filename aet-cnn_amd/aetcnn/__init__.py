@@ -692,7 +692,7 @@ def augment_image(src: np.ndarray, augment: Augment, seed: int, batch_no: int,
 
 
 def image_load(path: str, w: int, h: int, c: int) -> np.ndarray:
-    """an_image_load: a PNG / PPM / PGM file as float planes [c][h][w]"""
+    """an_image_load: a PNG / JPEG / PPM / PGM file as float planes [c][h][w]"""
     dst = np.empty((c, h, w), np.float32)
     check(net_lib().an_image_load(os.fsencode(path), w, h, c, dst.ctypes.data), "an_image_load")
     return dst

@@ -2180,13 +2180,25 @@ __global__ void __launch_bounds__(256) k_prepare_filters(PrepTable tab)
         return;
     }
     // flip: one thread per (filter, channel) copies its KK taps; neighbouring
-    // threads read adjacent tap runs and write adjacent channels of a tap
+    // threads read adjacent tap runs and write adjacent channels of a tap.
+    // 3x3 (and 5x5) filters load all their taps before the first store.
     const int fc = (b - J.tiles_t) * 256 + threadIdx.x;
     if (fc >= J.M * J.C) return;
     const int f = fc / J.C, c = fc - f * J.C, KK = J.KK;
     const float *src = J.w + (size_t)fc * KK;
     float *dst = J.wft + (size_t)f * KK * J.C + c;
-    for (int tap = 0; tap < KK; ++tap) dst[(size_t)tap * J.C] = src[KK - 1 - tap];
+    auto flip = [&](auto kk) {
+        constexpr int T = decltype(kk)::value;
+        float v[T];
+#pragma unroll
+        for (int tap = 0; tap < T; ++tap) v[tap] = src[T - 1 - tap];
+#pragma unroll
+        for (int tap = 0; tap < T; ++tap) dst[(size_t)tap * J.C] = v[tap];
+    };
+    if (KK == 9) flip(std::integral_constant<int, 9>());
+    else if (KK == 25) flip(std::integral_constant<int, 25>());
+    else
+        for (int tap = 0; tap < KK; ++tap) dst[(size_t)tap * J.C] = src[KK - 1 - tap];
 }
 
 // ---------------------------------------------------------------------------

@@ -20,13 +20,15 @@
  *
  * The reference decodes files with the vendored stb_image; this file has its
  * own decoders for PNG (8-bit, non-interlaced, every colour type; zlib's
- * inflate) and binary PPM / PGM.  The reference's random numbers come from
+ * inflate) and binary PPM / PGM, and host/jpeg.c one for baseline /
+ * extended sequential JPEG.  The reference's random numbers come from
  * the shared rand() stream; here every draw of image i of batch k is a
  * counter-based hash (an_feeder_sample) with its own salt, fed through the
  * reference's formulas with RAND_MAX = 2^31 - 1, so an image's augmentation
  * does not depend on the threads that load it.
  */
 #include "aetcnn_net.h"
+#include "jpeg.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -274,8 +276,11 @@ static int decode_file(const char *path, int *W, int *H, int *chans, unsigned ch
         rc = decode_png(path, buf, len, W, H, chans, px);
     else if (len >= 3 && buf[0] == 'P' && (buf[1] == '5' || buf[1] == '6'))
         rc = decode_pnm(path, buf, len, W, H, chans, px);
-    else
-        rc = fail(path, "unsupported format (PNG, binary PPM / PGM)");
+    else if (len >= 3 && buf[0] == 0xff && buf[1] == 0xd8 && buf[2] == 0xff) {
+        const char *why = NULL;
+        rc = an_jpeg_decode(buf, len, W, H, chans, px, &why) ? fail(path, why) : ACH_OK;
+    } else
+        rc = fail(path, "unsupported format (PNG, JPEG, binary PPM / PGM)");
     free(buf);
     return rc;
 }

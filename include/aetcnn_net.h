@@ -260,10 +260,12 @@ void an_image_distort(float *im, int w, int h, float hue, float sat, float val);
  * its row buffer cannot be allocated                                       */
 int an_image_resize(const float *src, int W, int H, int c, int w, int h, float *dst);
 /* NImage.reload (NImage.c:638-658): decodes a PNG (8-bit, non-interlaced;
- * grey, RGB, palette, grey+alpha, RGBA) or binary PPM / PGM file into host
- * planes dst[c][h][w] = sample / 255; the file must have exactly w x h
- * pixels and c channels (else ACH_EINVAL with a message).  The reference
- * decodes through stb_image; JPEG and other formats are not supported.     */
+ * grey, RGB, palette, grey+alpha, RGBA), a baseline / extended sequential
+ * JPEG (greyscale, YCbCr or Adobe RGB; any sampling; restart intervals) or
+ * a binary PPM / PGM file into host planes dst[c][h][w] = sample / 255; the
+ * file must have exactly w x h pixels and c channels (else ACH_EINVAL with a
+ * message).  The reference decodes through stb_image; progressive,
+ * arithmetic-coded, 12-bit and CMYK JPEG and other formats are refused.    */
 int an_image_load(const char *path, int w, int h, int c, float *dst);
 /* NImage.createImage (NImage.c:587-610): decodes a file at its own size
  * into *dst = malloc'd planes [c][*h][*w] (free with an_image_free), with
