@@ -270,19 +270,26 @@ def probe_setup(aetcnn, which, batch):
     xh, wh, dyh = config1_inputs(rng, batch, ci, co, hw, k, p)
     x, w, dy = D.from_numpy(xh), D.from_numpy(wh), D.from_numpy(dyh)
     y, dw = D(dyh.shape), D(wh.shape)
+    wt = D(wh.shape)
     wsz = max(ops.ach_conv_fwd_workspace(C.byref(d)),
               ops.ach_conv_bwd_filter_workspace(C.byref(d)), 256)
     ws = D(wsz // 4 + 64)
     if PROBES[which]["op"] == "fwd":
+        # the k-major filter made once, as the network does once per step
+        # for all its layers: each call is then the GEMM launch alone
+        job = aetcnn.FilterJob(d, w.ptr, wt.ptr, None)
+        aetcnn.check(ops.ach_conv_prepare_filters(1, C.byref(job), stream), "prepare")
+
         def call():
-            aetcnn.check(ops.ach_conv_fwd(C.byref(d), x.ptr, w.ptr, y.ptr, ws.ptr, wsz, stream))
+            aetcnn.check(ops.ach_conv_fwd_prepared(C.byref(d), x.ptr, wt.ptr, y.ptr, ws.ptr, wsz,
+                                                   stream))
     else:
         def call():
             aetcnn.check(ops.ach_conv_bwd_filter(C.byref(d), x.ptr, dy.ptr, dw.ptr, ws.ptr, wsz,
                                                  stream))
 
     def free():
-        for a in (x, w, dy, y, dw, ws):
+        for a in (x, w, dy, y, dw, ws, wt):
             a.free()
         ops.ach_stream_destroy(stream)
     oh = hw + 2 * p - k + 1
@@ -292,11 +299,11 @@ def probe_setup(aetcnn, which, batch):
 
 def roofline_phase(aetcnn, which, batch, reps):
     """A probe launched `reps` times back to back with HIP events around the
-    run on the probe's stream.  The forward call is the filter transpose
-    (k_weights_kmajor, ~1.5%) and the GEMM (128 x 128 tiles, 512 of them,
-    K unsplit); the weight-gradient call is the GEMM over chunked K and its
-    fixed-order split-K reduction (~5%).  The average is the whole call, so
-    it under-states the GEMM's own rate."""
+    run on the probe's stream.  The forward call is the GEMM launch alone
+    (ach_conv_fwd_prepared on a k-major filter made once: 512 workgroups of
+    two K groups over 128 x 128 tiles), so the average is that kernel's; the
+    weight-gradient call is the GEMM over chunked K and its fixed-order
+    split-K reduction (~5%), whose average is the whole call."""
     ops = aetcnn.ops()
     call, stream, free, flop, shape = probe_setup(aetcnn, which, batch)
     ms = time_launch(ops, stream, call, reps)
