@@ -142,17 +142,26 @@ def write_png(path, pix):
                      chunk(b"IDAT", zlib.compress(raw)) + chunk(b"IEND", b""))
 
 
-def test_paths_source(gpu, tmp_path):
+@pytest.mark.parametrize("fmt", ["png", "jpg"])
+def test_paths_source(gpu, tmp_path, fmt):
     """An image list with labels from path substrings (the reference's
     training list and fillTruthSmooth): every fed image is the augmented
-    decoded file, its truth the one-hot of the label in its name."""
+    decoded file, its truth the one-hot of the label in its name.  PNG and
+    (4:2:0 baseline) JPEG files; a JPEG's decoded pixels are the host
+    decoder's (an_image_load)."""
     rng = np.random.default_rng(1)
     (tmp_path / "train").mkdir()
     paths, pix = [], []
     for k in range(13):
-        p = tmp_path / "train" / f"img{k}{LABELS[k % 10]}.png"
+        p = tmp_path / "train" / f"img{k}{LABELS[k % 10]}.{fmt}"
         img = rng.integers(0, 256, (32, 32, 3), dtype=np.uint8)
-        write_png(p, img)
+        if fmt == "png":
+            write_png(p, img)
+        else:
+            from jpeg_writer import encode
+            p.write_bytes(encode(img, quality=90, sampling=((2, 2), (1, 1), (1, 1)))[0])
+            dec = aetcnn.image_load(str(p), 32, 32, 3)
+            img = np.rint(np.transpose(dec, (1, 2, 0)) * 255).astype(np.uint8)
         paths.append(str(p))
         pix.append(img)
     lst = tmp_path / "train.list"
