@@ -298,39 +298,50 @@ static int read_sof(jpg_t *j, const unsigned char *s, int len)
 }
 
 /* ---- sample reconstruction ---------------------------------------------------- */
-static uint8_t clamp255(double v)
-{
-    const double r = floor(v + 0.5);
-    return (uint8_t)(r < 0 ? 0 : (r > 255 ? 255 : r));
-}
 
 /* C(u)/2 * cos((2x+1) u pi / 16), set once for every decoding thread */
-static double cs[8][8];
+/* cst[u][x] = C(u)/2 * cos((2x+1) u pi / 16), x fastest */
+static float cst[8][8];
 static pthread_once_t cs_once = PTHREAD_ONCE_INIT;
 static void cs_init(void)
 {
-    for (int x = 0; x < 8; ++x)
-        for (int u = 0; u < 8; ++u)
-            cs[x][u] = (u == 0 ? sqrt(0.5) : 1.0) * 0.5 * cos((2 * x + 1) * u * M_PI / 16);
+    for (int u = 0; u < 8; ++u)
+        for (int x = 0; x < 8; ++x)
+            cst[u][x] = (float)((u == 0 ? sqrt(0.5) : 1.0) * 0.5 * cos((2 * x + 1) * u * M_PI / 16));
 }
 
-/* dequantised block -> 8x8 samples (T.81 A.3.3, separable, in double) */
+/* the nearest level (halves up), clamped to 0..255: for v in (0, 255)
+ * truncating v + 0.5 is floor(v + 0.5) */
+static inline uint8_t clamp255f(float v)
+{
+    return v <= 0.f ? 0 : (v >= 255.f ? 255 : (uint8_t)(int)(v + 0.5f));
+}
+
+/* dequantised block -> 8x8 samples (T.81 A.3.3, separable, in float; rows
+ * whose AC coefficients are all zero take their constant directly, which
+ * most rows of a quantised block are) */
 static void idct8x8(const int16_t *blk, const uint16_t *q, uint8_t *out, int stride)
 {
-    double f[64], t[64];
-    for (int i = 0; i < 64; ++i) f[i] = (double)blk[i] * q[i];
-    for (int v = 0; v < 8; ++v) /* rows: t[v][x] = sum_u cs[x][u] f[v][u] */
-        for (int x = 0; x < 8; ++x) {
-            double s = 0;
-            for (int u = 0; u < 8; ++u) s += cs[x][u] * f[v * 8 + u];
-            t[v * 8 + x] = s;
+    float t[8][8], o[8];
+    /* rows: t[v][x] = sum_u cst[u][x] F[v][u], over the nonzero F only */
+    for (int v = 0; v < 8; ++v) {
+        for (int x = 0; x < 8; ++x) t[v][x] = 0.f;
+        for (int u = 0; u < 8; ++u) {
+            const int c = blk[v * 8 + u];
+            if (!c) continue;
+            const float fu = (float)c * q[v * 8 + u];
+            for (int x = 0; x < 8; ++x) t[v][x] += cst[u][x] * fu;
         }
-    for (int y = 0; y < 8; ++y)
-        for (int x = 0; x < 8; ++x) {
-            double s = 0;
-            for (int v = 0; v < 8; ++v) s += cs[y][v] * t[v * 8 + x];
-            out[y * stride + x] = clamp255(s + 128.0);
+    }
+    /* columns: out[y][x] = sum_v cst[v][y] t[v][x] */
+    for (int y = 0; y < 8; ++y) {
+        for (int x = 0; x < 8; ++x) o[x] = 128.f;
+        for (int v = 0; v < 8; ++v) {
+            const float cv = cst[v][y];
+            for (int x = 0; x < 8; ++x) o[x] += cv * t[v][x];
         }
+        for (int x = 0; x < 8; ++x) out[y * stride + x] = clamp255f(o[x]);
+    }
 }
 
 /* a component's samples at its own resolution: [bh*8][bw*8] */
@@ -351,18 +362,6 @@ static uint8_t *component_plane(jpg_t *j, comp_t *c)
     return pl;
 }
 
-/* 2x along one axis with the triangle filter: n input samples (stride is) ->
- * 2n outputs (stride os); the nearer input weighs 3/4, the other 1/4 */
-static void up2(const int *in, int n, int is, int *out, int os, int scale, int bias)
-{
-    for (int i = 0; i < n; ++i) {
-        const int c = in[i * is], l = in[(i > 0 ? i - 1 : 0) * is],
-                  r = in[(i + 1 < n ? i + 1 : n - 1) * is];
-        out[(2 * i) * os] = (3 * c + l) * scale + bias;
-        out[(2 * i + 1) * os] = (3 * c + r) * scale + bias;
-    }
-}
-
 /* the component resampled to W x H (full resolution), 0..255 */
 static uint8_t *upsample(jpg_t *j, comp_t *c, const uint8_t *pl)
 {
@@ -376,41 +375,47 @@ static uint8_t *upsample(jpg_t *j, comp_t *c, const uint8_t *pl)
         return out;
     }
     if (exact && fx <= 2 && fy <= 2) {
-        /* triangle filter per doubled axis: the products carry 4 (one axis)
-         * or 16 (both) times the sample, rounded half up once at the end */
-        const int cw = c->xw, ch = c->yh;
-        const int ow = cw * fx, oh = ch * fy;
-        int *a = (int *)malloc(sizeof(int) * (size_t)ow * ch);
-        int *b = (int *)malloc(sizeof(int) * (size_t)ow * oh);
-        int *row = (int *)malloc(sizeof(int) * (size_t)(cw > ch ? cw : ch));
-        if (!a || !b || !row) {
-            free(a);
-            free(b);
-            free(row);
+        /* triangle filter per doubled axis (the nearer input sample weighs
+         * 3/4, the next one 1/4, edges repeat): one output row at a time, the
+         * vertical pass first; the integer sums carry 4 (one axis) or 16
+         * (both) times the sample and are rounded half up once at the end */
+        const int cw = c->xw, ch = c->yh, ow = cw * fx, oh = ch * fy;
+        int *v = (int *)malloc(sizeof(int) * (size_t)cw);
+        int *h = (int *)malloc(sizeof(int) * (size_t)ow);
+        if (!v || !h) {
+            free(v);
+            free(h);
             free(out);
             return NULL;
         }
-        for (int y = 0; y < ch; ++y) { /* horizontal */
-            for (int x = 0; x < cw; ++x) row[x] = pl[(size_t)y * pw + x];
-            if (fx == 2) up2(row, cw, 1, a + (size_t)y * ow, 1, 1, 0);
-            else
-                for (int x = 0; x < cw; ++x) a[(size_t)y * ow + x] = row[x];
-        }
-        for (int x = 0; x < ow; ++x) { /* vertical */
-            if (fy == 2) up2(a + x, ch, ow, b + x, ow, 1, 0);
-            else
-                for (int y = 0; y < ch; ++y) b[(size_t)y * ow + x] = a[(size_t)y * ow + x];
-        }
-        const int sh = (fx == 2 ? 2 : 0) + (fy == 2 ? 2 : 0), half = sh ? 1 << (sh - 1) : 0;
-        for (int y = 0; y < H; ++y)
-            for (int x = 0; x < W; ++x) {
-                const int v = (b[(size_t)(y < oh ? y : oh - 1) * ow + (x < ow ? x : ow - 1)] +
-                               half) >> sh;
-                out[(size_t)y * W + x] = (uint8_t)(v > 255 ? 255 : v);
+        const int sh = 2 * (fx - 1) + 2 * (fy - 1), half = sh ? 1 << (sh - 1) : 0;
+        const int wn = W < ow ? W : ow;
+        for (int y = 0; y < H; ++y) {
+            const int oy = y < oh ? y : oh - 1;
+            if (fy == 2) {
+                const int i = oy >> 1,
+                          k = (oy & 1) ? (i + 1 < ch ? i + 1 : ch - 1) : (i > 0 ? i - 1 : 0);
+                const uint8_t *r0 = pl + (size_t)i * pw, *r1 = pl + (size_t)k * pw;
+                for (int x = 0; x < cw; ++x) v[x] = 3 * r0[x] + r1[x];
+            } else {
+                const uint8_t *r0 = pl + (size_t)oy * pw;
+                for (int x = 0; x < cw; ++x) v[x] = r0[x];
             }
-        free(a);
-        free(b);
-        free(row);
+            if (fx == 2) {
+                for (int x = 0; x < cw; ++x) {
+                    const int l = v[x > 0 ? x - 1 : 0], r = v[x + 1 < cw ? x + 1 : cw - 1];
+                    h[2 * x] = 3 * v[x] + l;
+                    h[2 * x + 1] = 3 * v[x] + r;
+                }
+            } else {
+                memcpy(h, v, sizeof(int) * (size_t)cw);
+            }
+            uint8_t *o = out + (size_t)y * W; /* the sums stay <= 255 after the shift */
+            for (int x = 0; x < wn; ++x) o[x] = (uint8_t)((h[x] + half) >> sh);
+            for (int x = wn; x < W; ++x) o[x] = o[wn - 1];
+        }
+        free(v);
+        free(h);
         return out;
     }
     /* other ratios: nearest sample (replication) */
@@ -568,10 +573,10 @@ int an_jpeg_decode(const unsigned char *buf, size_t len, int *Wp, int *Hp, int *
                     rgb[3 * i + 2] = full[2][i];
                     continue;
                 }
-                const double y = full[0][i], cb = full[1][i] - 128.0, cr = full[2][i] - 128.0;
-                rgb[3 * i] = clamp255(y + 1.402 * cr);
-                rgb[3 * i + 1] = clamp255(y - 0.344136 * cb - 0.714136 * cr);
-                rgb[3 * i + 2] = clamp255(y + 1.772 * cb);
+                const float y = full[0][i], cb = full[1][i] - 128.f, cr = full[2][i] - 128.f;
+                rgb[3 * i] = clamp255f(y + 1.402f * cr);
+                rgb[3 * i + 1] = clamp255f(y - 0.344136f * cb - 0.714136f * cr);
+                rgb[3 * i + 2] = clamp255f(y + 1.772f * cb);
             }
         }
         for (int i = 0; i < 3; ++i) free(full[i]);
