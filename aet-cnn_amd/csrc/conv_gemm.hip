@@ -839,8 +839,8 @@ struct BWgradC {
 };
 
 // ---------------------------------------------------------------------------
-// Plain row-major GEMM operands (Gemm.c:116-144), BK = 16.
-template <bool T, int BR>
+// Plain row-major GEMM operands (Gemm.c:116-144), k-tiles of BK_ (16 or 32).
+template <bool T, int BR, int BK_ = 16>
 struct PlainOperand {
     // element (r, k) of op(X) where X is [R][K] (T = 0) or [K][R] (T = 1);
     // thread map: T = 0 -> k fastest (k = tid%16), T = 1 -> r fastest.
@@ -848,7 +848,7 @@ struct PlainOperand {
     // R-1: they feed only output rows / columns that are never stored); a
     // k-tile adds one uniform offset, and only a k-tile that reaches past
     // the end of its K range tests k per element (zero past the end).
-    static constexpr int BK = 16, RN = BR * BK / GNT, RA = RN, RB = RN, PAD = T ? LDP : 1;
+    static constexpr int BK = BK_, RN = BR * BK / GNT, RA = RN, RB = RN, PAD = T ? LDP : 1;
     __amdgpu_buffer_rsrc_t rs;
     int K, ld, r0;
     unsigned voff[RN];
@@ -1180,14 +1180,14 @@ struct GemmProblem {
 // Forward / input gradient: M = F, N = B, K = C; A = the k-major filter
 // Wt[K][M] (m contiguous), B[k][n] = x[n][k] read along k (PlainOperand,
 // k fastest); the K split and the output layout are those of FwdProblem.
-template <int BM_, bool VECA, bool EPI = false, bool NAT = false>
+template <int BM_, bool VECA, bool EPI = false, bool NAT = false, int BK_ = 16>
 struct FcProblem {
-    static constexpr int BM = BM_, BN = 128, BK = 16;
+    static constexpr int BM = BM_, BN = 128, BK = BK_;
     // NAT: w is the filter itself, W[M][K]; else its k-major copy Wt[K][M]
     using AL = typename std::conditional<
         NAT, AWeightsN<BM, BK>,
         typename std::conditional<VECA, AWeightsT4<BM, BK>, AWeightsT<BM, BK>>::type>::type;
-    using BLd = PlainOperand<false, 128>;
+    using BLd = PlainOperand<false, 128, BK>;
     const float *x, *w;
     float *y, *part;
     int M, N, K, kchunk, splits;
@@ -2364,6 +2364,10 @@ struct FwdPlan {
 // a 1x1 convolution of a 1x1 input (the fully connected layers once geom()
 // has flattened them): FcProblem / FcWgradProblem
 static bool fc_geom(const ConvGeom &g) { return g.KS == 1 && g.H == 1 && g.W == 1 && g.P == 0; }
+// k-tile of the fully connected GEMMs with 128-row tiles: their grids give
+// one 8-wave workgroup per CU (two waves per SIMD), too few to hide the
+// operand loads behind one 16-wide k-tile of MFMAs
+constexpr int FC_BK = 32;
 
 // 5x5 filters with a filter count divisible by 4 take the padded-tap
 // loaders (BIm2colK<5> / AWeightsT4K)
@@ -2491,7 +2495,7 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
     // the 16x16 layers of darknet run unsplit (512 tiles, no partial sums),
     // measured 1.2% faster on the step than 256 x 128 tiles split in two
     pl.bm = M <= 32 ? 32 : (M <= 64 ? 64 : 128);
-    pl.bk = g.KS == 3 ? BIm2col3::BK : 16;
+    pl.bk = g.KS == 3 ? BIm2col3::BK : (fc_geom(g) && pl.bm == 128 ? FC_BK : 16);
     if (fwd_padded_taps(g)) {  // 5x5: one channel + a zero row per k-tile
         pl.bk = BIm2colK<5>::BK;
         K = g.C * pl.bk;
@@ -2505,6 +2509,9 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
     }
     const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + 127) / 128);
     const int ktiles = (K + pl.bk - 1) / pl.bk;
+    // k-tiles per slice at least: 8, or 4 of the fully connected GEMMs'
+    // 32-wide ones (128 K either way)
+    const int min_kt = pl.bk == FC_BK && fc_geom(g) ? 4 : 8;
     int s = 1;
     // the padded-tap kernel fits two workgroups per CU: aim at two rounds
     // (measured 0.5% faster on AlexNet than one).  Input gradients (kg_ok
@@ -2523,7 +2530,7 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
         // AlexNet when its input gradients ran the same rule)
         s = (target + tiles / 2) / tiles;
         if (s > 32) s = 32;
-        if (s > ktiles / 8) s = ktiles / 8;  // keep >= 8 k-tiles per slice
+        if (s > ktiles / min_kt) s = ktiles / min_kt;
         if (s < 1) s = 1;
     }
     // Two K groups per 512-thread workgroup (k_mfma_gemm<P, 2>) for 3x3
@@ -2556,7 +2563,7 @@ static FwdPlan fwd_plan(const ConvGeom &g, bool kg_ok = true)
     // count is raised by one for it.  Alone: FC7 (4096 -> 4096, batch 128)
     // forward 66.5 -> 56.4 us, input gradient 61.1 -> 51.9 us.
     const bool fc_pairs = fc_geom(g) && pl.bm == 128 && (K % pl.bk) == 0;
-    if (fc_pairs && (s & 1) && s > 1 && s + 1 <= ktiles / 8 && ktiles % (s + 1) == 0) s += 1;
+    if (fc_pairs && (s & 1) && s > 1 && s + 1 <= ktiles / min_kt && ktiles % (s + 1) == 0) s += 1;
     pl.kchunk = ((ktiles + s - 1) / s) * pl.bk;
     pl.splits = (K + pl.kchunk - 1) / pl.kchunk;
     if (fwd_small_k(g)) pl.splits = 1;  // k_conv_fwd_smallk: whole K per tile
@@ -2611,22 +2618,25 @@ static int fwd_bm(const ConvGeom &g, const FwdPlan &pl, const float *x, const fl
     if constexpr (BM <= 128) {
         if (fc_geom(g)) {
             const size_t xb = (size_t)N * K * sizeof(float);
+            constexpr int FBK = BM == 128 ? FC_BK : 16;
             if (w_nat) {
-                FcProblem<BM, false, EPI, true> p{x, w, y, part, M, N, K, pl.kchunk, psplits,
-                                                  xb};
+                FcProblem<BM, false, EPI, true, FBK> p{x, w, y, part, M, N, K, pl.kchunk,
+                                                       psplits, xb};
                 p.e = e;
                 if constexpr (BM == 128)
                     if (kg2) return launch_gemm<decltype(p), 2>(p, M, N, pl.splits, st);
                 return launch_gemm(p, M, N, pl.splits, st);
             }
             if ((M & 3) == 0) {
-                FcProblem<BM, true, EPI> p{x, w, y, part, M, N, K, pl.kchunk, psplits, xb};
+                FcProblem<BM, true, EPI, false, FBK> p{x, w, y, part, M, N, K, pl.kchunk,
+                                                       psplits, xb};
                 p.e = e;
                 if constexpr (BM == 128)
                     if (kg2) return launch_gemm<decltype(p), 2>(p, M, N, pl.splits, st);
                 return launch_gemm(p, M, N, pl.splits, st);
             }
-            FcProblem<BM, false, EPI> p{x, w, y, part, M, N, K, pl.kchunk, psplits, xb};
+            FcProblem<BM, false, EPI, false, FBK> p{x, w, y, part, M, N, K, pl.kchunk, psplits,
+                                                    xb};
             p.e = e;
             if constexpr (BM == 128)
                 if (kg2) return launch_gemm<decltype(p), 2>(p, M, N, pl.splits, st);

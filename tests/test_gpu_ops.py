@@ -119,6 +119,8 @@ CONV_SHAPES = [
     (16, 256, 3, 3, 200, 3, 1, 0), # kernel covering a 3x3 input: 2304 -> 200
     (8, 64, 1, 1, 48, 1, 1, 0),    # 64 -> 48, 64-row tiles
     (16, 2048, 1, 1, 8192, 1, 1, 0),  # pairs of K slices per workgroup (fwd and dgrad)
+    (4, 1000, 1, 1, 256, 1, 1, 0),  # 128-row tiles, K ending inside a 32-wide k-tile
+    (3, 1001, 1, 1, 130, 1, 1, 0),  # K and M not multiples of 4: scalar loaders
     # split K on 169-position planes with N % 4 == 0: partials reduced in
     # their own order, four sums of one plane stored at once
     (4, 64, 13, 13, 96, 3, 1, 1),
