@@ -932,6 +932,8 @@ struct Epi {
 template <int BM_, class BL, bool VECA = false, bool EPI = false>
 struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
+    // the next B tile is stored two k-steps before the end of a k-tile
+    static constexpr bool EARLY_B = true;
     // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
     using AL = typename std::conditional<
         RowTaps<BL>::value, AWeightsT4Row<BM, RowTaps<BL>::ks>,
@@ -1111,6 +1113,7 @@ struct WgradProblem {
 template <int BM_, int BN_, int KS_T>
 struct WgradProblemC {
     static constexpr int kWPE = 4;  // waves per SIMD (k_mfma_gemm)
+    static constexpr bool EARLY_B = false;  // (k_mfma_gemm's KB_STORE)
     static constexpr int BM = BM_, BN = BN_, BK = WGRAD_BK;
     using AL = AWgradC<BM, BK>;
     using BLd = BWgradC<BN, BK, KS_T>;
@@ -1183,6 +1186,7 @@ struct GemmProblem {
 template <int BM_, bool VECA, bool EPI = false, bool NAT = false, int BK_ = 16>
 struct FcProblem {
     static constexpr int BM = BM_, BN = 128, BK = BK_;
+    static constexpr bool EARLY_B = true;
     // NAT: w is the filter itself, W[M][K]; else its k-major copy Wt[K][M]
     using AL = typename std::conditional<
         NAT, AWeightsN<BM, BK>,
@@ -1218,6 +1222,7 @@ struct FcProblem {
 // images with a fixed-order reduction when planned).
 template <int BM_, bool VECA>
 struct FcWgradProblem {
+    static constexpr bool EARLY_B = false;  // (k_mfma_gemm's KB_STORE)
     // 4 waves per SIMD (k_mfma_gemm): accumulators in VGPRs, 118-122
     // registers instead of 104 + 64 AGPRs; AlexNet step 7.65 -> 7.57 ms
     static constexpr int kWPE = 4;
@@ -1267,6 +1272,9 @@ struct has_store_tile<P, std::void_t<decltype(std::declval<const P &>().store_ti
 // other stream (batch-norm backward reduction: 44 VGPRs, one wave per SIMD
 // beside the 152-register waves before); darknet step 6.69 -> 6.64 ms,
 // AlexNet 7.69 -> 7.65 ms, the GEMM alone unchanged.
+template <class P, class = void> struct early_b_store : std::false_type {};
+template <class P>
+struct early_b_store<P, std::void_t<decltype(P::EARLY_B)>> : std::bool_constant<P::EARLY_B> {};
 template <class P, class = void> struct WavesPerEU { static constexpr int v = 1; };
 template <class P> struct WavesPerEU<P, std::void_t<decltype(P::kWPE)>> {
     static constexpr int v = P::kWPE;
@@ -1362,6 +1370,14 @@ k_mfma_gemm(P p, int mt, int nt)
 
     const int lrow = lane >> 5, lcol = lane & 31;
     constexpr int KB_LOAD = BK > 2 ? 2 : 0;  // k-step that issues the B loads
+    // k-step that stores the B operand's next tile: two before the last for
+    // problems that ask for it (EARLY_B) when the k-tile allows, so the
+    // stores complete behind the last MFMAs and the wait before the barrier
+    // is short.  The forward / input-gradient and fully connected problems
+    // take it (forward probe -1.5%, AlexNet step -0.9%, darknet unchanged);
+    // the weight-gradient problems do not: they run beside the critical
+    // stream, and faster they made the darknet step 1.3% slower.
+    constexpr int KB_STORE = BK >= 8 && early_b_store<P>::value ? BK - 4 : BK - 2;
     for (int kt = 0; kt < nkt; ++kt) {
         const int cur = kt & 1;
         // next k-tile (past ke on the last tile: the loaders read zeros or
@@ -1396,10 +1412,8 @@ k_mfma_gemm(P p, int mt, int nt)
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][i], b[s][j], acc[i][j],
                                                                      0, 0, 0);
-            if (kk == BK - 2) {
-                al.template store<LA>(As[cur ^ 1], ra);
-                bl.template store<LB>(Bs[cur ^ 1], rb);
-            }
+            if (kk == KB_STORE) bl.template store<LB>(Bs[cur ^ 1], rb);
+            if (kk == BK - 2) al.template store<LA>(As[cur ^ 1], ra);
             // interleave: per MFMA one LDS read, a few VALU and one global
             // load (k-steps 0 and 2) or two LDS writes (last k-step)
             // (group masks: 0x008 MFMA, 0x100 DS read, 0x002 VALU,
@@ -1412,7 +1426,7 @@ k_mfma_gemm(P p, int mt, int nt)
                     __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
                 }
-            } else if (kk == BK - 2) {
+            } else if (kk == BK - 2 || kk == KB_STORE) {
 #pragma unroll
                 for (int t = 0; t < TM * TN; ++t) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
