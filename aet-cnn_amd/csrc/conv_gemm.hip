@@ -155,6 +155,7 @@ __device__ __forceinline__ float4 bload4_so(__amdgpu_buffer_rsrc_t r, unsigned v
 
 template <int BM, int BK>
 struct AWeightsT4 {
+    static constexpr bool SPILL = BK == 18;
     static constexpr int C4 = BM / 4;                      // float4 per tile row
     static constexpr int NV = (BK * C4 + GNT - 1) / GNT;   // float4 per thread
     static constexpr int RA = 4 * NV, PAD = LDP_FWD;
@@ -179,21 +180,31 @@ struct AWeightsT4 {
         }
     }
     // The last pass may run past the BK rows of the stage (BK*C4 not a
-    // multiple of 256: 18 x 32 float4 for 3x3 filters and 128-row tiles);
-    // those stores are skipped.  For the 3x3 and 5x5 tiles of 128 and 256
-    // rows the cut falls on a wave boundary, so the branch is uniform per
-    // wave.  (Allocating the
-    // overflow rows instead cost 6 of the 24 A rows of LDS and left 3
-    // 128-row workgroups per CU instead of 4.)
+    // multiple of 256: 18 x 32 float4 for 3x3 filters and 128-row tiles).
+    // With SPILL (the 3x3 k-tiles) those lanes store to a 1 KB slot that
+    // nobody reads (shared by the overflowing waves) instead of branching
+    // around the store, so the store stays in the MFMA interleave and the
+    // barrier no longer waits for it: darknet step -0.4%, AlexNet unchanged;
+    // the 5x5 k-tiles (BK = 26) keep the branch (AlexNet +0.3% with it).
+    // (Allocating the overflow rows instead cost 6 of the 24 A rows of LDS
+    // and left 3 128-row workgroups per CU instead of 4.)
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
     {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int f = ltid() + GNT * i;
-            if (i + 1 < NV || NV * GNT <= BK * C4 || f < BK * C4)
-                *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) =
-                    make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
+            const float4 v = make_float4(ra[4 * i], ra[4 * i + 1], ra[4 * i + 2], ra[4 * i + 3]);
+            if (i + 1 < NV || NV * GNT <= BK * C4) {
+                *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) = v;
+            } else if constexpr (!SPILL) {
+                if (f < BK * C4) *reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)]) = v;
+            } else {
+                __shared__ float4 spill[64];
+                float4 *dst = f < BK * C4 ? reinterpret_cast<float4 *>(&S[f / C4][4 * (f % C4)])
+                                          : &spill[threadIdx.x & 63];
+                *dst = v;
+            }
         }
     }
 };
