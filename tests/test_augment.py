@@ -228,6 +228,34 @@ def test_distort_closed_forms():
     assert np.array_equal(im.ravel(), [1, 1, 0])
 
 
+def test_distort_matches_colorsys():
+    """distort = rgbToHsv, scale S and V, shift H (one wrap), hsvToRgb, clamp
+    to [0, 1] (NImage.c:201-323), recomputed in float64 with the standard
+    library's HSV conversions (colorsys, the same textbook algorithm in its
+    own arithmetic): random pixels and distortions, saturation and exposure
+    beyond 1 included, within float32 rounding."""
+    import colorsys
+    rng = np.random.default_rng(21)
+    for k in range(12):
+        im = rng.random((3, 9, 11), dtype=np.float32)
+        im[:, 0, :3] = rng.random(3, dtype=np.float32)[:, None]  # greys
+        hue = float(rng.uniform(-0.5, 0.5))
+        sat, val = float(rng.uniform(0.3, 1.8)), float(rng.uniform(0.3, 1.8))
+        got = distort(im, hue, sat, val)
+        want = np.empty_like(got, dtype=np.float64)
+        for y in range(im.shape[1]):
+            for x in range(im.shape[2]):
+                h, s_, v = colorsys.rgb_to_hsv(*(float(c) for c in im[:, y, x]))
+                s_, v = s_ * sat, v * val
+                h += hue
+                if h > 1:
+                    h -= 1
+                if h < 0:
+                    h += 1
+                want[:, y, x] = np.clip(colorsys.hsv_to_rgb(h, s_, v), 0, 1)
+        assert np.abs(got - want).max() <= 2e-6, (k, np.abs(got - want).max())
+
+
 def test_resize_closed_form():
     src = np.array([[[1.0, 3.0], [5.0, 9.0]]], np.float32)  # 1 x 2 x 2
     dst = np.empty((1, 3, 3), np.float32)
