@@ -34,6 +34,7 @@
 namespace ach {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int GNT = 256;     // threads per workgroup
 // thread index within a GNT-thread group: a GEMM workgroup may hold
@@ -945,6 +946,8 @@ struct FwdProblem {
     static constexpr int BM = BM_, BN = 128, BK = BL::BK;
     // the next B tile is stored two k-steps before the end of a k-tile
     static constexpr bool EARLY_B = true;
+    // the padded-tap loaders end every k-tile with a zero row
+    static constexpr bool ODD_K = PaddedTaps<BL>::value;
     // w points at the k-major copy Wt[K][M]; float4 loads when M % 4 == 0
     using AL = typename std::conditional<
         RowTaps<BL>::value, AWeightsT4Row<BM, RowTaps<BL>::ks>,
@@ -1283,6 +1286,9 @@ struct has_store_tile<P, std::void_t<decltype(std::declval<const P &>().store_ti
 // other stream (batch-norm backward reduction: 44 VGPRs, one wave per SIMD
 // beside the 152-register waves before); darknet step 6.69 -> 6.64 ms,
 // AlexNet 7.69 -> 7.65 ms, the GEMM alone unchanged.
+template <class P, class = void> struct odd_last_k : std::false_type {};
+template <class P>
+struct odd_last_k<P, std::void_t<decltype(P::ODD_K)>> : std::bool_constant<P::ODD_K> {};
 template <class P, class = void> struct early_b_store : std::false_type {};
 template <class P>
 struct early_b_store<P, std::void_t<decltype(P::EARLY_B)>> : std::bool_constant<P::EARLY_B> {};
@@ -1389,6 +1395,24 @@ k_mfma_gemm(P p, int mt, int nt)
     // the weight-gradient problems do not: they run beside the critical
     // stream, and faster they made the darknet step 1.3% slower.
     constexpr int KB_STORE = BK >= 8 && early_b_store<P>::value ? BK - 4 : BK - 2;
+    // ODD_K problems end every k-tile with a zero row (an odd tap count
+    // padded to whole k-steps).  They multiply row by row with two-block
+    // MFMAs (v_mfma_f32_32x32x1_2b_f32: two 32x32 outer products, one row of
+    // K each), each pairing two fragments that share an operand, which one
+    // half of the lanes broadcasts: ODD_COLS pairs a wave's two column
+    // fragments (A broadcast, CBSZ 1, ABID = the row's lane half), ODD_ROWS
+    // its row fragments 0 and 1 (B broadcast, BLGP 1 / 2).  A k-step of two
+    // rows issues as many MFMAs as before, and the last one, whose second
+    // row is the zero row, half as many (ODD_ROWS: one fewer).  The sums
+    // round after every row instead of every pair of rows.
+    constexpr bool ODD_COLS = odd_last_k<P>::value && TN == 2;
+    constexpr bool ODD_ROWS = odd_last_k<P>::value && TN == 1 && TM >= 2;
+    constexpr int NMF_LAST = ODD_COLS ? TM : (ODD_ROWS ? TM - 1 : TM * TN);
+    v32f accw[ODD_COLS ? TM : 1];  // ODD_COLS: fragments (i, 0) and (i, 1); ODD_ROWS: (0, 0) and (1, 0)
+#pragma unroll
+    for (int i = 0; i < (ODD_COLS ? TM : 1); ++i)
+#pragma unroll
+        for (int r = 0; r < 32; ++r) accw[i][r] = 0.f;
     for (int kt = 0; kt < nkt; ++kt) {
         const int cur = kt & 1;
         // next k-tile (past ke on the last tile: the loaders read zeros or
@@ -1398,31 +1422,61 @@ k_mfma_gemm(P p, int mt, int nt)
         // fragments of k-step kk+2 are read from LDS while the MFMAs of
         // k-step kk issue, so the LDS latency hides behind the matrix pipe
         float a[2][TM], b[2][TN];
+        float xo[2][2];  // ODD_COLS: B rows k, k+1 of both column fragments; ODD_ROWS: A of row fragments 0, 1
+        auto read_step = [&](int t, int k) {
+            if constexpr (ODD_COLS) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[0][i] = rda(cur, lrow, (i * WM + wm) * 32 + lcol);
+                for (int i = 0; i < TM; ++i) a[t][i] = rda(cur, k + lrow, (i * WM + wm) * 32 + lcol);
+                xo[t][0] = rdb(cur, k, (lrow * WN + wn) * 32 + lcol);
+                if (k + 2 < BK) xo[t][1] = rdb(cur, k + 1, (lrow * WN + wn) * 32 + lcol);
+            } else if constexpr (ODD_ROWS) {
+                xo[t][0] = rda(cur, k, (lrow * WM + wm) * 32 + lcol);
+                if (k + 2 < BK) xo[t][1] = rda(cur, k + 1, (lrow * WM + wm) * 32 + lcol);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[0][j] = rdb(cur, lrow, (j * WN + wn) * 32 + lcol);
+                for (int i = 2; i < TM; ++i) a[t][i] = rda(cur, k + lrow, (i * WM + wm) * 32 + lcol);
+                b[t][0] = rdb(cur, k + lrow, wn * 32 + lcol);
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) a[t][i] = rda(cur, k + lrow, (i * WM + wm) * 32 + lcol);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) b[t][j] = rdb(cur, k + lrow, (j * WN + wn) * 32 + lcol);
+            }
+        };
+        read_step(0, 0);
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
             const int s = (kk >> 1) & 1;
-            if (kk + 2 < BK) {
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-                    a[s ^ 1][i] = rda(cur, kk + 2 + lrow, (i * WM + wm) * 32 + lcol);
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    b[s ^ 1][j] = rdb(cur, kk + 2 + lrow, (j * WN + wn) * 32 + lcol);
-            }
+            if (kk + 2 < BK) read_step(s ^ 1, kk + 2);
             // keep the scheduler from sinking those reads below the MFMAs
             __builtin_amdgcn_sched_barrier(0);
             if (kk == 0) al.load(k0n, ke, ra);
             if (kk == KB_LOAD) bl.load(k0n, ke, rb);
+            if constexpr (ODD_COLS) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
+                    accw[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(a[s][i], xo[s][0], accw[i], 1, 0, 0);
+                if (kk + 2 < BK) {
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][i], b[s][j], acc[i][j],
-                                                                     0, 0, 0);
+                    for (int i = 0; i < TM; ++i)
+                        accw[i] = __builtin_amdgcn_mfma_f32_32x32x1f32(a[s][i], xo[s][1], accw[i], 1, 1,
+                                                                       0);
+                }
+            } else if constexpr (ODD_ROWS) {
+                accw[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(xo[s][0], b[s][0], accw[0], 0, 0, 1);
+                if (kk + 2 < BK)
+                    accw[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(xo[s][1], b[s][0], accw[0], 0, 0, 2);
+#pragma unroll
+                for (int i = 2; i < TM; ++i)
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][i], b[s][0], acc[i][0], 0, 0,
+                                                                     0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s][i], b[s][j], acc[i][j],
+                                                                         0, 0, 0);
+            }
             if (kk == KB_STORE) bl.template store<LB>(Bs[cur ^ 1], rb);
             if (kk == BK - 2) al.template store<LA>(As[cur ^ 1], ra);
             // interleave: per MFMA one LDS read, a few VALU and one global
@@ -1439,7 +1493,7 @@ k_mfma_gemm(P p, int mt, int nt)
                 }
             } else if (kk == BK - 2 || kk == KB_STORE) {
 #pragma unroll
-                for (int t = 0; t < TM * TN; ++t) {
+                for (int t = 0; t < (kk == BK - 2 ? NMF_LAST : TM * TN); ++t) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                     __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                     __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
@@ -1447,6 +1501,20 @@ k_mfma_gemm(P p, int mt, int nt)
             }
         }
         __syncthreads();
+    }
+    if constexpr (ODD_COLS) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            acc[i][0] = __builtin_shufflevector(accw[i], accw[i], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10,
+                                                11, 12, 13, 14, 15);
+            acc[i][1] = __builtin_shufflevector(accw[i], accw[i], 16, 17, 18, 19, 20, 21, 22, 23, 24,
+                                                25, 26, 27, 28, 29, 30, 31);
+        }
+    } else if constexpr (ODD_ROWS) {
+        acc[0][0] = __builtin_shufflevector(accw[0], accw[0], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11,
+                                            12, 13, 14, 15);
+        acc[1][0] = __builtin_shufflevector(accw[0], accw[0], 16, 17, 18, 19, 20, 21, 22, 23, 24, 25,
+                                            26, 27, 28, 29, 30, 31);
     }
 
     if constexpr (KG > 1) {
