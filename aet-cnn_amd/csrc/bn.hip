@@ -263,6 +263,84 @@ __global__ void __launch_bounds__(BN_NT) k_bn_apply(
                    biases[c], act);
 }
 
+// ---- forward of a small channel in one workgroup ---------------------------------
+// A channel of at most BN_CH_NT*V float4 (batch*HW <= 32768 floats: darknet's
+// 16x16 and 8x8 layers at batch 128) is loaded once into registers, summed
+// (double: each thread's values in order, then the block's fixed tree) and
+// normalized from the registers: one read and one write of the tensor in one
+// launch, instead of the statistics pass, the apply pass' second read and a
+// second launch.  The moments, the rolling statistics and the outputs are
+// those of k_bn_stats + k_bn_apply up to the order of the double sums; src
+// may be out (every thread writes only what it read, after the block's
+// barrier); xcopy / xnorm optional as in k_bn_apply.
+constexpr int BN_CH_NT = 1024;
+constexpr int BN_CH_MAXV = 8;  // float4 per thread
+template <int V>
+__global__ void __launch_bounds__(BN_CH_NT) k_bn_fwd_channel(
+    const float *src, float *xcopy, float *xnorm, float *out, int batch, int C, int HW, int hw4,
+    float *__restrict__ mean, float *__restrict__ variance, float *__restrict__ rmean,
+    float *__restrict__ rvar, const float *__restrict__ scales, const float *__restrict__ biases,
+    int act)
+{
+    __shared__ double sh[BN_CH_NT / 64];
+    __shared__ float sp[2];
+    const int c = blockIdx.x, tot = batch * hw4;
+    const float4 *s4 = reinterpret_cast<const float4 *>(src);
+    float4 v[V];
+    int at[V];
+    double s1 = 0, s2 = 0;
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        const int e = threadIdx.x + u * BN_CH_NT, b = e / hw4;
+        at[u] = e < tot ? (b * C + c) * hw4 + (e - b * hw4) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < V; ++u)
+        if (at[u] >= 0) v[u] = s4[at[u]];
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        if (at[u] < 0) continue;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float e = comp(v[u], k);
+            s1 += (double)e;
+            s2 += (double)(e * e);
+        }
+    }
+    const double t1 = block_sum<BN_CH_NT / 64>(s1, sh);
+    const double t2 = block_sum<BN_CH_NT / 64>(s2, sh);
+    if (threadIdx.x == 0) {
+        float m, var;
+        bn_moments(t1, t2, batch, HW, m, var);
+        mean[c] = m;
+        variance[c] = var;
+        if (rmean) {
+            const float keep = .9f, take = .1f;
+            float r = rmean[c] * keep;
+            rmean[c] = r + take * m;
+            r = rvar[c] * keep;
+            rvar[c] = r + take * var;
+        }
+        sp[0] = m;
+        sp[1] = bn_inv(var);
+    }
+    __syncthreads();
+    const float mu = sp[0], iv = sp[1], sc = scales[c], bb = biases[c];
+    float4 *o4 = reinterpret_cast<float4 *>(out);
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+        if (at[u] < 0) continue;
+        if (xcopy) reinterpret_cast<float4 *>(xcopy)[at[u]] = v[u];
+        float4 n, o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) comp(n, k) = (comp(v[u], k) - mu) * iv;
+        if (xnorm) reinterpret_cast<float4 *>(xnorm)[at[u]] = n;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) comp(o, k) = act_forward(__fmaf_rn(comp(n, k), sc, bb), act);
+        o4[at[u]] = o;
+    }
+}
+
 // ---- inference ------------------------------------------------------------------
 // NormData.normalizeByRoll (NormData.c:291-326): the rolling statistics
 // replace the batch statistics, inv = 1/(sqrt(rolling_var) + 1e-6) in double.
@@ -479,6 +557,19 @@ static int bn_fwd(const float *src, float *xcopy, float *xnorm, float *out, int 
                              aligned16(src) && aligned16(out) && aligned16(xcopy) &&
                                  aligned16(xnorm),
                              BN_FWD_APPLY_BLOCKS, BN_FWD_RED_BLOCKS);
+    // one workgroup per channel when the channel fits its registers and the
+    // channels alone give about a workgroup per CU
+    const long long ch4 = (long long)batch * p.hwv;
+    if (p.vec && C >= 128 && ch4 <= (long long)BN_CH_NT * BN_CH_MAXV) {
+        const int V = ch4 <= BN_CH_NT ? 1 : (ch4 <= 2 * BN_CH_NT ? 2 : (ch4 <= 4 * BN_CH_NT ? 4 : 8));
+        void (*kern)(const float *, float *, float *, float *, int, int, int, int, float *, float *,
+                     float *, float *, const float *, const float *, int) =
+            V == 1 ? k_bn_fwd_channel<1>
+                   : (V == 2 ? k_bn_fwd_channel<2> : (V == 4 ? k_bn_fwd_channel<4> : k_bn_fwd_channel<8>));
+        hipLaunchKernelGGL(kern, dim3(C), dim3(BN_CH_NT), 0, st, src, xcopy, xnorm, out, batch, C,
+                           HW, p.hwv, mean, variance, rmean, rvar, scales, biases, act);
+        return check_launch();
+    }
     if (p.vec)
         hipLaunchKernelGGL(k_bn_stats<true>, p.reduce_grid, dim3(BN_NT), 0, st, src, batch, C,
                            p.hwv, p.per, part);

@@ -254,7 +254,9 @@ def _bn_inputs(B, Cc, H, W, seed):
 
 
 @pytest.mark.parametrize("B,Cc,H,W", [(8, 16, 32, 32), (4, 24, 13, 13), (128, 32, 8, 8),
-                                      (3, 5, 1, 1)])
+                                      (3, 5, 1, 1),
+                                      # one workgroup per channel (at most 32768 values):
+                                      (32, 256, 16, 16), (7, 130, 6, 6), (9, 128, 2, 2)])
 @pytest.mark.parametrize("act", [aetcnn.LINEAR, aetcnn.LEAKY])
 def test_bn_train_fwd(gpu, oracle, B, Cc, H, W, act):
     out, sc, bi, rm, rv = _bn_inputs(B, Cc, H, W, B + Cc + act)
