@@ -1402,13 +1402,15 @@ k_mfma_gemm(P p, int mt, int nt)
     // half of the lanes broadcasts: ODD_COLS pairs a wave's two column
     // fragments (A broadcast, CBSZ 1, ABID = the row's lane half), ODD_ROWS
     // its row fragments 0 and 1 (B broadcast, BLGP 1 / 2).  A k-step of two
-    // rows issues as many MFMAs as before, and the last one, whose second
-    // row is the zero row, half as many (ODD_ROWS: one fewer).  The sums
-    // round after every row instead of every pair of rows.
+    // rows issues as many MFMAs as the 32x32x2 form, and the last one, whose
+    // second row is the zero row, half as many (ODD_ROWS: one fewer).  The
+    // sums round after every row instead of every pair of rows.
     constexpr bool ODD_COLS = odd_last_k<P>::value && TN == 2;
     constexpr bool ODD_ROWS = odd_last_k<P>::value && TN == 1 && TM >= 2;
     constexpr int NMF_LAST = ODD_COLS ? TM : (ODD_ROWS ? TM - 1 : TM * TN);
-    v32f accw[ODD_COLS ? TM : 1];  // ODD_COLS: fragments (i, 0) and (i, 1); ODD_ROWS: (0, 0) and (1, 0)
+    // pairs of accumulator fragments: ODD_COLS (i, 0) and (i, 1) for each i,
+    // ODD_ROWS (0, 0) and (1, 0)
+    v32f accw[ODD_COLS ? TM : 1];
 #pragma unroll
     for (int i = 0; i < (ODD_COLS ? TM : 1); ++i)
 #pragma unroll
@@ -1422,7 +1424,9 @@ k_mfma_gemm(P p, int mt, int nt)
         // fragments of k-step kk+2 are read from LDS while the MFMAs of
         // k-step kk issue, so the LDS latency hides behind the matrix pipe
         float a[2][TM], b[2][TN];
-        float xo[2][2];  // ODD_COLS: B rows k, k+1 of both column fragments; ODD_ROWS: A of row fragments 0, 1
+        // the broadcast pair operand of rows k and k+1: ODD_COLS the B values
+        // of both column fragments, ODD_ROWS the A values of row fragments 0, 1
+        float xo[2][2];
         auto read_step = [&](int t, int k) {
             if constexpr (ODD_COLS) {
 #pragma unroll
