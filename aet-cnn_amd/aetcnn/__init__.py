@@ -43,8 +43,9 @@ _u32 = C.c_uint32
 
 
 class ConvDesc(C.Structure):
+    """ach_conv_desc; stride_y 0 (the default) means the same as stride"""
     _fields_ = [("batch", _i), ("c", _i), ("h", _i), ("w", _i), ("n", _i),
-                ("size", _i), ("stride", _i), ("pad", _i)]
+                ("size", _i), ("stride", _i), ("pad", _i), ("stride_y", _i)]
 
 
 class LayerOptions(C.Structure):
@@ -145,6 +146,8 @@ _OPS = {
     "ach_maxpool_out": (_i, [_i, _i, _i, _i]),
     "ach_maxpool_fwd": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     "ach_maxpool_bwd": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp]),
+    "ach_maxpool_fwd_xy": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "ach_maxpool_bwd_xy": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp]),
     "ach_maxpool_bwd_act": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp]),
     "ach_maxpool_bwd_act_planes": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp,
                                         _vp]),
@@ -172,6 +175,8 @@ _NET = {
     "an_add_convolutional": (_i, [_vp, _i, _i, _i, _i, _i, _i]),
     "an_add_connected": (_i, [_vp, _i, _i, _i]),
     "an_add_maxpool": (_i, [_vp, _i, _i, _i]),
+    "an_add_convolutional_xy": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i]),
+    "an_add_maxpool_xy": (_i, [_vp, _i, _i, _i, _i]),
     "an_add_avgpool": (_i, [_vp]),
     "an_add_dropout": (_i, [_vp, _f]),
     "an_add_softmax": (_i, [_vp, _i, _f]),
@@ -386,8 +391,14 @@ class Network:
         o = LayerOptions(**cur)
         check(self.lib.an_set_layer_options(self.h, i, C.byref(o)), "an_set_layer_options")
 
-    def conv(self, filters, size, stride, pad, activation, bn):
-        r = self.lib.an_add_convolutional(self.h, filters, size, stride, pad, activation, int(bn))
+    def conv(self, filters, size, stride, pad, activation, bn, stride_y=None):
+        """stride is the width stride; stride_y (default: stride) the height one"""
+        if stride_y is None:
+            r = self.lib.an_add_convolutional(self.h, filters, size, stride, pad, activation,
+                                              int(bn))
+        else:
+            r = self.lib.an_add_convolutional_xy(self.h, filters, size, stride, stride_y, pad,
+                                                 activation, int(bn))
         if r < 0:
             raise ValueError(f"an_add_convolutional: {r}")
         return r
@@ -398,8 +409,11 @@ class Network:
             raise ValueError(f"an_add_connected: {r}")
         return r
 
-    def maxpool(self, size, stride, padding):
-        r = self.lib.an_add_maxpool(self.h, size, stride, padding)
+    def maxpool(self, size, stride, padding, stride_y=None):
+        if stride_y is None:
+            r = self.lib.an_add_maxpool(self.h, size, stride, padding)
+        else:
+            r = self.lib.an_add_maxpool_xy(self.h, size, stride, stride_y, padding)
         if r < 0:
             raise ValueError(f"an_add_maxpool: {r}")
         return r

@@ -13,9 +13,10 @@ import numpy as np
 LOGISTIC, RELU, LINEAR, LEAKY = 0, 1, 3, 7
 
 # name -> dict(batch, h, w, c, classes, lr, momentum, decay, layers)
-# layer tuples: ("conv", filters, size, stride, pad, activation, bn)
+# layer tuples: ("conv", filters, size, stride, pad, activation, bn[, stride_y])
 #               ("connected", outputs, activation, bn)
-#               ("maxpool", size, stride, padding)   ("avgpool",)
+#               ("maxpool", size, stride, padding[, stride_y])   ("avgpool",)
+# (stride is the width stride; stride_y, when given, the height stride)
 #               ("dropout", p)   ("softmax",)
 CONFIGS = {
     # config 0: tiny CNN
@@ -38,6 +39,18 @@ CONFIGS = {
                   layers=[("conv", 8, 3, 1, 1, LEAKY, 1), ("maxpool", 2, 2, 1),
                           ("connected", 24, LEAKY, 1), ("dropout", 0.5),
                           ("connected", 10, LINEAR, 0), ("softmax",)]),
+    # unequal width / height strides (test net, not a benchmark config): a
+    # conv entry's optional 8th field and a maxpool entry's optional 5th are
+    # the height stride (the 4th / 3rd being the width stride).  BN conv
+    # 2x1, pool 1x2, a plain conv (128-position planes) under a 2x1 pool, a
+    # 1x2 conv and a 2x1 1x1 conv.
+    "stridenet": dict(batch=16, h=16, w=32, c=3, classes=10, lr=0.05, momentum=0.9,
+                      decay=5e-4,
+                      layers=[("conv", 8, 3, 2, 1, LEAKY, 1, 1), ("maxpool", 2, 1, 1, 2),
+                              ("conv", 12, 3, 1, 1, RELU, 0), ("maxpool", 2, 2, 0, 1),
+                              ("conv", 16, 3, 1, 1, LEAKY, 0, 2),
+                              ("conv", 10, 1, 2, 0, LINEAR, 0, 1), ("avgpool",),
+                              ("softmax",)]),
     # config 4: AlexNet-style; FC layers expressed as convolutions
     "alexnet": dict(batch=128, h=227, w=227, c=3, classes=1000, lr=0.01, momentum=0.9,
                     decay=5e-4,
@@ -100,13 +113,15 @@ def step_gflop(name: str, batch: int | None = None) -> float:
     for layer in cfg["layers"]:
         if layer[0] == "conv":
             f, k, s, p = layer[1:5]
-            oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+            sy = layer[7] if len(layer) > 7 else s
+            oh, ow = (h + 2 * p - k) // sy + 1, (w + 2 * p - k) // s + 1
             tot += 2.0 * B * f * oh * ow * c * k * k * (2 if first else 3)
             first = False
             h, w, c = oh, ow, f
         elif layer[0] == "maxpool":
             k, s, p = layer[1:4]
-            h, w = (h + p - k) // s + 1, (w + p - k) // s + 1
+            sy = layer[4] if len(layer) > 4 else s
+            h, w = (h + p - k) // sy + 1, (w + p - k) // s + 1
         elif layer[0] == "avgpool":
             h = w = 1
     return tot / 1e9

@@ -2314,16 +2314,19 @@ static int launch_gemm(const P &p, int M, int N, int splits, hipStream_t st)
 static bool conv_ok(const ach_conv_desc *d)
 {
     return d && d->batch > 0 && d->c > 0 && d->h > 0 && d->w > 0 && d->n > 0 &&
-           d->size > 0 && d->stride > 0 && d->pad >= 0 &&
+           d->size > 0 && d->stride > 0 && d->stride_y >= 0 && d->pad >= 0 &&
            (d->h + 2 * d->pad - d->size) >= 0 && (d->w + 2 * d->pad - d->size) >= 0;
 }
+
+// height stride (stride_y 0: the width stride)
+static int stride_h(const ach_conv_desc *d) { return d->stride_y > 0 ? d->stride_y : d->stride; }
 
 static ConvGeom geom(const ach_conv_desc *d)
 {
     ConvGeom g;
     g.B = d->batch; g.C = d->c; g.H = d->h; g.W = d->w;
     g.F = d->n; g.KS = d->size; g.S = d->stride; g.P = d->pad;
-    g.OH = (d->h + 2 * d->pad - d->size) / d->stride + 1;
+    g.OH = (d->h + 2 * d->pad - d->size) / stride_h(d) + 1;
     g.OW = (d->w + 2 * d->pad - d->size) / d->stride + 1;
     // A kernel that covers the whole unpadded input (one output position: the
     // fully connected layers expressed as convolutions) is a 1x1 convolution
@@ -2349,6 +2352,61 @@ static bool fits_int(const ach_conv_desc *d)
     const double in = (double)g.B * g.C * g.H * g.W;
     const double out = (double)g.B * g.F * g.OH * g.OW;
     return in <= lim && out <= lim && (double)g.F * g.C * g.KS * g.KS <= lim;
+}
+
+// ---- unequal width / height strides ----------------------------------------
+// The reference's per-image passes (ConvolutionalLayer.c:790-803, 913-945),
+// each image's im2col, GEMM and col2im a device launch of ach_im2col /
+// ach_gemm / ach_col2im over one image's column buffer [C*k*k][OH*OW] in
+// the workspace.  The tiled implicit-GEMM loaders take one stride; a fully
+// connected geometry (one output position) is unaffected by the strides and
+// keeps its own path.
+static bool fc_geom(const ConvGeom &g);
+static bool conv_xy(const ach_conv_desc *d)
+{
+    return stride_h(d) != d->stride && !fc_geom(geom(d));
+}
+
+static size_t xy_col_bytes(const ConvGeom &g)
+{
+    return (size_t)g.C * g.KS * g.KS * g.OH * g.OW * sizeof(float);
+}
+
+// y_b = W * im2col(x_b); w is [F][K], or k-major [K][F] when kmajor
+static int xy_fwd(const ach_conv_desc *d, const float *x, const float *w, bool kmajor, float *y,
+                  void *ws, size_t ws_bytes, ach_stream_t st)
+{
+    const ConvGeom g = geom(d);
+    if (!ws || ws_bytes < xy_col_bytes(g)) return ACH_EWORKSPACE;
+    const int m = g.F, k = g.C * g.KS * g.KS, n = g.OH * g.OW;
+    float *col = (float *)ws;
+    for (int i = 0; i < g.B; ++i) {
+        int rc = ach_im2col(x + (size_t)i * g.C * g.H * g.W, g.C, g.H, g.W, g.KS, g.KS, g.P, g.P,
+                            stride_h(d), d->stride, 1, 1, col, st);
+        if (rc) return rc;
+        rc = kmajor ? ach_gemm(1, 0, m, n, k, 1.f, w, m, col, n, 0.f, y + (size_t)i * m * n, n, st)
+                    : ach_gemm(0, 0, m, n, k, 1.f, w, k, col, n, 0.f, y + (size_t)i * m * n, n, st);
+        if (rc) return rc;
+    }
+    return ACH_OK;
+}
+
+// dw += dy_b * im2col(x_b)^T over the images in order
+static int xy_bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, float *dw,
+                         void *ws, size_t ws_bytes, ach_stream_t st)
+{
+    const ConvGeom g = geom(d);
+    if (!ws || ws_bytes < xy_col_bytes(g)) return ACH_EWORKSPACE;
+    const int m = g.F, n = g.C * g.KS * g.KS, k = g.OH * g.OW;
+    float *col = (float *)ws;
+    for (int i = 0; i < g.B; ++i) {
+        int rc = ach_im2col(x + (size_t)i * g.C * g.H * g.W, g.C, g.H, g.W, g.KS, g.KS, g.P, g.P,
+                            stride_h(d), d->stride, 1, 1, col, st);
+        if (rc) return rc;
+        rc = ach_gemm(0, 1, m, n, k, 1.f, dy + (size_t)i * m * k, k, col, k, 1.f, dw, n, st);
+        if (rc) return rc;
+    }
+    return ACH_OK;
 }
 
 // y[b][m][p] = sum_z part[z][m][b*OHW+p], z ascending (fixed order), then
@@ -3143,6 +3201,7 @@ size_t ach_conv_fwd_workspace(const ach_conv_desc *d)
 {
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
+    if (conv_xy(d)) return xy_col_bytes(g);
     return align256((size_t)g.F * g.C * g.KS * g.KS * sizeof(float)) + fwd_part_bytes(g);
 }
 
@@ -3152,6 +3211,7 @@ int ach_conv_fwd(const ach_conv_desc *d, const float *x, const float *w, float *
     if (!conv_ok(d) || !x || !w || !y) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     if (!ws || ws_bytes < ach_conv_fwd_workspace(d)) return ACH_EWORKSPACE;
+    if (conv_xy(d)) return xy_fwd(d, x, w, false, y, ws, ws_bytes, stream);
     const ConvGeom g = geom(d);
     hipStream_t st = as_stream(stream);
     const int M = g.F, K = g.C * g.KS * g.KS;
@@ -3186,6 +3246,7 @@ size_t ach_conv_bwd_data_workspace(const ach_conv_desc *d)
 {
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
+    if (conv_xy(d)) return xy_col_bytes(g);
     size_t wf = (size_t)g.F * g.C * g.KS * g.KS * sizeof(float);
     if (g.S == 1 && g.P <= g.KS - 1) return align256(wf) + fwd_part_bytes(dgrad_as_fwd(g), false);
     // strided fallback: one image's column buffer
@@ -3201,8 +3262,9 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
     if (!ws || ws_bytes < need) return ACH_EWORKSPACE;
     const ConvGeom g = geom(d);
     hipStream_t st = as_stream(stream);
-    if (dgrad_small_c(g) && !fc_geom(g)) return dgrad_small_c_launch(g, dy, w, dx, st);
-    if (g.S == 1 && g.P <= g.KS - 1) {
+    const bool xy = conv_xy(d);
+    if (!xy && dgrad_small_c(g) && !fc_geom(g)) return dgrad_small_c_launch(g, dy, w, dx, st);
+    if (!xy && g.S == 1 && g.P <= g.KS - 1) {
         const size_t tot = (size_t)g.F * g.C * g.KS * g.KS;
         float *part = (float *)((char *)ws + align256(tot * sizeof(float)));
         // 1x1: the flipped k-major filter Wft[f][c] is W itself
@@ -3214,15 +3276,16 @@ int ach_conv_bwd_data(const ach_conv_desc *d, const float *dy, const float *w, f
         if (rc) return rc;
         return fwd_impl(dgrad_as_fwd(g), dy, wf, dx, part, st, Epi(), false, false);
     }
-    // Strided convolution: the reference's per-image TN GEMM + col2im
-    // (ConvolutionalLayer.c:933-945).  Not on any benchmark path.
+    // Strided convolution (unequal strides included): the reference's
+    // per-image TN GEMM + col2im (ConvolutionalLayer.c:933-945).  Not on any
+    // benchmark path.
     const int m = g.F, n = g.C * g.KS * g.KS, k = g.OH * g.OW;
     float *col = (float *)ws;
     for (int i = 0; i < g.B; ++i) {
         int rc = ach_gemm(1, 0, n, k, m, 1.f, w, n, dy + (size_t)i * m * k, k, 0.f, col, k,
                           stream);
         if (rc) return rc;
-        rc = ach_col2im(col, g.C, g.H, g.W, g.KS, g.KS, g.P, g.P, g.S, g.S, 1, 1,
+        rc = ach_col2im(col, g.C, g.H, g.W, g.KS, g.KS, g.P, g.P, stride_h(d), d->stride, 1, 1,
                         dx + (size_t)i * g.C * g.H * g.W, stream);
         if (rc) return rc;
     }
@@ -3255,7 +3318,7 @@ int ach_conv_prepare_filters(int njobs, const ach_filter_job *jobs, ach_stream_t
             // fully connected geometry: the forward reads W itself, no copy
             J.tiles_t = fc_geom(g) ? 0 : ((K + 31) / 32) * ((J.M + 31) / 32);
             J.tiles_f = 0;
-            if (q.wft && dgrad_flips(g))
+            if (q.wft && dgrad_flips(g) && !conv_xy(&q.desc))
                 J.tiles_f = (int)(((long long)J.M * J.C + 255) / 256);
             blocks += J.tiles_t + J.tiles_f;
         }
@@ -3273,6 +3336,7 @@ int ach_conv_fwd_prepared(const ach_conv_desc *d, const float *x, const float *w
 {
     if (!conv_ok(d) || !x || !wt || !y) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
+    if (conv_xy(d)) return xy_fwd(d, x, wt, true, y, ws, ws_bytes, stream);
     const ConvGeom g = geom(d);
     const size_t need = fwd_part_bytes(g);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
@@ -3294,6 +3358,12 @@ int ach_conv_fwd_bias_act_prepared(const ach_conv_desc *d, const float *x, const
         return ACH_EUNSUPPORTED;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
+    if (conv_xy(d)) {  // the three passes, as ach_conv_fwd_prepared + bias + activation
+        int rc = xy_fwd(d, x, wt, true, y, ws, ws_bytes, stream);
+        if (!rc && bias) rc = ach_add_bias(y, bias, g.B, g.F, g.OH * g.OW, stream);
+        if (rc) return rc;
+        return ach_activate(y, (size_t)g.B * g.F * g.OH * g.OW, activation, stream);
+    }
     const size_t need = fwd_part_bytes(g);
     if (need && (!ws || ws_bytes < need)) return ACH_EWORKSPACE;
     Epi e;
@@ -3313,7 +3383,8 @@ int ach_conv_bwd_data_prepared(const ach_conv_desc *d, const float *dy, const fl
     if (!conv_ok(d) || !dy || !w || !dx) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
-    if (!(g.S == 1 && g.P <= g.KS - 1)) return ACH_EUNSUPPORTED;  // strided: ach_conv_bwd_data
+    if (conv_xy(d) || !(g.S == 1 && g.P <= g.KS - 1))
+        return ACH_EUNSUPPORTED;  // strided: ach_conv_bwd_data
     if (dgrad_small_c(g) && !fc_geom(g)) return dgrad_small_c_launch(g, dy, w, dx, as_stream(stream));
     if (g.KS > 1 && !wft) return ACH_EINVAL;
     const ConvGeom t = dgrad_as_fwd(g);
@@ -3327,6 +3398,7 @@ size_t ach_conv_bwd_filter_workspace(const ach_conv_desc *d)
 {
     if (!conv_ok(d)) return 0;
     const ConvGeom g = geom(d);
+    if (conv_xy(d)) return xy_col_bytes(g);
     // (the one-pass 1x1 kernel needs none, but unaligned operands take the
     // GEMM, so its workspace is reported)
     int splits, kchunk;
@@ -3345,6 +3417,12 @@ static int bwd_filter(const ach_conv_desc *d, const float *x, const float *dy, f
     if (!conv_ok(d) || !x || !dy || !dw) return ACH_EINVAL;
     if (!fits_int(d)) return ACH_EUNSUPPORTED;
     const ConvGeom g = geom(d);
+    if (conv_xy(d)) {
+        const int rc = xy_bwd_filter(d, x, dy, dw, ws, ws_bytes, stream);
+        if (rc || !sgd.w) return rc;
+        return ach_sgd_update((size_t)g.F * g.C * g.KS * g.KS, sgd.w, dw, sgd.dc, sgd.lc, sgd.mom,
+                              stream);
+    }
     // (float4 loads: 16-byte aligned operands; planes are multiples of 4)
     if (wgrad_1x1_smallf(g) &&
         ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy)) & 15) == 0)
@@ -3427,7 +3505,7 @@ int ach_conv_bwd_filter_sgd(const ach_conv_desc *d, const float *x, const float 
 
 int ach_conv_bwd_data_reads_w(const ach_conv_desc *d)
 {
-    if (!conv_ok(d)) return 1;
+    if (!conv_ok(d) || conv_xy(d)) return 1;
     const ConvGeom g = geom(d);
     // ach_conv_bwd_data_prepared reads wft only for the GEMM path of a
     // stride-1 layer whose filter is wider than 1x1

@@ -348,14 +348,16 @@ __global__ void __launch_bounds__(256) k_bias_from_planes(const double *__restri
 // ---- max-pool --------------------------------------------------------------------
 // Input element counts are below 2^31 (the indexes are int32), so all index
 // arithmetic is 32-bit.
+// sx_ / sy_: the width / height strides when STRIDE is 0 (else STRIDE both)
 template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_fwd(const float *__restrict__ in, int total,
-                                                     int H, int W, int size_, int stride_,
+                                                     int H, int W, int size_, int sx_, int sy_,
                                                      int pad, FastDiv dOH, FastDiv dOW,
                                                      float *__restrict__ out,
                                                      int32_t *__restrict__ idx)
 {
-    const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
+    const int size = SIZE ? SIZE : size_;
+    const int sx = STRIDE ? STRIDE : sx_, sy = STRIDE ? STRIDE : sy_;
     const int off = -pad / 2;
     const int o = blockIdx.x * blockDim.x + threadIdx.x;
     if (o >= total) return;
@@ -365,7 +367,7 @@ __global__ void __launch_bounds__(256) k_maxpool_fwd(const float *__restrict__ i
     int mi = -1;
     for (int n = 0; n < size; ++n)
         for (int m = 0; m < size; ++m) {
-            const int ch = off + i * stride + n, cw = off + j * stride + m;
+            const int ch = off + i * sy + n, cw = off + j * sx + m;
             const int index = cw + W * (ch + H * bc);
             const bool valid = ch >= 0 && ch < H && cw >= 0 && cw < W;
             const float v = valid ? in[index] : -FLT_MAX;
@@ -524,20 +526,21 @@ template <int SIZE, int STRIDE>
 __global__ void __launch_bounds__(256) k_maxpool_bwd(const float *__restrict__ dout,
                                                      const int32_t *__restrict__ idx, int total,
                                                      FastDiv dH, FastDiv dW, int size_,
-                                                     int stride_, int pad, int OH, int OW,
+                                                     int sx_, int sy_, int pad, int OH, int OW,
                                                      float *din, int accumulate, GradIn gi)
 {
-    const int size = SIZE ? SIZE : size_, stride = STRIDE ? STRIDE : stride_;
+    const int size = SIZE ? SIZE : size_;
+    const int sx = STRIDE ? STRIDE : sx_, sy = STRIDE ? STRIDE : sy_;
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= total) return;
     const int row = fdiv(p, dW), w = p - row * (int)dW.d;  // row = bc*H + h
     const int bc = fdiv(row, dH), h = row - bc * (int)dH.d;
     const int off = -pad / 2;
-    // output row i covers rows off + i*stride .. + size-1
-    const int i0 = max(floor_div(h - off - size, stride) + 1, 0);
-    const int i1 = min(floor_div(h - off, stride), OH - 1);
-    const int j0 = max(floor_div(w - off - size, stride) + 1, 0);
-    const int j1 = min(floor_div(w - off, stride), OW - 1);
+    // output row i covers rows off + i*sy .. + size-1 (columns likewise)
+    const int i0 = max(floor_div(h - off - size, sy) + 1, 0);
+    const int i1 = min(floor_div(h - off, sy), OH - 1);
+    const int j0 = max(floor_div(w - off - size, sx) + 1, 0);
+    const int j1 = min(floor_div(w - off, sx), OW - 1);
     float v = accumulate ? din[p] : 0.f;
     const int obase = bc * OH * OW;
     if constexpr (SIZE > 0 && STRIDE > 0) {
@@ -1240,13 +1243,13 @@ static int maxpool_fwd(const float *in, int batch, int c, int h, int w, int size
     }
     if (size == 3 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_fwd<3, 2>), grid, dim3(256), 0, as_stream(s), in, total, h,
-                           w, size, stride, pad, dOH, dOW, out, idx);
+                           w, size, stride, stride, pad, dOH, dOW, out, idx);
     else if (size == 2 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_fwd<2, 2>), grid, dim3(256), 0, as_stream(s), in, total, h,
-                           w, size, stride, pad, dOH, dOW, out, idx);
+                           w, size, stride, stride, pad, dOH, dOW, out, idx);
     else
         hipLaunchKernelGGL((k_maxpool_fwd<0, 0>), grid, dim3(256), 0, as_stream(s), in, total, h,
-                           w, size, stride, pad, dOH, dOW, out, idx);
+                           w, size, stride, stride, pad, dOH, dOW, out, idx);
     return check_launch();
 }
 
@@ -1255,6 +1258,23 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w, int size, i
 {
     DropIn none{};
     return maxpool_fwd(in, batch, c, h, w, size, stride, pad, out, idx, none, s);
+}
+
+// Unequal strides: the general window kernels (one thread per output in the
+// forward, one per input pixel in the gather backward).
+int ach_maxpool_fwd_xy(const float *in, int batch, int c, int h, int w, int size, int sx, int sy,
+                       int pad, float *out, int32_t *idx, ach_stream_t s)
+{
+    if (sx == sy) return ach_maxpool_fwd(in, batch, c, h, w, size, sx, pad, out, idx, s);
+    if (!in || !out || !pool_ok(batch, c, h, w, size, sx, pad) ||
+        !pool_ok(batch, c, h, w, size, sy, pad))
+        return ACH_EINVAL;
+    const int OH = ach_maxpool_out(h, size, sy, pad), OW = ach_maxpool_out(w, size, sx, pad);
+    const int total = batch * c * OH * OW;  // < 2^31: at most the input's count
+    const FastDiv dOH = make_fastdiv((unsigned)OH), dOW = make_fastdiv((unsigned)OW);
+    hipLaunchKernelGGL((k_maxpool_fwd<0, 0>), dim3((total + 255) / 256), dim3(256), 0,
+                       as_stream(s), in, total, h, w, size, sx, sy, pad, dOH, dOW, out, idx);
+    return check_launch();
 }
 
 int ach_maxpool_fwd_dropout(const float *in, int batch, int c, int h, int w, int size,
@@ -1336,13 +1356,13 @@ static int maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, 
     }
     if (size == 3 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<3, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, dH, dW, size, stride, pad, OH, OW, din, acc, gi);
+                           total, dH, dW, size, stride, stride, pad, OH, OW, din, acc, gi);
     else if (size == 2 && stride == 2)
         hipLaunchKernelGGL((k_maxpool_bwd<2, 2>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, dH, dW, size, stride, pad, OH, OW, din, acc, gi);
+                           total, dH, dW, size, stride, stride, pad, OH, OW, din, acc, gi);
     else
         hipLaunchKernelGGL((k_maxpool_bwd<0, 0>), grid, dim3(256), 0, as_stream(s), dout, idx,
-                           total, dH, dW, size, stride, pad, OH, OW, din, acc, gi);
+                           total, dH, dW, size, stride, stride, pad, OH, OW, din, acc, gi);
     return check_launch();
 }
 
@@ -1351,6 +1371,24 @@ int ach_maxpool_bwd(const float *dout, const int32_t *idx, int batch, int c, int
 {
     return maxpool_bwd(dout, idx, batch, c, h, w, size, stride, pad, din, accumulate,
                        GradIn{nullptr, 0}, DropIn{}, s);
+}
+
+int ach_maxpool_bwd_xy(const float *dout, const int32_t *idx, int batch, int c, int h, int w,
+                       int size, int sx, int sy, int pad, float *din, int accumulate,
+                       ach_stream_t s)
+{
+    if (sx == sy)
+        return ach_maxpool_bwd(dout, idx, batch, c, h, w, size, sx, pad, din, accumulate, s);
+    if (!dout || !idx || !din || !pool_ok(batch, c, h, w, size, sx, pad) ||
+        !pool_ok(batch, c, h, w, size, sy, pad))
+        return ACH_EINVAL;
+    const int OH = ach_maxpool_out(h, size, sy, pad), OW = ach_maxpool_out(w, size, sx, pad);
+    const int total = batch * c * h * w;  // < 2^31: pool_ok
+    const FastDiv dH = make_fastdiv((unsigned)h), dW = make_fastdiv((unsigned)w);
+    hipLaunchKernelGGL((k_maxpool_bwd<0, 0>), dim3((total + 255) / 256), dim3(256), 0,
+                       as_stream(s), dout, idx, total, dH, dW, size, sx, sy, pad, OH, OW, din,
+                       accumulate ? 1 : 0, GradIn{nullptr, 0});
+    return check_launch();
 }
 
 int ach_maxpool_bwd_dropout(float *dout, const int32_t *idx, int batch, int c, int h, int w,

@@ -30,8 +30,7 @@
  * Keys the reference reads whose non-default values change its CPU
  * training step but this build does not implement (groups, dilation,
  * xnor, binary, bin_output, antialiasing, cbn, deformable sway / rotate /
- * stretch, assisted_excitation, share_index, unequal stride_x / stride_y,
- * maxpool_depth, dropblock, softmax spatial / noloss / tree, [net]
+ * stretch, assisted_excitation, share_index, maxpool_depth, dropblock, softmax spatial / noloss / tree, [net]
  * time_steps) are rejected with a message.  Keys the reference reads but
  * its CPU path never acts on are accepted; keys it does not read are
  * reported as unused (darknet's behaviour).
@@ -221,22 +220,23 @@ static void report_unused(const cfg_group *g, const char *const *own, int layer)
 }
 
 /* stride_x / stride_y as createConvolutional / createMaxPool resolve them
- * (NetworkFactory.c:83-93, 545-546); a non-square stride is not built.
- * Returns the stride or -1.                                                */
-static int square_stride(const cfg_group *g, int conv)
+ * (NetworkFactory.c:83-93, 545-546): a convolution's missing or nonpositive
+ * value falls back to stride, a pool's missing one.  Returns 0, or -1 for a
+ * stride below 1 (which the layer constructors reject).                   */
+static int layer_strides(const cfg_group *g, int conv, int *sx, int *sy)
 {
     const int stride = geti(g, "stride", 1);
-    int sx = geti(g, "stride_x", conv ? -1 : stride), sy = geti(g, "stride_y", conv ? -1 : stride);
-    if (conv && (sx < 1 || sy < 1)) {
-        if (sx < 1) sx = stride;
-        if (sy < 1) sy = stride;
+    *sx = geti(g, "stride_x", conv ? -1 : stride);
+    *sy = geti(g, "stride_y", conv ? -1 : stride);
+    if (conv && (*sx < 1 || *sy < 1)) {
+        if (*sx < 1) *sx = stride;
+        if (*sy < 1) *sy = stride;
     }
-    if (sx != sy) {
-        fprintf(stderr, "an_parse_cfg: [%s] stride_x=%d stride_y=%d: non-square strides are "
-                        "not supported\n", g->name, sx, sy);
+    if (*sx < 1 || *sy < 1) {
+        fprintf(stderr, "an_parse_cfg: [%s] stride_x=%d stride_y=%d\n", g->name, *sx, *sy);
         return -1;
     }
-    return sx;
+    return 0;
 }
 
 /* the createLayer / createNetwork options of layer `idx` */
@@ -382,8 +382,8 @@ an_network *an_parse_cfg_unfinalized(const char *path)
                 unsupported(g, "stretch_sway", 0) || unsupported(g, "assisted_excitation", 0) ||
                 present_unsupported(g, "share_index"))
                 goto fail;
-            const int stride = square_stride(g, 1);
-            if (stride < 0) goto fail;
+            int sx, sy;
+            if (layer_strides(g, 1, &sx, &sy)) goto fail;
             int padding = geti(g, "padding", 0);
             if (geti(g, "pad", 0)) padding = size / 2;
             const char *an = find(g, "activation");
@@ -392,8 +392,8 @@ an_network *an_parse_cfg_unfinalized(const char *path)
                 fprintf(stderr, "an_parse_cfg: activation %s is not supported\n", an);
                 goto fail;
             }
-            rc = an_add_convolutional(net, geti(g, "filters", 1), size, stride, padding, act,
-                                      geti(g, "batch_normalize", 0));
+            rc = an_add_convolutional_xy(net, geti(g, "filters", 1), size, sx, sy, padding, act,
+                                         geti(g, "batch_normalize", 0));
         } else if (!strcmp(g->name, "connected") || !strcmp(g->name, "conn")) {
             report_unused(g, CONN_KEYS, 1);
             const char *an = find(g, "activation");
@@ -407,10 +407,11 @@ an_network *an_parse_cfg_unfinalized(const char *path)
             report_unused(g, MAXPOOL_KEYS, 1);
             if (unsupported(g, "maxpool_depth", 0) || unsupported(g, "antialiasing", 0))
                 goto fail;
-            const int stride = square_stride(g, 0);
-            if (stride < 0) goto fail;
-            const int size = geti(g, "size", stride);
-            rc = an_add_maxpool(net, size, stride, geti(g, "padding", size - 1));
+            int sx, sy;
+            if (layer_strides(g, 0, &sx, &sy)) goto fail;
+            /* the size defaults to the stride key, not the resolved strides */
+            const int size = geti(g, "size", geti(g, "stride", 1));
+            rc = an_add_maxpool_xy(net, size, sx, sy, geti(g, "padding", size - 1));
         } else if (!strcmp(g->name, "avgpool") || !strcmp(g->name, "avg")) {
             report_unused(g, NO_KEYS, 1);
             rc = an_add_avgpool(net);

@@ -175,8 +175,9 @@ static ach_conv_desc conv_desc(const an_layer *l)
     d.w = l->w;
     d.n = l->n;
     d.size = l->size;
-    d.stride = l->stride;
+    d.stride = l->stride_x;
     d.pad = l->pad;
+    d.stride_y = l->stride_y;
     return d;
 }
 
@@ -235,7 +236,7 @@ static int output_masked_unreverted(const an_network *net, const an_layer *l)
 static int conv_input_gradient(const an_layer *l, const ach_conv_desc *d, an_state st,
                                ach_stream_t s)
 {
-    return l->stride == 1
+    return l->stride_x == 1 && l->stride_y == 1
                ? ach_conv_bwd_data_prepared(d, l->delta, l->weights, l->weights_flipped, st.delta,
                                             st.workspace, st.workspace_bytes, s)
                : ach_conv_bwd_data(d, l->delta, l->weights, st.delta, st.workspace,
@@ -334,10 +335,11 @@ static int conv_update(an_network *net, an_layer *l, int batch, float lr, float 
 
 /* flatten != 0: the layer reads the previous output [batch][c][h][w] as
  * [batch][c*h*w][1][1] (the same memory), for an_add_connected */
-static int add_conv(an_network *net, int filters, int size, int stride, int pad, int activation,
-                    int batch_normalize, int flatten)
+static int add_conv(an_network *net, int filters, int size, int stride_x, int stride_y, int pad,
+                    int activation, int batch_normalize, int flatten)
 {
-    if (!net || filters <= 0 || size <= 0 || stride <= 0 || pad < 0) return ACH_EINVAL;
+    if (!net || filters <= 0 || size <= 0 || stride_x <= 0 || stride_y <= 0 || pad < 0)
+        return ACH_EINVAL;
     if (activation != ACH_LEAKY && activation != ACH_RELU && activation != ACH_LINEAR &&
         activation != ACH_LOGISTIC)
         return ACH_EUNSUPPORTED;
@@ -351,12 +353,13 @@ static int add_conv(an_network *net, int filters, int size, int stride, int pad,
     l->type = AN_CONVOLUTIONAL;
     l->n = filters;
     l->size = size;
-    l->stride = stride;
+    l->stride = l->stride_x = stride_x;
+    l->stride_y = stride_y;
     l->pad = pad;
     l->activation = activation;
     l->batch_normalize = batch_normalize ? 1 : 0;
-    l->out_h = (l->h + 2 * pad - size) / stride + 1;
-    l->out_w = (l->w + 2 * pad - size) / stride + 1;
+    l->out_h = (l->h + 2 * pad - size) / stride_y + 1;
+    l->out_w = (l->w + 2 * pad - size) / stride_x + 1;
     l->out_c = filters;
     if (l->h + 2 * pad < size || l->w + 2 * pad < size || l->out_h <= 0 || l->out_w <= 0) {
         free(l);
@@ -382,7 +385,13 @@ static int add_conv(an_network *net, int filters, int size, int stride, int pad,
 int an_add_convolutional(an_network *net, int filters, int size, int stride, int pad,
                          int activation, int batch_normalize)
 {
-    return add_conv(net, filters, size, stride, pad, activation, batch_normalize, 0);
+    return add_conv(net, filters, size, stride, stride, pad, activation, batch_normalize, 0);
+}
+
+int an_add_convolutional_xy(an_network *net, int filters, int size, int stride_x, int stride_y,
+                            int pad, int activation, int batch_normalize)
+{
+    return add_conv(net, filters, size, stride_x, stride_y, pad, activation, batch_normalize, 0);
 }
 
 /* A fully connected layer: the previous output flattened to c*h*w features
@@ -392,7 +401,7 @@ int an_add_convolutional(an_network *net, int filters, int size, int stride, int
  * the convolution's rule with k = 1. */
 int an_add_connected(an_network *net, int outputs, int activation, int batch_normalize)
 {
-    return add_conv(net, outputs, 1, 1, 0, activation, batch_normalize, 1);
+    return add_conv(net, outputs, 1, 1, 1, 0, activation, batch_normalize, 1);
 }
 
 /* ======================================================================== */
@@ -411,13 +420,18 @@ static an_layer *pool_act_target(an_network *net, const an_layer *l, const float
 
 static int maxpool_forward(an_network *net, an_layer *l, an_state st)
 {
-    return ach_maxpool_fwd(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride, l->pad,
-                           l->output, l->indexes, net->stream);
+    return ach_maxpool_fwd_xy(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride_x,
+                              l->stride_y, l->pad, l->output, l->indexes, net->stream);
 }
 
 static int maxpool_backward(an_network *net, an_layer *l, an_state st)
 {
     if (!st.delta) return ACH_OK;
+    /* unequal strides: the general gather, and the layer below applies its
+     * own activation gradient */
+    if (l->stride_x != l->stride_y)
+        return ach_maxpool_bwd_xy(l->delta, l->indexes, l->batch, l->c, l->h, l->w, l->size,
+                                  l->stride_x, l->stride_y, l->pad, st.delta, 0, net->stream);
     /* the only contribution to the previous delta, which the reference
      * zeroes in forward: write the sums instead of adding to zeros.  In the
      * whole backward loop, when that delta is a plain conv layer's own (no
@@ -466,15 +480,21 @@ static int maxpool_backward(an_network *net, an_layer *l, an_state st)
 
 int an_add_maxpool(an_network *net, int size, int stride, int padding)
 {
-    if (!net || size <= 0 || stride <= 0 || padding < 0) return ACH_EINVAL;
+    return an_add_maxpool_xy(net, size, stride, stride, padding);
+}
+
+int an_add_maxpool_xy(an_network *net, int size, int stride_x, int stride_y, int padding)
+{
+    if (!net || size <= 0 || stride_x <= 0 || stride_y <= 0 || padding < 0) return ACH_EINVAL;
     an_layer *l = push_layer(net);
     if (!l) return ACH_EINVAL;
     l->type = AN_MAXPOOL;
     l->size = size;
-    l->stride = stride;
+    l->stride = l->stride_x = stride_x;
+    l->stride_y = stride_y;
     l->pad = padding;
-    l->out_h = ach_maxpool_out(l->h, size, stride, padding);
-    l->out_w = ach_maxpool_out(l->w, size, stride, padding);
+    l->out_h = ach_maxpool_out(l->h, size, stride_y, padding);
+    l->out_w = ach_maxpool_out(l->w, size, stride_x, padding);
     l->out_c = l->c;
     if (l->out_h <= 0 || l->out_w <= 0) {
         free(l);

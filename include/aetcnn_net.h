@@ -62,6 +62,9 @@ struct an_layer {
     int h, w, c, out_h, out_w, out_c;
     /* convolutional (ConvolutionalLayer.h:20-114) */
     int n, size, stride, pad, activation, batch_normalize, nweights;
+    /* conv and maxpool: width / height strides, stride == stride_x
+     * (ConvolutionalLayer.c:77-79, MaxPoolLayer.c:47-49)                    */
+    int stride_x, stride_y;
     int connected;          /* an_add_connected: input read flattened       */
     float *weights, *weight_updates, *biases, *bias_updates;
     float *scales, *scale_updates;
@@ -120,6 +123,15 @@ int an_add_convolutional(an_network *net, int filters, int size, int stride, int
  * flattened input.  Init sqrt(2/inputs) * randUniform(-1,1).               */
 int an_add_connected(an_network *net, int outputs, int activation, int batch_normalize);
 int an_add_maxpool(an_network *net, int size, int stride, int padding);
+/* The same layers with a width stride stride_x and a height stride stride_y
+ * (createConvolutional / createMaxPool, NetworkFactory.c:83-90, 544-547;
+ * output sizes ConvolutionalLayer.c:337-344, MaxPoolLayer.c:40-41).  A
+ * convolution with unequal strides runs the reference's per-image im2col /
+ * GEMM / col2im passes on the device (see ach_conv_desc.stride_y), a pool
+ * the general window kernels.                                              */
+int an_add_convolutional_xy(an_network *net, int filters, int size, int stride_x, int stride_y,
+                            int pad, int activation, int batch_normalize);
+int an_add_maxpool_xy(an_network *net, int size, int stride_x, int stride_y, int padding);
 int an_add_avgpool(an_network *net);
 int an_add_dropout(an_network *net, float probability);
 int an_add_softmax(an_network *net, int groups, float temperature);
@@ -184,17 +196,17 @@ void an_free(an_network *net);
 /* Builds a network from a darknet-style .cfg file (ConfigFile.c:12-208,
  * NetworkFactory.c:615-1013): [net] batch/subdivisions/width/height/channels/
  * learning_rate/momentum/decay and the policy keys policy/burn_in/power/
- * step/scale/steps/scales/gamma/max_batches; [convolutional] filters/size/stride/pad/
- * padding/activation/batch_normalize; [connected] output/activation/
- * batch_normalize (darknet's keys, an_add_connected); [maxpool] size/stride/
- * padding; [avgpool]; [dropout] probability; [softmax] groups/temperature;
- * in every layer section the options of an_layer_options (stopbackward,
- * onlyforward, dontload, dontloadscales, learning_rate, and flipped for
- * [convolutional]); stride_x / stride_y when they give one square stride.
+ * step/scale/steps/scales/gamma/max_batches; [convolutional] filters/size/stride/
+ * stride_x/stride_y/pad/padding/activation/batch_normalize; [connected]
+ * output/activation/batch_normalize (darknet's keys, an_add_connected);
+ * [maxpool] size/stride/stride_x/stride_y/padding; [avgpool]; [dropout]
+ * probability; [softmax] groups/temperature; in every layer section the
+ * options of an_layer_options (stopbackward, onlyforward, dontload,
+ * dontloadscales, learning_rate, and flipped for [convolutional]).
  * Keys the reference reads that change its CPU training step but this
  * build does not implement (groups != 1, dilation != 1, xnor, binary,
  * bin_output, antialiasing, cbn, deformable sway / rotate / stretch,
- * assisted_excitation, share_index, stride_x != stride_y, maxpool_depth,
+ * assisted_excitation, share_index, maxpool_depth,
  * dropblock, softmax spatial / noloss / tree, [net] time_steps != 1) make
  * the parse fail with a message; keys the reference reads but its CPU path
  * never acts on (e.g. dontsave, clip, train_only_bn, dont_update, adam,

@@ -93,11 +93,22 @@ int ach_col2im(const float *col, int channels, int height, int width,
                int kh, int kw, int ph, int pw, int sh, int sw,
                int dilation_h, int dilation_w, float *im, ach_stream_t stream);
 
-/* ---- convolution (ConvolutionalLayer.c:684-803, 906-947) ---------------- */
+/* ---- convolution (ConvolutionalLayer.c:684-803, 906-947) ----------------
+ * stride is the width stride (the layer's stride_x, ConvolutionalLayer.c:
+ * 77-79) and stride_y the height stride, 0 meaning the same as stride; the
+ * output is ((h + 2*pad - size)/stride_y + 1) x ((w + 2*pad - size)/stride
+ * + 1) (ConvolutionalLayer.c:337-344).  With unequal strides every entry
+ * point below runs the reference's per-image passes on the device -- the
+ * forward im2col + GEMM (ConvolutionalLayer.c:790-803), the weight
+ * gradient im2col + GEMM added into dw and the input gradient GEMM +
+ * col2im (:913-945) -- with one image's column buffer as workspace, except
+ * for a fully connected geometry (one output position, which no stride
+ * moves), and ach_conv_bwd_data_prepared returns ACH_EUNSUPPORTED.       */
 typedef struct {
     int batch, c, h, w;   /* input  [batch][c][h][w]                     */
     int n;                /* filters (output channels)                   */
     int size, stride, pad;/* square kernel, stride, padding (groups = 1) */
+    int stride_y;         /* height stride; 0: the same as stride        */
 } ach_conv_desc;
 
 int ach_conv_out_h(const ach_conv_desc *d);
@@ -291,6 +302,15 @@ int ach_maxpool_fwd(const float *in, int batch, int c, int h, int w,
 int ach_maxpool_bwd(const float *delta_out, const int32_t *indexes,
                     int batch, int c, int h, int w, int size, int stride, int padding,
                     float *delta_in, int accumulate, ach_stream_t stream);
+/* The same pool with a width stride stride_x and a height stride stride_y
+ * (MaxPoolLayer.c:40-41, 255-256: out w = (w + padding - size)/stride_x + 1,
+ * h likewise with stride_y); equal strides take the calls above.           */
+int ach_maxpool_fwd_xy(const float *in, int batch, int c, int h, int w, int size, int stride_x,
+                       int stride_y, int padding, float *out, int32_t *indexes,
+                       ach_stream_t stream);
+int ach_maxpool_bwd_xy(const float *delta_out, const int32_t *indexes, int batch, int c, int h,
+                       int w, int size, int stride_x, int stride_y, int padding, float *delta_in,
+                       int accumulate, ach_stream_t stream);
 /* A dropout layer that follows the max-pool and shares its output
  * (DropoutLayer.c:55-86, NetworkFactory.c:644-650), applied by the pool:
  * the forward writes the masked output (ach_maxpool_fwd + ach_dropout_fwd on

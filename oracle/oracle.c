@@ -177,7 +177,8 @@ void or_col2im(const float *data_col, int channels, int height, int width,
 /* ------------------------------------------------------------------------ */
 /* Convolution GEMM parts: ConvolutionalLayer.c:337-344 (out size),
  * :684-803 (forward, fp32 branch), :906-947 (backward loop).               */
-int or_conv_out_h(const or_conv_shape *s) { return (s->h + 2 * s->pad - s->size) / s->stride + 1; }
+static int stride_h(const or_conv_shape *s) { return s->stride_y > 0 ? s->stride_y : s->stride; }
+int or_conv_out_h(const or_conv_shape *s) { return (s->h + 2 * s->pad - s->size) / stride_h(s) + 1; }
 int or_conv_out_w(const or_conv_shape *s) { return (s->w + 2 * s->pad - s->size) / s->stride + 1; }
 
 size_t or_conv_workspace_floats(const or_conv_shape *s)
@@ -195,11 +196,14 @@ void or_conv_forward(const or_conv_shape *s, const float *input, const float *we
         const float *im = input + (size_t)i * s->c * s->h * s->w;
         const float *b = workspace;
         float *c = output + (size_t)i * n * m;
-        if (s->size == 1 && s->stride == 1) {
+        /* (the reference tests stride_x alone here, ConvolutionalLayer.c:788,
+         * and would read a 1x1 layer with stride_x 1 and stride_y > 1 as if
+         * unstrided: that case takes im2col) */
+        if (s->size == 1 && s->stride == 1 && stride_h(s) == 1) {
             b = im;
         } else {
             or_im2col(im, s->c, s->h, s->w, s->size, s->size, s->pad, s->pad,
-                      s->stride, s->stride, 1, 1, workspace);
+                      stride_h(s), s->stride, 1, 1, workspace);
         }
         or_gemm(0, 0, m, n, k, 1, weights, k, b, n, 1, c, n);
     }
@@ -216,12 +220,12 @@ void or_conv_backward(const or_conv_shape *s, const float *input, const float *m
         float *b = workspace;
         const float *im = input + (size_t)i * s->c * s->h * s->w;
         or_im2col(im, s->c, s->h, s->w, s->size, s->size, s->pad, s->pad,
-                  s->stride, s->stride, 1, 1, b);
+                  stride_h(s), s->stride, 1, 1, b);
         or_gemm(0, 1, m, n, k, 1, a, k, b, k, 1, weight_updates, n);
         if (delta) {
             or_gemm(1, 0, n, k, m, 1, weights, n, a, k, 0, workspace, k);
             or_col2im(workspace, s->c, s->h, s->w, s->size, s->size, s->pad, s->pad,
-                      s->stride, s->stride, 1, 1, delta + (size_t)i * s->c * s->h * s->w);
+                      stride_h(s), s->stride, 1, 1, delta + (size_t)i * s->c * s->h * s->w);
         }
     }
 }
@@ -472,9 +476,15 @@ int or_maxpool_out(int in, int size, int stride, int padding)
 void or_maxpool_forward(const float *input, int batch, int c, int lh, int lw,
                         int size, int stride, int pad, float *output, int *indexes)
 {
+    or_maxpool_forward_xy(input, batch, c, lh, lw, size, stride, stride, pad, output, indexes);
+}
+
+void or_maxpool_forward_xy(const float *input, int batch, int c, int lh, int lw, int size,
+                           int stride_x, int stride_y, int pad, float *output, int *indexes)
+{
     const int w_offset = -pad / 2, h_offset = -pad / 2;
-    const int h = or_maxpool_out(lh, size, stride, pad);
-    const int w = or_maxpool_out(lw, size, stride, pad);
+    const int h = or_maxpool_out(lh, size, stride_y, pad);
+    const int w = or_maxpool_out(lw, size, stride_x, pad);
     for (int b = 0; b < batch; ++b)
         for (int k = 0; k < c; ++k)
             for (int i = 0; i < h; ++i)
@@ -484,8 +494,8 @@ void or_maxpool_forward(const float *input, int batch, int c, int lh, int lw,
                     int max_i = -1;
                     for (int n = 0; n < size; ++n)
                         for (int m = 0; m < size; ++m) {
-                            int cur_h = h_offset + i * stride + n;
-                            int cur_w = w_offset + j * stride + m;
+                            int cur_h = h_offset + i * stride_y + n;
+                            int cur_w = w_offset + j * stride_x + m;
                             int index = cur_w + lw * (cur_h + lh * (k + b * c));
                             int valid = (cur_h >= 0 && cur_h < lh && cur_w >= 0 && cur_w < lw);
                             float val = valid ? input[index] : -FLT_MAX;
@@ -658,6 +668,7 @@ typedef struct {
     int h, w, c, out_h, out_w, out_c;
     /* conv */
     int n, size, stride, pad, activation, batch_normalize, nweights;
+    int stride_y; /* conv and maxpool: height stride (stride is the width one) */
     float *weights, *weight_updates, *biases, *bias_updates;
     float *scales, *scale_updates, *mean, *variance, *rolling_mean, *rolling_variance;
     float *x, *x_norm, *mean_delta, *variance_delta;
@@ -752,8 +763,8 @@ static or_layer *push_layer(or_net *net)
 
 static float *fzalloc(size_t n) { return (float *)calloc(n ? n : 1, sizeof(float)); }
 
-static int add_conv(or_net *net, int filters, int size, int stride, int pad, int activation,
-                    int batch_normalize, int flatten)
+static int add_conv(or_net *net, int filters, int size, int stride, int stride_y, int pad,
+                    int activation, int batch_normalize, int flatten)
 {
     or_layer *l = push_layer(net);
     if (flatten) { /* [batch][c][h][w] read as [batch][c*h*w][1][1] */
@@ -764,10 +775,11 @@ static int add_conv(or_net *net, int filters, int size, int stride, int pad, int
     l->n = filters;
     l->size = size;
     l->stride = stride;
+    l->stride_y = stride_y;
     l->pad = pad;
     l->activation = activation;
     l->batch_normalize = batch_normalize;
-    l->out_h = (l->h + 2 * pad - size) / stride + 1;
+    l->out_h = (l->h + 2 * pad - size) / stride_y + 1;
     l->out_w = (l->w + 2 * pad - size) / stride + 1;
     l->out_c = filters;
     if (l->out_h <= 0 || l->out_w <= 0) return -1;
@@ -802,7 +814,13 @@ static int add_conv(or_net *net, int filters, int size, int stride, int pad, int
 int or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
                     int activation, int batch_normalize)
 {
-    return add_conv(net, filters, size, stride, pad, activation, batch_normalize, 0);
+    return add_conv(net, filters, size, stride, stride, pad, activation, batch_normalize, 0);
+}
+
+int or_net_add_conv_xy(or_net *net, int filters, int size, int stride_x, int stride_y, int pad,
+                       int activation, int batch_normalize)
+{
+    return add_conv(net, filters, size, stride_x, stride_y, pad, activation, batch_normalize, 0);
 }
 
 /* A fully connected layer (darknet's [connected]; the reference builds none,
@@ -812,18 +830,24 @@ int or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
  * sqrt(2/inputs)*randUniform(-1,1) (WeightData.c:153-166 with k = 1).      */
 int or_net_add_connected(or_net *net, int outputs, int activation, int batch_normalize)
 {
-    return add_conv(net, outputs, 1, 1, 0, activation, batch_normalize, 1);
+    return add_conv(net, outputs, 1, 1, 1, 0, activation, batch_normalize, 1);
 }
 
 int or_net_add_maxpool(or_net *net, int size, int stride, int padding)
 {
+    return or_net_add_maxpool_xy(net, size, stride, stride, padding);
+}
+
+int or_net_add_maxpool_xy(or_net *net, int size, int stride_x, int stride_y, int padding)
+{
     or_layer *l = push_layer(net);
     l->type = L_MAXPOOL;
     l->size = size;
-    l->stride = stride;
+    l->stride = stride_x;
+    l->stride_y = stride_y;
     l->pad = padding;
-    l->out_h = or_maxpool_out(l->h, size, stride, padding);
-    l->out_w = or_maxpool_out(l->w, size, stride, padding);
+    l->out_h = or_maxpool_out(l->h, size, stride_y, padding);
+    l->out_w = or_maxpool_out(l->w, size, stride_x, padding);
     l->out_c = l->c;
     if (l->out_h <= 0 || l->out_w <= 0) return -1;
     l->outputs = l->out_h * l->out_w * l->out_c;
@@ -985,7 +1009,8 @@ int or_net_finalize(or_net *net)
     for (int i = 0; i < net->n; ++i) {
         or_layer *l = &net->layers[i];
         if (l->type != L_CONV) continue;
-        or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad};
+        or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad,
+                           l->stride_y};
         size_t need = or_conv_workspace_floats(&s);
         if (need > ws) ws = need;
     }
@@ -1029,7 +1054,8 @@ typedef struct {
 
 static void conv_forward(or_net *net, or_layer *l, or_state st)
 {
-    or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad};
+    or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad,
+                       l->stride_y};
     const int spatial = l->out_h * l->out_w;
     or_conv_forward(&s, st.input, l->weights, l->output, net->workspace);
     if (l->batch_normalize && !st.train) {
@@ -1054,7 +1080,8 @@ static void conv_forward(or_net *net, or_layer *l, or_state st)
 
 static void conv_backward(or_net *net, or_layer *l, or_state st)
 {
-    or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad};
+    or_conv_shape s = {l->batch, l->c, l->h, l->w, l->n, l->size, l->stride, l->pad,
+                       l->stride_y};
     const int spatial = l->out_h * l->out_w;
     or_gradient(l->output, l->batch * l->outputs, l->activation, l->delta);
     if (l->batch_normalize)
@@ -1072,8 +1099,8 @@ static void layer_forward(or_net *net, or_layer *l, or_state st)
     switch (l->type) {
     case L_CONV: conv_forward(net, l, st); break;
     case L_MAXPOOL:
-        or_maxpool_forward(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride,
-                           l->pad, l->output, l->indexes);
+        or_maxpool_forward_xy(st.input, l->batch, l->c, l->h, l->w, l->size, l->stride,
+                              l->stride_y, l->pad, l->output, l->indexes);
         break;
     case L_AVGPOOL:
         or_avgpool_forward(st.input, l->batch, l->c, l->h * l->w, l->output);

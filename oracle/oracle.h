@@ -54,7 +54,8 @@ void or_col2im(const float *col, int channels, int height, int width,
 /* ---- convolution GEMM parts of ConvolutionalLayer (groups=1, dilation=1) - */
 typedef struct {
     int batch, c, h, w;      /* input  [batch][c][h][w]   */
-    int n, size, stride, pad;/* filters, kernel, stride, padding */
+    int n, size, stride, pad;/* filters, kernel, stride (= stride_x), padding */
+    int stride_y;            /* height stride; 0: the same as stride       */
 } or_conv_shape;
 int  or_conv_out_h(const or_conv_shape *s);
 int  or_conv_out_w(const or_conv_shape *s);
@@ -112,6 +113,10 @@ int  or_maxpool_out(int in, int size, int stride, int padding);
 void or_maxpool_forward(const float *in, int batch, int c, int h, int w,
                         int size, int stride, int padding,
                         float *out, int *indexes);
+/* the same scan with a width stride stride_x and a height stride stride_y
+ * (out w = (w + padding - size)/stride_x + 1, h likewise with stride_y)    */
+void or_maxpool_forward_xy(const float *in, int batch, int c, int h, int w, int size,
+                           int stride_x, int stride_y, int padding, float *out, int *indexes);
 void or_maxpool_backward(const float *delta_out, const int *indexes, int n_out,
                          float *delta_in);
 
@@ -165,6 +170,11 @@ int  or_net_add_conv(or_net *net, int filters, int size, int stride, int pad,
 /* fully connected: previous output flattened to c*h*w, then a 1x1 conv   */
 int  or_net_add_connected(or_net *net, int outputs, int activation, int batch_normalize);
 int  or_net_add_maxpool(or_net *net, int size, int stride, int padding);
+/* separate width / height strides (createConvolutional / createMaxPool,
+ * NetworkFactory.c:83-90, 545-546: the layer's stride is stride_x)          */
+int  or_net_add_conv_xy(or_net *net, int filters, int size, int stride_x, int stride_y, int pad,
+                        int activation, int batch_normalize);
+int  or_net_add_maxpool_xy(or_net *net, int size, int stride_x, int stride_y, int padding);
 int  or_net_add_avgpool(or_net *net);
 int  or_net_add_dropout(or_net *net, float probability);
 int  or_net_add_softmax(or_net *net, int groups, float temperature);

@@ -16,7 +16,7 @@ _vp, _i, _f, _sz, _u64, _u32 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_u
 
 class OrConvShape(C.Structure):
     _fields_ = [("batch", _i), ("c", _i), ("h", _i), ("w", _i), ("n", _i), ("size", _i),
-                ("stride", _i), ("pad", _i)]
+                ("stride", _i), ("pad", _i), ("stride_y", _i)]
 
 
 _SIGS = {
@@ -43,6 +43,7 @@ _SIGS = {
     "or_gradient": (None, [_vp, _i, _i, _vp]),
     "or_maxpool_out": (_i, [_i, _i, _i, _i]),
     "or_maxpool_forward": (None, [_vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "or_maxpool_forward_xy": (None, [_vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "or_maxpool_backward": (None, [_vp, _vp, _i, _vp]),
     "or_avgpool_forward": (None, [_vp, _i, _i, _i, _vp]),
     "or_avgpool_backward": (None, [_vp, _i, _i, _i, _vp]),
@@ -58,6 +59,8 @@ _SIGS = {
     "or_net_add_conv": (_i, [_vp, _i, _i, _i, _i, _i, _i]),
     "or_net_add_connected": (_i, [_vp, _i, _i, _i]),
     "or_net_add_maxpool": (_i, [_vp, _i, _i, _i]),
+    "or_net_add_conv_xy": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i]),
+    "or_net_add_maxpool_xy": (_i, [_vp, _i, _i, _i, _i]),
     "or_net_add_avgpool": (_i, [_vp]),
     "or_net_add_dropout": (_i, [_vp, _f]),
     "or_net_add_softmax": (_i, [_vp, _i, _f]),
@@ -132,13 +135,14 @@ def gemm(TA, TB, M, N, K, alpha, A, lda, B, ldb, beta, Cm, ldc):
     return Cm
 
 
-def conv_shape(batch, c, h, w, n, size, stride, pad):
-    return OrConvShape(batch, c, h, w, n, size, stride, pad)
+def conv_shape(batch, c, h, w, n, size, stride, pad, stride_y=0):
+    """stride: the width stride; stride_y 0: the same as stride"""
+    return OrConvShape(batch, c, h, w, n, size, stride, pad, stride_y)
 
 
-def conv_forward(x, w, n, size, stride, pad):
+def conv_forward(x, w, n, size, stride, pad, stride_y=0):
     B, Cc, H, W = x.shape
-    s = conv_shape(B, Cc, H, W, n, size, stride, pad)
+    s = conv_shape(B, Cc, H, W, n, size, stride, pad, stride_y)
     oh, ow = lib().or_conv_out_h(C.byref(s)), lib().or_conv_out_w(C.byref(s))
     y = np.zeros((B, n, oh, ow), np.float32)
     ws = np.zeros(max(1, lib().or_conv_workspace_floats(C.byref(s))), np.float32)
@@ -146,10 +150,10 @@ def conv_forward(x, w, n, size, stride, pad):
     return y
 
 
-def conv_backward(x, dy, w, size, stride, pad, dw0=None, want_dx=True):
+def conv_backward(x, dy, w, size, stride, pad, dw0=None, want_dx=True, stride_y=0):
     B, Cc, H, W = x.shape
     n = dy.shape[1]
-    s = conv_shape(B, Cc, H, W, n, size, stride, pad)
+    s = conv_shape(B, Cc, H, W, n, size, stride, pad, stride_y)
     dw = np.zeros(w.shape, np.float32) if dw0 is None else f32(dw0).copy()
     dx = np.zeros(x.shape, np.float32) if want_dx else None
     ws = np.zeros(max(1, lib().or_conv_workspace_floats(C.byref(s))), np.float32)
@@ -219,13 +223,19 @@ def gradient(y, act, delta):
     return d
 
 
-def maxpool_forward(x, size, stride, pad):
+def maxpool_forward(x, size, stride, pad, stride_y=None):
+    """stride: the width stride; stride_y (default: stride) the height one"""
     B, Cc, H, W = x.shape
-    oh = lib().or_maxpool_out(H, size, stride, pad)
+    sy = stride if stride_y is None else stride_y
+    oh = lib().or_maxpool_out(H, size, sy, pad)
     ow = lib().or_maxpool_out(W, size, stride, pad)
     out = np.zeros((B, Cc, oh, ow), np.float32)
     idx = np.zeros((B, Cc, oh, ow), np.int32)
-    lib().or_maxpool_forward(P(f32(x)), B, Cc, H, W, size, stride, pad, P(out), P(idx))
+    if stride_y is None:
+        lib().or_maxpool_forward(P(f32(x)), B, Cc, H, W, size, stride, pad, P(out), P(idx))
+    else:
+        lib().or_maxpool_forward_xy(P(f32(x)), B, Cc, H, W, size, stride, sy, pad, P(out),
+                                    P(idx))
     return out, idx
 
 
@@ -288,8 +298,12 @@ class OracleNet:
         self.h = self.L.or_net_create(batch, h, w, c)
         self.batch = batch
 
-    def conv(self, filters, size, stride, pad, act, bn):
-        r = self.L.or_net_add_conv(self.h, filters, size, stride, pad, act, int(bn))
+    def conv(self, filters, size, stride, pad, act, bn, stride_y=None):
+        if stride_y is None:
+            r = self.L.or_net_add_conv(self.h, filters, size, stride, pad, act, int(bn))
+        else:
+            r = self.L.or_net_add_conv_xy(self.h, filters, size, stride, stride_y, pad, act,
+                                          int(bn))
         assert r >= 0
         return r
 
@@ -298,8 +312,11 @@ class OracleNet:
         assert r >= 0
         return r
 
-    def maxpool(self, size, stride, padding):
-        r = self.L.or_net_add_maxpool(self.h, size, stride, padding)
+    def maxpool(self, size, stride, padding, stride_y=None):
+        if stride_y is None:
+            r = self.L.or_net_add_maxpool(self.h, size, stride, padding)
+        else:
+            r = self.L.or_net_add_maxpool_xy(self.h, size, stride, stride_y, padding)
         assert r >= 0
         return r
 

@@ -3,22 +3,25 @@ GPU parity tests (independent of both implementations)."""
 import numpy as np
 
 
-def conv_ref(x, w, s, p):
+# s is the width stride and sy the height stride (default: s)
+def conv_ref(x, w, s, p, sy=None):
+    sy = s if sy is None else sy
     x = x.astype(np.float64)
     w = w.astype(np.float64)
     B, Cc, H, W = x.shape
     F, _, k, _ = w.shape
-    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    OH, OW = (H + 2 * p - k) // sy + 1, (W + 2 * p - k) // s + 1
     xp = np.pad(x, ((0, 0), (0, 0), (p, p), (p, p)))
     out = np.zeros((B, F, OH, OW))
     for ki in range(k):
         for kj in range(k):
-            patch = xp[:, :, ki:ki + s * (OH - 1) + 1:s, kj:kj + s * (OW - 1) + 1:s]
+            patch = xp[:, :, ki:ki + sy * (OH - 1) + 1:sy, kj:kj + s * (OW - 1) + 1:s]
             out += np.einsum("bchw,fc->bfhw", patch, w[:, :, ki, kj])
     return out
 
 
-def dgrad_ref(dy, w, xshape, s, p):
+def dgrad_ref(dy, w, xshape, s, p, sy=None):
+    sy = s if sy is None else sy
     dy = dy.astype(np.float64)
     w = w.astype(np.float64)
     B, Cc, H, W = xshape
@@ -27,12 +30,13 @@ def dgrad_ref(dy, w, xshape, s, p):
     dxp = np.zeros((B, Cc, H + 2 * p, W + 2 * p))
     for ki in range(k):
         for kj in range(k):
-            dxp[:, :, ki:ki + s * (OH - 1) + 1:s, kj:kj + s * (OW - 1) + 1:s] += \
+            dxp[:, :, ki:ki + sy * (OH - 1) + 1:sy, kj:kj + s * (OW - 1) + 1:s] += \
                 np.einsum("bfhw,fc->bchw", dy, w[:, :, ki, kj])
     return dxp[:, :, p:p + H, p:p + W]
 
 
-def wgrad_ref(x, dy, k, s, p):
+def wgrad_ref(x, dy, k, s, p, sy=None):
+    sy = s if sy is None else sy
     x = x.astype(np.float64)
     dy = dy.astype(np.float64)
     B, Cc, H, W = x.shape
@@ -41,7 +45,7 @@ def wgrad_ref(x, dy, k, s, p):
     dw = np.zeros((F, Cc, k, k))
     for ki in range(k):
         for kj in range(k):
-            patch = xp[:, :, ki:ki + s * (OH - 1) + 1:s, kj:kj + s * (OW - 1) + 1:s]
+            patch = xp[:, :, ki:ki + sy * (OH - 1) + 1:sy, kj:kj + s * (OW - 1) + 1:s]
             dw[:, :, ki, kj] = np.einsum("bfhw,bchw->fc", dy, patch)
     return dw
 

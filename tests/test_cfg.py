@@ -60,26 +60,37 @@ def test_flipped_only_on_convolutional(tmp_path):
     net.close()
 
 
-@pytest.mark.parametrize("keys,ok,stride", [
-    ("stride_x=2\nstride_y=2\n", True, 2),        # both given and equal: used
-    ("stride=2\n", True, 2),
-    ("stride_x=2\nstride_y=1\n", False, None),    # non-square: not built
-    ("stride_x=2\n", False, None),                # stride_y falls back to stride = 1
-    ("stride=2\nstride_x=2\n", True, 2),          # stride_y falls back to stride = 2
+# (keys, stride_x, stride_y) as createConvolutional resolves them
+# (NetworkFactory.c:83-90): a missing or nonpositive one falls back to stride
+@pytest.mark.parametrize("keys,sx,sy", [
+    ("stride_x=2\nstride_y=2\n", 2, 2),
+    ("stride=2\n", 2, 2),
+    ("stride_x=2\nstride_y=1\n", 2, 1),
+    ("stride_x=2\n", 2, 1),                      # stride_y falls back to stride = 1
+    ("stride=2\nstride_x=2\n", 2, 2),            # stride_y falls back to stride = 2
+    ("stride=3\nstride_y=0\nstride_x=1\n", 1, 3),
 ])
-def test_conv_stride_xy(tmp_path, keys, ok, stride):
+def test_conv_stride_xy(tmp_path, keys, sx, sy):
     net = parse(tmp_path, NET + "[convolutional]\nfilters=4\nsize=3\npad=1\n" + keys + TAIL)
-    assert (net is not None) == ok
-    if net is not None:
-        assert net.shape(0)[2] == (8 + 2 - 3) // stride + 1
-        net.close()
-
-
-def test_maxpool_stride_xy(tmp_path):
-    net = parse(tmp_path, NET + CONV + "[maxpool]\nsize=2\nstride_x=2\nstride_y=2\n" + TAIL)
-    assert net is not None and net.shape(1)[2] == 4  # stride 1 -> 2 by stride_x/y
+    assert net is not None
+    assert net.shape(0)[2:4] == [(8 + 2 - 3) // sy + 1, (8 + 2 - 3) // sx + 1]
     net.close()
-    assert parse(tmp_path, NET + CONV + "[maxpool]\nsize=2\nstride=2\nstride_y=1\n" + TAIL) is None
+
+
+# (keys, out_h, out_w) on the 8x8 conv output, createMaxPool's keys
+# (NetworkFactory.c:544-547): stride_x / stride_y default to stride, size to
+# the stride key, padding to size - 1
+@pytest.mark.parametrize("keys,oh,ow", [
+    ("size=2\nstride_x=2\nstride_y=2\n", 4, 4),
+    ("size=2\nstride=2\nstride_y=1\n", 8, 4),
+    ("stride_x=2\nstride_y=3\n", 3, 4),         # size 1 (the stride key), padding 0
+    ("size=3\nstride=1\nstride_x=2\n", 8, 4),
+])
+def test_maxpool_stride_xy(tmp_path, keys, oh, ow):
+    net = parse(tmp_path, NET + CONV + "[maxpool]\n" + keys + TAIL)
+    assert net is not None and net.shape(1)[2:4] == [oh, ow]
+    net.close()
+    assert parse(tmp_path, NET + CONV + "[maxpool]\nsize=2\nstride_x=0\n" + TAIL) is None
 
 
 @pytest.mark.parametrize("section,key", [

@@ -56,20 +56,21 @@ def dw_truth(onet, name, i, batch, delta_in, x_img):
     _, F, OH, OW, Cin, H, W, _ = onet.info(i)
     layer = configs.CONFIGS[name]["layers"][i]
     if layer[0] == "connected":  # a 1x1 convolution of the flattened input
-        (_, f, act, bn), k, s, p = layer, 1, 1, 0
+        (_, f, act, bn), k, s, p, sy = layer, 1, 1, 0, 1
     else:
-        _, f, k, s, p, act, bn = layer
+        _, f, k, s, p, act, bn = layer[:7]
+        sy = layer[7] if len(layer) > 7 else s
     shp = (batch, F, OH, OW)
     d64, _ = bn_backward_ref(delta_in.reshape(shp), onet.buffer(i, 0).reshape(shp),
                              onet.buffer(i, 12).reshape(shp), onet.buffer(i, 10),
                              onet.buffer(i, 11), onet.buffer(i, 6),
                              act_leaky=(act == configs.LEAKY))
     inp = x_img if i == 0 else onet.buffer(owner(onet, i - 1), 0).reshape(batch, Cin, H, W)
-    return wgrad_ref(inp, d64, k, s, p).ravel()
+    return wgrad_ref(inp, d64, k, s, p, sy=sy).ravel()
 
 
 @pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("alexnet", 2),
-                                        ("fcnet", 16)])
+                                        ("fcnet", 16), ("stridenet", 16)])
 def test_teacher_forced_layers(gpu, oracle, name, batch):
     """Every layer of one training step, fed the oracle's exact inputs and
     state (layer input, incoming delta, BN statistics, argmax indices):
@@ -148,7 +149,8 @@ def test_teacher_forced_layers(gpu, oracle, name, batch):
     print(name, {k: f"{v:.1e}" for k, v in errs.items()})
 
 
-@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("fcnet", 16)])
+@pytest.mark.parametrize("name,batch", [("tiny", 128), ("darknet", 8), ("fcnet", 16),
+                                        ("stridenet", 16)])
 def test_free_running_step(gpu, oracle, name, batch):
     """One untaught step: loss within 1e-3 and predicted labels agree."""
     oracle.lib().or_set_gemm_parallel(1)

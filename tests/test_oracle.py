@@ -108,6 +108,36 @@ def test_conv_backward_vs_direct_and_adjoint(shape):
     assert abs(ip - float((w.astype(np.float64) * (dw - dw0)).sum())) <= 1e-4 * abs(ip) + 1e-4
 
 
+# unequal width / height strides (B, C, H, W, F, k, stride_x, stride_y, pad): the
+# last is a 1x1 filter with stride_x 1, which the reference's forward would
+# read as unstrided (ConvolutionalLayer.c:788 tests stride_x alone)
+SHAPES_XY = [(2, 3, 9, 8, 4, 3, 2, 1, 1), (1, 2, 11, 7, 3, 5, 1, 3, 2),
+             (1, 3, 12, 10, 5, 4, 3, 2, 1), (2, 2, 7, 7, 3, 1, 1, 2, 0)]
+
+
+@pytest.mark.parametrize("shape", SHAPES_XY)
+def test_conv_unequal_strides_vs_direct_and_adjoint(shape):
+    B, Cc, H, W, F, k, sx, sy, p = shape
+    rng = np.random.default_rng(sum(shape) + 7)
+    x = rng.uniform(-1, 1, (B, Cc, H, W)).astype(np.float32)
+    w = rng.standard_normal((F, Cc, k, k)).astype(np.float32)
+    y = O.conv_forward(x, w, F, k, sx, p, stride_y=sy)
+    ref = conv_ref(x, w, sx, p, sy=sy)
+    assert y.shape == ref.shape == (B, F, (H + 2 * p - k) // sy + 1, (W + 2 * p - k) // sx + 1)
+    assert rel_err(y, ref) < 1e-6
+    dy = rng.standard_normal(y.shape).astype(np.float32)
+    dw, dx = O.conv_backward(x, dy, w, k, sx, p, stride_y=sy)
+    assert rel_err(dw, wgrad_ref(x, dy, k, sx, p, sy=sy)) < 1e-6
+    assert rel_err(dx, dgrad_ref(dy, w, x.shape, sx, p, sy=sy)) < 1e-6
+    ip = float((ref * dy).sum())
+    assert abs(ip - float((x.astype(np.float64) * dx).sum())) <= 1e-5 * abs(ip) + 1e-5
+    assert abs(ip - float((w.astype(np.float64) * dw).sum())) <= 1e-4 * abs(ip) + 1e-4
+    # the transposed problem: strides and axes swapped give the transposed result
+    yt = O.conv_forward(np.ascontiguousarray(x.transpose(0, 1, 3, 2)),
+                        np.ascontiguousarray(w.transpose(0, 1, 3, 2)), F, k, sy, p, stride_y=sx)
+    assert rel_err(yt.transpose(0, 1, 3, 2), ref) < 1e-6
+
+
 # ---- bias ------------------------------------------------------------------------
 def test_bias_add_and_grad():
     rng = np.random.default_rng(4)
@@ -200,12 +230,16 @@ def test_activations_exact():
 
 
 # ---- pooling -------------------------------------------------------------------------
-@pytest.mark.parametrize("B,Cc,H,W,size,stride,pad", [(2, 2, 6, 6, 2, 2, 1), (1, 2, 9, 9, 3, 2, 0),
-                                                       (1, 1, 5, 7, 3, 2, 2)])
-def test_maxpool_brute_force(B, Cc, H, W, size, stride, pad):
+# (stride, stride_y): stride_y None takes or_maxpool_forward, else the _xy scan
+@pytest.mark.parametrize("B,Cc,H,W,size,stride,sy,pad", [
+    (2, 2, 6, 6, 2, 2, None, 1), (1, 2, 9, 9, 3, 2, None, 0), (1, 1, 5, 7, 3, 2, None, 2),
+    (2, 2, 7, 9, 3, 2, 1, 2), (1, 3, 10, 6, 2, 1, 3, 1), (2, 1, 8, 8, 3, 3, 2, 0)])
+def test_maxpool_brute_force(B, Cc, H, W, size, stride, sy, pad):
     rng = np.random.default_rng(H + size)
     x = rng.integers(-2, 3, (B, Cc, H, W)).astype(np.float32)  # ties
-    out, idx = O.maxpool_forward(x, size, stride, pad)
+    out, idx = O.maxpool_forward(x, size, stride, pad, stride_y=sy)
+    sy = stride if sy is None else sy
+    assert out.shape[2:] == ((H + pad - size) // sy + 1, (W + pad - size) // stride + 1)
     OH, OW = out.shape[2:]
     off = -(pad // 2)
     flat = x.ravel()
@@ -216,7 +250,7 @@ def test_maxpool_brute_force(B, Cc, H, W, size, stride, pad):
                     best, bi = -np.finfo(np.float32).max, -1
                     for n in range(size):
                         for m in range(size):
-                            h, w = off + i * stride + n, off + j * stride + m
+                            h, w = off + i * sy + n, off + j * stride + m
                             if 0 <= h < H and 0 <= w < W:
                                 k = ((b * Cc + c) * H + h) * W + w
                                 if flat[k] > best:  # strict: first max wins
