@@ -115,6 +115,40 @@ def test_layer_constructors_reject_bad_shapes():
     assert lib.an_network_create(0, 4, 4, 3) is None
 
 
+def test_unequal_strides_shapes_and_errors():
+    """Width / height strides on the host: output sizes
+    (ConvolutionalLayer.c:337-344, MaxPoolLayer.c:40-41), the per-image
+    column buffer as every workspace, and the builders' argument checks."""
+    ops = aetcnn.ops()
+    d = aetcnn.ConvDesc(4, 5, 13, 10, 6, 3, 2, 1, 3)  # stride_x 2, stride_y 3
+    oh, ow = (13 + 2 - 3) // 3 + 1, (10 + 2 - 3) // 2 + 1
+    assert (ops.ach_conv_out_h(C.byref(d)), ops.ach_conv_out_w(C.byref(d))) == (oh, ow)
+    col = 5 * 9 * oh * ow * 4
+    for q in (ops.ach_conv_fwd_workspace, ops.ach_conv_bwd_data_workspace,
+              ops.ach_conv_bwd_filter_workspace):
+        assert q(C.byref(d)) == col
+    assert ops.ach_conv_bwd_data_reads_w(C.byref(d)) == 1
+    assert ops.ach_conv_is_fully_connected(C.byref(d)) == 0
+    # stride_y 0 or equal to stride: the square-stride descriptor, unchanged
+    for sy in (0, 2):
+        e = aetcnn.ConvDesc(4, 5, 13, 10, 6, 3, 2, 1, sy)
+        sq = aetcnn.ConvDesc(4, 5, 13, 10, 6, 3, 2, 1)
+        assert ops.ach_conv_out_h(C.byref(e)) == (13 + 2 - 3) // 2 + 1
+        assert ops.ach_conv_fwd_workspace(C.byref(e)) == ops.ach_conv_fwd_workspace(C.byref(sq))
+    assert ops.ach_conv_out_h(C.byref(aetcnn.ConvDesc(4, 5, 13, 10, 6, 3, 2, 1, -1))) == -1
+    lib = aetcnn.net_lib()
+    h = lib.an_network_create(2, 12, 20, 3)
+    assert lib.an_add_convolutional_xy(h, 8, 3, 0, 1, 1, aetcnn.LEAKY, 1) == aetcnn.ACH_EINVAL
+    assert lib.an_add_convolutional_xy(h, 8, 3, 2, 0, 1, aetcnn.LEAKY, 1) == aetcnn.ACH_EINVAL
+    assert lib.an_add_convolutional_xy(h, 8, 3, 2, 1, 1, aetcnn.LEAKY, 1) == 0   # 12 x 10
+    assert lib.an_add_maxpool_xy(h, 2, 1, 0, 1) == aetcnn.ACH_EINVAL
+    assert lib.an_add_maxpool_xy(h, 3, 1, 2, 2) == 1                           # 6 x 10
+    shape = (C.c_int * 8)()
+    assert lib.an_layer_shape(h, 0, shape) == 0 and list(shape)[1:4] == [8, 12, 10]
+    assert lib.an_layer_shape(h, 1, shape) == 0 and list(shape)[1:4] == [8, 6, 10]
+    lib.an_free(h)
+
+
 def test_cfg_parser_error_paths(tmp_path):
     lib = aetcnn.net_lib()
     assert lib.an_parse_cfg(str(tmp_path / "missing.cfg").encode()) is None
