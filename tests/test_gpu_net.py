@@ -253,7 +253,7 @@ def test_alexnet_step(gpu, oracle):
         assert abs(l_gpu - l_ref) <= 1e-3 * max(1, abs(l_ref)), (step, l_gpu, l_ref)
 
 
-@pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8)])
+@pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8), ("stridenet", 16)])
 def test_predict_matches_oracle(gpu, oracle, name, batch):
     """NNetwork.predict (inference: BN on rolling statistics, dropout off):
     after the oracle trains 3 steps, its parameters and rolling statistics are
@@ -285,7 +285,7 @@ def test_predict_matches_oracle(gpu, oracle, name, batch):
     onet.close()
 
 
-@pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8)])
+@pytest.mark.parametrize("name,batch", [("tiny", 16), ("darknet", 8), ("stridenet", 16)])
 def test_fused_predict_matches_oracle(gpu, oracle, name, batch, tmp_path):
     """NNetwork.fuseConvBatchnorm then predict: the oracle's trained parameters
     are loaded into the GPU network, both sides fold; the folded filters and
@@ -445,7 +445,8 @@ def test_cfg_policy_keys(gpu, oracle, tmp_path):
 
 
 @pytest.mark.parametrize("name,batch,steps", [("tiny", 32, 3), ("darknet", 8, 1),
-                                              ("alexnet", 2, 1), ("fcnet", 16, 1)])
+                                              ("alexnet", 2, 1), ("fcnet", 16, 1),
+                                              ("stridenet", 16, 2)])
 def test_train_step_updates_like_separate_update(gpu, name, batch, steps):
     """an_train_step updates each layer right after its gradients (on the
     weight-gradient stream); the parameters equal, bit for bit, those of
