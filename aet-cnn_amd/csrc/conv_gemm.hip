@@ -764,9 +764,29 @@ struct BWgrad {
 // floats): a thread writes its 16-position run along one row, and a
 // fragment's two k-steps are a fixed small offset apart, so the loop reads
 // them without address arithmetic.
-template <int BM, int BK_>
+// Row of element i of thread t when the rows a store instruction writes are
+// spread (SPREAD): the four 16-lane groups of a wave take rows 16 apart, so
+// at 17 floats per row their 16-bank runs tile the 64 banks (and each
+// half-wave's two runs the 32) instead of meeting on a bank, as the four
+// consecutive rows of the plain order do.
+template <int R>
+__device__ __forceinline__ int kc_spread_row(int t, int i)
+{
+    static_assert(R % 4 == 0, "four rows per thread per 64 rows");
+    return (t >> 6) + 4 * (i & 3) + 16 * ((t >> 4) & 3) + 64 * (i >> 2);
+}
+
+template <int BM, int BK_, bool SPREAD = false>
 struct AWgradC {
     static constexpr int BK = BK_, RPI = GNT / BK, RA = BM / RPI, PAD = WG_PAD;
+    // tile row of element i of thread t
+    __device__ __forceinline__ static int row(int t, int i)
+    {
+        if constexpr (SPREAD)
+            return kc_spread_row<RA>(t, i);
+        else
+            return t / BK + RPI * i;
+    }
     static constexpr bool KC = true;  // stored as S[m][k]
     static_assert(BK == 16, "one 16-position chunk per k-tile");
     __amdgpu_buffer_rsrc_t rs;
@@ -783,7 +803,7 @@ struct AWgradC {
         const int p = fdiv(kb >> 4, db) * 16 + tid % BK;
 #pragma unroll
         for (int i = 0; i < RA; ++i) {
-            const int m = m0 + tid / BK + RPI * i;
+            const int m = m0 + row(tid, i);
             voff[i] = m < M && p < ohw ? (unsigned)(m * ohw + p) * 4u : kOOB;
         }
     }
@@ -798,9 +818,9 @@ struct AWgradC {
     template <int LD>
     __device__ __forceinline__ void store(float (*S)[LD], const float *ra) const
     {
-        const int r = threadIdx.x / BK, kc = threadIdx.x % BK;
+        const int kc = threadIdx.x % BK;
 #pragma unroll
-        for (int i = 0; i < RA; ++i) S[r + RPI * i][kc] = ra[i];
+        for (int i = 0; i < RA; ++i) S[row(threadIdx.x, i)][kc] = ra[i];
     }
 };
 
@@ -1129,7 +1149,14 @@ struct WgradProblemC {
     static constexpr int kWPE = 4;  // waves per SIMD (k_mfma_gemm)
     static constexpr bool EARLY_B = false;  // (k_mfma_gemm's KB_STORE)
     static constexpr int BM = BM_, BN = BN_, BK = WGRAD_BK;
-    using AL = AWgradC<BM, BK>;
+    // the delta operand's stores spread over the banks for the 128 x 96
+    // tiles of 3x3 layers (darknet step 6.506-6.513 -> 6.426-6.427 ms and
+    // 6.593-6.607 -> 6.523-6.536 ms, three A/B rounds each on two boxes;
+    // alone 0.291 -> 0.293 ms).  Spreading AlexNet's tiles too made that
+    // step 0.7% slower, and spreading the im2col operand's stores as well
+    // (different channels' taps in one load instead of adjacent taps)
+    // gained less.
+    using AL = AWgradC<BM, BK, BN == 96 && KS_T == 3>;
     using BLd = BWgradC<BN, BK, KS_T>;
     const float *x, *dy;
     float *dw, *part;
